@@ -1,0 +1,224 @@
+/*
+ * yue2_hip.h -- C ABI of the MI355X (gfx950) decode library for YuE2's
+ * autoregressive token step.
+ *
+ * Two groups of entry points:
+ *
+ *  1. Drop-in twins of the reference's native decode bridge.  Each has the
+ *     same arguments, the same meaning and the same 1 = done / 0 = "not
+ *     done, fall back to the CPU" convention as the yue2_metal_* function it
+ *     replaces (declared at src/tensor.rs:91-220, implemented in
+ *     src/metal.m).  A Rust caller changes only the symbol prefix.
+ *
+ *  2. A device-resident session API for the fast path: weights uploaded
+ *     once, BF16 KV caches, positions, the RoPE table and the sampler state
+ *     stay in HBM; one captured hipGraph runs one token step, and only token
+ *     ids cross PCIe.  These mirror the Rust model-step API
+ *     (Model::forward / forward_phase / prefill_phase, Cache::new,
+ *     sampling::generate) and return 0 on success or a negative Yue2Error,
+ *     the codes standing for the reference's InvalidData messages
+ *     (src/lib.rs:14-18).
+ *
+ * All entry points are thread-safe: one library lock serialises them, as the
+ * reference's global NSLock does (src/metal.m:21).
+ */
+#ifndef YUE2_HIP_H
+#define YUE2_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* 1. Twins of the reference's native bridge                               */
+/* ---------------------------------------------------------------------- */
+
+/* GpuWeight / GpuLayer (src/tensor.rs:221-237 = src/metal.m:363-368).
+ * dtype: 0 BF16, 1 F32, 2 F16.  norms: input, q_norm, k_norm, post_attention.
+ * key/value: the host KV mirror, rows of kv*dim f32 (BF16-exact). */
+typedef struct Yue2GpuWeight {
+    const uint8_t *raw;
+    size_t mapping, rows, cols;
+    int32_t dtype, rounded;
+} Yue2GpuWeight;
+
+typedef struct Yue2GpuLayer {
+    Yue2GpuWeight weights[7]; /* q, k, v, o, gate, up, down */
+    const float *norms[4];
+    const float *key;
+    const float *value;
+} Yue2GpuLayer;
+
+/* yue2_metal_available (src/tensor.rs:118): 1 when a gfx950 device is usable. */
+int32_t yue2_hip_available(void);
+/* yue2_metal_vector_default (src/tensor.rs:119): 1 when the single-row GEMV
+ * path should be used by default (device memory >= 2 GiB). */
+int32_t yue2_hip_vector_default(void);
+/* yue2_metal_name (src/tensor.rs:193): device name, "CPU" without a device. */
+const char *yue2_hip_name(void);
+/* yue2_physical_memory (src/tensor.rs:131): host physical memory in bytes. */
+uint64_t yue2_physical_memory(void);
+
+/* yue2_metal_vector (src/tensor.rs:120-130; src/metal.m:545-603):
+ * out[r] = sum_c W[r,c] * input[c] for r < rows, f32 accumulation in the DOT
+ * order, NOT rounded (the caller's Linear::finish rounds).  Weights are
+ * uploaded on first use and cached under (mapping, raw, rows, cols, dtype).
+ * F32/F16 weights are accepted when rounded != 0 (they are rounded to BF16 on
+ * upload, as the reference's converted path does); otherwise returns 0. */
+int32_t yue2_hip_vector(const float *input, const uint8_t *raw, size_t mapping, int32_t dtype,
+                        int32_t rounded, int32_t priority, float *out, size_t rows, size_t cols);
+
+/* yue2_metal_ar_stack (src/tensor.rs:146-163; src/metal.m:718-874): one
+ * decode token through `count` AR layers.  input = embedded token (1 x hidden);
+ * out = hidden state before the final norm; shadow = per layer [K(kv*dim),
+ * V(kv*dim)] of the new token as f32; prefix = position; cos/sin = that
+ * position's RoPE row (dim/2 each); cache = the Rust Cache id.  The device KV
+ * context of (cache, layer) is mirrored from layers[i].key/value. */
+int32_t yue2_hip_ar_stack(const float *input, float *out, float *shadow,
+                          const Yue2GpuLayer *layers, size_t count, size_t hidden, size_t heads,
+                          size_t kv, size_t dim, size_t intermediate, size_t prefix,
+                          size_t capacity, size_t cache, float eps, const float *cos,
+                          const float *sin);
+
+/* yue2_metal_cached_attention (src/tensor.rs:181-192; src/metal.m:669-687):
+ * single-query GQA attention over `keys` rows of the host K/V mirror
+ * (rows of kv*dim f32); out = heads*dim, BF16-rounded. */
+int32_t yue2_hip_cached_attention(const float *q, const float *k, const float *v, float *out,
+                                  size_t keys, size_t heads, size_t kv, size_t dim, size_t cache,
+                                  size_t layer);
+
+/* Lifetime (src/tensor.rs:132-134; src/metal.m:73-103). */
+void yue2_hip_release_cache(size_t cache);
+void yue2_hip_clear_weights(void);
+void yue2_hip_release_model(void);
+
+/* ---------------------------------------------------------------------- */
+/* 2. Device-resident session API                                          */
+/* ---------------------------------------------------------------------- */
+
+typedef enum Yue2Error {
+    YUE2_OK = 0,
+    YUE2_ERR_CONTEXT = -1,  /* "AR input exceeds cache/model context" (src/model.rs:529) */
+    YUE2_ERR_TOKEN = -2,    /* "Token outside model vocabulary" (src/model.rs:457) */
+    YUE2_ERR_VOCAB = -3,    /* "Vocabulary does not support native music protocol" */
+    YUE2_ERR_LOGITS = -4,   /* "Model produced invalid logits" (src/sampling.rs:146) */
+    YUE2_ERR_EMPTY = -5,    /* "Empty sampling distribution" */
+    YUE2_ERR_SAMPLING = -6, /* "Invalid sampling configuration" (src/protocol.rs:191) */
+    YUE2_ERR_BUDGET = -7,   /* "Prefix + requested generation budget exceeds 24576" */
+    YUE2_ERR_GUIDANCE = -8, /* "Guidance requires negative prefix" */
+    YUE2_ERR_CODEC = -9,    /* "Incomplete codec vocabulary" */
+    YUE2_ERR_ALLOC = -10,   /* device or host allocation failed */
+    YUE2_ERR_CONFIG = -11,  /* "Invalid transformer configuration" (src/model.rs:71) */
+    YUE2_ERR_DEVICE = -12,  /* no usable device, or a HIP call failed */
+    YUE2_ERR_ARG = -13,     /* a null pointer or an unsupported shape */
+    YUE2_ERR_TIES = -14     /* top-k survivors exceed the device sort capacity */
+} Yue2Error;
+
+/* Phases of project_phase/choose (src/sampling.rs:81-99).  NONE is the full
+ * vocabulary with no end token (Model::forward), used by synthetic
+ * vocabularies smaller than the music protocol's ids. */
+enum { YUE2_PHASE_NONE = 0, YUE2_PHASE_ABC = 1, YUE2_PHASE_SEMANTIC = 2 };
+
+/* Config (src/model.rs:11-27). */
+typedef struct Yue2Config {
+    int32_t hidden_size, num_hidden_layers, num_attention_heads, num_key_value_heads;
+    int32_t head_dim, intermediate_size, vocab_size, max_position_embeddings;
+    float rms_norm_eps, rope_theta;
+} Yue2Config;
+
+/* One AR layer's host weights: BF16 matrices [out, in]; norm gammas as f32
+ * (rounded to BF16 on upload, Norm::new src/tensor.rs:1126-1136). */
+typedef struct Yue2LayerWeights {
+    const uint16_t *q_proj, *k_proj, *v_proj, *o_proj, *gate_proj, *up_proj, *down_proj;
+    const float *input_layernorm, *q_norm, *k_norm, *post_attention_layernorm;
+} Yue2LayerWeights;
+
+/* Sampling (src/protocol.rs:143-152). */
+typedef struct Yue2Sampling {
+    float temperature, top_p;
+    int32_t top_k;
+    float repetition_penalty;
+    int32_t penalty_window, min_tokens, max_tokens;
+} Yue2Sampling;
+
+typedef struct Yue2Model Yue2Model;
+typedef struct Yue2Cache Yue2Cache;
+typedef struct Yue2Decoder Yue2Decoder;
+
+/* Config::read validation (src/model.rs:50-72); 0 or YUE2_ERR_CONFIG. */
+int32_t yue2_hip_config_validate(const Yue2Config *c);
+
+/* Model::open (src/model.rs:418-451) from host arrays: the weights are copied
+ * into one HBM allocation and stay resident.  NULL on failure
+ * (yue2_hip_last_error tells why). */
+Yue2Model *yue2_hip_model_open(const Yue2Config *c, const uint16_t *embed_tokens,
+                               const uint16_t *lm_head, const float *final_norm,
+                               const Yue2LayerWeights *layers);
+/* Model's Drop (src/model.rs:411-416). */
+void yue2_hip_model_free(Yue2Model *m);
+
+/* Cache::new (src/model.rs:292-305): a device BF16 KV cache of `capacity`
+ * positions, layout [layers][K,V][kv_heads][capacity][head_dim]. */
+Yue2Cache *yue2_hip_cache_new(Yue2Model *m, int32_t capacity);
+void yue2_hip_cache_free(Yue2Cache *c);
+int32_t yue2_hip_cache_length(const Yue2Cache *c);
+
+/* Model::forward_phase (src/model.rs:465-477): run n ids through the model,
+ * appending to the cache; write the logits of the last row (vocab_size f32,
+ * BF16-exact) when logits != NULL. */
+int32_t yue2_hip_forward(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t n,
+                         int32_t phase, float *logits);
+/* Model::prefill_phase (src/model.rs:508-522) into an existing empty cache. */
+int32_t yue2_hip_prefill(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t n,
+                         int32_t phase, float *logits);
+
+/* A decode loop bound to one cache (batch 1) or to a conditional and an
+ * unconditional cache (CFG batch 2).  Each step is one hipGraph launch:
+ * embed -> layers -> LM head -> CFG mix -> choose -> next id.  The caches
+ * must already be prefilled; `first_logits` seeds step 0 (the prefill
+ * logits, rows x vocab f32, cond first).  sampling NULL means greedy argmax. */
+Yue2Decoder *yue2_hip_decoder_new(Yue2Model *m, Yue2Cache *cond, Yue2Cache *uncond,
+                                  const Yue2Sampling *sampling, uint64_t seed, int32_t phase,
+                                  float scale, int32_t legacy);
+void yue2_hip_decoder_free(Yue2Decoder *d);
+/* Run `steps` token steps.  tokens receives the chosen ids; step_ms (may be
+ * NULL) the per-step device time from HIP events.  Returns the number of
+ * steps run (it stops at the phase's end token) or a negative Yue2Error. */
+int32_t yue2_hip_decoder_run(Yue2Decoder *d, const float *first_logits, int32_t steps,
+                             int32_t *tokens, float *step_ms);
+
+/* sampling::generate (src/sampling.rs:222-294) on the device. */
+int32_t yue2_hip_generate(Yue2Model *m, const int32_t *prefix, int32_t prefix_len,
+                          const Yue2Sampling *sampling, uint64_t seed, int32_t phase,
+                          const int32_t *negative, int32_t negative_len, float scale,
+                          int32_t legacy, int32_t *tokens, int32_t *count, int32_t *truncated);
+
+/* Message of the last failure on this thread ("" if none). */
+const char *yue2_hip_last_error(void);
+/* Wait for all device work issued by the library. */
+int32_t yue2_hip_synchronize(void);
+
+/* ---------------------------------------------------------------------- */
+/* Support entry points (no counterpart in the reference)                  */
+/* ---------------------------------------------------------------------- */
+
+/* Synthetic checkpoint values: BF16 ~ N(0, stddev) from a counter-based
+ * generator (SplitMix64 + Box-Muller with the library's own log/sin/cos), so
+ * every machine produces the same bits.  Replaces the real checkpoint, which
+ * the reference downloads (src/checkpoint.rs:16-161).  threads <= 0: all. */
+void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t tensor,
+                             float stddev, int32_t threads);
+
+/* Diagnostics: evaluate a device math routine elementwise on host arrays
+ * (which: 0 exp f32, 1 log1p f64, 2 round_bf16, 3 SiLU).  Returns 0 or a
+ * negative Yue2Error. */
+int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
+/* Diagnostics: RMSNorm guard fallbacks taken since the model was opened. */
+int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,183 @@
+/*
+ * oracle.h -- CPU restatement of the YuE2 autoregressive decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (yue2_rs_amd/, include/)
+ * includes, links or loads this code.  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg use it, and only as the checker / the CPU
+ * baseline, never as the thing measured on the GPU.
+ *
+ * The reference (twally3/yue2_rs) is Rust + Apple Accelerate + Metal and
+ * cannot be built on Linux (build.rs:6-9).  This file restates its CPU token
+ * step (YUE2_BACKEND=cpu) operation by operation, keeping every BF16
+ * rounding point of src/tensor.rs, src/model.rs and src/sampling.rs.
+ * Accelerate's free reductions (cblas_sgemv/sgemm, vDSP_sve) are replaced by
+ * one documented order (the "order spec" below); vvexpf and f64::ln_1p are
+ * replaced by our own functions written from named methods.
+ *
+ * ORDER SPEC (shared with the HIP kernels; both sides implement it)
+ *   DOT(a, b, K)   K % 8 == 0.  Chunk c = elements [8c, 8c+8).  Chunk c
+ *                  belongs to lane c mod 64.  Each lane: acc = +0; for its
+ *                  chunks in ascending order, for e = 0..7:
+ *                  acc = fma(a[8c+e], b[8c+e], acc).  Then an xor butterfly
+ *                  over the 64 lanes with offsets 32,16,8,4,2,1:
+ *                  acc[l] = acc[l] + acc[l ^ s].  Result: acc[0].
+ *                  Used for every Linear row (cblas_sgemv/sgemm substitute,
+ *                  src/tensor.rs:847-883, 1026-1081) and for the attention
+ *                  scores q.K_j (src/model.rs:362-374).
+ *   SOFTMAX SUM    keys in blocks of 64 (block b = keys [64b, 64b+64));
+ *                  block sum = xor butterfly (32..1) over lane = key - 64b,
+ *                  missing keys = +0; total = ((blk0 + blk1) + blk2) + ...
+ *                  (vDSP_sve substitute, src/tensor.rs:721).
+ *   PV             per output dim d, block of 64 keys, S = 512/head_dim
+ *                  streams; key j of the block goes to stream (j-64b) mod S;
+ *                  stream: acc = +0, acc = fma(p_j, V[j,d], acc) ascending;
+ *                  streams combined by xor butterfly over the stream index
+ *                  with offsets S/2, ..., 1; blocks summed left to right
+ *                  (cblas_sgemv transpose substitute, src/model.rs:380-392).
+ *   RMSNorm sum    sequential f32 sum as the reference defines it
+ *                  (src/tensor.rs:1144, 1160): no substitute needed.
+ *
+ * Parity pins (what checks each function; see tests/):
+ *   round_bf16       closed form + exhaustive-in-sample check against numpy.
+ *   y2o_expf         equals the correctly rounded exp on all sampled inputs
+ *                    (numpy float64 exp rounded to f32) -- pins vvexpf and
+ *                    f32::exp up to their own (unpublished) ulp behaviour.
+ *   y2o_log1p        within 2 ulp of numpy log1p; the f32 cast equals.
+ *   DOT / linear     one-hot inputs, small-integer exactness, f64 bound.
+ *   norm             closed form on constant rows.
+ *   rotary           position 0 is the identity.
+ *   attention        the reference's own known-answer generator and
+ *                    tolerance (src/tensor.rs:9-83) against f64.
+ *   MT19937          std::mt19937 known answer (10000th draw of 5489).
+ *   choose           brute force on small vocabularies, greedy closed form.
+ *   Accelerate's exact summation order, macOS libm cos/sin/powf and the real
+ *   checkpoint's logits cannot be run here: parity with those is unpinned
+ *   beyond the checks above.
+ */
+#ifndef YUE2_ORACLE_H
+#define YUE2_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model configuration (src/model.rs:11-27). */
+typedef struct {
+    int32_t hidden, layers, heads, kv_heads, head_dim, intermediate, vocab;
+    int32_t max_pos;
+    float eps, theta;
+} y2o_config;
+
+/* One AR layer: BF16 matrices [out, in] row-major, norm gammas as f32
+ * (already BF16-rounded, src/tensor.rs:1126-1136). */
+typedef struct {
+    const uint16_t *q, *k, *v, *o, *gate, *up, *down;
+    const float *input_norm, *q_norm, *k_norm, *post_norm;
+} y2o_layer;
+
+typedef struct {
+    y2o_config c;
+    const uint16_t *embed;   /* [vocab, hidden] */
+    const uint16_t *lm_head; /* [vocab, hidden] */
+    const float *final_norm; /* [hidden] */
+    const y2o_layer *layers; /* [layers] */
+} y2o_model;
+
+/* Host KV mirror (src/model.rs:276-306): per layer f32 [capacity, kv*dim]. */
+typedef struct {
+    int32_t layers, width, capacity, length;
+    float *key;   /* [layers][capacity][width] */
+    float *value; /* [layers][capacity][width] */
+} y2o_cache;
+
+/* Sampling (src/protocol.rs:143-165). */
+typedef struct {
+    float temperature, top_p;
+    int32_t top_k;
+    float repetition_penalty;
+    int32_t penalty_window, min_tokens, max_tokens;
+} y2o_sampling;
+
+typedef struct {
+    uint32_t state[624];
+    int32_t next;
+} y2o_mt;
+
+enum { Y2O_PHASE_NONE = 0, Y2O_PHASE_ABC = 1, Y2O_PHASE_SEMANTIC = 2 };
+enum {
+    Y2O_OK = 0,
+    Y2O_ERR_CONTEXT = -1,   /* "AR input exceeds cache/model context" */
+    Y2O_ERR_TOKEN = -2,     /* "Token outside model vocabulary" */
+    Y2O_ERR_VOCAB = -3,     /* "Vocabulary does not support native music protocol" */
+    Y2O_ERR_LOGITS = -4,    /* "Model produced invalid logits" */
+    Y2O_ERR_EMPTY = -5,     /* "Empty sampling distribution" */
+    Y2O_ERR_SAMPLING = -6,  /* "Invalid sampling configuration" */
+    Y2O_ERR_BUDGET = -7,    /* "Prefix + requested generation budget exceeds 24576" */
+    Y2O_ERR_GUIDANCE = -8,  /* "Guidance requires negative prefix" */
+    Y2O_ERR_CODEC = -9,     /* "Incomplete codec vocabulary" */
+    Y2O_ERR_ALLOC = -10
+};
+
+void y2o_set_threads(int n);
+int y2o_get_threads(void);
+
+float y2o_round_bf16(float v);
+float y2o_bf16_to_f32(uint16_t b);
+float y2o_expf(float x);
+double y2o_log1p(double x);
+
+float y2o_dot_bf16(const uint16_t *a, const float *b, int k);
+float y2o_dot_f32(const float *a, const float *b, int k);
+/* y[r*out + i] = rb(DOT(W[i], x[r])) for r < rows (src/tensor.rs:946-1118) */
+void y2o_linear(const uint16_t *w, int out, int in, const float *x, int rows, float *y);
+/* out[i] = DOT(W[i], x) without rounding (yue2_metal_vector's contract) */
+void y2o_gemv_raw(const uint16_t *w, int rows, int cols, const float *x, float *out);
+
+float y2o_norm_scale(const float *x, int n, float eps);
+void y2o_norm_apply(const float *x, int rows, int n, const float *gamma, float eps, float *out);
+void y2o_norm_heads(float *x, int heads, int dim, const float *gamma, float eps);
+
+void y2o_rotary_table(int start, int rows, int head_dim, float theta, float *cos, float *sin);
+void y2o_rotary_apply(float *x, int rows, int cols, int half, const float *cos, const float *sin);
+
+/* Single-query GQA attention over `keys` cached rows; K/V rows have stride
+ * kv*dim (src/model.rs:313-397 with rows == 1). */
+void y2o_attention_row(const float *q, const float *key, const float *value, int keys,
+                       int heads, int kv, int dim, float *out);
+
+y2o_cache *y2o_cache_new(const y2o_config *c, int capacity);
+void y2o_cache_free(y2o_cache *cache);
+int y2o_cache_length(const y2o_cache *cache);
+
+/* Model::hidden (src/model.rs:523-591): x_out = final_norm(x) for all rows. */
+int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out);
+/* Model::forward (src/model.rs:465-468): logits of the last row. */
+int y2o_forward(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *logits);
+/* Model::forward_phase / project_phase (src/model.rs:469-507). */
+int y2o_forward_phase(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,
+                      int phase, float *logits);
+int y2o_project_phase(const y2o_model *m, const float *x, int phase, float *logits);
+/* Model::prefill (src/model.rs:592-610): 256-token chunks, logits of the last row. */
+int y2o_prefill(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *logits);
+
+void y2o_mt_seed(y2o_mt *g, uint64_t seed);
+uint32_t y2o_mt_next(y2o_mt *g);
+void y2o_mt_discard(y2o_mt *g, uint64_t count);
+double y2o_mt_uniform_f64(y2o_mt *g);
+
+void y2o_cfg_mix(const float *cond, const float *uncond, int n, float scale, float *out);
+int y2o_choose(const float *logits, int n, const y2o_sampling *s, const int32_t *history,
+               int history_len, int step, int phase, int legacy, y2o_mt *rng, int32_t *out);
+
+/* sampling::generate (src/sampling.rs:222-294).  negative may be NULL. */
+int y2o_generate(const y2o_model *m, const int32_t *prefix, int prefix_len,
+                 const y2o_sampling *s, uint64_t seed, int phase, const int32_t *negative,
+                 int negative_len, float scale, int legacy, int32_t *tokens, int *count,
+                 int *truncated);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,253 @@
+"""ctypes binding of the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker and the CPU baseline.  The
+product (yue2_rs_amd) never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "liboracle.so"
+
+PHASE_NONE, PHASE_ABC, PHASE_SEMANTIC = 0, 1, 2
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+class Config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "hidden", "layers", "heads", "kv_heads", "head_dim", "intermediate", "vocab", "max_pos")] + [
+        ("eps", C.c_float), ("theta", C.c_float)]
+
+
+class Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "q", "k", "v", "o", "gate", "up", "down", "input_norm", "q_norm", "k_norm", "post_norm")]
+
+
+class ModelS(C.Structure):
+    _fields_ = [("c", Config), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
+                ("final_norm", C.c_void_p), ("layers", C.POINTER(Layer))]
+
+
+class CacheS(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("width", C.c_int32), ("capacity", C.c_int32),
+                ("length", C.c_int32), ("key", C.POINTER(C.c_float)), ("value", C.POINTER(C.c_float))]
+
+
+class SamplingS(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32),
+                ("repetition_penalty", C.c_float), ("penalty_window", C.c_int32),
+                ("min_tokens", C.c_int32), ("max_tokens", C.c_int32)]
+
+
+class MT(C.Structure):
+    _fields_ = [("state", C.c_uint32 * 624), ("next", C.c_int32)]
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        vp, i32, f32, f64 = C.c_void_p, C.c_int32, C.c_float, C.c_double
+        sig = {
+            "y2o_set_threads": (None, [i32]),
+            "y2o_round_bf16": (f32, [f32]),
+            "y2o_expf": (f32, [f32]),
+            "y2o_log1p": (f64, [f64]),
+            "y2o_dot_bf16": (f32, [vp, vp, i32]),
+            "y2o_dot_f32": (f32, [vp, vp, i32]),
+            "y2o_linear": (None, [vp, i32, i32, vp, i32, vp]),
+            "y2o_gemv_raw": (None, [vp, i32, i32, vp, vp]),
+            "y2o_norm_scale": (f32, [vp, i32, f32]),
+            "y2o_norm_apply": (None, [vp, i32, i32, vp, f32, vp]),
+            "y2o_norm_heads": (None, [vp, i32, i32, vp, f32]),
+            "y2o_rotary_table": (None, [i32, i32, i32, f32, vp, vp]),
+            "y2o_rotary_apply": (None, [vp, i32, i32, i32, vp, vp]),
+            "y2o_attention_row": (None, [vp, vp, vp, i32, i32, i32, i32, vp]),
+            "y2o_cache_new": (C.POINTER(CacheS), [vp, i32]),
+            "y2o_cache_free": (None, [C.POINTER(CacheS)]),
+            "y2o_hidden": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
+            "y2o_forward": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
+            "y2o_forward_phase": (i32, [vp, C.POINTER(CacheS), vp, i32, i32, vp]),
+            "y2o_prefill": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
+            "y2o_mt_seed": (None, [vp, C.c_uint64]),
+            "y2o_mt_next": (C.c_uint32, [vp]),
+            "y2o_mt_discard": (None, [vp, C.c_uint64]),
+            "y2o_mt_uniform_f64": (f64, [vp]),
+            "y2o_cfg_mix": (None, [vp, vp, i32, f32, vp]),
+            "y2o_choose": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, vp, vp]),
+            "y2o_generate": (i32, [vp, vp, i32, vp, C.c_uint64, i32, vp, i32, f32, i32, vp, vp, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def set_threads(n: int) -> None:
+    lib().y2o_set_threads(n)
+
+
+class Model:
+    """Oracle model over the same host arrays the GPU model was opened from."""
+
+    def __init__(self, ckpt):
+        c = ckpt.config
+        self.config = c
+        self._ckpt = ckpt
+        self._layers = (Layer * c.num_hidden_layers)()
+        for i, w in enumerate(ckpt.layers):
+            L = self._layers[i]
+            L.q, L.k, L.v, L.o = _p(w.q_proj), _p(w.k_proj), _p(w.v_proj), _p(w.o_proj)
+            L.gate, L.up, L.down = _p(w.gate_proj), _p(w.up_proj), _p(w.down_proj)
+            L.input_norm, L.q_norm = _p(w.input_layernorm), _p(w.q_norm)
+            L.k_norm, L.post_norm = _p(w.k_norm), _p(w.post_attention_layernorm)
+        cfg = Config(c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads,
+                     c.head_dim, c.intermediate_size, c.vocab_size, c.max_position_embeddings,
+                     c.rms_norm_eps, c.rope_theta)
+        self._m = ModelS(cfg, _p(ckpt.embed_tokens), _p(ckpt.lm_head), _p(ckpt.final_norm), self._layers)
+
+    @property
+    def ref(self):
+        return C.byref(self._m)
+
+    def cache(self, capacity: int) -> "Cache":
+        return Cache(self, capacity)
+
+    def forward_phase(self, ids: Sequence[int], cache: "Cache", phase: int = PHASE_NONE) -> np.ndarray:
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.config.vocab_size, dtype=np.float32)
+        rc = lib().y2o_forward_phase(self.ref, cache.ptr, _p(arr), len(arr), phase, _p(out))
+        if rc:
+            raise RuntimeError(f"oracle error {rc}")
+        return out
+
+    def forward(self, ids, cache):
+        return self.forward_phase(ids, cache, PHASE_NONE)
+
+    def prefill(self, ids, capacity: int, phase: int = PHASE_NONE):
+        cache = Cache(self, capacity)
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.config.vocab_size, dtype=np.float32)
+        # chunks of 256 like Model::prefill_phase (src/model.rs:516)
+        rc = 0
+        for s in range(0, len(arr), 256):
+            chunk = np.ascontiguousarray(arr[s:s + 256])
+            rc = lib().y2o_forward_phase(self.ref, cache.ptr, _p(chunk), len(chunk), phase, _p(out))
+            if rc:
+                raise RuntimeError(f"oracle error {rc}")
+        return cache, out
+
+
+class Cache:
+    def __init__(self, model: Model, capacity: int):
+        self.ptr = lib().y2o_cache_new(C.byref(model._m.c), capacity)
+        if not self.ptr:
+            raise MemoryError("oracle cache")
+        self.capacity = capacity
+
+    @property
+    def length(self) -> int:
+        return self.ptr.contents.length
+
+    def keys(self, layer: int) -> np.ndarray:
+        c = self.ptr.contents
+        n = c.length * c.width
+        base = layer * c.capacity * c.width
+        return np.ctypeslib.as_array(c.key, shape=(c.layers * c.capacity * c.width,))[base:base + n].reshape(c.length, c.width)
+
+    def values(self, layer: int) -> np.ndarray:
+        c = self.ptr.contents
+        n = c.length * c.width
+        base = layer * c.capacity * c.width
+        return np.ctypeslib.as_array(c.value, shape=(c.layers * c.capacity * c.width,))[base:base + n].reshape(c.length, c.width)
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().y2o_cache_free(self.ptr)
+                self.ptr = None
+        except Exception:
+            pass
+
+
+class Generator:
+    """MT19937 of src/sampling.rs:10-63."""
+
+    def __init__(self, seed: int):
+        self._s = MT()
+        lib().y2o_mt_seed(C.byref(self._s), seed)
+
+    def next_u32(self) -> int:
+        return lib().y2o_mt_next(C.byref(self._s))
+
+    def discard(self, n: int) -> None:
+        lib().y2o_mt_discard(C.byref(self._s), n)
+
+    def uniform_f64(self) -> float:
+        return lib().y2o_mt_uniform_f64(C.byref(self._s))
+
+    @property
+    def ref(self):
+        return C.byref(self._s)
+
+
+def sampling(s) -> SamplingS:
+    return SamplingS(s.temperature, s.top_p, s.top_k, s.repetition_penalty, s.penalty_window,
+                     s.min_tokens, s.max_tokens)
+
+
+def choose(logits: np.ndarray, s, history: Sequence[int], step: int, phase: int, legacy: bool,
+           rng: Generator) -> int:
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    h = np.ascontiguousarray(history, dtype=np.int32)
+    out = C.c_int32(-1)
+    ss = sampling(s)
+    rc = lib().y2o_choose(_p(lg), len(lg), C.byref(ss), _p(h) if len(h) else None, len(h), step, phase,
+                          int(legacy), rng.ref, C.byref(out))
+    if rc:
+        raise RuntimeError(f"oracle choose error {rc}")
+    return out.value
+
+
+def cfg_mix(cond: np.ndarray, uncond: np.ndarray, scale: float) -> np.ndarray:
+    out = np.empty_like(cond)
+    lib().y2o_cfg_mix(_p(cond), _p(uncond), len(cond), scale, _p(out))
+    return out
+
+
+def generate(model: Model, prefix, s, seed: int, phase: int = PHASE_NONE, negative=None,
+             scale: float = 1.0, legacy: bool = False):
+    p = np.ascontiguousarray(prefix, dtype=np.int32)
+    n = None if negative is None else np.ascontiguousarray(negative, dtype=np.int32)
+    out = np.zeros(max(s.max_tokens, 1), dtype=np.int32)
+    count, trunc = C.c_int32(0), C.c_int32(0)
+    ss = sampling(s)
+    rc = lib().y2o_generate(model.ref, _p(p), len(p), C.byref(ss), seed, phase, _p(n),
+                            0 if n is None else len(n), scale, int(legacy), _p(out), C.byref(count),
+                            C.byref(trunc))
+    if rc:
+        raise RuntimeError(f"oracle generate error {rc}")
+    return out[:count.value].tolist(), bool(trunc.value)

@@ -1,0 +1,50 @@
+"""Full token step on the GPU against the oracle: logits bit-exact at every
+step, greedy ids equal, for the reduced config (256-token prompt, 64 greedy
+steps) and a short run of the 3B-class config."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yue2_rs_amd import synthetic
+import yue2_rs_amd as y2
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def reduced(gpu, oracle_threads):
+    ck = synthetic.checkpoint(synthetic.REDUCED, seed=0)
+    return ck, y2.Model.open(ck), O.Model(ck)
+
+
+def test_reduced_prefill_and_64_greedy_steps(reduced):
+    ck, gm, om = reduced
+    ids = synthetic.prompt(256, ck.config.vocab_size, seed=0)
+    gcache, glog = gm.prefill_phase(ids, 256 + 64)
+    ocache, olog = om.prefill(ids, 256 + 64)
+    assert np.array_equal(_bits(glog), _bits(olog)), "prefill logits differ"
+    for step in range(64):
+        gt, ot = int(np.argmax(glog)), int(np.argmax(olog))
+        assert gt == ot, f"greedy id differs at step {step}"
+        glog = gm.forward([gt], gcache)
+        olog = om.forward([ot], ocache)
+        assert np.array_equal(_bits(glog), _bits(olog)), f"logits differ at step {step}"
+    assert gcache.length == ocache.length == 256 + 64
+
+
+def test_3b_short_run_bit_exact(gpu, oracle_threads):
+    ck = synthetic.checkpoint(synthetic.CLASS_3B, seed=0)
+    gm, om = y2.Model.open(ck), O.Model(ck)
+    ids = synthetic.prompt(20, ck.config.vocab_size, seed=0)
+    gcache, glog = gm.prefill_phase(ids, 32)
+    ocache, olog = om.prefill(ids, 32)
+    assert np.array_equal(_bits(glog), _bits(olog))
+    for step in range(4):
+        t = int(np.argmax(olog))
+        glog, olog = gm.forward([t], gcache), om.forward([t], ocache)
+        assert np.array_equal(_bits(glog), _bits(olog)), f"3B logits differ at step {step}"
+    gm.close()

@@ -1,0 +1,343 @@
+"""Python binding of include/yue2_hip.h, shaped like the reference's Rust API.
+
+Model.open / Model.forward / Model.forward_phase / Model.prefill_phase /
+Cache / Sampling / generate mirror src/model.rs and src/sampling.rs; errors
+raise Yue2Error carrying the library's code and message (the reference's
+InvalidData errors).  Everything runs on the HIP library; there is no CPU
+path, and loading fails loudly when the library is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libyue2_hip.so"
+
+PHASE_NONE, PHASE_ABC, PHASE_SEMANTIC = 0, 1, 2
+ERRORS = {
+    -1: "AR input exceeds cache/model context",
+    -2: "Token outside model vocabulary",
+    -3: "Vocabulary does not support native music protocol",
+    -4: "Model produced invalid logits",
+    -5: "Empty sampling distribution",
+    -6: "Invalid sampling configuration",
+    -7: "Prefix + requested generation budget exceeds 24576",
+    -8: "Guidance requires negative prefix",
+    -9: "Incomplete codec vocabulary",
+    -10: "allocation failed",
+    -11: "Invalid transformer configuration",
+    -12: "device error",
+    -13: "invalid argument",
+    -14: "top-k survivors exceed the device sort capacity",
+}
+
+
+class Yue2Error(RuntimeError):
+    def __init__(self, code: int, message: str = ""):
+        self.code = code
+        super().__init__(f"{message or ERRORS.get(code, 'error')} (code {code})")
+
+
+class _Config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "hidden_size", "num_hidden_layers", "num_attention_heads", "num_key_value_heads",
+        "head_dim", "intermediate_size", "vocab_size", "max_position_embeddings")] + [
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class _LayerWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
+        "input_layernorm", "q_norm", "k_norm", "post_attention_layernorm")]
+
+
+class _Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32),
+                ("repetition_penalty", C.c_float), ("penalty_window", C.c_int32),
+                ("min_tokens", C.c_int32), ("max_tokens", C.c_int32)]
+
+
+class _GpuWeight(C.Structure):
+    _fields_ = [("raw", C.c_void_p), ("mapping", C.c_size_t), ("rows", C.c_size_t),
+                ("cols", C.c_size_t), ("dtype", C.c_int32), ("rounded", C.c_int32)]
+
+
+class _GpuLayer(C.Structure):
+    _fields_ = [("weights", _GpuWeight * 7), ("norms", C.c_void_p * 4), ("key", C.c_void_p),
+                ("value", C.c_void_p)]
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def lib() -> C.CDLL:
+    """Load libyue2_hip.so (built by yue2_rs_amd.build); raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise FileNotFoundError(f"{LIB_PATH} is missing: run python -m yue2_rs_amd.build")
+    L = C.CDLL(str(LIB_PATH))
+    vp, i32, u64, sz, f32 = C.c_void_p, C.c_int32, C.c_uint64, C.c_size_t, C.c_float
+    sig = {
+        "yue2_hip_available": (i32, []),
+        "yue2_hip_vector_default": (i32, []),
+        "yue2_hip_name": (C.c_char_p, []),
+        "yue2_physical_memory": (u64, []),
+        "yue2_hip_vector": (i32, [vp, vp, sz, i32, i32, i32, vp, sz, sz]),
+        "yue2_hip_ar_stack": (i32, [vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, sz, sz, f32, vp, vp]),
+        "yue2_hip_cached_attention": (i32, [vp, vp, vp, vp, sz, sz, sz, sz, sz, sz]),
+        "yue2_hip_release_cache": (None, [sz]),
+        "yue2_hip_clear_weights": (None, []),
+        "yue2_hip_release_model": (None, []),
+        "yue2_hip_config_validate": (i32, [vp]),
+        "yue2_hip_model_open": (vp, [vp, vp, vp, vp, vp]),
+        "yue2_hip_model_free": (None, [vp]),
+        "yue2_hip_cache_new": (vp, [vp, i32]),
+        "yue2_hip_cache_free": (None, [vp]),
+        "yue2_hip_cache_length": (i32, [vp]),
+        "yue2_hip_forward": (i32, [vp, vp, vp, i32, i32, vp]),
+        "yue2_hip_prefill": (i32, [vp, vp, vp, i32, i32, vp]),
+        "yue2_hip_decoder_new": (vp, [vp, vp, vp, vp, u64, i32, f32, i32]),
+        "yue2_hip_decoder_free": (None, [vp]),
+        "yue2_hip_decoder_run": (i32, [vp, vp, i32, vp, vp]),
+        "yue2_hip_generate": (i32, [vp, vp, i32, vp, u64, i32, vp, i32, f32, i32, vp, vp, vp]),
+        "yue2_hip_last_error": (C.c_char_p, []),
+        "yue2_hip_synchronize": (i32, []),
+        "yue2_hip_synthetic_bf16": (None, [vp, sz, u64, u64, f32, i32]),
+        "yue2_hip_selftest_math": (i32, [i32, vp, vp, sz]),
+        "yue2_hip_norm_fallbacks": (i32, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _ptr(a: Optional[np.ndarray]) -> Optional[int]:
+    return None if a is None else a.ctypes.data
+
+
+def _check(code: int) -> int:
+    if code < 0:
+        raise Yue2Error(code, lib().yue2_hip_last_error().decode())
+    return code
+
+
+def available() -> bool:
+    return bool(lib().yue2_hip_available())
+
+
+def synchronize() -> None:
+    _check(lib().yue2_hip_synchronize())
+
+
+@dataclass
+class Config:
+    """Config (src/model.rs:11-27) with the reference's defaults."""
+    hidden_size: int = 2048
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 6144
+    vocab_size: int = 184704
+    max_position_embeddings: int = 24576
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    def c(self) -> _Config:
+        return _Config(**{f: getattr(self, f) for f, _ in _Config._fields_})
+
+    def validate(self) -> None:
+        cfg = self.c()
+        _check(lib().yue2_hip_config_validate(C.byref(cfg)))
+
+
+@dataclass
+class Sampling:
+    """Sampling (src/protocol.rs:143-165) with Sampling::default values."""
+    temperature: float = 1.0
+    top_p: float = 0.95
+    top_k: int = 100
+    repetition_penalty: float = 1.2
+    penalty_window: int = 50
+    min_tokens: int = 200
+    max_tokens: int = 9000
+
+    def c(self) -> _Sampling:
+        return _Sampling(self.temperature, self.top_p, self.top_k, self.repetition_penalty,
+                         self.penalty_window, self.min_tokens, self.max_tokens)
+
+
+@dataclass
+class LayerWeights:
+    q_proj: np.ndarray
+    k_proj: np.ndarray
+    v_proj: np.ndarray
+    o_proj: np.ndarray
+    gate_proj: np.ndarray
+    up_proj: np.ndarray
+    down_proj: np.ndarray
+    input_layernorm: np.ndarray
+    q_norm: np.ndarray
+    k_norm: np.ndarray
+    post_attention_layernorm: np.ndarray
+
+
+@dataclass
+class Checkpoint:
+    """Host weights of one AR model: BF16 matrices as uint16 arrays [out, in],
+    norm gammas as float32 arrays."""
+    config: Config
+    embed_tokens: np.ndarray
+    lm_head: np.ndarray
+    final_norm: np.ndarray
+    layers: list = field(default_factory=list)
+
+
+class Model:
+    """Model (src/model.rs:398-610) with device-resident weights."""
+
+    def __init__(self, handle: int, config: Config, checkpoint: Checkpoint):
+        self._h = handle
+        self.config = config
+        self._ckpt = checkpoint  # host arrays stay alive with the model
+
+    @classmethod
+    def open(cls, checkpoint: Checkpoint) -> "Model":
+        L = lib()
+        cfg = checkpoint.config.c()
+        layers = (_LayerWeights * len(checkpoint.layers))()
+        for i, w in enumerate(checkpoint.layers):
+            for f, _ in _LayerWeights._fields_:
+                setattr(layers[i], f, _ptr(getattr(w, f)))
+        h = L.yue2_hip_model_open(C.byref(cfg), _ptr(checkpoint.embed_tokens), _ptr(checkpoint.lm_head),
+                                  _ptr(checkpoint.final_norm), layers)
+        if not h:
+            raise Yue2Error(-12, L.yue2_hip_last_error().decode())
+        return cls(h, checkpoint.config, checkpoint)
+
+    def close(self) -> None:
+        if self._h:
+            lib().yue2_hip_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward_phase(self, ids: Sequence[int], cache: "Cache", phase: int = PHASE_NONE) -> np.ndarray:
+        """Model::forward_phase: logits of the last row (vocab_size f32)."""
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.config.vocab_size, dtype=np.float32)
+        _check(lib().yue2_hip_forward(self._h, cache._h, _ptr(arr), len(arr), phase, _ptr(out)))
+        return out
+
+    def forward(self, ids: Sequence[int], cache: "Cache") -> np.ndarray:
+        """Model::forward (full vocabulary head)."""
+        return self.forward_phase(ids, cache, PHASE_NONE)
+
+    def prefill_phase(self, ids: Sequence[int], capacity: int, phase: int = PHASE_NONE):
+        """Model::prefill_phase: (Cache, logits of the last prompt row)."""
+        cache = Cache(self, capacity)
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.config.vocab_size, dtype=np.float32)
+        _check(lib().yue2_hip_prefill(self._h, cache._h, _ptr(arr), len(arr), phase, _ptr(out)))
+        return cache, out
+
+    def norm_fallbacks(self) -> int:
+        return int(lib().yue2_hip_norm_fallbacks(self._h))
+
+
+class Cache:
+    """Cache::new (src/model.rs:292-305): a device BF16 KV cache."""
+
+    def __init__(self, model: Model, capacity: int):
+        self.model = model
+        self._h = lib().yue2_hip_cache_new(model._h, capacity)
+        if not self._h:
+            raise Yue2Error(-10, lib().yue2_hip_last_error().decode())
+        self.capacity = capacity
+
+    @property
+    def length(self) -> int:
+        return int(lib().yue2_hip_cache_length(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            lib().yue2_hip_cache_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Decoder:
+    """The captured token loop (one hipGraph launch per step)."""
+
+    def __init__(self, model: Model, cond: Cache, uncond: Optional[Cache] = None,
+                 sampling: Optional[Sampling] = None, seed: int = 0, phase: int = PHASE_NONE,
+                 scale: float = 1.0, legacy: bool = False):
+        self.model = model
+        self._caches = (cond, uncond)
+        s = sampling.c() if sampling is not None else None
+        self._h = lib().yue2_hip_decoder_new(model._h, cond._h, uncond._h if uncond else None,
+                                             C.byref(s) if s is not None else None, seed, phase,
+                                             scale, int(legacy))
+        if not self._h:
+            raise Yue2Error(-13, lib().yue2_hip_last_error().decode())
+        self.rows = 2 if scale != 1.0 else 1
+
+    def run(self, steps: int, first_logits: Optional[np.ndarray] = None, timing: bool = False):
+        """Run `steps` steps; returns (tokens, step_ms or None)."""
+        fl = None
+        if first_logits is not None:
+            fl = np.ascontiguousarray(first_logits, dtype=np.float32)
+        tokens = np.zeros(max(steps, 1), dtype=np.int32)
+        ms = np.zeros(max(steps, 1), dtype=np.float32) if timing else None
+        n = _check(lib().yue2_hip_decoder_run(self._h, _ptr(fl), steps, _ptr(tokens), _ptr(ms)))
+        return tokens[:n], (ms[:n] if timing else None)
+
+    def close(self) -> None:
+        if self._h:
+            lib().yue2_hip_decoder_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class Generated:
+    tokens: list
+    truncated: bool
+
+
+def generate(model: Model, prefix: Sequence[int], sampling: Sampling, seed: int,
+             phase: int = PHASE_NONE, negative: Optional[Sequence[int]] = None,
+             scale: float = 1.0, legacy: bool = False) -> Generated:
+    """sampling::generate (src/sampling.rs:222-294) on the device."""
+    p = np.ascontiguousarray(prefix, dtype=np.int32)
+    n = None if negative is None else np.ascontiguousarray(negative, dtype=np.int32)
+    out = np.zeros(max(sampling.max_tokens, 1), dtype=np.int32)
+    count, trunc = C.c_int32(0), C.c_int32(0)
+    s = sampling.c()
+    _check(lib().yue2_hip_generate(model._h, _ptr(p), len(p), C.byref(s), seed, phase, _ptr(n),
+                                   0 if n is None else len(n), scale, int(legacy), _ptr(out),
+                                   C.byref(count), C.byref(trunc)))
+    return Generated(out[:count.value].tolist(), bool(trunc.value))

@@ -1,0 +1,347 @@
+// decoder.hip -- the captured token loop of sampling::generate
+// (src/sampling.rs:222-294) on the device.
+//
+// One hipGraph holds a whole loop iteration: choose() over the previous
+// logits (with the CFG mix of a batch-2 decoder) -> embed the chosen id ->
+// every layer for every row -> LM head -> advance the device positions.  When
+// the sampler needs random numbers, a side branch of the same graph
+// generates the next token's block of 2 * vocab MT19937 outputs while the
+// layers run.  Positions, ids, the step counter and the penalty history live
+// in device memory, so the graph replays without parameter updates and only
+// the chosen ids are copied back.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/yue2_hip.h"
+#include "kernels.h"
+#include "runtime.h"
+#include "sampler.h"
+#include "y2_math.h"
+
+using namespace y2;
+
+struct Yue2Decoder {
+    Yue2Model* m = nullptr;
+    Yue2Cache* caches[kMaxRows] = {nullptr, nullptr};
+    int rows = 1, phase = YUE2_PHASE_NONE;
+    bool need_rng = false;
+    Workspace w;
+    SampleArgs sa{};
+    MtState* mt = nullptr;
+    uint32_t* streams = nullptr;
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    bool started = false;
+    int steps_done = 0;
+    bool ended = false;
+    std::vector<hipEvent_t> events;
+    uint64_t seed = 0;
+};
+
+static int validate_sampling(const Yue2Sampling* s) {
+    if (!std::isfinite(s->temperature) || !(s->temperature >= 0.0f && s->temperature <= 5.0f) ||
+        !std::isfinite(s->top_p) || s->top_p <= 0.0f || s->top_p > 1.0f || s->top_k < 1 ||
+        !std::isfinite(s->repetition_penalty) || s->repetition_penalty <= 0.0f ||
+        s->penalty_window < 1 || s->penalty_window > 100 || s->min_tokens > s->max_tokens ||
+        s->max_tokens < 1)
+        return fail(YUE2_ERR_SAMPLING, "Invalid sampling configuration");
+    return YUE2_OK;
+}
+
+// MT19937 seeding (src/sampling.rs:15-24).
+static void mt_seed(MtState* out, uint64_t seed) {
+    out->state[0] = (uint32_t)seed;
+    for (int i = 1; i < 624; ++i)
+        out->state[i] = 1812433253u * (out->state[i - 1] ^ (out->state[i - 1] >> 30)) + (uint32_t)i;
+    out->next = 624;
+}
+
+static KvView kv_view(const Yue2Decoder* d) {
+    KvView kv{};
+    for (int b = 0; b < d->rows; ++b) {
+        kv.base[b] = d->caches[b]->kv;
+        kv.capacity[b] = d->caches[b]->capacity;
+    }
+    return kv;
+}
+
+static void decoder_release(Yue2Decoder* d) {
+    if (d->exec) (void)hipGraphExecDestroy(d->exec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    for (hipEvent_t e : d->events) (void)hipEventDestroy(e);
+    if (d->fork) (void)hipEventDestroy(d->fork);
+    if (d->join) (void)hipEventDestroy(d->join);
+    if (d->side) (void)hipStreamDestroy(d->side);
+    if (d->mt) (void)hipFree(d->mt);
+    if (d->streams) (void)hipFree(d->streams);
+    d->w.release();
+}
+
+extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2Cache* uncond,
+                                             const Yue2Sampling* sampling, uint64_t seed,
+                                             int32_t phase, float scale, int32_t legacy) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || !cond || cond->m != m || (uncond && uncond->m != m)) {
+        fail(YUE2_ERR_ARG, "null or foreign model/cache");
+        return nullptr;
+    }
+    if (sampling && validate_sampling(sampling) != YUE2_OK) return nullptr;
+    if (check_phase_vocab(phase, m->c.vocab_size) != YUE2_OK) return nullptr;
+    // The unconditional row is used only when guidance is on (src/sampling.rs:250-255).
+    if (scale != 1.0f && !uncond) {
+        fail(YUE2_ERR_GUIDANCE, "Guidance requires negative prefix");
+        return nullptr;
+    }
+    auto* d = new Yue2Decoder();
+    d->m = m;
+    d->phase = phase;
+    d->seed = seed;
+    d->caches[0] = cond;
+    d->rows = 1;
+    if (scale != 1.0f) {
+        d->caches[1] = uncond;
+        d->rows = 2;
+    }
+    int cap = cond->capacity;
+    if (d->rows == 2) cap = std::max(cap, uncond->capacity);
+    const int V = m->c.vocab_size;
+    int rc = d->w.ensure(d->rows, (cap + kBlockKeys - 1) / kBlockKeys, m->c);
+    d->need_rng = sampling && sampling->temperature != 0.0f;
+    hipError_t e = hipSuccess;
+    if (rc == YUE2_OK && d->need_rng) {
+        e = hipMalloc(&d->mt, sizeof(MtState));
+        if (e == hipSuccess) e = hipMalloc(&d->streams, sizeof(uint32_t) * 4 * (size_t)V);
+        if (e == hipSuccess) {
+            MtState host;
+            mt_seed(&host, seed);
+            e = hipMemcpy(d->mt, &host, sizeof(MtState), hipMemcpyHostToDevice);
+        }
+    }
+    if (rc == YUE2_OK && e == hipSuccess) e = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);
+    if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->fork, hipEventDisableTiming);
+    if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->join, hipEventDisableTiming);
+    if (rc != YUE2_OK || e != hipSuccess) {
+        if (e != hipSuccess) hip_fail(e, "decoder allocation");
+        decoder_release(d);
+        delete d;
+        return nullptr;
+    }
+    SampleArgs& a = d->sa;
+    a.logits = d->w.logits;
+    a.scores = d->w.mixed;
+    a.stream[0] = d->streams;
+    a.stream[1] = d->streams ? d->streams + 2 * (size_t)V : nullptr;
+    a.token_log = d->w.token_log;
+    a.st = d->w.st;
+    a.rows = d->rows;
+    a.vocab = V;
+    a.phase = phase;
+    a.end_id = phase_end_id(phase);
+    a.mode = sampling ? 1 : 0;
+    a.cfg_scale = scale;
+    a.legacy = legacy;
+    if (sampling) {
+        a.temperature = sampling->temperature;
+        a.top_p = sampling->top_p;
+        a.top_k = sampling->top_k;
+        a.repetition_penalty = sampling->repetition_penalty;
+        a.window = sampling->penalty_window;
+        a.min_tokens = sampling->min_tokens;
+    }
+    return d;
+}
+
+extern "C" void yue2_hip_decoder_free(Yue2Decoder* d) {
+    if (!d) return;
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    (void)hipStreamSynchronize(d->m->stream);
+    decoder_release(d);
+    delete d;
+}
+
+// Capture one loop iteration (choose -> forward -> advance) as a graph.
+static int capture(Yue2Decoder* d) {
+    Yue2Model* m = d->m;
+    hipStream_t s = m->stream;
+    const size_t draws = 2 * (size_t)m->c.vocab_size;
+    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
+    int rc = YUE2_OK;
+    if (d->need_rng) {
+        (void)hipEventRecord(d->fork, s);
+        (void)hipStreamWaitEvent(d->side, d->fork, 0);
+        launch_mt_generate(d->side, d->mt, d->streams, d->streams + draws, draws, d->w.st, 1);
+        (void)hipEventRecord(d->join, d->side);
+    }
+    launch_choose(s, d->sa);
+    rc = enqueue_step(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+    if (d->need_rng) (void)hipStreamWaitEvent(s, d->join, 0);
+    launch_advance(s, d->w.st, d->rows);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(s, &g);
+    if (rc != YUE2_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    d->graph = g;
+    e = hipGraphInstantiate(&d->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    return YUE2_OK;
+}
+
+static int start(Yue2Decoder* d, const float* first_logits) {
+    Yue2Model* m = d->m;
+    hipStream_t s = m->stream;
+    const size_t V = m->c.vocab_size;
+    if (!first_logits) return fail(YUE2_ERR_ARG, "first logits required");
+    hipError_t e = hipMemcpyAsync(d->w.logits, first_logits, sizeof(float) * V * d->rows,
+                                  hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return hip_fail(e, "logits upload");
+    launch_reset_state(s, d->w.st);
+    launch_set_state(s, d->w.st, d->rows, d->caches[0]->length,
+                     d->rows > 1 ? d->caches[1]->length : 0, 0, 0);
+    if (d->need_rng)
+        launch_mt_generate(s, d->mt, d->streams, d->streams + 2 * V, 2 * V, d->w.st, 0);
+    if (int rc = capture(d)) return rc;
+    d->started = true;
+    return YUE2_OK;
+}
+
+static int check_room(Yue2Decoder* d, int steps) {
+    for (int b = 0; b < d->rows; ++b) {
+        const Yue2Cache* c = d->caches[b];
+        if (c->length + steps > c->capacity || c->length + steps > d->m->c.max_position_embeddings)
+            return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    }
+    if (d->steps_done + steps + 1 > d->w.log_cap) return fail(YUE2_ERR_CONTEXT, "token log full");
+    return YUE2_OK;
+}
+
+static int read_tokens(Yue2Decoder* d, int from, int n, int32_t* tokens) {
+    if (n <= 0 || !tokens) return YUE2_OK;
+    hipError_t e = hipMemcpy(tokens, d->w.token_log + from, sizeof(int32_t) * n, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "token readback");
+}
+
+extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logits, int32_t steps,
+                                        int32_t* tokens, float* step_ms) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!d || steps < 0) return fail(YUE2_ERR_ARG, "null decoder or negative steps");
+    if (d->ended || steps == 0) return 0;
+    if (int rc = check_room(d, steps)) return rc;
+    if (!d->started)
+        if (int rc = start(d, first_logits)) return rc;
+    hipStream_t s = d->m->stream;
+    if (step_ms && (int)d->events.size() < 2 * steps) {
+        while ((int)d->events.size() < 2 * steps) {
+            hipEvent_t ev;
+            if (hipEventCreate(&ev) != hipSuccess) return fail(YUE2_ERR_DEVICE, "hipEventCreate");
+            d->events.push_back(ev);
+        }
+    }
+    const int end = phase_end_id(d->phase);
+    int ran = 0;
+    for (int i = 0; i < steps; ++i) {
+        if (step_ms) (void)hipEventRecord(d->events[2 * i], s);
+        hipError_t e = hipGraphLaunch(d->exec, s);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+        if (step_ms) (void)hipEventRecord(d->events[2 * i + 1], s);
+        ++ran;
+        if (end >= 0) {
+            // Phases with an end token: stop at the first end id.
+            int32_t id = -1;
+            if (int rc = read_step_error(d->w, s)) return rc;
+            if (int rc = read_tokens(d, d->steps_done + i, 1, &id)) return rc;
+            if (id == end) {
+                d->ended = true;
+                break;
+            }
+        }
+    }
+    if (int rc = read_step_error(d->w, s)) return rc;
+    if (step_ms)
+        for (int i = 0; i < ran; ++i)
+            (void)hipEventElapsedTime(&step_ms[i], d->events[2 * i], d->events[2 * i + 1]);
+    if (int rc = read_tokens(d, d->steps_done, ran, tokens)) return rc;
+    for (int b = 0; b < d->rows; ++b) d->caches[b]->length += ran;
+    d->steps_done += ran;
+    return ran;
+}
+
+// The loop's last choose() without a following forward (src/sampling.rs:281).
+static int choose_only(Yue2Decoder* d, const float* first_logits, int32_t* token) {
+    if (!d->started)
+        if (int rc = start(d, first_logits)) return rc;
+    hipStream_t s = d->m->stream;
+    launch_choose(s, d->sa);
+    if (int rc = read_step_error(d->w, s)) return rc;
+    return read_tokens(d, d->steps_done, 1, token);
+}
+
+extern "C" int32_t yue2_hip_generate(Yue2Model* m, const int32_t* prefix, int32_t prefix_len,
+                                     const Yue2Sampling* sampling, uint64_t seed, int32_t phase,
+                                     const int32_t* negative, int32_t negative_len, float scale,
+                                     int32_t legacy, int32_t* tokens, int32_t* count,
+                                     int32_t* truncated) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || !sampling || !tokens || !count || !truncated) return fail(YUE2_ERR_ARG, "null argument");
+    if (int rc = validate_sampling(sampling)) return rc;
+    if (prefix_len + sampling->max_tokens > kContext ||
+        (negative && negative_len + sampling->max_tokens > kContext))
+        return fail(YUE2_ERR_BUDGET, "Prefix + requested generation budget exceeds 24576; no implicit truncation");
+    if (scale != 1.0f && !negative) return fail(YUE2_ERR_GUIDANCE, "Guidance requires negative prefix");
+    if (int rc = check_phase_vocab(phase, m->c.vocab_size)) return rc;
+    if (prefix_len <= 0 || (scale != 1.0f && negative_len <= 0)) return fail(YUE2_ERR_ARG, "Empty prefill");
+    *count = 0;
+    *truncated = 1;
+    const size_t V = m->c.vocab_size;
+    std::vector<float> first(V * 2);
+    Yue2Cache* cond = yue2_hip_cache_new(m, prefix_len + sampling->max_tokens);
+    Yue2Cache* neg = nullptr;
+    Yue2Decoder* d = nullptr;
+    int rc = cond ? YUE2_OK : YUE2_ERR_ALLOC;
+    if (rc == YUE2_OK) rc = yue2_hip_prefill(m, cond, prefix, prefix_len, phase, first.data());
+    if (rc == YUE2_OK && scale != 1.0f) {
+        neg = yue2_hip_cache_new(m, negative_len + sampling->max_tokens);
+        rc = neg ? YUE2_OK : YUE2_ERR_ALLOC;
+        if (rc == YUE2_OK) rc = yue2_hip_prefill(m, neg, negative, negative_len, phase, first.data() + V);
+    }
+    if (rc == YUE2_OK) {
+        d = yue2_hip_decoder_new(m, cond, neg, sampling, seed, phase, scale, legacy);
+        if (!d) rc = YUE2_ERR_ALLOC;
+    }
+    const int end = phase_end_id(phase);
+    if (rc == YUE2_OK) {
+        const int loop = sampling->max_tokens - 1;
+        int ran = loop > 0 ? yue2_hip_decoder_run(d, first.data(), loop, tokens, nullptr) : 0;
+        if (ran < 0) rc = ran;
+        if (rc == YUE2_OK) {
+            if (d->ended) {
+                *count = ran - 1;  // the end id is not pushed (:268-271)
+                *truncated = 0;
+            } else {
+                int32_t last = -1;
+                rc = choose_only(d, first.data(), &last);
+                if (rc == YUE2_OK) {
+                    if (last == end) {
+                        *count = ran;
+                        *truncated = 0;
+                    } else {
+                        tokens[ran] = last;
+                        *count = ran + 1;
+                    }
+                }
+            }
+        }
+    }
+    if (d) yue2_hip_decoder_free(d);
+    yue2_hip_cache_free(neg);
+    yue2_hip_cache_free(cond);
+    return rc;
+}

@@ -1,0 +1,81 @@
+// runtime.h -- internal types shared by the runtime, the decoder and the
+// reference twins.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/yue2_hip.h"
+#include "kernels.h"
+
+namespace y2 {
+
+// Protocol ids (src/protocol.rs:6-16).
+constexpr int kEod = 151643;
+constexpr int kAbcEnd = 151848;
+constexpr int kMusicEnd = 151852;
+constexpr int kCodecOffset = 151853;
+constexpr int kCodecSize = 32768;
+constexpr int kContext = 24576;
+
+struct LayerDev {
+    uint16_t *wqkv, *wo, *wg, *wu, *wd;
+    float *in_norm, *q_norm, *k_norm, *post_norm;
+};
+
+// Activations and attention scratch for one batch size.
+struct Workspace {
+    int rows = 0, max_blocks = 0, score_stride = 0, blk_stride = 0, log_cap = 0;
+    void* block = nullptr;
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
+    float *logits = nullptr, *mixed = nullptr;
+    float *scores = nullptr, *bmax = nullptr, *bsum = nullptr, *part = nullptr;
+    StepState* st = nullptr;
+    int32_t* token_log = nullptr;
+    int ensure(int rows, int max_blocks, const Yue2Config& c);
+    void release();
+    ~Workspace() { release(); }
+};
+
+}  // namespace y2
+
+struct Yue2Model {
+    Yue2Config c{};
+    hipStream_t stream = nullptr;
+    void* block = nullptr;
+    size_t block_bytes = 0;
+    uint16_t *embed = nullptr, *lm_head = nullptr;
+    float *final_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+    std::vector<y2::LayerDev> layers;
+    y2::Workspace ws;  // batch-1 workspace of the parity API
+    int norm_fallbacks = 0;
+};
+
+struct Yue2Cache {
+    Yue2Model* m = nullptr;
+    int capacity = 0;
+    int length = 0;
+    uint16_t* kv = nullptr;
+};
+
+namespace y2 {
+
+std::recursive_mutex& library_lock();
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+bool device_ready();
+int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
+                 hipStream_t s);
+void phase_range(int phase, int* start, int* end, int* stop);
+int phase_end_id(int phase);
+int check_phase_vocab(int phase, int vocab);
+int read_step_error(Workspace& w, hipStream_t s);
+
+// Small state kernels (kernels.hip).
+void launch_fill(hipStream_t s, float* p, size_t n, float v);
+void launch_reset_state(hipStream_t s, StepState* st);
+void launch_set_state(hipStream_t s, StepState* st, int rows, int pos0, int pos1, int id0, int id1);
+
+}  // namespace y2

@@ -1,0 +1,511 @@
+// runtime.hip -- device-resident model, KV caches and the captured token step
+// behind the session half of include/yue2_hip.h.
+//
+// Model::open / Cache::new / forward_phase / prefill_phase / generate of the
+// reference (src/model.rs:292-610, src/sampling.rs:222-294) become: weights
+// uploaded once into one HBM allocation; BF16 KV caches in HBM; a workspace
+// per batch size; and a token step that is enqueued either directly (parity
+// API) or captured once as a hipGraph and replayed (decoder).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/yue2_hip.h"
+#include "kernels.h"
+#include "runtime.h"
+#include "y2_math.h"
+
+using namespace y2;
+
+namespace y2 {
+
+std::recursive_mutex& library_lock() {
+    static std::recursive_mutex m;
+    return m;
+}
+
+static thread_local std::string t_error;
+
+int fail(int code, const std::string& msg) {
+    t_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(YUE2_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool device_ready() {
+    static int state = -1;  // -1 unknown, 0 no, 1 yes
+    if (state < 0) {
+        int count = 0;
+        state = 0;
+        if (hipGetDeviceCount(&count) == hipSuccess && count > 0) {
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, 0) == hipSuccess &&
+                std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 && hipSetDevice(0) == hipSuccess)
+                state = 1;
+        }
+    }
+    return state == 1;
+}
+
+static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Bump allocator over one device allocation.
+struct Carve {
+    size_t offset = 0;
+    template <typename T>
+    size_t take(size_t count) {
+        const size_t at = offset;
+        offset = align_up(offset + count * sizeof(T), 256);
+        return at;
+    }
+};
+
+int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
+    if (block && rows == want_rows && max_blocks >= want_blocks) return YUE2_OK;
+    release();
+    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads;
+    const int Hkv = c.num_key_value_heads, I = c.intermediate_size, V = c.vocab_size;
+    const int qkvw = (Hq + 2 * Hkv) * D;
+    rows = want_rows;
+    max_blocks = want_blocks;
+    score_stride = max_blocks * kBlockKeys;
+    blk_stride = max_blocks;
+    log_cap = 24576 + 64;
+    Carve cv;
+    const size_t o_x = cv.take<float>((size_t)rows * H);
+    const size_t o_h = cv.take<float>((size_t)rows * H);
+    const size_t o_qkv = cv.take<float>((size_t)rows * qkvw);
+    const size_t o_att = cv.take<float>((size_t)rows * Hq * D);
+    const size_t o_act = cv.take<float>((size_t)rows * I);
+    const size_t o_logits = cv.take<float>((size_t)rows * V);
+    const size_t o_mixed = cv.take<float>((size_t)V);
+    const size_t o_scores = cv.take<float>((size_t)rows * Hq * score_stride);
+    const size_t o_bmax = cv.take<float>((size_t)rows * Hq * blk_stride);
+    const size_t o_bsum = cv.take<float>((size_t)rows * Hq * blk_stride);
+    const size_t o_part = cv.take<float>((size_t)rows * Hq * blk_stride * D);
+    const size_t o_st = cv.take<StepState>(1);
+    const size_t o_log = cv.take<int32_t>((size_t)log_cap);
+    hipError_t e = hipMalloc(&block, cv.offset);
+    if (e != hipSuccess) {
+        block = nullptr;
+        return hip_fail(e, "hipMalloc(workspace)");
+    }
+    char* p = static_cast<char*>(block);
+    x = reinterpret_cast<float*>(p + o_x);
+    h = reinterpret_cast<float*>(p + o_h);
+    qkv = reinterpret_cast<float*>(p + o_qkv);
+    att = reinterpret_cast<float*>(p + o_att);
+    act = reinterpret_cast<float*>(p + o_act);
+    logits = reinterpret_cast<float*>(p + o_logits);
+    mixed = reinterpret_cast<float*>(p + o_mixed);
+    scores = reinterpret_cast<float*>(p + o_scores);
+    bmax = reinterpret_cast<float*>(p + o_bmax);
+    bsum = reinterpret_cast<float*>(p + o_bsum);
+    part = reinterpret_cast<float*>(p + o_part);
+    st = reinterpret_cast<StepState*>(p + o_st);
+    token_log = reinterpret_cast<int32_t*>(p + o_log);
+    e = hipMemset(st, 0, sizeof(StepState));
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(step state)");
+    return YUE2_OK;
+}
+
+void Workspace::release() {
+    if (block) (void)hipFree(block);
+    block = nullptr;
+    rows = max_blocks = 0;
+}
+
+// Enqueue one token step for `rows` batch rows reading ids/positions from the
+// workspace's StepState.  head: 0 none, else the phase's LM head.
+int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
+                 hipStream_t s) {
+    const Yue2Config& c = m->c;
+    const int H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads;
+    const int Hkv = c.num_key_value_heads, I = c.intermediate_size, V = c.vocab_size;
+    const int qkvw = (Hq + 2 * Hkv) * D, qw = Hq * D;
+    const float eps = c.rms_norm_eps;
+    hipError_t e;
+    launch_embed(s, m->embed, w.st, w.x, H, V, rows);
+    for (int l = 0; l < c.num_hidden_layers; ++l) {
+        const LayerDev& L = m->layers[l];
+        launch_rmsnorm(s, w.x, H, L.in_norm, w.h, H, H, eps, rows, w.st);
+        GemvArgs qa{L.wqkv, nullptr, w.h, w.qkv, H, qkvw, qkvw, H, rows};
+        if ((e = launch_gemv(s, EPI_STORE, qa)) != hipSuccess) return hip_fail(e, "gemv(qkv)");
+        HeadArgs ha{w.qkv, qkvw, L.q_norm, L.k_norm, m->rope_cos, m->rope_sin, kv,
+                    l, c.num_hidden_layers, Hq, Hkv, D, rows, eps, w.st};
+        launch_heads(s, ha);
+        AttnArgs aa{};
+        aa.q = w.qkv;
+        aa.q_stride = qkvw;
+        aa.kv = kv;
+        aa.layer = l;
+        aa.layers = c.num_hidden_layers;
+        aa.heads = Hq;
+        aa.kv_heads = Hkv;
+        aa.dim = D;
+        aa.scale = 1.0f / std::sqrt((float)D);
+        aa.scores = w.scores;
+        aa.bmax = w.bmax;
+        aa.bsum = w.bsum;
+        aa.part = w.part;
+        aa.out = w.att;
+        aa.out_stride = qw;
+        aa.score_stride = w.score_stride;
+        aa.blk_stride = w.blk_stride;
+        aa.max_blocks = w.max_blocks;
+        aa.rows = rows;
+        aa.st = w.st;
+        launch_attention(s, aa);
+        GemvArgs oa{L.wo, nullptr, w.att, w.x, qw, H, H, qw, rows};
+        if ((e = launch_gemv(s, EPI_RESID, oa)) != hipSuccess) return hip_fail(e, "gemv(o)");
+        launch_rmsnorm(s, w.x, H, L.post_norm, w.h, H, H, eps, rows, w.st);
+        GemvArgs ga{L.wg, L.wu, w.h, w.act, H, I, I, H, rows};
+        if ((e = launch_gemv(s, EPI_SWIGLU, ga)) != hipSuccess) return hip_fail(e, "gemv(gate/up)");
+        GemvArgs da{L.wd, nullptr, w.act, w.x, I, H, H, I, rows};
+        if ((e = launch_gemv(s, EPI_RESID, da)) != hipSuccess) return hip_fail(e, "gemv(down)");
+    }
+    launch_rmsnorm(s, w.x, H, m->final_norm, w.h, H, H, eps, rows, w.st);
+    if (!head) return YUE2_OK;
+    if (phase == YUE2_PHASE_NONE) {
+        GemvArgs la{m->lm_head, nullptr, w.h, w.logits, H, V, V, H, rows};
+        if ((e = launch_gemv(s, EPI_STORE, la)) != hipSuccess) return hip_fail(e, "gemv(lm_head)");
+        return YUE2_OK;
+    }
+    // project_phase (src/model.rs:478-507): the phase's rows plus the stop
+    // row; every other logit is -inf.
+    int start, end, stop;
+    phase_range(phase, &start, &end, &stop);
+    launch_fill(s, w.logits, (size_t)rows * V, -INFINITY);
+    GemvArgs ra{m->lm_head + (size_t)start * H, nullptr, w.h, w.logits + start, H, V, end - start, H, rows};
+    if ((e = launch_gemv(s, EPI_STORE, ra)) != hipSuccess) return hip_fail(e, "gemv(lm_head range)");
+    GemvArgs sa{m->lm_head + (size_t)stop * H, nullptr, w.h, w.logits + stop, H, V, 1, H, rows};
+    if ((e = launch_gemv(s, EPI_STORE, sa)) != hipSuccess) return hip_fail(e, "gemv(lm_head stop)");
+    return YUE2_OK;
+}
+
+void phase_range(int phase, int* start, int* end, int* stop) {
+    if (phase == YUE2_PHASE_ABC) {
+        *start = 0;
+        *end = kEod;
+        *stop = kAbcEnd;
+    } else {
+        *start = kCodecOffset;
+        *end = kCodecOffset + kCodecSize;
+        *stop = kMusicEnd;
+    }
+}
+
+int phase_end_id(int phase) {
+    return phase == YUE2_PHASE_ABC ? kAbcEnd : phase == YUE2_PHASE_SEMANTIC ? kMusicEnd : -1;
+}
+
+int check_phase_vocab(int phase, int vocab) {
+    if (phase == YUE2_PHASE_NONE) return YUE2_OK;
+    if (phase != YUE2_PHASE_ABC && phase != YUE2_PHASE_SEMANTIC) return fail(YUE2_ERR_ARG, "unknown phase");
+    int start, end, stop;
+    phase_range(phase, &start, &end, &stop);
+    if (vocab <= stop || vocab < end)
+        return fail(YUE2_ERR_VOCAB, "Vocabulary does not support native music protocol");
+    return YUE2_OK;
+}
+
+int read_step_error(Workspace& w, hipStream_t s) {
+    StepState st;
+    hipError_t e = hipMemcpyAsync(&st, w.st, sizeof(StepState), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "step state readback");
+    if (st.error == 1) return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    if (st.error == 2) return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
+    if (st.error == 3) return fail(YUE2_ERR_EMPTY, "Empty sampling distribution");
+    if (st.error == 4) return fail(YUE2_ERR_LOGITS, "Model produced invalid logits");
+    if (st.error == 5) return fail(YUE2_ERR_TIES, "top-k survivors exceed the device sort capacity");
+    if (st.error != 0) return fail(YUE2_ERR_DEVICE, "device error " + std::to_string(st.error));
+    return YUE2_OK;
+}
+
+}  // namespace y2
+
+// ---------------------------------------------------------------------------
+// C ABI: configuration, model, cache
+// ---------------------------------------------------------------------------
+
+extern "C" const char* yue2_hip_last_error(void) { return t_error.c_str(); }
+
+extern "C" int32_t yue2_hip_config_validate(const Yue2Config* c) {
+    if (!c) return fail(YUE2_ERR_ARG, "null config");
+    const int32_t sizes[] = {c->hidden_size, c->num_hidden_layers, c->num_attention_heads,
+                             c->num_key_value_heads, c->head_dim, c->intermediate_size,
+                             c->vocab_size, c->max_position_embeddings};
+    for (int32_t v : sizes)
+        if (v <= 0) return fail(YUE2_ERR_CONFIG, "Invalid transformer configuration");
+    if (c->num_attention_heads % c->num_key_value_heads != 0 || c->head_dim % 2 != 0 ||
+        !(c->rope_theta > 0.0f) || !std::isfinite(c->rope_theta) || !(c->rms_norm_eps > 0.0f) ||
+        !std::isfinite(c->rms_norm_eps))
+        return fail(YUE2_ERR_CONFIG, "Invalid transformer configuration");
+    return YUE2_OK;
+}
+
+// Shapes the kernels support (beyond Config validation).
+static int check_supported(const Yue2Config* c) {
+    const int D = c->head_dim;
+    if (D != 64 && D != 128 && D != 256) return fail(YUE2_ERR_ARG, "head_dim must be 64, 128 or 256");
+    if (c->num_attention_heads / c->num_key_value_heads > 8)
+        return fail(YUE2_ERR_ARG, "at most 8 query heads per KV head");
+    if (c->hidden_size % 8 || c->intermediate_size % 8)
+        return fail(YUE2_ERR_ARG, "hidden and intermediate sizes must be multiples of 8");
+    if (c->hidden_size > 16384 || c->intermediate_size > 16384 ||
+        c->num_attention_heads * D > 16384)
+        return fail(YUE2_ERR_ARG, "GEMV inner dimension above 16384");
+    if (c->max_position_embeddings > 24576) return fail(YUE2_ERR_ARG, "context above 24576");
+    return YUE2_OK;
+}
+
+extern "C" Yue2Model* yue2_hip_model_open(const Yue2Config* c, const uint16_t* embed,
+                                          const uint16_t* lm_head, const float* final_norm,
+                                          const Yue2LayerWeights* layers) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (yue2_hip_config_validate(c) != YUE2_OK) return nullptr;
+    if (check_supported(c) != YUE2_OK) return nullptr;
+    if (!embed || !lm_head || !final_norm || !layers) {
+        fail(YUE2_ERR_ARG, "null weight pointer");
+        return nullptr;
+    }
+    if (!device_ready()) {
+        fail(YUE2_ERR_DEVICE, "no gfx950 device");
+        return nullptr;
+    }
+    const int H = c->hidden_size, D = c->head_dim, Hq = c->num_attention_heads;
+    const int Hkv = c->num_key_value_heads, I = c->intermediate_size, V = c->vocab_size;
+    const int qkvw = (Hq + 2 * Hkv) * D, qw = Hq * D, kw = Hkv * D;
+    auto* m = new Yue2Model();
+    m->c = *c;
+    Carve cv;
+    const size_t o_embed = cv.take<uint16_t>((size_t)V * H);
+    const size_t o_head = cv.take<uint16_t>((size_t)V * H);
+    const size_t o_fnorm = cv.take<float>((size_t)H);
+    const int half = D / 2;
+    const size_t o_cos = cv.take<float>((size_t)c->max_position_embeddings * half);
+    const size_t o_sin = cv.take<float>((size_t)c->max_position_embeddings * half);
+    struct Off { size_t qkv, o, g, u, d, in, qn, kn, post; };
+    std::vector<Off> offs(c->num_hidden_layers);
+    for (auto& o : offs) {
+        o.qkv = cv.take<uint16_t>((size_t)qkvw * H);
+        o.o = cv.take<uint16_t>((size_t)H * qw);
+        o.g = cv.take<uint16_t>((size_t)I * H);
+        o.u = cv.take<uint16_t>((size_t)I * H);
+        o.d = cv.take<uint16_t>((size_t)H * I);
+        o.in = cv.take<float>(H);
+        o.qn = cv.take<float>(D);
+        o.kn = cv.take<float>(D);
+        o.post = cv.take<float>(H);
+    }
+    hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipStreamCreate");
+        delete m;
+        return nullptr;
+    }
+    e = hipMalloc(&m->block, cv.offset);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipMalloc(weights)");
+        (void)hipStreamDestroy(m->stream);
+        delete m;
+        return nullptr;
+    }
+    m->block_bytes = cv.offset;
+    char* base = static_cast<char*>(m->block);
+    m->embed = reinterpret_cast<uint16_t*>(base + o_embed);
+    m->lm_head = reinterpret_cast<uint16_t*>(base + o_head);
+    m->final_norm = reinterpret_cast<float*>(base + o_fnorm);
+    m->rope_cos = reinterpret_cast<float*>(base + o_cos);
+    m->rope_sin = reinterpret_cast<float*>(base + o_sin);
+    bool ok = true;
+    auto up = [&](void* dst, const void* src, size_t bytes) {
+        if (ok && hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) != hipSuccess) ok = false;
+    };
+    // Norm gammas are rounded to BF16 as Norm::new does with bf16 = true.
+    auto up_norm = [&](float* dst, const float* src, int n) {
+        std::vector<float> tmp(src, src + n);
+        for (float& v : tmp) v = rb(v);
+        up(dst, tmp.data(), sizeof(float) * n);
+    };
+    up(m->embed, embed, sizeof(uint16_t) * (size_t)V * H);
+    up(m->lm_head, lm_head, sizeof(uint16_t) * (size_t)V * H);
+    up_norm(m->final_norm, final_norm, H);
+    // RoPE table for every position, Rotary::new (src/model.rs:137-149):
+    // libm powf/cosf/sinf in f32, each value rounded to BF16.
+    {
+        std::vector<float> ct((size_t)c->max_position_embeddings * half), st(ct.size());
+        for (int i = 0; i < half; ++i) {
+            const float freq = 1.0f / powf(c->rope_theta, (float)(2 * i) / (float)D);
+            for (int p = 0; p < c->max_position_embeddings; ++p) {
+                const float angle = (float)p * freq;
+                ct[(size_t)p * half + i] = rb(cosf(angle));
+                st[(size_t)p * half + i] = rb(sinf(angle));
+            }
+        }
+        up(m->rope_cos, ct.data(), sizeof(float) * ct.size());
+        up(m->rope_sin, st.data(), sizeof(float) * st.size());
+    }
+    m->layers.resize(c->num_hidden_layers);
+    for (int l = 0; l < c->num_hidden_layers && ok; ++l) {
+        const Yue2LayerWeights& src = layers[l];
+        if (!src.q_proj || !src.k_proj || !src.v_proj || !src.o_proj || !src.gate_proj ||
+            !src.up_proj || !src.down_proj || !src.input_layernorm || !src.q_norm || !src.k_norm ||
+            !src.post_attention_layernorm) {
+            ok = false;
+            fail(YUE2_ERR_ARG, "null layer weight");
+            break;
+        }
+        LayerDev& L = m->layers[l];
+        const Off& o = offs[l];
+        L.wqkv = reinterpret_cast<uint16_t*>(base + o.qkv);
+        L.wo = reinterpret_cast<uint16_t*>(base + o.o);
+        L.wg = reinterpret_cast<uint16_t*>(base + o.g);
+        L.wu = reinterpret_cast<uint16_t*>(base + o.u);
+        L.wd = reinterpret_cast<uint16_t*>(base + o.d);
+        L.in_norm = reinterpret_cast<float*>(base + o.in);
+        L.q_norm = reinterpret_cast<float*>(base + o.qn);
+        L.k_norm = reinterpret_cast<float*>(base + o.kn);
+        L.post_norm = reinterpret_cast<float*>(base + o.post);
+        up(L.wqkv, src.q_proj, sizeof(uint16_t) * (size_t)qw * H);
+        up(L.wqkv + (size_t)qw * H, src.k_proj, sizeof(uint16_t) * (size_t)kw * H);
+        up(L.wqkv + (size_t)(qw + kw) * H, src.v_proj, sizeof(uint16_t) * (size_t)kw * H);
+        up(L.wo, src.o_proj, sizeof(uint16_t) * (size_t)H * qw);
+        up(L.wg, src.gate_proj, sizeof(uint16_t) * (size_t)I * H);
+        up(L.wu, src.up_proj, sizeof(uint16_t) * (size_t)I * H);
+        up(L.wd, src.down_proj, sizeof(uint16_t) * (size_t)H * I);
+        up_norm(L.in_norm, src.input_layernorm, H);
+        up_norm(L.q_norm, src.q_norm, D);
+        up_norm(L.k_norm, src.k_norm, D);
+        up_norm(L.post_norm, src.post_attention_layernorm, H);
+    }
+    if (!ok) {
+        if (t_error.empty()) fail(YUE2_ERR_DEVICE, "weight upload failed");
+        yue2_hip_model_free(m);
+        return nullptr;
+    }
+    return m;
+}
+
+extern "C" void yue2_hip_model_free(Yue2Model* m) {
+    if (!m) return;
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    (void)hipStreamSynchronize(m->stream);
+    m->ws.release();
+    if (m->block) (void)hipFree(m->block);
+    (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+extern "C" int32_t yue2_hip_norm_fallbacks(const Yue2Model* m) {
+    if (!m) return 0;
+    return m->norm_fallbacks;
+}
+
+extern "C" Yue2Cache* yue2_hip_cache_new(Yue2Model* m, int32_t capacity) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || capacity <= 0) {
+        fail(YUE2_ERR_ARG, "invalid cache capacity");
+        return nullptr;
+    }
+    const Yue2Config& c = m->c;
+    const size_t elems = (size_t)c.num_hidden_layers * 2 * c.num_key_value_heads * capacity * c.head_dim;
+    auto* cache = new Yue2Cache();
+    cache->m = m;
+    cache->capacity = capacity;
+    hipError_t e = hipMalloc(&cache->kv, elems * sizeof(uint16_t));
+    if (e != hipSuccess) {
+        hip_fail(e, "hipMalloc(kv cache)");
+        delete cache;
+        return nullptr;
+    }
+    return cache;
+}
+
+extern "C" void yue2_hip_cache_free(Yue2Cache* c) {
+    if (!c) return;
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    (void)hipStreamSynchronize(c->m->stream);
+    (void)hipFree(c->kv);
+    delete c;
+}
+
+extern "C" int32_t yue2_hip_cache_length(const Yue2Cache* c) { return c ? c->length : 0; }
+
+// Model::forward_phase: token-by-token through the decode-order kernels, so a
+// prefill produces bit-for-bit the cache a sequence of decode steps would.
+extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int32_t n,
+                                    int32_t phase, float* logits) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || !c || !ids || c->m != m) return fail(YUE2_ERR_ARG, "null model, cache or ids");
+    if (int rc = check_phase_vocab(phase, m->c.vocab_size)) return rc;
+    if (n <= 0 || c->length + n > c->capacity || c->length + n > m->c.max_position_embeddings)
+        return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= m->c.vocab_size)
+            return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
+    const int blocks = (c->capacity + kBlockKeys - 1) / kBlockKeys;
+    if (int rc = m->ws.ensure(1, blocks, m->c)) return rc;
+    KvView kv{};
+    kv.base[0] = c->kv;
+    kv.capacity[0] = c->capacity;
+    hipStream_t s = m->stream;
+    launch_reset_state(s, m->ws.st);
+    for (int t = 0; t < n; ++t) {
+        launch_set_state(s, m->ws.st, 1, c->length + t, 0, ids[t], 0);
+        const bool head = logits && t == n - 1;
+        if (int rc = enqueue_step(m, m->ws, kv, 1, head, phase, s)) return rc;
+    }
+    if (int rc = read_step_error(m->ws, s)) return rc;
+    StepState st;
+    if (hipMemcpy(&st, m->ws.st, sizeof(st), hipMemcpyDeviceToHost) == hipSuccess)
+        m->norm_fallbacks += st.norm_fallbacks;
+    c->length += n;
+    if (logits) {
+        hipError_t e = hipMemcpy(logits, m->ws.logits, sizeof(float) * m->c.vocab_size,
+                                 hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "logits readback");
+    }
+    return YUE2_OK;
+}
+
+extern "C" int32_t yue2_hip_prefill(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int32_t n,
+                                    int32_t phase, float* logits) {
+    if (!c) return fail(YUE2_ERR_ARG, "null cache");
+    if (n <= 0 || c->length != 0) return fail(YUE2_ERR_ARG, "Invalid prefill/cache capacity");
+    return yue2_hip_forward(m, c, ids, n, phase, logits);
+}
+
+extern "C" int32_t yue2_hip_synchronize(void) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 device");
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "hipDeviceSynchronize");
+}
+
+extern "C" int32_t yue2_hip_selftest_math(int32_t which, const void* in, void* out, size_t n) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 device");
+    if (which < 0 || which > 3 || !in || !out) return fail(YUE2_ERR_ARG, "bad selftest request");
+    const size_t elem = which == 1 ? sizeof(double) : sizeof(float);
+    void *din = nullptr, *dout = nullptr;
+    hipError_t e = hipMalloc(&din, n * elem);
+    if (e == hipSuccess) e = hipMalloc(&dout, n * elem);
+    if (e == hipSuccess) e = hipMemcpy(din, in, n * elem, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        launch_math_selftest(nullptr, which, din, dout, n);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(out, dout, n * elem, hipMemcpyDeviceToHost);
+    (void)hipFree(din);
+    (void)hipFree(dout);
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "selftest");
+}

@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Decode throughput of the 3B-class YuE2-style AR decoder on one MI355X.
+
+Workload (the reference's token loop, sampling::generate src/sampling.rs:222-294):
+  28 layers, hidden 3072, 24 q heads / 8 KV heads, head_dim 128, SwiGLU 8192,
+  vocab 84000; random-init BF16 weights ~N(0, 0.02) (synthetic: the real
+  checkpoint is not available offline); seed-0 2048-token prompt (the
+  unconditional row: seed-1 prompt); sampling T 0.9, top-k 50, top-p 0.93,
+  repetition penalty 1.2 over 50 tokens; CFG batch 2 with guidance 1.5.
+A step is one loop iteration: CFG mix + choose() + one token through all 28
+layers for both rows + LM head, all on the device as one hipGraph launch;
+only the token id comes back.  Weights, KV caches and prompts are resident in
+HBM before the timed region.  The batch-1 line (no CFG) is measured the same
+way on its own cache.
+
+Prints one JSON line.  Progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "AR decode tokens/s @1 GPU (bs1 & CFG bs2) + % of HBM roofline; p50 ms/token"
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def weight_bytes(c) -> int:
+    H, D, I, V = c.hidden_size, c.head_dim, c.intermediate_size, c.vocab_size
+    q, kv = c.num_attention_heads * D, c.num_key_value_heads * D
+    per_layer = 2 * (H * (q + 2 * kv) + q * H + 3 * H * I) + 4 * (2 * H + 2 * D)
+    return c.num_hidden_layers * per_layer + 2 * V * H + 4 * H
+
+
+def kv_bytes_per_position(c) -> int:
+    return c.num_hidden_layers * 2 * c.num_key_value_heads * c.head_dim * 2
+
+
+def step_bytes(c, rows: int, context: float) -> float:
+    """Algorithmic HBM bytes of one step: every weight once, each row's KV for
+    `context` attended positions plus the new token's K/V, its embedding row."""
+    return weight_bytes(c) + rows * (kv_bytes_per_position(c) * (context + 1) + 2 * c.hidden_size)
+
+
+def measure(y2, model, caches, first, sampling, scale, warmup, steps, c):
+    dec = y2.Decoder(model, caches[0], caches[1] if len(caches) > 1 else None, sampling=sampling, seed=0,
+                     scale=scale)
+    dec.run(warmup, first_logits=first)
+    ctx0 = caches[0].length
+    y2.synchronize()
+    t0 = time.perf_counter()
+    tokens, ms = dec.run(steps, timing=True)
+    y2.synchronize()
+    wall = time.perf_counter() - t0
+    assert len(tokens) == steps
+    rows = len(caches)
+    ctx = [ch.length for ch in caches]
+    mean_ctx = np.mean([(ctx0 + steps / 2.0) for _ in caches])
+    return dec, {
+        "wall_s": wall,
+        "ms_per_step": 1000.0 * wall / steps,
+        "tokens_per_s": steps / wall,
+        "p50_ms": float(np.percentile(ms, 50)),
+        "p90_ms": float(np.percentile(ms, 90)),
+        "mean_event_ms": float(np.mean(ms)),
+        "context_start": int(ctx0),
+        "context_end": [int(x) for x in ctx],
+        "hbm_roofline_frac": step_bytes(c, rows, mean_ctx) / (wall / steps) / HBM_PEAK,
+        "bytes_per_step": step_bytes(c, rows, mean_ctx),
+    }
+
+
+def cpu_baseline(ckpt, c, prompt_len, scale, sampling, threads, budget_s, max_steps):
+    """The oracle's CFG step on the host cores: both rows' forward over a
+    synthetic BF16 KV cache of prompt_len positions, CFG mix and choose()."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import oracle as O
+
+    O.set_threads(threads)
+    om = O.Model(ckpt)
+    caches = [O.Cache(om, prompt_len + max_steps + 1) for _ in range(2)]
+    for i, ch in enumerate(caches):
+        ch.fill_random(prompt_len, seed=100 + i)
+    rng = O.Generator(0)
+    ids = [1, 2]
+    logits = [om.forward([ids[i]], caches[i]) for i in range(2)]
+    history = []
+    t0 = time.perf_counter()
+    steps = 0
+    while steps < max_steps and (steps == 0 or time.perf_counter() - t0 < budget_s):
+        mixed = O.cfg_mix(logits[0], logits[1], scale)
+        tok = O.choose(mixed, sampling, history, steps, O.PHASE_NONE, False, rng)
+        history.append(tok)
+        logits = [om.forward([tok], caches[i]) for i in range(2)]
+        steps += 1
+    wall = time.perf_counter() - t0
+    return {"value": steps / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "ms_per_step": 1000.0 * wall / steps,
+            "sample": f"{steps} CFG batch-2 steps of the C oracle (restated reference CPU token step, "
+                      f"portable DOT order in place of Accelerate) at context {prompt_len}, synthetic "
+                      f"BF16 KV, {threads} threads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--scale", type=float, default=1.5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--kernel-iters", type=int, default=112)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)",
+              file=sys.stderr)
+        return 2
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import yue2_rs_amd as y2
+    from yue2_rs_amd import synthetic
+
+    if not y2.available():
+        print("no gfx950 device available", file=sys.stderr)
+        return 1
+    c = synthetic.CLASS_3B
+    W, K, P = args.warmup, args.steps, args.prompt
+    log("generating synthetic 3B-class weights")
+    t = time.perf_counter()
+    ckpt = synthetic.checkpoint(c, seed=0, threads=16)
+    log(f"weights ready in {time.perf_counter() - t:.1f}s; uploading")
+    model = y2.Model.open(ckpt)
+    cond_ids = synthetic.prompt(P, c.vocab_size, seed=0)
+    neg_ids = synthetic.prompt(P, c.vocab_size, seed=1)
+    cap = P + W + K + 1
+    sampling = y2.Sampling(temperature=0.9, top_p=0.93, top_k=50, repetition_penalty=1.2, penalty_window=50,
+                           min_tokens=0, max_tokens=W + K + 1)
+    log(f"prefilling 3 x {P} tokens (decode-order kernels)")
+    t = time.perf_counter()
+    c_bs1, l_bs1 = model.prefill_phase(cond_ids, cap)
+    c_pos, l_pos = model.prefill_phase(cond_ids, cap)
+    c_neg, l_neg = model.prefill_phase(neg_ids, cap)
+    y2.synchronize()
+    log(f"prefill done in {time.perf_counter() - t:.1f}s")
+
+    log(f"batch 1: {W} warmup + {K} timed steps")
+    d1, bs1 = measure(y2, model, [c_bs1], l_bs1, sampling, 1.0, W, K, c)
+    d1.close()
+    log(f"batch 1: {bs1['tokens_per_s']:.1f} tokens/s, p50 {bs1['p50_ms']:.3f} ms")
+    log(f"CFG batch 2: {W} warmup + {K} timed steps")
+    d2, cfg = measure(y2, model, [c_pos, c_neg], np.concatenate([l_pos, l_neg]), sampling, args.scale, W, K, c)
+    log(f"CFG batch 2: {cfg['tokens_per_s']:.1f} steps/s, p50 {cfg['p50_ms']:.3f} ms")
+
+    # Dominant kernel: the gate/up GEMV with the SwiGLU epilogue (100.7 MB of
+    # weights per launch, 28 launches per step).
+    kms, kbytes = d2.time_kernel("gate_up", args.kernel_iters)
+    achieved = kbytes / (kms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(achieved / 8000.0, 4), "traffic": None,
+                "kernel": "gemv_kernel<2, EPI_SWIGLU, 6> (gate+up 2x8192x3072 BF16, CFG batch 2)",
+                "launch_ms": round(kms, 5), "bytes_per_launch": int(kbytes)}
+    others = {}
+    for name in ("down", "qkv", "o", "lm_head"):
+        ms, by = d2.time_kernel(name, args.kernel_iters if name != "lm_head" else 16)
+        others[name] = {"launch_ms": round(ms, 5), "GB_s": round(by / (ms * 1e-3) / 1e9, 1)}
+    d2.close()
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle on host cores)")
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 64)
+        log(f"CPU baseline: {cpu['value']:.3f} steps/s with {threads} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(cfg["tokens_per_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(cfg["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "3B-class AR decode loop, CFG batch 2 (guidance 1.5), T 0.9 / top-k 50 / "
+                               "top-p 0.93 / penalty 1.2, 2048-token prompts, 1024 steps",
+                   "layers": c.num_hidden_layers, "hidden": c.hidden_size, "heads": c.num_attention_heads,
+                   "kv_heads": c.num_key_value_heads, "head_dim": c.head_dim,
+                   "intermediate": c.intermediate_size, "vocab": c.vocab_size, "prompt": P,
+                   "global_batch": 2, "parallelism": "none (1 GPU)"},
+        "p50_ms": round(cfg["p50_ms"], 4),
+        "p90_ms": round(cfg["p90_ms"], 4),
+        "hbm_roofline_frac": round(cfg["hbm_roofline_frac"], 4),
+        "bytes_per_step": int(cfg["bytes_per_step"]),
+        "row_tokens_per_s": round(2 * cfg["tokens_per_s"], 2),
+        "bs1": {"tokens_per_s": round(bs1["tokens_per_s"], 2), "ms_per_step": round(bs1["ms_per_step"], 4),
+                "p50_ms": round(bs1["p50_ms"], 4), "p90_ms": round(bs1["p90_ms"], 4),
+                "hbm_roofline_frac": round(bs1["hbm_roofline_frac"], 4),
+                "bytes_per_step": int(bs1["bytes_per_step"])},
+        "roofline": roofline,
+        "kernels": others,
+        "cpu_baseline": cpu,
+        "norm_fallbacks": model.norm_fallbacks(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

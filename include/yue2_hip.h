@@ -218,6 +218,15 @@ int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t 
 /* Diagnostics: RMSNorm guard fallbacks taken since the model was opened. */
 int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);
 
+/* Diagnostics: time one of the decoder's own kernels with HIP events on the
+ * decoder's stream, cycling through the layers so that no launch finds its
+ * weights in the last-level cache.  kernel: 0 gate/up GEMV with the SwiGLU
+ * epilogue, 1 down GEMV, 2 fused QKV GEMV, 3 O GEMV, 4 LM-head GEMV.
+ * avg_ms = mean launch duration; bytes = algorithmic HBM bytes per launch.
+ * The decoder must have run at least one step. */
+int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t iters, float *avg_ms,
+                                     double *bytes);
+
 #ifdef __cplusplus
 }
 #endif

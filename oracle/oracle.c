@@ -340,7 +340,8 @@ void y2o_cache_free(y2o_cache *cache) {
 int y2o_cache_length(const y2o_cache *cache) { return cache->length; }
 
 /* Model::hidden (src/model.rs:523-591), CPU branch (:571-590). */
-int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out) {
+static int hidden_impl(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,
+                       float *x_out, int final_norm) {
     const y2o_config *c = &m->c;
     if (n <= 0 || cache->length + n > cache->capacity || cache->length + n > c->max_pos ||
         cache->layers != c->layers)
@@ -401,10 +402,21 @@ int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, 
         for (size_t i = 0; i < (size_t)n * H; ++i) x[i] = rb(x[i] + h[i]);
     }
     cache->length += n;
-    y2o_norm_apply(x, n, H, m->final_norm, c->eps, x_out);
+    if (final_norm) y2o_norm_apply(x, n, H, m->final_norm, c->eps, x_out);
+    else memcpy(x_out, x, sizeof(float) * (size_t)n * H);
 done:
     free(x); free(h); free(q); free(k); free(v); free(att); free(g); free(u); free(cs); free(sn);
     return rc;
+}
+
+int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out) {
+    return hidden_impl(m, cache, ids, n, x_out, 1);
+}
+
+/* The hidden state before final_norm: what yue2_metal_ar_stack returns
+ * (src/metal.m:836-846; Rust applies the final norm, src/model.rs:567). */
+int y2o_hidden_prenorm(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out) {
+    return hidden_impl(m, cache, ids, n, x_out, 0);
 }
 
 int y2o_forward(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,

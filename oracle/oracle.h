@@ -153,6 +153,8 @@ int y2o_cache_length(const y2o_cache *cache);
 
 /* Model::hidden (src/model.rs:523-591): x_out = final_norm(x) for all rows. */
 int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out);
+/* The same without the final norm (yue2_metal_ar_stack's `out`). */
+int y2o_hidden_prenorm(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out);
 /* Model::forward (src/model.rs:465-468): logits of the last row. */
 int y2o_forward(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *logits);
 /* Model::forward_phase / project_phase (src/model.rs:469-507). */

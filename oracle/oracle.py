@@ -83,6 +83,7 @@ def lib() -> C.CDLL:
             "y2o_cache_new": (C.POINTER(CacheS), [vp, i32]),
             "y2o_cache_free": (None, [C.POINTER(CacheS)]),
             "y2o_hidden": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
+            "y2o_hidden_prenorm": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_forward": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_forward_phase": (i32, [vp, C.POINTER(CacheS), vp, i32, i32, vp]),
             "y2o_prefill": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
@@ -183,6 +184,19 @@ class Cache:
         n = c.length * c.width
         base = layer * c.capacity * c.width
         return np.ctypeslib.as_array(c.value, shape=(c.layers * c.capacity * c.width,))[base:base + n].reshape(c.length, c.width)
+
+    def fill_random(self, length: int, seed: int) -> None:
+        """Give the cache `length` positions of BF16-exact N(0, 1) keys and
+        values (for timing a step at a given context without a prefill)."""
+        c = self.ptr.contents
+        assert length <= c.capacity
+        n = c.layers * c.capacity * c.width
+        rng = np.random.default_rng(seed)
+        for arr in (np.ctypeslib.as_array(c.key, shape=(n,)), np.ctypeslib.as_array(c.value, shape=(n,))):
+            v = arr.reshape(c.layers, c.capacity, c.width)
+            x = rng.standard_normal((c.layers, length, c.width), dtype=np.float32)
+            v[:, :length, :] = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
+        c.length = length
 
     def __del__(self):
         try:

@@ -13,3 +13,14 @@ def rb(x) -> np.ndarray:
 
 def bits(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+_mapping = [1000]
+
+
+def fresh_mapping() -> int:
+    """A new `mapping` id for yue2_hip_vector/ar_stack weights: the device
+    weight cache is keyed by (mapping, address, shape, dtype), and the
+    mapping id is what keeps a reused host address from aliasing."""
+    _mapping[0] += 1
+    return _mapping[0]

@@ -11,7 +11,7 @@ from oracle import oracle as O
 from yue2_rs_amd import synthetic
 import yue2_rs_amd as y2
 
-from helpers import bits, rb
+from helpers import bits, fresh_mapping, rb
 
 pytestmark = pytest.mark.gpu
 
@@ -29,7 +29,7 @@ def test_vector_matches_oracle(gpu, oracle_threads, shape):
     w = synthetic.bf16_normal((n, k), seed=7, tensor=n * 131 + k)
     x = _bf16_exact(np.random.default_rng(n + k).normal(0, 1, k))
     got = np.empty(n, np.float32)
-    ok = y2.lib().yue2_hip_vector(x.ctypes.data, w.ctypes.data, 1, 0, 1, 1, got.ctypes.data, n, k)
+    ok = y2.lib().yue2_hip_vector(x.ctypes.data, w.ctypes.data, fresh_mapping(), 0, 1, 1, got.ctypes.data, n, k)
     assert ok == 1, y2.lib().yue2_hip_last_error()
     want = np.empty(n, np.float32)
     O.lib().y2o_gemv_raw(w.ctypes.data, n, k, x.ctypes.data, want.ctypes.data)
@@ -40,11 +40,12 @@ def test_vector_one_hot_reproduces_columns(gpu):
     n, k = 256, 1024
     w = synthetic.bf16_normal((n, k), seed=3, tensor=99)
     wf = (w.astype(np.uint32) << 16).view(np.float32)
+    mapping = fresh_mapping()
     for col in (0, 7, 8, 511, 512, 1023):
         x = np.zeros(k, np.float32)
         x[col] = 1.0
         got = np.empty(n, np.float32)
-        assert y2.lib().yue2_hip_vector(x.ctypes.data, w.ctypes.data, 2, 0, 1, 1, got.ctypes.data, n, k) == 1
+        assert y2.lib().yue2_hip_vector(x.ctypes.data, w.ctypes.data, mapping, 0, 1, 1, got.ctypes.data, n, k) == 1
         assert np.array_equal(got, wf[:, col])
 
 

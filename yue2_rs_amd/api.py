@@ -111,6 +111,7 @@ def lib() -> C.CDLL:
         "yue2_hip_synthetic_bf16": (None, [vp, sz, u64, u64, f32, i32]),
         "yue2_hip_selftest_math": (i32, [i32, vp, vp, sz]),
         "yue2_hip_norm_fallbacks": (i32, [vp]),
+        "yue2_hip_decoder_time_kernel": (i32, [vp, i32, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -309,6 +310,16 @@ class Decoder:
         ms = np.zeros(max(steps, 1), dtype=np.float32) if timing else None
         n = _check(lib().yue2_hip_decoder_run(self._h, _ptr(fl), steps, _ptr(tokens), _ptr(ms)))
         return tokens[:n], (ms[:n] if timing else None)
+
+    KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "o": 3, "lm_head": 4}
+
+    def time_kernel(self, kernel: str, iters: int = 112):
+        """(mean launch ms, algorithmic bytes per launch) of one of the
+        decoder's GEMV kernels, timed with HIP events on its stream."""
+        ms, by = C.c_float(0), C.c_double(0)
+        _check(lib().yue2_hip_decoder_time_kernel(self._h, self.KERNELS[kernel], iters, C.byref(ms),
+                                                  C.byref(by)))
+        return float(ms.value), float(by.value)
 
     def close(self) -> None:
         if self._h:

@@ -284,6 +284,62 @@ static int choose_only(Yue2Decoder* d, const float* first_logits, int32_t* token
     return read_tokens(d, d->steps_done, 1, token);
 }
 
+extern "C" int32_t yue2_hip_decoder_time_kernel(Yue2Decoder* d, int32_t kernel, int32_t iters,
+                                                float* avg_ms, double* bytes) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!d || !avg_ms || !bytes || iters <= 0 || kernel < 0 || kernel > 4)
+        return fail(YUE2_ERR_ARG, "bad kernel timing request");
+    if (!d->started) return fail(YUE2_ERR_ARG, "decoder has not run");
+    Yue2Model* m = d->m;
+    const Yue2Config& c = m->c;
+    const int H = c.hidden_size, D = c.head_dim, I = c.intermediate_size, V = c.vocab_size;
+    const int qw = c.num_attention_heads * D, qkvw = qw + 2 * c.num_key_value_heads * D;
+    const int rows = d->rows, L = c.num_hidden_layers;
+    const size_t out_n = (size_t)rows * std::max(std::max(V, qkvw), std::max(I, H));
+    float* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, out_n * sizeof(float));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(timing)");
+    hipEvent_t b0, b1;
+    (void)hipEventCreate(&b0);
+    (void)hipEventCreate(&b1);
+    hipStream_t s = m->stream;
+    auto args = [&](int l, int* epi) {
+        const LayerDev& Lw = m->layers[l];
+        switch (kernel) {
+            case 0: *epi = EPI_SWIGLU; return GemvArgs{Lw.wg, Lw.wu, d->w.x, tmp, H, I, I, H, rows, Lw.post_norm, c.rms_norm_eps, nullptr};
+            case 1: *epi = EPI_RESID; return GemvArgs{Lw.wd, nullptr, d->w.act, tmp, I, H, H, I, rows};
+            case 2: *epi = EPI_STORE; return GemvArgs{Lw.wqkv, nullptr, d->w.x, tmp, H, qkvw, qkvw, H, rows, Lw.in_norm, c.rms_norm_eps, nullptr};
+            case 3: *epi = EPI_RESID; return GemvArgs{Lw.wo, nullptr, d->w.att, tmp, qw, H, H, qw, rows};
+            default: *epi = EPI_STORE; return GemvArgs{m->lm_head, nullptr, d->w.x, tmp, H, V, V, H, rows, m->final_norm, c.rms_norm_eps, nullptr};
+        }
+    };
+    int rc = YUE2_OK;
+    // one untimed pass over every layer, then the timed launches
+    for (int i = 0; i < L + iters && rc == YUE2_OK; ++i) {
+        if (i == L) (void)hipEventRecord(b0, s);
+        int epi;
+        const GemvArgs a = args(i % L, &epi);
+        if ((e = launch_gemv(s, epi, a)) != hipSuccess) rc = hip_fail(e, "timed gemv");
+    }
+    (void)hipEventRecord(b1, s);
+    if (rc == YUE2_OK && (e = hipEventSynchronize(b1)) != hipSuccess) rc = hip_fail(e, "timing sync");
+    float ms = 0.0f;
+    if (rc == YUE2_OK) (void)hipEventElapsedTime(&ms, b0, b1);
+    *avg_ms = ms / (float)iters;
+    const double w = 2.0, f = 4.0;
+    switch (kernel) {
+        case 0: *bytes = w * 2.0 * I * H + f * rows * (H + (double)I); break;
+        case 1: *bytes = w * (double)H * I + f * rows * ((double)I + 2.0 * H); break;
+        case 2: *bytes = w * (double)qkvw * H + f * rows * ((double)H + qkvw); break;
+        case 3: *bytes = w * (double)H * qw + f * rows * ((double)qw + 2.0 * H); break;
+        default: *bytes = w * (double)V * H + f * rows * ((double)H + V); break;
+    }
+    (void)hipEventDestroy(b0);
+    (void)hipEventDestroy(b1);
+    (void)hipFree(tmp);
+    return rc;
+}
+
 extern "C" int32_t yue2_hip_generate(Yue2Model* m, const int32_t* prefix, int32_t prefix_len,
                                      const Yue2Sampling* sampling, uint64_t seed, int32_t phase,
                                      const int32_t* negative, int32_t negative_len, float scale,

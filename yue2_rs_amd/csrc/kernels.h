@@ -33,41 +33,39 @@ struct GemvArgs {
     float* y;            // output / residual, [rows, y_stride]
     int x_stride, y_stride;
     int n, k, rows;
+    const float* gamma;  // non-null: the input is RMSNorm(x) with these gammas
+    float eps;
+    StepState* st;       // counts RMSNorm guard fallbacks (may be null)
 };
 
 struct AttnArgs {
-    const float* q;      // [rows, q_stride]; head h at h*dim
-    int q_stride;
+    const float* qkv;    // [rows, qkv_stride]: q heads, then k heads, then v heads (rounded GEMV outputs)
+    int qkv_stride;
     KvView kv;
-    int layer, layers, heads, kv_heads, dim;
-    float scale;
-    float* scores;       // [rows][heads][score_stride] scaled scores, then exps
-    float* bmax;         // [rows][heads][blk_stride]
-    float* bsum;         // [rows][heads][blk_stride]
-    float* part;         // [rows][heads][blk_stride][dim]
+    int layer, heads, kv_heads, dim, rows;
+    float scale, eps;
+    const float *q_norm, *k_norm;  // null: q is final and the cache already holds position pos
+    const float *cos_t, *sin_t;    // RoPE table [positions][dim/2]
+    float* bmax;         // [rows][heads][blk_stride] block maxima
+    float* bsum;         // [rows][heads][blk_stride] block sums
+    float* part;         // [rows][heads][blk_stride][dim] partial PV
     float* out;          // [rows, out_stride]
-    int out_stride, score_stride, blk_stride, max_blocks, rows;
-    const StepState* st;
+    int out_stride, blk_stride;
+    int wgs, bpw;        // workgroups per (kv head, row); 64-key blocks per workgroup
+    int* counters;       // [rows][kv_heads][4], zero between launches
+    StepState* st;
 };
 
-struct HeadArgs {
-    float* qkv;          // [rows, qkv_stride]: q heads, k heads, v heads
-    int qkv_stride;
-    const float *q_norm, *k_norm;
-    const float *cos_t, *sin_t;  // [max_pos][dim/2]
-    KvView kv;
-    int layer, layers, heads, kv_heads, dim, rows;
-    float eps;
-    const StepState* st;
-};
+// Workgroups per (kv head, row) and 64-key blocks per workgroup for caches
+// of max_blocks blocks.
+void attention_geometry(int kv_heads, int rows, int max_blocks, int* wgs, int* bpw);
 
 void launch_embed(hipStream_t s, const uint16_t* embed, const StepState* st, float* x, int hidden,
                   int vocab, int rows);
 void launch_rmsnorm(hipStream_t s, const float* x, int x_stride, const float* gamma, float* out,
                     int out_stride, int n, float eps, int rows, StepState* st);
 hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a);
-void launch_heads(hipStream_t s, const HeadArgs& a);
-void launch_attention(hipStream_t s, const AttnArgs& a);
+hipError_t launch_attention(hipStream_t s, const AttnArgs& a);
 void launch_argmax(hipStream_t s, const float* logits, int stride, int n, StepState* st,
                    int32_t* token_log, int rows);
 void launch_advance(hipStream_t s, StepState* st, int rows);

@@ -129,320 +129,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// BF16 GEMV with FP32 accumulation in the DOT order (Linear::apply_range +
-// finish, src/tensor.rs:946-1118).  One wave owns one weight row at a time;
-// each lane streams its 16-byte chunks with 128-bit loads.  Inputs are staged
-// in LDS once per workgroup and reused for every row and batch row.
-//   EPI_STORE   y = rb(dot)
-//   EPI_RESID   y = rb(y + rb(dot))               (Tensor::add, :632-640)
-//   EPI_SWIGLU  y = rb(rb(silu(rb(g))) * rb(u))   (Mlp::apply, src/model.rs:206-214)
-//   EPI_RAW     y = dot, unrounded                (yue2_metal_vector, src/metal.m:545-603)
-// ---------------------------------------------------------------------------
-template <int B, int EPI, int IT>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
-    extern __shared__ float xs[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int k = a.k, nchunk = k >> 3;
-    for (int b = 0; b < B; ++b)
-        for (int i = tid; i < k; i += 256) xs[b * k + i] = a.x[(size_t)b * a.x_stride + i];
-    __syncthreads();
-    for (int row = blockIdx.x * 4 + wave; row < a.n; row += gridDim.x * 4) {
-        const uint4* wr = reinterpret_cast<const uint4*>(a.w + (size_t)row * k);
-        uint4 wv[IT];
-        uint4 wv2[EPI == EPI_SWIGLU ? IT : 1];
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int c = lane + 64 * it;
-            wv[it] = c < nchunk ? wr[c] : make_uint4(0, 0, 0, 0);
-        }
-        if constexpr (EPI == EPI_SWIGLU) {
-            const uint4* wr2 = reinterpret_cast<const uint4*>(a.w2 + (size_t)row * k);
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const int c = lane + 64 * it;
-                wv2[it] = c < nchunk ? wr2[c] : make_uint4(0, 0, 0, 0);
-            }
-        }
-        float acc[B], acc2[B];
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[b] = acc2[b] = 0.0f;
-#pragma unroll
-        for (int it = 0; it < IT; ++it) {
-            const int c = lane + 64 * it;
-            if (c < nchunk) {
-                float wf[8];
-                unpack8(wv[it], wf);
-                float wf2[8];
-                if constexpr (EPI == EPI_SWIGLU) unpack8(wv2[it], wf2);
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const float4* xp = reinterpret_cast<const float4*>(xs + b * k + 8 * c);
-                    const float4 x0 = xp[0], x1 = xp[1];
-                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-                    float s = acc[b];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) s = __builtin_fmaf(wf[e], xv[e], s);
-                    acc[b] = s;
-                    if constexpr (EPI == EPI_SWIGLU) {
-                        float s2 = acc2[b];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) s2 = __builtin_fmaf(wf2[e], xv[e], s2);
-                        acc2[b] = s2;
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            acc[b] = butterfly64(acc[b]);
-            if constexpr (EPI == EPI_SWIGLU) acc2[b] = butterfly64(acc2[b]);
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                float* yp = a.y + (size_t)b * a.y_stride + row;
-                if constexpr (EPI == EPI_RAW) {
-                    *yp = acc[b];
-                } else if constexpr (EPI == EPI_STORE) {
-                    *yp = rb(acc[b]);
-                } else if constexpr (EPI == EPI_RESID) {
-                    *yp = rb(*yp + rb(acc[b]));
-                } else {
-                    const float g = silu_rb(rb(acc[b]));
-                    *yp = rb(g * rb(acc2[b]));
-                }
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Per-head QK RMSNorm + rotate-half RoPE + KV append (src/tensor.rs:1158-1172,
-// src/model.rs:151-168, :576-577).  One wave per (head, row).  The head norm's
-// sum runs sequentially in lane 0 (dim <= 256 terms).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void heads_kernel(const HeadArgs a) {
-    __shared__ float v[512];
-    const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-    const int D = a.dim, half = D >> 1;
-    const int pos = a.st->pos[b];
-    if (pos < 0 || pos >= a.kv.capacity[b]) {
-        if (lane == 0) set_error(const_cast<StepState*>(a.st), DEV_ERR_CONTEXT);
-        return;
-    }
-    float* row = a.qkv + (size_t)b * a.qkv_stride;
-    const bool is_q = h < a.heads;
-    const int kvh = is_q ? 0 : h - a.heads;
-    float* src = row + (size_t)(is_q ? h : a.heads + kvh) * D;
-    const float* gamma = is_q ? a.q_norm : a.k_norm;
-    for (int i = lane; i < D; i += 64) v[i] = src[i];
-    __syncthreads();
-    float scale = 0.0f;
-    if (lane == 0) {
-        float sum = -0.0f;
-        for (int i = 0; i < D; ++i) sum = sum + v[i] * v[i];
-        scale = norm_scale_from_sum(sum, D, a.eps);
-    }
-    scale = __shfl(scale, 0, 64);
-    const float* cs = a.cos_t + (size_t)pos * half;
-    const float* sn = a.sin_t + (size_t)pos * half;
-    uint16_t* kdst = a.kv.base[b] + kv_offset(a.layer, 0, a.kv_heads, kvh, a.kv.capacity[b], pos, D);
-    for (int i = lane; i < half; i += 64) {
-        const float x0 = rb(rb(v[i] * scale) * gamma[i]);
-        const float x1 = rb(rb(v[i + half] * scale) * gamma[i + half]);
-        const float c = cs[i], s = sn[i];
-        const float y0 = rb(rb(x0 * c) - rb(x1 * s));
-        const float y1 = rb(rb(x1 * c) + rb(x0 * s));
-        if (is_q) {
-            src[i] = y0;
-            src[i + half] = y1;
-        } else {
-            kdst[i] = bf16_bits(y0);
-            kdst[i + half] = bf16_bits(y1);
-        }
-    }
-    if (!is_q) {
-        const float* vs = row + (size_t)(a.heads + a.kv_heads + kvh) * D;
-        uint16_t* vdst =
-            a.kv.base[b] + kv_offset(a.layer, 1, a.kv_heads, kvh, a.kv.capacity[b], pos, D);
-        for (int d = lane; d < D; d += 64) vdst[d] = bf16_bits(vs[d]);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Attention, phase 1: scaled scores s_j = DOT(q, K_j) * scale and 64-key
-// block maxima (src/model.rs:362-374; vDSP_vsmul/maxv, src/tensor.rs:715-716).
-// One workgroup per (kv head, 64-key block, row); each K row is read once and
-// serves all query heads of the group.  dim/8 lanes hold one key.
-// ---------------------------------------------------------------------------
-constexpr int kMaxGroup = 8;
-
-template <int D>
-__global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
-    const int g = blockIdx.x, blk = blockIdx.y, b = blockIdx.z;
-    const int L = a.st->pos[b] + 1;
-    const int j0 = blk * kBlockKeys;
-    if (j0 >= L || L > a.kv.capacity[b]) return;
-    constexpr int CPL = D / 8, KPW = 64 / CPL;
-    const int G = a.heads / a.kv_heads;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = lane % CPL, kk = lane / CPL;
-    __shared__ float smax[4][kMaxGroup];
-    float qv[kMaxGroup][8];
-    const float* qrow = a.q + (size_t)b * a.q_stride;
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-        if (h < G) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qv[h][e] = qrow[(size_t)(g * G + h) * D + 8 * c + e];
-        }
-    const uint16_t* K = a.kv.base[b] + kv_offset(a.layer, 0, a.kv_heads, g, a.kv.capacity[b], 0, D);
-    float lmax[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) lmax[h] = -__builtin_huge_valf();
-#pragma unroll
-    for (int it = 0; it < 16 / KPW; ++it) {
-        const int j = j0 + wave * 16 + it * KPW + kk;
-        const bool valid = j < L;
-        float kf[8];
-        const uint4 k4 = valid ? *reinterpret_cast<const uint4*>(K + (size_t)j * D + 8 * c)
-                               : make_uint4(0, 0, 0, 0);
-        unpack8(k4, kf);
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
-            if (h < G) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
-#pragma unroll
-                for (int s = CPL / 2; s >= 1; s >>= 1) acc = acc + __shfl_xor(acc, s, 64);
-                const float sc = acc * a.scale;
-                if (valid) {
-                    if (c == 0) a.scores[((size_t)b * a.heads + g * G + h) * a.score_stride + j] = sc;
-                    lmax[h] = fmaxf(lmax[h], sc);
-                }
-            }
-    }
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-        if (h < G) {
-            float m = lmax[h];
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
-            if (lane == 0) smax[wave][h] = m;
-        }
-    __syncthreads();
-    if (tid < G) {
-        const float m = fmaxf(fmaxf(smax[0][tid], smax[1][tid]), fmaxf(smax[2][tid], smax[3][tid]));
-        a.bmax[((size_t)b * a.heads + g * G + tid) * a.blk_stride + blk] = m;
-    }
-}
-
-// Phase 2: global max, e_j = exp(s_j - M), 64-key block sums by butterfly
-// (vDSP_vsadd + vvexpf + vDSP_sve, src/tensor.rs:717-721).
-__global__ __launch_bounds__(64) void attn_exp_kernel(const AttnArgs a) {
-    const int h = blockIdx.x, blk = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
-    const int L = a.st->pos[b] + 1;
-    const int j0 = blk * kBlockKeys;
-    if (j0 >= L || L > a.kv.capacity[b]) return;
-    const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const size_t hb = (size_t)b * a.heads + h;
-    const float* bm = a.bmax + hb * a.blk_stride;
-    float m = -__builtin_huge_valf();
-    for (int i = lane; i < nb; i += 64) m = fmaxf(m, bm[i]);
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
-    float* sc = a.scores + hb * a.score_stride;
-    const int j = j0 + lane;
-    float e = 0.0f;
-    if (j < L) {
-        e = expf_cr(sc[j] - m);
-        sc[j] = e;
-    }
-    e = butterfly64(e);
-    if (lane == 0) a.bsum[hb * a.blk_stride + blk] = e;
-}
-
-// Phase 3: total = block sums left to right, p_j = e_j / total (vDSP_vsdiv),
-// partial PV per block in the stream order (src/model.rs:380-392).
-template <int D>
-__global__ __launch_bounds__(64) void attn_pv_kernel(const AttnArgs a) {
-    const int g = blockIdx.x, blk = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
-    const int L = a.st->pos[b] + 1;
-    const int j0 = blk * kBlockKeys;
-    if (j0 >= L || L > a.kv.capacity[b]) return;
-    const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const int G = a.heads / a.kv_heads;
-    __shared__ float p[kMaxGroup][kBlockKeys];
-    __shared__ float stot[kMaxGroup];
-    if (lane < G) {
-        const float* bs = a.bsum + ((size_t)b * a.heads + g * G + lane) * a.blk_stride;
-        float tot = bs[0];
-        for (int i = 1; i < nb; ++i) tot = tot + bs[i];
-        stot[lane] = tot;
-    }
-    __syncthreads();
-    for (int h = 0; h < G; ++h) {
-        const int j = j0 + lane;
-        const float* sc = a.scores + ((size_t)b * a.heads + g * G + h) * a.score_stride;
-        p[h][lane] = j < L ? sc[j] / stot[h] : 0.0f;
-    }
-    __syncthreads();
-    constexpr int CPL = D / 8, S = 64 / CPL;
-    const int t = lane / CPL, c = lane % CPL;
-    const uint16_t* V = a.kv.base[b] + kv_offset(a.layer, 1, a.kv_heads, g, a.kv.capacity[b], 0, D);
-    float acc[kMaxGroup][8];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kBlockKeys / S; ++i) {
-        const int jj = t + S * i, j = j0 + jj;
-        if (j < L) {
-            float vf[8];
-            unpack8(*reinterpret_cast<const uint4*>(V + (size_t)j * D + 8 * c), vf);
-#pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h)
-                if (h < G) {
-                    const float pj = p[h][jj];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(pj, vf[e], acc[h][e]);
-                }
-        }
-    }
-#pragma unroll
-    for (int s = 32; s >= CPL; s >>= 1)
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
-            if (h < G)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] + __shfl_xor(acc[h][e], s, 64);
-    if (t == 0) {
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
-            if (h < G) {
-                float* dst = a.part + (((size_t)b * a.heads + g * G + h) * a.blk_stride + blk) * D + 8 * c;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) dst[e] = acc[h][e];
-            }
-    }
-}
-
-// Phase 4: blocks added left to right, rounded to BF16 (Tensor::rounded).
-__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnArgs a) {
-    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    if (d >= a.dim) return;
-    const int L = a.st->pos[b] + 1;
-    if (L > a.kv.capacity[b]) return;
-    const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const float* pp = a.part + ((size_t)b * a.heads + h) * a.blk_stride * a.dim + d;
-    float o = pp[0];
-    for (int i = 1; i < nb; ++i) o = o + pp[(size_t)i * a.dim];
-    a.out[(size_t)b * a.out_stride + (size_t)h * a.dim + d] = rb(o);
-}
-
-// ---------------------------------------------------------------------------
 // Greedy selection: argmax under f32::total_cmp with the lowest index on ties
 // (src/sampling.rs:148-156); the id feeds every row's next embedding.
 // ---------------------------------------------------------------------------
@@ -507,73 +193,6 @@ void launch_rmsnorm(hipStream_t s, const float* x, int x_stride, const float* ga
                     int out_stride, int n, float eps, int rows, StepState* st) {
     rmsnorm_kernel<<<rows, 256, (size_t)n * sizeof(float), s>>>(x, x_stride, gamma, out,
                                                                  out_stride, n, eps, st);
-}
-
-template <int B, int EPI>
-static hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a) {
-    const int iters = (a.k / 8 + 63) / 64;
-    const int blocks = std::min((a.n + 3) / 4, 1024);
-    const size_t lds = (size_t)B * a.k * sizeof(float);
-#define Y2_GEMV_CASE(N)                                                            \
-    if (iters <= N) {                                                              \
-        auto fn = gemv_kernel<B, EPI, N>;                                          \
-        if (lds > 65536) {                                                         \
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),  \
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);             \
-            if (e != hipSuccess) return e;                                         \
-        }                                                                          \
-        fn<<<blocks, 256, lds, s>>>(a);                                            \
-        return hipGetLastError();                                                  \
-    }
-    Y2_GEMV_CASE(1)
-    Y2_GEMV_CASE(2)
-    Y2_GEMV_CASE(4)
-    Y2_GEMV_CASE(6)
-    Y2_GEMV_CASE(8)
-    Y2_GEMV_CASE(12)
-    Y2_GEMV_CASE(16)
-    Y2_GEMV_CASE(24)
-    Y2_GEMV_CASE(32)
-#undef Y2_GEMV_CASE
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a) {
-    if (a.k % 8 != 0 || a.k > 32 * 512 || a.rows < 1 || a.rows > kMaxRows) return hipErrorInvalidValue;
-    if ((size_t)a.rows * a.k * sizeof(float) > 160 * 1024) return hipErrorInvalidValue;
-    if (a.rows == 1) {
-        if (epi == EPI_STORE) return gemv_dispatch<1, EPI_STORE>(s, a);
-        if (epi == EPI_RESID) return gemv_dispatch<1, EPI_RESID>(s, a);
-        if (epi == EPI_RAW) return gemv_dispatch<1, EPI_RAW>(s, a);
-        return gemv_dispatch<1, EPI_SWIGLU>(s, a);
-    }
-    if (epi == EPI_RAW) return gemv_dispatch<2, EPI_RAW>(s, a);
-    if (epi == EPI_STORE) return gemv_dispatch<2, EPI_STORE>(s, a);
-    if (epi == EPI_RESID) return gemv_dispatch<2, EPI_RESID>(s, a);
-    return gemv_dispatch<2, EPI_SWIGLU>(s, a);
-}
-
-void launch_heads(hipStream_t s, const HeadArgs& a) {
-    dim3 grid(a.heads + a.kv_heads, a.rows);
-    heads_kernel<<<grid, 64, 0, s>>>(a);
-}
-
-void launch_attention(hipStream_t s, const AttnArgs& a) {
-    dim3 g_kv(a.kv_heads, a.max_blocks, a.rows), g_q(a.heads, a.max_blocks, a.rows);
-    if (a.dim == 64) {
-        attn_scores_kernel<64><<<g_kv, 256, 0, s>>>(a);
-        attn_exp_kernel<<<g_q, 64, 0, s>>>(a);
-        attn_pv_kernel<64><<<g_kv, 64, 0, s>>>(a);
-    } else if (a.dim == 128) {
-        attn_scores_kernel<128><<<g_kv, 256, 0, s>>>(a);
-        attn_exp_kernel<<<g_q, 64, 0, s>>>(a);
-        attn_pv_kernel<128><<<g_kv, 64, 0, s>>>(a);
-    } else {
-        attn_scores_kernel<256><<<g_kv, 256, 0, s>>>(a);
-        attn_exp_kernel<<<g_q, 64, 0, s>>>(a);
-        attn_pv_kernel<256><<<g_kv, 64, 0, s>>>(a);
-    }
-    attn_merge_kernel<<<dim3(a.heads, a.rows), 256, 0, s>>>(a);
 }
 
 void launch_argmax(hipStream_t s, const float* logits, int stride, int n, StepState* st,

@@ -27,11 +27,12 @@ struct LayerDev {
 
 // Activations and attention scratch for one batch size.
 struct Workspace {
-    int rows = 0, max_blocks = 0, score_stride = 0, blk_stride = 0, log_cap = 0;
+    int rows = 0, max_blocks = 0, blk_stride = 0, log_cap = 0;
     void* block = nullptr;
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
     float *logits = nullptr, *mixed = nullptr;
-    float *scores = nullptr, *bmax = nullptr, *bsum = nullptr, *part = nullptr;
+    float *bmax = nullptr, *bsum = nullptr, *part = nullptr;
+    int32_t* counters = nullptr;  // attention group counters, zero between launches
     StepState* st = nullptr;
     int32_t* token_log = nullptr;
     int ensure(int rows, int max_blocks, const Yue2Config& c);

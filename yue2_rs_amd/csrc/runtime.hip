@@ -75,7 +75,6 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     const int qkvw = (Hq + 2 * Hkv) * D;
     rows = want_rows;
     max_blocks = want_blocks;
-    score_stride = max_blocks * kBlockKeys;
     blk_stride = max_blocks;
     log_cap = 24576 + 64;
     Carve cv;
@@ -86,7 +85,7 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     const size_t o_act = cv.take<float>((size_t)rows * I);
     const size_t o_logits = cv.take<float>((size_t)rows * V);
     const size_t o_mixed = cv.take<float>((size_t)V);
-    const size_t o_scores = cv.take<float>((size_t)rows * Hq * score_stride);
+    const size_t o_counters = cv.take<int32_t>((size_t)rows * Hkv * 4);
     const size_t o_bmax = cv.take<float>((size_t)rows * Hq * blk_stride);
     const size_t o_bsum = cv.take<float>((size_t)rows * Hq * blk_stride);
     const size_t o_part = cv.take<float>((size_t)rows * Hq * blk_stride * D);
@@ -105,13 +104,14 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     act = reinterpret_cast<float*>(p + o_act);
     logits = reinterpret_cast<float*>(p + o_logits);
     mixed = reinterpret_cast<float*>(p + o_mixed);
-    scores = reinterpret_cast<float*>(p + o_scores);
+    counters = reinterpret_cast<int32_t*>(p + o_counters);
     bmax = reinterpret_cast<float*>(p + o_bmax);
     bsum = reinterpret_cast<float*>(p + o_bsum);
     part = reinterpret_cast<float*>(p + o_part);
     st = reinterpret_cast<StepState*>(p + o_st);
     token_log = reinterpret_cast<int32_t*>(p + o_log);
     e = hipMemset(st, 0, sizeof(StepState));
+    if (e == hipSuccess) e = hipMemset(counters, 0, sizeof(int32_t) * rows * Hkv * 4);
     if (e != hipSuccess) return hip_fail(e, "hipMemset(step state)");
     return YUE2_OK;
 }
@@ -135,46 +135,46 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
     launch_embed(s, m->embed, w.st, w.x, H, V, rows);
     for (int l = 0; l < c.num_hidden_layers; ++l) {
         const LayerDev& L = m->layers[l];
-        launch_rmsnorm(s, w.x, H, L.in_norm, w.h, H, H, eps, rows, w.st);
-        GemvArgs qa{L.wqkv, nullptr, w.h, w.qkv, H, qkvw, qkvw, H, rows};
+        // RMSNorm(x) is computed in the GEMV prologue of every workgroup.
+        GemvArgs qa{L.wqkv, nullptr, w.x, w.qkv, H, qkvw, qkvw, H, rows, L.in_norm, eps, w.st};
         if ((e = launch_gemv(s, EPI_STORE, qa)) != hipSuccess) return hip_fail(e, "gemv(qkv)");
-        HeadArgs ha{w.qkv, qkvw, L.q_norm, L.k_norm, m->rope_cos, m->rope_sin, kv,
-                    l, c.num_hidden_layers, Hq, Hkv, D, rows, eps, w.st};
-        launch_heads(s, ha);
+        // QK-norm + RoPE + KV append + attention: one kernel.
         AttnArgs aa{};
-        aa.q = w.qkv;
-        aa.q_stride = qkvw;
+        aa.qkv = w.qkv;
+        aa.qkv_stride = qkvw;
         aa.kv = kv;
         aa.layer = l;
-        aa.layers = c.num_hidden_layers;
         aa.heads = Hq;
         aa.kv_heads = Hkv;
         aa.dim = D;
+        aa.rows = rows;
         aa.scale = 1.0f / std::sqrt((float)D);
-        aa.scores = w.scores;
+        aa.eps = eps;
+        aa.q_norm = L.q_norm;
+        aa.k_norm = L.k_norm;
+        aa.cos_t = m->rope_cos;
+        aa.sin_t = m->rope_sin;
         aa.bmax = w.bmax;
         aa.bsum = w.bsum;
         aa.part = w.part;
         aa.out = w.att;
         aa.out_stride = qw;
-        aa.score_stride = w.score_stride;
         aa.blk_stride = w.blk_stride;
-        aa.max_blocks = w.max_blocks;
-        aa.rows = rows;
+        attention_geometry(Hkv, rows, w.max_blocks, &aa.wgs, &aa.bpw);
+        aa.counters = w.counters;
         aa.st = w.st;
-        launch_attention(s, aa);
+        if ((e = launch_attention(s, aa)) != hipSuccess) return hip_fail(e, "attention");
         GemvArgs oa{L.wo, nullptr, w.att, w.x, qw, H, H, qw, rows};
         if ((e = launch_gemv(s, EPI_RESID, oa)) != hipSuccess) return hip_fail(e, "gemv(o)");
-        launch_rmsnorm(s, w.x, H, L.post_norm, w.h, H, H, eps, rows, w.st);
-        GemvArgs ga{L.wg, L.wu, w.h, w.act, H, I, I, H, rows};
+        GemvArgs ga{L.wg, L.wu, w.x, w.act, H, I, I, H, rows, L.post_norm, eps, w.st};
         if ((e = launch_gemv(s, EPI_SWIGLU, ga)) != hipSuccess) return hip_fail(e, "gemv(gate/up)");
         GemvArgs da{L.wd, nullptr, w.act, w.x, I, H, H, I, rows};
         if ((e = launch_gemv(s, EPI_RESID, da)) != hipSuccess) return hip_fail(e, "gemv(down)");
     }
-    launch_rmsnorm(s, w.x, H, m->final_norm, w.h, H, H, eps, rows, w.st);
     if (!head) return YUE2_OK;
+    // final_norm (src/model.rs:590) runs in the LM-head GEMV prologue.
     if (phase == YUE2_PHASE_NONE) {
-        GemvArgs la{m->lm_head, nullptr, w.h, w.logits, H, V, V, H, rows};
+        GemvArgs la{m->lm_head, nullptr, w.x, w.logits, H, V, V, H, rows, m->final_norm, eps, w.st};
         if ((e = launch_gemv(s, EPI_STORE, la)) != hipSuccess) return hip_fail(e, "gemv(lm_head)");
         return YUE2_OK;
     }
@@ -183,9 +183,11 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
     int start, end, stop;
     phase_range(phase, &start, &end, &stop);
     launch_fill(s, w.logits, (size_t)rows * V, -INFINITY);
-    GemvArgs ra{m->lm_head + (size_t)start * H, nullptr, w.h, w.logits + start, H, V, end - start, H, rows};
+    GemvArgs ra{m->lm_head + (size_t)start * H, nullptr, w.x, w.logits + start, H, V, end - start, H, rows,
+                m->final_norm, eps, w.st};
     if ((e = launch_gemv(s, EPI_STORE, ra)) != hipSuccess) return hip_fail(e, "gemv(lm_head range)");
-    GemvArgs sa{m->lm_head + (size_t)stop * H, nullptr, w.h, w.logits + stop, H, V, 1, H, rows};
+    GemvArgs sa{m->lm_head + (size_t)stop * H, nullptr, w.x, w.logits + stop, H, V, 1, H, rows,
+                m->final_norm, eps, nullptr};
     if ((e = launch_gemv(s, EPI_STORE, sa)) != hipSuccess) return hip_fail(e, "gemv(lm_head stop)");
     return YUE2_OK;
 }

@@ -50,6 +50,7 @@ struct TwinState {
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     StepState* st = nullptr;
+    int32_t* counters = nullptr;  // attention group counters (zero between launches)
 };
 
 TwinState& twin() {
@@ -62,6 +63,10 @@ bool twin_ready() {
     TwinState& t = twin();
     if (!t.stream && hipStreamCreateWithFlags(&t.stream, hipStreamNonBlocking) != hipSuccess) return false;
     if (!t.st && hipMalloc(&t.st, sizeof(StepState)) != hipSuccess) return false;
+    if (!t.counters) {
+        if (hipMalloc(&t.counters, 4096 * sizeof(int32_t)) != hipSuccess) return false;
+        if (hipMemset(t.counters, 0, 4096 * sizeof(int32_t)) != hipSuccess) return false;
+    }
     return true;
 }
 
@@ -167,24 +172,22 @@ Context* context_entry(const float* k, const float* v, size_t keys, size_t kv, s
 
 // Attention scratch for one row with `keys` keys.
 struct AttnScratch {
-    float *q, *out, *scores, *bmax, *bsum, *part;
+    float *q, *out, *bmax, *bsum, *part;
     int blocks;
 };
 
 bool attn_scratch(size_t heads, size_t dim, size_t keys, size_t extra, AttnScratch* s, float** extra_out) {
     const int blocks = (int)((keys + kBlockKeys - 1) / kBlockKeys);
-    const size_t n_q = heads * dim, n_scores = heads * (size_t)blocks * kBlockKeys;
+    const size_t n_q = heads * dim;
     const size_t n_blk = heads * (size_t)blocks, n_part = n_blk * dim;
     auto al = [](size_t n) { return (n + 63) & ~(size_t)63; };
-    const size_t total = al(n_q) * 2 + al(n_scores) + 2 * al(n_blk) + al(n_part) + al(extra);
+    const size_t total = al(n_q) * 2 + 2 * al(n_blk) + al(n_part) + al(extra);
     float* p = static_cast<float*>(scratch(total * sizeof(float)));
     if (!p) return false;
     s->q = p;
     p += al(n_q);
     s->out = p;
     p += al(n_q);
-    s->scores = p;
-    p += al(n_scores);
     s->bmax = p;
     p += al(n_blk);
     s->bsum = p;
@@ -196,29 +199,29 @@ bool attn_scratch(size_t heads, size_t dim, size_t keys, size_t extra, AttnScrat
     return true;
 }
 
-AttnArgs attn_args(const AttnScratch& s, const float* q, const Context& e, int heads, int dim,
-                   float* out, int out_stride) {
+// Attention over one context entry.  qkv_stride = heads*dim when q is final
+// (no norms); the ar_stack passes the whole q|k|v row with its norms.
+AttnArgs attn_args(const AttnScratch& s, const float* qkv, int qkv_stride, const Context& e, int heads,
+                   int dim, float* out, int out_stride) {
     AttnArgs a{};
-    a.q = q;
-    a.q_stride = heads * dim;
+    a.qkv = qkv;
+    a.qkv_stride = qkv_stride;
     a.kv.base[0] = e.data;
     a.kv.capacity[0] = (int)e.capacity;
     a.layer = 0;
-    a.layers = 1;
     a.heads = heads;
     a.kv_heads = (int)e.kv;
     a.dim = dim;
+    a.rows = 1;
     a.scale = 1.0f / std::sqrt((float)dim);
-    a.scores = s.scores;
     a.bmax = s.bmax;
     a.bsum = s.bsum;
     a.part = s.part;
     a.out = out;
     a.out_stride = out_stride;
-    a.score_stride = s.blocks * kBlockKeys;
     a.blk_stride = s.blocks;
-    a.max_blocks = s.blocks;
-    a.rows = 1;
+    attention_geometry((int)e.kv, 1, s.blocks, &a.wgs, &a.bpw);
+    a.counters = twin().counters;
     a.st = twin().st;
     return a;
 }
@@ -299,7 +302,9 @@ extern "C" int32_t yue2_hip_cached_attention(const float* q, const float* k, con
         return 0;
     launch_reset_state(st, twin().st);
     launch_set_state(st, twin().st, 1, (int)keys - 1, 0, 0, 0);
-    launch_attention(st, attn_args(s, s.q, *e, (int)heads, (int)dim, s.out, (int)(heads * dim)));
+    if (launch_attention(st, attn_args(s, s.q, (int)(heads * dim), *e, (int)heads, (int)dim, s.out,
+                                       (int)(heads * dim))) != hipSuccess)
+        return 0;
     if (hipMemcpyAsync(out, s.out, heads * dim * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess)
         return 0;
     return hipStreamSynchronize(st) == hipSuccess ? 1 : 0;
@@ -372,22 +377,23 @@ extern "C" int32_t yue2_hip_ar_stack(const float* input, float* out, float* shad
             std::memcpy(gam.data() + 2 * hidden, L.norms[1], dim * 4);
             std::memcpy(gam.data() + 2 * hidden + dim, L.norms[2], dim * 4);
             ok = hipMemcpyAsync(g_in, gam.data(), gam.size() * 4, hipMemcpyHostToDevice, s) == hipSuccess;
-            launch_rmsnorm(s, x, (int)hidden, g_in, h, (int)hidden, (int)hidden, eps, 1, t.st);
-            GemvArgs qa{w[0], nullptr, h, qkv, (int)hidden, (int)qkvw, (int)qw, (int)hidden, 1};
-            GemvArgs ka{w[1], nullptr, h, qkv + qw, (int)hidden, (int)qkvw, (int)kw, (int)hidden, 1};
-            GemvArgs va{w[2], nullptr, h, qkv + qw + kw, (int)hidden, (int)qkvw, (int)kw, (int)hidden, 1};
+            // input RMSNorm in each projection's prologue
+            GemvArgs qa{w[0], nullptr, x, qkv, (int)hidden, (int)qkvw, (int)qw, (int)hidden, 1, g_in, eps, t.st};
+            GemvArgs ka{w[1], nullptr, x, qkv + qw, (int)hidden, (int)qkvw, (int)kw, (int)hidden, 1, g_in, eps, nullptr};
+            GemvArgs va{w[2], nullptr, x, qkv + qw + kw, (int)hidden, (int)qkvw, (int)kw, (int)hidden, 1, g_in, eps, nullptr};
             ok = ok && launch_gemv(s, EPI_STORE, qa) == hipSuccess &&
                  launch_gemv(s, EPI_STORE, ka) == hipSuccess && launch_gemv(s, EPI_STORE, va) == hipSuccess;
-            KvView kvv{};
-            kvv.base[0] = e->data;
-            kvv.capacity[0] = (int)e->capacity;
-            HeadArgs ha{qkv, (int)qkvw, g_q, g_k, cos_t, sin_t, kvv, 0, 1, (int)heads, (int)kv, (int)dim, 1, eps, t.st};
-            launch_heads(s, ha);
-            launch_attention(s, attn_args(as, qkv, *e, (int)heads, (int)dim, att, (int)qw));
+            // QK-norm + RoPE + append of the new K/V + attention
+            AttnArgs aa = attn_args(as, qkv, (int)qkvw, *e, (int)heads, (int)dim, att, (int)qw);
+            aa.q_norm = g_q;
+            aa.k_norm = g_k;
+            aa.eps = eps;
+            aa.cos_t = cos_t;
+            aa.sin_t = sin_t;
+            ok = ok && launch_attention(s, aa) == hipSuccess;
             GemvArgs oa{w[3], nullptr, att, x, (int)qw, (int)hidden, (int)hidden, (int)qw, 1};
             ok = ok && launch_gemv(s, EPI_RESID, oa) == hipSuccess;
-            launch_rmsnorm(s, x, (int)hidden, g_post, h, (int)hidden, (int)hidden, eps, 1, t.st);
-            GemvArgs ga{w[4], w[5], h, act, (int)hidden, (int)intermediate, (int)intermediate, (int)hidden, 1};
+            GemvArgs ga{w[4], w[5], x, act, (int)hidden, (int)intermediate, (int)intermediate, (int)hidden, 1, g_post, eps, nullptr};
             GemvArgs da{w[6], nullptr, act, x, (int)intermediate, (int)hidden, (int)hidden, (int)intermediate, 1};
             ok = ok && launch_gemv(s, EPI_SWIGLU, ga) == hipSuccess && launch_gemv(s, EPI_RESID, da) == hipSuccess;
             // gammas are reused by the next layer's upload: wait for this layer

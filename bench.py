@@ -119,6 +119,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--kernel-iters", type=int, default=112)
+    ap.add_argument("--step-kernel", type=int, default=0, choices=[0, 1],
+                    help="1: one persistent kernel per token instead of one kernel per phase")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)",
@@ -139,6 +141,7 @@ def main() -> int:
     ckpt = synthetic.checkpoint(c, seed=0, threads=16)
     log(f"weights ready in {time.perf_counter() - t:.1f}s; uploading")
     model = y2.Model.open(ckpt)
+    step_kernel = model.set_step_kernel(bool(args.step_kernel))
     cond_ids = synthetic.prompt(P, c.vocab_size, seed=0)
     neg_ids = synthetic.prompt(P, c.vocab_size, seed=1)
     cap = P + W + K + 1
@@ -199,7 +202,8 @@ def main() -> int:
                    "layers": c.num_hidden_layers, "hidden": c.hidden_size, "heads": c.num_attention_heads,
                    "kv_heads": c.num_key_value_heads, "head_dim": c.head_dim,
                    "intermediate": c.intermediate_size, "vocab": c.vocab_size, "prompt": P,
-                   "global_batch": 2, "parallelism": "none (1 GPU)"},
+                   "global_batch": 2, "parallelism": "none (1 GPU)",
+                   "execution": "persistent step kernel" if step_kernel else "one kernel per phase"},
         "p50_ms": round(cfg["p50_ms"], 4),
         "p90_ms": round(cfg["p90_ms"], 4),
         "hbm_roofline_frac": round(cfg["hbm_roofline_frac"], 4),

@@ -149,6 +149,8 @@ typedef struct Yue2Decoder Yue2Decoder;
 
 /* Config::read validation (src/model.rs:50-72); 0 or YUE2_ERR_CONFIG. */
 int32_t yue2_hip_config_validate(const Yue2Config *c);
+/* Sampling::validate (src/protocol.rs:191-207); 0 or YUE2_ERR_SAMPLING. */
+int32_t yue2_hip_sampling_validate(const Yue2Sampling *s);
 
 /* Model::open (src/model.rs:418-451) from host arrays: the weights are copied
  * into one HBM allocation and stay resident.  NULL on failure
@@ -215,6 +217,12 @@ void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t te
  * (which: 0 exp f32, 1 log1p f64, 2 round_bf16, 3 SiLU).  Returns 0 or a
  * negative Yue2Error. */
 int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
+/* Execution choice: run decode steps (yue2_hip_forward and decoders created
+ * afterwards) through the persistent token-step kernel -- one launch per
+ * token, grid barriers between phases -- instead of one kernel per phase.
+ * Both produce the same bits.  Returns 1 when enabled, 0 when off or when
+ * the model's shape has no step kernel. */
+int32_t yue2_hip_model_set_step_kernel(Yue2Model *m, int32_t on);
 /* Diagnostics: RMSNorm guard fallbacks taken since the model was opened. */
 int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);
 
@@ -226,6 +234,18 @@ int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);
  * The decoder must have run at least one step. */
 int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t iters, float *avg_ms,
                                      double *bytes);
+
+/* Diagnostics: one decode step of token `id` at the cache's next position
+ * through the persistent token-step kernel (appends to the cache like
+ * yue2_hip_forward, computes no logits), recording the device wall clock
+ * (100 MHz) per workgroup: stamps[s * wgs + w] for slot s = 0 at the start,
+ * then per layer 14 slots -- QKV start, arrive, depart (QKV barrier),
+ * arrive, depart (attention barrier), O start, arrive, depart, gate/up
+ * start, arrive, depart, down start, arrive, depart.  cap = entries
+ * available in stamps; *wgs and *slots receive the trace shape.
+ * YUE2_ERR_ARG when the shape has no step kernel or cap is too small. */
+int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, int32_t id, uint64_t *stamps, int32_t cap,
+                            int32_t *wgs, int32_t *slots);
 
 #ifdef __cplusplus
 }

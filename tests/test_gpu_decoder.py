@@ -14,10 +14,12 @@ from helpers import bits
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def reduced(gpu, oracle_threads):
+@pytest.fixture(scope="module", params=[False, True], ids=["phase-kernels", "step-kernel"])
+def reduced(request, gpu, oracle_threads):
     ck = synthetic.checkpoint(synthetic.REDUCED, seed=0)
-    return ck, y2.Model.open(ck), O.Model(ck)
+    gm = y2.Model.open(ck)
+    assert gm.set_step_kernel(request.param) == request.param
+    return ck, gm, O.Model(ck)
 
 
 def test_greedy_decoder_matches_forward_loop(reduced):
@@ -98,3 +100,30 @@ def test_generate_rejects_bad_requests(reduced):
     with pytest.raises(y2.Yue2Error) as e:
         y2.generate(gm, [1, 2, 3], s, seed=0, phase=y2.PHASE_SEMANTIC)
     assert e.value.code == -3
+
+
+def test_3b_cfg_greedy_step_kernel_matches_oracle(gpu, oracle_threads):
+    """Batch-2 CFG through the 3B-shape step kernel (head_dim 128, GQA 3)."""
+    ck = synthetic.checkpoint(synthetic.CLASS_3B, seed=0)
+    gm = y2.Model.open(ck)
+    assert gm.set_step_kernel(True)
+    om = O.Model(ck)
+    V = ck.config.vocab_size
+    pos = synthetic.prompt(9, V, seed=0)
+    neg = synthetic.prompt(6, V, seed=1)
+    steps, scale = 3, 1.5
+    c1, l1 = gm.prefill_phase(pos, 16)
+    c2, l2 = gm.prefill_phase(neg, 16)
+    dec = y2.Decoder(gm, c1, c2, scale=scale)
+    toks, _ = dec.run(steps, first_logits=np.concatenate([l1, l2]))
+    dec.close()
+    o1, ol1 = om.prefill(pos, 16)
+    o2, ol2 = om.prefill(neg, 16)
+    assert np.array_equal(bits(l1), bits(ol1)) and np.array_equal(bits(l2), bits(ol2))
+    want = []
+    for _ in range(steps):
+        t = int(np.argmax(O.cfg_mix(ol1, ol2, scale)))
+        want.append(t)
+        ol1, ol2 = om.forward([t], o1), om.forward([t], o2)
+    assert list(toks) == want
+    gm.close()

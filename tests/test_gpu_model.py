@@ -21,8 +21,10 @@ def reduced(gpu, oracle_threads):
     return ck, y2.Model.open(ck), O.Model(ck)
 
 
-def test_reduced_prefill_and_64_greedy_steps(reduced):
+@pytest.mark.parametrize("step_kernel", [False, True], ids=["phase-kernels", "step-kernel"])
+def test_reduced_prefill_and_64_greedy_steps(reduced, step_kernel):
     ck, gm, om = reduced
+    assert gm.set_step_kernel(step_kernel) == step_kernel
     ids = synthetic.prompt(256, ck.config.vocab_size, seed=0)
     gcache, glog = gm.prefill_phase(ids, 256 + 64)
     ocache, olog = om.prefill(ids, 256 + 64)
@@ -36,9 +38,11 @@ def test_reduced_prefill_and_64_greedy_steps(reduced):
     assert gcache.length == ocache.length == 256 + 64
 
 
-def test_3b_short_run_bit_exact(gpu, oracle_threads):
+@pytest.mark.parametrize("step_kernel", [False, True], ids=["phase-kernels", "step-kernel"])
+def test_3b_short_run_bit_exact(gpu, oracle_threads, step_kernel):
     ck = synthetic.checkpoint(synthetic.CLASS_3B, seed=0)
     gm, om = y2.Model.open(ck), O.Model(ck)
+    assert gm.set_step_kernel(step_kernel) == step_kernel
     ids = synthetic.prompt(20, ck.config.vocab_size, seed=0)
     gcache, glog = gm.prefill_phase(ids, 32)
     ocache, olog = om.prefill(ids, 32)

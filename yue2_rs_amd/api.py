@@ -95,6 +95,7 @@ def lib() -> C.CDLL:
         "yue2_hip_clear_weights": (None, []),
         "yue2_hip_release_model": (None, []),
         "yue2_hip_config_validate": (i32, [vp]),
+        "yue2_hip_sampling_validate": (i32, [vp]),
         "yue2_hip_model_open": (vp, [vp, vp, vp, vp, vp]),
         "yue2_hip_model_free": (None, [vp]),
         "yue2_hip_cache_new": (vp, [vp, i32]),
@@ -112,6 +113,8 @@ def lib() -> C.CDLL:
         "yue2_hip_selftest_math": (i32, [i32, vp, vp, sz]),
         "yue2_hip_norm_fallbacks": (i32, [vp]),
         "yue2_hip_decoder_time_kernel": (i32, [vp, i32, i32, vp, vp]),
+        "yue2_hip_trace_step": (i32, [vp, vp, i32, vp, i32, vp, vp]),
+        "yue2_hip_model_set_step_kernel": (i32, [vp, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -175,6 +178,11 @@ class Sampling:
     def c(self) -> _Sampling:
         return _Sampling(self.temperature, self.top_p, self.top_k, self.repetition_penalty,
                          self.penalty_window, self.min_tokens, self.max_tokens)
+
+    def validate(self) -> None:
+        """Sampling::validate (src/protocol.rs:191-207): raises Yue2Error(-6)."""
+        s = self.c()
+        _check(lib().yue2_hip_sampling_validate(C.byref(s)))
 
 
 @dataclass
@@ -255,8 +263,24 @@ class Model:
         _check(lib().yue2_hip_prefill(self._h, cache._h, _ptr(arr), len(arr), phase, _ptr(out)))
         return cache, out
 
+    def set_step_kernel(self, on: bool) -> bool:
+        """Use the persistent token-step kernel for decode steps; returns
+        whether it is in use (False when the shape has none)."""
+        return bool(_check(lib().yue2_hip_model_set_step_kernel(self._h, 1 if on else 0)))
+
     def norm_fallbacks(self) -> int:
         return int(lib().yue2_hip_norm_fallbacks(self._h))
+
+    def trace_step(self, token: int, cache: "Cache") -> np.ndarray:
+        """One decode step through the persistent step kernel with phase
+        stamps: uint64 array [slot, workgroup] of the device wall clock
+        (100 MHz); slot 0 = start, then 14 per layer (see yue2_hip.h)."""
+        cap = (1 + 14 * self.config.num_hidden_layers) * 1024
+        out = np.zeros(cap, dtype=np.uint64)
+        wgs, slots = C.c_int32(0), C.c_int32(0)
+        _check(lib().yue2_hip_trace_step(self._h, cache._h, int(token), _ptr(out), cap,
+                                         C.byref(wgs), C.byref(slots)))
+        return out[: slots.value * wgs.value].reshape(slots.value, wgs.value)
 
 
 class Cache:

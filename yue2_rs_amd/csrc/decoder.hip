@@ -43,7 +43,9 @@ struct Yue2Decoder {
     uint64_t seed = 0;
 };
 
+// Sampling::validate (src/protocol.rs:191-207).
 static int validate_sampling(const Yue2Sampling* s) {
+    if (!s) return fail(YUE2_ERR_ARG, "null sampling");
     if (!std::isfinite(s->temperature) || !(s->temperature >= 0.0f && s->temperature <= 5.0f) ||
         !std::isfinite(s->top_p) || s->top_p <= 0.0f || s->top_p > 1.0f || s->top_k < 1 ||
         !std::isfinite(s->repetition_penalty) || s->repetition_penalty <= 0.0f ||
@@ -52,6 +54,8 @@ static int validate_sampling(const Yue2Sampling* s) {
         return fail(YUE2_ERR_SAMPLING, "Invalid sampling configuration");
     return YUE2_OK;
 }
+
+extern "C" int32_t yue2_hip_sampling_validate(const Yue2Sampling* s) { return validate_sampling(s); }
 
 // MT19937 seeding (src/sampling.rs:15-24).
 static void mt_seed(MtState* out, uint64_t seed) {
@@ -179,7 +183,8 @@ static int capture(Yue2Decoder* d) {
         (void)hipEventRecord(d->join, d->side);
     }
     launch_choose(s, d->sa);
-    rc = enqueue_step(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+    rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+    if (rc == 1) rc = enqueue_step(m, d->w, kv_view(d), d->rows, true, d->phase, s);
     if (d->need_rng) (void)hipStreamWaitEvent(s, d->join, 0);
     launch_advance(s, d->w.st, d->rows);
     hipGraph_t g = nullptr;
@@ -203,7 +208,7 @@ static int start(Yue2Decoder* d, const float* first_logits) {
     hipError_t e = hipMemcpyAsync(d->w.logits, first_logits, sizeof(float) * V * d->rows,
                                   hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return hip_fail(e, "logits upload");
-    launch_reset_state(s, d->w.st);
+    d->w.reset(s);
     launch_set_state(s, d->w.st, d->rows, d->caches[0]->length,
                      d->rows > 1 ? d->caches[1]->length : 0, 0, 0);
     if (d->need_rng)

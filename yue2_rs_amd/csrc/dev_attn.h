@@ -1,0 +1,313 @@
+// dev_attn.h -- device body of the single-query GQA decode attention with
+// the per-head QK RMSNorm, rotate-half RoPE and KV append of the new token
+// fused in (src/model.rs:121-130, 151-168, 313-397; src/tensor.rs:706-724,
+// 1158-1172).  Shared by the standalone attention kernel and the persistent
+// token-step kernel.
+//
+// The reference normalises by the global maximum and the global sum before
+// the PV product (p_j = exp(s_j - M) / sum, then sum_j p_j V_j), so the result
+// cannot be merged from independently normalised partitions without changing
+// its rounding.  The work of one (kv head, row) group is split over W
+// workgroups by 64-key blocks and runs the exact schedule in three phases
+// separated by syncs among those W workgroups only:
+//   1. q-norm + RoPE (every workgroup, for its group's query heads); the
+//      workgroup owning the newest key also norms/ropes k and appends K/V;
+//      scaled scores of its blocks into LDS, block maxima to HBM.
+//   2. M = max of the group's block maxima; e_j = exp(s_j - M) in LDS; block
+//      sums (64-lane butterfly) to HBM.
+//   3. total = block sums left to right; p_j = e_j / total; partial PV per
+//      block (512/dim key streams, butterfly over streams) to HBM; the last
+//      workgroup to finish adds the blocks left to right and rounds to BF16.
+// Each sync waits on a counter with a bounded spin: on timeout the device
+// error is set and the workgroup leaves, so every launch terminates.  All
+// workgroups of a group must be resident at once (callers launch at most one
+// workgroup per CU).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "kernels.h"
+#include "y2_math.h"
+
+namespace y2 {
+
+constexpr int kDevErrTimeout = 6;
+
+__device__ __forceinline__ void unpack8a(const uint4 w, float* f) {
+    f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+    f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+    f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+    f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+__device__ __forceinline__ size_t kv_off(int layer, int which, int kv_heads, int head, int capacity,
+                                         int pos, int dim) {
+    return ((((size_t)layer * 2 + which) * kv_heads + head) * capacity + pos) * dim;
+}
+
+// Release this workgroup's writes (the caller has passed a workgroup
+// barrier after them) and add one to *cnt; returns the old value.  The
+// acquire half makes the last arriver see everyone's writes.
+__device__ __forceinline__ int signal(int* cnt) {
+    return __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait (thread 0 spins, bounded) until *cnt >= target.  false on timeout or
+// when another workgroup has already reported an error.  The spin reads with
+// relaxed agent-scope loads (through to memory, no cache maintenance); one
+// acquire fence follows, and the workgroup barrier passes it on.
+__device__ bool wait_for(int* cnt, int target, StepState* st) {
+    __shared__ int s_ok;
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        unsigned spins = 0;
+        while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (++spins > (1u << 22) || __hip_atomic_load(&st->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                atomicCAS(&st->error, 0, kDevErrTimeout);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        s_ok = ok;
+    }
+    __syncthreads();
+    return s_ok != 0;
+}
+
+// One workgroup's share of the attention of kv head g, batch row b: the
+// workgroup handles 64-key blocks [wg * bpw, (wg + 1) * bpw) of that head.
+// G = heads / kv_heads <= MAXG query heads share the K/V rows.  e_s: LDS
+// scratch of G * bpw * 64 floats.  Returns false when a group sync timed out
+// (the device error is set).
+template <int NT, int D, int MAXG>
+__device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) {
+    constexpr int NW = NT / 64;
+    __shared__ float q_s[MAXG][D];
+    __shared__ float k_s[D];
+    __shared__ float hscale[MAXG + 1];
+    __shared__ float m_s[MAXG], t_s[MAXG];
+    constexpr int CPL = D / 8;     // lanes per key row
+    constexpr int KPW = 64 / CPL;  // keys per wave load
+    constexpr int S = KPW;         // PV key streams per 64-key block
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    StepState* st = a.st;
+    const int pos = st->pos[b];
+    const int L = pos + 1, cap = a.kv.capacity[b];
+    if (pos < 0 || L > cap) {
+        if (tid == 0 && wg == 0) atomicCAS(&st->error, 0, 1);
+        return true;
+    }
+    const int nb = (L + kBlockKeys - 1) / kBlockKeys;
+    const int W = (nb + a.bpw - 1) / a.bpw;
+    if (wg >= W) return true;
+    const int G = a.heads / a.kv_heads;
+    const int blk0 = wg * a.bpw, blk1 = min(nb, blk0 + a.bpw), nbl = blk1 - blk0;
+    const int j0 = blk0 * kBlockKeys, j1 = min(L, blk1 * kBlockKeys), nk = j1 - j0;
+    const int estride = a.bpw * kBlockKeys;
+    int* cnt = a.counters + ((size_t)b * a.kv_heads + g) * 4;
+    const float* row = a.qkv + (size_t)b * a.qkv_stride;
+    uint16_t* Kc = a.kv.base[b] + kv_off(a.layer, 0, a.kv_heads, g, cap, 0, D);
+    uint16_t* Vc = a.kv.base[b] + kv_off(a.layer, 1, a.kv_heads, g, cap, 0, D);
+    const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
+
+    // ---- phase 0: queries (and the new key/value) -------------------------
+    for (int i = tid; i < G * D; i += NT) q_s[i / D][i % D] = row[(size_t)(g * G) * D + i];
+    const bool owns_new = j1 == L && a.q_norm != nullptr;
+    if (owns_new)
+        for (int d = tid; d < D; d += NT) k_s[d] = row[(size_t)(a.heads + g) * D + d];
+    __syncthreads();
+    if (a.q_norm) {
+        // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
+        if (tid < G || (owns_new && tid == G)) {
+            const float* v = tid < G ? q_s[tid] : k_s;
+            float sum = -0.0f;
+            for (int d = 0; d < D; ++d) sum = sum + v[d] * v[d];
+            hscale[tid] = norm_scale_from_sum(sum, D, a.eps);
+        }
+        __syncthreads();
+        const int half = D / 2;
+        const float* cs = a.cos_t + (size_t)pos * half;
+        const float* sn = a.sin_t + (size_t)pos * half;
+        const int pairs = (G + (owns_new ? 1 : 0)) * half;
+        for (int i = tid; i < pairs; i += NT) {
+            const int h = i / half, d = i % half;
+            float* v = h < G ? q_s[h] : k_s;
+            const float* gam = h < G ? a.q_norm : a.k_norm;
+            const float s = hscale[h];
+            const float x0 = rb(rb(v[d] * s) * gam[d]);
+            const float x1 = rb(rb(v[d + half] * s) * gam[d + half]);
+            const float c = cs[d], si = sn[d];
+            const float y0 = rb(rb(x0 * c) - rb(x1 * si));
+            const float y1 = rb(rb(x1 * c) + rb(x0 * si));
+            v[d] = y0;
+            v[d + half] = y1;
+            if (h == G) {
+                Kc[(size_t)pos * D + d] = bf16_bits(y0);
+                Kc[(size_t)pos * D + d + half] = bf16_bits(y1);
+            }
+        }
+        if (owns_new) {
+            const float* vs = row + (size_t)(a.heads + a.kv_heads + g) * D;
+            for (int d = tid; d < D; d += NT) Vc[(size_t)pos * D + d] = bf16_bits(vs[d]);
+        }
+        __syncthreads();
+    }
+
+    // ---- phase 1: scaled scores and block maxima ---------------------------
+    {
+        const int c = lane % CPL, kk = lane / CPL;
+        float qv[MAXG][8];
+#pragma unroll
+        for (int h = 0; h < MAXG; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[h][e] = h < G ? q_s[h][8 * c + e] : 0.0f;
+        // each wave takes R consecutive key slots of KPW keys per round
+        constexpr int R = 8;
+        for (int base = j0 + wave * R * KPW; base < j1; base += NW * R * KPW) {
+            uint4 kr[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int j = base + r * KPW + kk;
+                kr[r] = j < j1 ? *reinterpret_cast<const uint4*>(Kc + (size_t)j * D + 8 * c)
+                               : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int j = base + r * KPW + kk;
+                float kf[8];
+                unpack8a(kr[r], kf);
+#pragma unroll
+                for (int h = 0; h < MAXG; ++h) {
+                    if (h >= G) break;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
+#pragma unroll
+                    for (int s = CPL / 2; s >= 1; s >>= 1) acc = acc + __shfl_xor(acc, s, 64);
+                    if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = wave; i < G * nbl; i += NW) {
+            const int h = i / nbl, bl = i % nbl;
+            const int jl = bl * kBlockKeys + lane;
+            float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            if (lane == 0) a.bmax[hbase + (size_t)h * a.blk_stride + blk0 + bl] = m;
+        }
+        __syncthreads();
+        if (tid == 0) signal(&cnt[0]);
+        if (!wait_for(&cnt[0], W, st)) return false;
+    }
+
+    // ---- phase 2: exp(s - M) and block sums --------------------------------
+    {
+        for (int h = wave; h < G; h += NW) {
+            const float* bm = a.bmax + hbase + (size_t)h * a.blk_stride;
+            float m = -__builtin_huge_valf();
+            for (int i = lane; i < nb; i += 64) m = fmaxf(m, bm[i]);
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            if (lane == 0) m_s[h] = m;
+        }
+        __syncthreads();
+        for (int i = tid; i < G * nk; i += NT) {
+            const int h = i / nk, jl = i % nk;
+            e_s[h * estride + jl] = expf_cr(e_s[h * estride + jl] - m_s[h]);
+        }
+        __syncthreads();
+        for (int i = wave; i < G * nbl; i += NW) {
+            const int h = i / nbl, bl = i % nbl;
+            const int jl = bl * kBlockKeys + lane;
+            float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
+            if (lane == 0) a.bsum[hbase + (size_t)h * a.blk_stride + blk0 + bl] = v;
+        }
+        __syncthreads();
+        if (tid == 0) signal(&cnt[1]);
+        if (!wait_for(&cnt[1], W, st)) return false;
+    }
+
+    // ---- phase 3: p = e / total, partial PV, merge by the last workgroup ---
+    {
+        if (tid < G) {
+            const float* bs = a.bsum + hbase + (size_t)tid * a.blk_stride;
+            float tot = bs[0];
+            for (int i = 1; i < nb; ++i) tot = tot + bs[i];
+            t_s[tid] = tot;
+        }
+        __syncthreads();
+        for (int i = tid; i < G * nk; i += NT) {
+            const int h = i / nk, jl = i % nk;
+            e_s[h * estride + jl] = e_s[h * estride + jl] / t_s[h];
+        }
+        __syncthreads();
+        const int t = lane / CPL, c = lane % CPL;
+        for (int bl = wave; bl < nbl; bl += NW) {
+            const int jb = (blk0 + bl) * kBlockKeys;
+            uint4 vr[kBlockKeys / S];
+#pragma unroll
+            for (int i = 0; i < kBlockKeys / S; ++i) {
+                const int j = jb + t + S * i;
+                vr[i] = j < L ? *reinterpret_cast<const uint4*>(Vc + (size_t)j * D + 8 * c)
+                              : make_uint4(0, 0, 0, 0);
+            }
+            float acc[MAXG][8];
+#pragma unroll
+            for (int h = 0; h < MAXG; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kBlockKeys / S; ++i) {
+                const int jj = t + S * i;
+                if (jb + jj < L) {
+                    float vf[8];
+                    unpack8a(vr[i], vf);
+#pragma unroll
+                    for (int h = 0; h < MAXG; ++h) {
+                        if (h >= G) break;
+                        const float p = e_s[h * estride + bl * kBlockKeys + jj];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p, vf[e], acc[h][e]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 32; s >= CPL; s >>= 1)
+#pragma unroll
+                for (int h = 0; h < MAXG; ++h)
+                    if (h < G)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] + __shfl_xor(acc[h][e], s, 64);
+            if (t == 0) {
+#pragma unroll
+                for (int h = 0; h < MAXG; ++h)
+                    if (h < G) {
+                        float* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) dst[e] = acc[h][e];
+                    }
+            }
+        }
+        __syncthreads();
+        __shared__ int s_last;
+        if (tid == 0) s_last = signal(&cnt[2]) == W - 1;
+        __syncthreads();
+        if (!s_last) return true;
+        for (int i = tid; i < G * D; i += NT) {
+            const int h = i / D, d = i % D;
+            const float* pp = a.part + (hbase + (size_t)h * a.blk_stride) * D + d;
+            float o = pp[0];
+            for (int blk = 1; blk < nb; ++blk) o = o + pp[(size_t)blk * D];
+            a.out[(size_t)b * a.out_stride + (size_t)(g * G + h) * D + d] = rb(o);
+        }
+        if (tid < 3) cnt[tid] = 0;
+    }
+    return true;
+}
+
+}  // namespace y2

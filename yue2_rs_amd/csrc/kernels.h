@@ -22,6 +22,8 @@ struct StepState {
     int32_t error;           // sticky device error code (0 = ok)
     int32_t norm_fallbacks;  // RMSNorm guard fallbacks (diagnostic)
     int32_t done;            // set when the phase's end token was chosen
+    int32_t seq;             // launches of the persistent step kernel (barrier parity)
+    int32_t pad[3];
 };
 
 enum GemvEpilogue { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_RAW = 3 };

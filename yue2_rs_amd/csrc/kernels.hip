@@ -230,13 +230,17 @@ __global__ void set_state_kernel(StepState* st, int rows, int pos0, int pos1, in
     }
 }
 
-__global__ void reset_state_kernel(StepState* st) {
+// Clears the step state and the sync counters: after a launch that stopped
+// on an error the counters may hold arrivals that never completed.
+__global__ void reset_state_kernel(StepState* st, int32_t* c0, int n0, int32_t* c1, int n1) {
     if (threadIdx.x == 0) {
         st->step = 0;
         st->error = 0;
         st->norm_fallbacks = 0;
         st->done = 0;
     }
+    for (int i = threadIdx.x; i < n0; i += blockDim.x) c0[i] = 0;
+    for (int i = threadIdx.x; i < n1; i += blockDim.x) c1[i] = 0;
 }
 
 void launch_fill(hipStream_t s, float* p, size_t n, float v) {
@@ -248,6 +252,8 @@ void launch_set_state(hipStream_t s, StepState* st, int rows, int pos0, int pos1
     set_state_kernel<<<1, 64, 0, s>>>(st, rows, pos0, pos1, id0, id1);
 }
 
-void launch_reset_state(hipStream_t s, StepState* st) { reset_state_kernel<<<1, 64, 0, s>>>(st); }
+void launch_reset_state(hipStream_t s, StepState* st, int32_t* c0, int n0, int32_t* c1, int n1) {
+    reset_state_kernel<<<1, 256, 0, s>>>(st, c0, c0 ? n0 : 0, c1, c1 ? n1 : 0);
+}
 
 }  // namespace y2

@@ -20,6 +20,10 @@ constexpr int kCodecOffset = 151853;
 constexpr int kCodecSize = 32768;
 constexpr int kContext = 24576;
 
+struct StepState;
+void launch_reset_state(hipStream_t s, StepState* st, int32_t* c0 = nullptr, int n0 = 0,
+                        int32_t* c1 = nullptr, int n1 = 0);
+
 struct LayerDev {
     uint16_t *wqkv, *wo, *wg, *wu, *wd;
     float *in_norm, *q_norm, *k_norm, *post_norm;
@@ -27,15 +31,18 @@ struct LayerDev {
 
 // Activations and attention scratch for one batch size.
 struct Workspace {
-    int rows = 0, max_blocks = 0, blk_stride = 0, log_cap = 0;
+    int rows = 0, max_blocks = 0, blk_stride = 0, log_cap = 0, counter_n = 0;
     void* block = nullptr;
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr;
     float *logits = nullptr, *mixed = nullptr;
     float *bmax = nullptr, *bsum = nullptr, *part = nullptr;
     int32_t* counters = nullptr;  // attention group counters, zero between launches
+    int32_t* bars = nullptr;      // two grid-barrier counters of the step kernel
     StepState* st = nullptr;
     int32_t* token_log = nullptr;
     int ensure(int rows, int max_blocks, const Yue2Config& c);
+    // Clear the step state and every sync counter (stream-ordered).
+    void reset(hipStream_t s) { launch_reset_state(s, st, counters, counter_n, bars, 2); }
     void release();
     ~Workspace() { release(); }
 };
@@ -50,6 +57,9 @@ struct Yue2Model {
     uint16_t *embed = nullptr, *lm_head = nullptr;
     float *final_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
     std::vector<y2::LayerDev> layers;
+    y2::LayerDev* layers_dev = nullptr;  // the same table in device memory (step kernel)
+    int cus = 0;                         // compute units: workgroups of the step kernel
+    bool step_kernel = false;            // run decode steps through the persistent kernel
     y2::Workspace ws;  // batch-1 workspace of the parity API
     int norm_fallbacks = 0;
 };
@@ -69,6 +79,10 @@ int hip_fail(hipError_t e, const char* what);
 bool device_ready();
 int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
                  hipStream_t s);
+// The same step as one persistent kernel when the shape has one (full
+// vocabulary head only); returns 1 when it cannot be used.
+int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
+                       hipStream_t s, unsigned long long* trace = nullptr, int trace_slots = 0);
 void phase_range(int phase, int* start, int* end, int* stop);
 int phase_end_id(int phase);
 int check_phase_vocab(int phase, int vocab);
@@ -76,7 +90,6 @@ int read_step_error(Workspace& w, hipStream_t s);
 
 // Small state kernels (kernels.hip).
 void launch_fill(hipStream_t s, float* p, size_t n, float v);
-void launch_reset_state(hipStream_t s, StepState* st);
 void launch_set_state(hipStream_t s, StepState* st, int rows, int pos0, int pos1, int id0, int id1);
 
 }  // namespace y2

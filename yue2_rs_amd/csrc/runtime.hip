@@ -17,6 +17,7 @@
 #include "../../include/yue2_hip.h"
 #include "kernels.h"
 #include "runtime.h"
+#include "step.h"
 #include "y2_math.h"
 
 using namespace y2;
@@ -86,6 +87,7 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     const size_t o_logits = cv.take<float>((size_t)rows * V);
     const size_t o_mixed = cv.take<float>((size_t)V);
     const size_t o_counters = cv.take<int32_t>((size_t)rows * Hkv * 4);
+    const size_t o_bars = cv.take<int32_t>(2);
     const size_t o_bmax = cv.take<float>((size_t)rows * Hq * blk_stride);
     const size_t o_bsum = cv.take<float>((size_t)rows * Hq * blk_stride);
     const size_t o_part = cv.take<float>((size_t)rows * Hq * blk_stride * D);
@@ -105,13 +107,16 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     logits = reinterpret_cast<float*>(p + o_logits);
     mixed = reinterpret_cast<float*>(p + o_mixed);
     counters = reinterpret_cast<int32_t*>(p + o_counters);
+    bars = reinterpret_cast<int32_t*>(p + o_bars);
     bmax = reinterpret_cast<float*>(p + o_bmax);
     bsum = reinterpret_cast<float*>(p + o_bsum);
     part = reinterpret_cast<float*>(p + o_part);
     st = reinterpret_cast<StepState*>(p + o_st);
     token_log = reinterpret_cast<int32_t*>(p + o_log);
     e = hipMemset(st, 0, sizeof(StepState));
+    counter_n = rows * Hkv * 4;
     if (e == hipSuccess) e = hipMemset(counters, 0, sizeof(int32_t) * rows * Hkv * 4);
+    if (e == hipSuccess) e = hipMemset(bars, 0, sizeof(int32_t) * 2);
     if (e != hipSuccess) return hip_fail(e, "hipMemset(step state)");
     return YUE2_OK;
 }
@@ -190,6 +195,62 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
                 m->final_norm, eps, nullptr};
     if ((e = launch_gemv(s, EPI_STORE, sa)) != hipSuccess) return hip_fail(e, "gemv(lm_head stop)");
     return YUE2_OK;
+}
+
+int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
+                       hipStream_t s, unsigned long long* trace, int trace_slots) {
+    const Yue2Config& c = m->c;
+    if (!trace && !m->step_kernel) return 1;
+    if ((head && phase != YUE2_PHASE_NONE) || !step_supported(c, rows, m->cus)) return 1;
+    const int D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
+    const int qw = Hq * D, qkvw = (Hq + 2 * Hkv) * D;
+    StepArgs a{};
+    a.layers = m->layers_dev;
+    a.embed = m->embed;
+    a.lm_head = m->lm_head;
+    a.final_norm = m->final_norm;
+    a.layers_n = c.num_hidden_layers;
+    a.hidden = c.hidden_size;
+    a.intermediate = c.intermediate_size;
+    a.vocab = c.vocab_size;
+    a.heads = Hq;
+    a.kv_heads = Hkv;
+    a.rows = rows;
+    a.head = head ? 1 : 0;
+    a.eps = c.rms_norm_eps;
+    a.x = w.x;
+    a.qkv = w.qkv;
+    a.att = w.att;
+    a.act = w.act;
+    a.logits = w.logits;
+    a.bars = w.bars;
+    a.st = w.st;
+    a.trace = trace;
+    a.trace_slots = trace ? trace_slots : 0;
+    AttnArgs& at = a.attn;
+    at.qkv = w.qkv;
+    at.qkv_stride = qkvw;
+    at.kv = kv;
+    at.heads = Hq;
+    at.kv_heads = Hkv;
+    at.dim = D;
+    at.rows = rows;
+    at.scale = 1.0f / std::sqrt((float)D);
+    at.eps = c.rms_norm_eps;
+    at.cos_t = m->rope_cos;
+    at.sin_t = m->rope_sin;
+    at.bmax = w.bmax;
+    at.bsum = w.bsum;
+    at.part = w.part;
+    at.out = w.att;
+    at.out_stride = qw;
+    at.blk_stride = w.blk_stride;
+    at.wgs = m->cus / (Hkv * rows);
+    at.bpw = (w.max_blocks + at.wgs - 1) / at.wgs;
+    at.counters = w.counters;
+    at.st = w.st;
+    hipError_t e = launch_step(s, a, m->cus);
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "step kernel");
 }
 
 void phase_range(int phase, int* start, int* end, int* stop) {
@@ -389,6 +450,12 @@ extern "C" Yue2Model* yue2_hip_model_open(const Yue2Config* c, const uint16_t* e
         up_norm(L.k_norm, src.k_norm, D);
         up_norm(L.post_norm, src.post_attention_layernorm, H);
     }
+    // The layer table in device memory, for the persistent step kernel.
+    if (ok && hipMalloc(&m->layers_dev, sizeof(LayerDev) * m->layers.size()) != hipSuccess) ok = false;
+    up(m->layers_dev, m->layers.data(), sizeof(LayerDev) * m->layers.size());
+    if (ok && (hipDeviceGetAttribute(&m->cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess ||
+               m->cus <= 0))
+        ok = false;
     if (!ok) {
         if (t_error.empty()) fail(YUE2_ERR_DEVICE, "weight upload failed");
         yue2_hip_model_free(m);
@@ -402,9 +469,17 @@ extern "C" void yue2_hip_model_free(Yue2Model* m) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     (void)hipStreamSynchronize(m->stream);
     m->ws.release();
+    if (m->layers_dev) (void)hipFree(m->layers_dev);
     if (m->block) (void)hipFree(m->block);
     (void)hipStreamDestroy(m->stream);
     delete m;
+}
+
+extern "C" int32_t yue2_hip_model_set_step_kernel(Yue2Model* m, int32_t on) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m) return fail(YUE2_ERR_ARG, "null model");
+    m->step_kernel = on != 0 && step_supported(m->c, 1, m->cus);
+    return m->step_kernel ? 1 : 0;
 }
 
 extern "C" int32_t yue2_hip_norm_fallbacks(const Yue2Model* m) {
@@ -460,11 +535,13 @@ extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* i
     kv.base[0] = c->kv;
     kv.capacity[0] = c->capacity;
     hipStream_t s = m->stream;
-    launch_reset_state(s, m->ws.st);
+    m->ws.reset(s);
     for (int t = 0; t < n; ++t) {
         launch_set_state(s, m->ws.st, 1, c->length + t, 0, ids[t], 0);
         const bool head = logits && t == n - 1;
-        if (int rc = enqueue_step(m, m->ws, kv, 1, head, phase, s)) return rc;
+        int rc = enqueue_step_fused(m, m->ws, kv, 1, head, phase, s);
+        if (rc == 1) rc = enqueue_step(m, m->ws, kv, 1, head, phase, s);
+        if (rc) return rc;
     }
     if (int rc = read_step_error(m->ws, s)) return rc;
     StepState st;
@@ -476,6 +553,42 @@ extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* i
                                  hipMemcpyDeviceToHost);
         if (e != hipSuccess) return hip_fail(e, "logits readback");
     }
+    return YUE2_OK;
+}
+
+extern "C" int32_t yue2_hip_trace_step(Yue2Model* m, Yue2Cache* c, int32_t id, uint64_t* stamps,
+                                       int32_t cap, int32_t* wgs, int32_t* slots) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || !c || !stamps || !wgs || !slots || c->m != m)
+        return fail(YUE2_ERR_ARG, "null model, cache or output");
+    if (!step_supported(m->c, 1, m->cus)) return fail(YUE2_ERR_ARG, "no step kernel for this shape");
+    if (c->length + 1 > c->capacity || c->length + 1 > m->c.max_position_embeddings)
+        return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    if (id < 0 || id >= m->c.vocab_size) return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
+    const int nb = 1 + kTraceSlotsPerLayer * m->c.num_hidden_layers;
+    const size_t n = (size_t)nb * m->cus;
+    if ((size_t)cap < n) return fail(YUE2_ERR_ARG, "stamp buffer too small");
+    const int blocks = (c->capacity + kBlockKeys - 1) / kBlockKeys;
+    if (int rc = m->ws.ensure(1, blocks, m->c)) return rc;
+    unsigned long long* dev = nullptr;
+    if (hipMalloc(&dev, n * sizeof(*dev)) != hipSuccess) return fail(YUE2_ERR_ALLOC, "trace buffer");
+    KvView kv{};
+    kv.base[0] = c->kv;
+    kv.capacity[0] = c->capacity;
+    hipStream_t s = m->stream;
+    m->ws.reset(s);
+    launch_set_state(s, m->ws.st, 1, c->length, 0, id, 0);
+    int rc = enqueue_step_fused(m, m->ws, kv, 1, false, YUE2_PHASE_NONE, s, dev, nb);
+    if (rc == 0) rc = read_step_error(m->ws, s);
+    if (rc == 0) {
+        hipError_t e = hipMemcpy(stamps, dev, n * sizeof(*dev), hipMemcpyDeviceToHost);
+        if (e != hipSuccess) rc = hip_fail(e, "trace readback");
+    }
+    (void)hipFree(dev);
+    if (rc) return rc;
+    c->length += 1;
+    *wgs = m->cus;
+    *slots = nb;
     return YUE2_OK;
 }
 

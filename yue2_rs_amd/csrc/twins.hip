@@ -300,7 +300,7 @@ extern "C" int32_t yue2_hip_cached_attention(const float* q, const float* k, con
     hipStream_t st = twin().stream;
     if (hipMemcpyAsync(s.q, q, heads * dim * sizeof(float), hipMemcpyHostToDevice, st) != hipSuccess)
         return 0;
-    launch_reset_state(st, twin().st);
+    launch_reset_state(st, twin().st, twin().counters, 4096);
     launch_set_state(st, twin().st, 1, (int)keys - 1, 0, 0, 0);
     if (launch_attention(st, attn_args(s, s.q, (int)(heads * dim), *e, (int)heads, (int)dim, s.out,
                                        (int)(heads * dim))) != hipSuccess)
@@ -344,7 +344,7 @@ extern "C" int32_t yue2_hip_ar_stack(const float* input, float* out, float* shad
         float* g_post = g_in + hidden;
         float* g_q = g_post + hidden;
         float* g_k = g_q + dim;
-        launch_reset_state(s, t.st);
+        launch_reset_state(s, t.st, t.counters, 4096);
         launch_set_state(s, t.st, 1, (int)prefix, 0, 0, 0);
         ok = hipMemcpyAsync(x, input, hidden * 4, hipMemcpyHostToDevice, s) == hipSuccess &&
              hipMemcpyAsync(cos_t + prefix * half, cos_row, half * 4, hipMemcpyHostToDevice, s) == hipSuccess &&

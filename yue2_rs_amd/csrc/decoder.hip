@@ -115,6 +115,7 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     if (d->rows == 2) cap = std::max(cap, uncond->capacity);
     const int V = m->c.vocab_size;
     int rc = d->w.ensure(d->rows, (cap + kBlockKeys - 1) / kBlockKeys, m->c);
+    if (rc == YUE2_OK && m->step_kernel && prepare_step(m, d->w) < 0) rc = YUE2_ERR_DEVICE;
     d->need_rng = sampling && sampling->temperature != 0.0f;
     hipError_t e = hipSuccess;
     if (rc == YUE2_OK && d->need_rng) {

@@ -21,10 +21,19 @@
 // Each sync waits on a counter with a bounded spin: on timeout the device
 // error is set and the workgroup leaves, so every launch terminates.  All
 // workgroups of a group must be resident at once (callers launch at most one
-// workgroup per CU).
+// workgroup per CU).  The blocks per workgroup follow the live length, so a
+// short context still spreads over every workgroup of its group.
+//
+// Data crossing workgroups inside a launch (the projected q/k/v rows, block
+// maxima and sums, partial outputs, the merged output) is written and read
+// with agent-scope relaxed atomics: on gfx950 these are sc1 accesses, which
+// write through to and read from the device-coherent level, so no L2
+// write-back or invalidate is needed.  A workgroup completes its stores
+// (s_waitcnt) before it signals a counter.
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "dev_mem.h"
 #include "kernels.h"
 #include "y2_math.h"
 
@@ -44,31 +53,25 @@ __device__ __forceinline__ size_t kv_off(int layer, int which, int kv_heads, int
     return ((((size_t)layer * 2 + which) * kv_heads + head) * capacity + pos) * dim;
 }
 
-// Release this workgroup's writes (the caller has passed a workgroup
-// barrier after them) and add one to *cnt; returns the old value.  The
-// acquire half makes the last arriver see everyone's writes.
-__device__ __forceinline__ int signal(int* cnt) {
-    return __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Add one to *cnt and return the old value.  Callers complete their stores
+// (stores_done) and pass a workgroup barrier first.
+__device__ __forceinline__ int signal(int* cnt) { return add_dev(cnt, 1); }
 
-// Wait (thread 0 spins, bounded) until *cnt >= target.  false on timeout or
-// when another workgroup has already reported an error.  The spin reads with
-// relaxed agent-scope loads (through to memory, no cache maintenance); one
-// acquire fence follows, and the workgroup barrier passes it on.
-__device__ bool wait_for(int* cnt, int target, StepState* st) {
+// Wait (thread 0 spins on relaxed loads, bounded) until *cnt >= target.
+// false on timeout or when another workgroup has already reported an error.
+__device__ __forceinline__ bool wait_for(int* cnt, int target, StepState* st) {
     __shared__ int s_ok;
     if (threadIdx.x == 0) {
         int ok = 1;
         unsigned spins = 0;
-        while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (++spins > (1u << 22) || __hip_atomic_load(&st->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                atomicCAS(&st->error, 0, kDevErrTimeout);
+        while (ld_dev_i(cnt) < target) {
+            if (++spins > (1u << 22) || ld_dev_i(&st->error)) {
+                set_error(&st->error, kDevErrTimeout);
                 ok = 0;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         s_ok = ok;
     }
     __syncthreads();
@@ -81,7 +84,7 @@ __device__ bool wait_for(int* cnt, int target, StepState* st) {
 // scratch of G * bpw * 64 floats.  Returns false when a group sync timed out
 // (the device error is set).
 template <int NT, int D, int MAXG>
-__device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) {
+__device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) {
     constexpr int NW = NT / 64;
     __shared__ float q_s[MAXG][D];
     __shared__ float k_s[D];
@@ -92,37 +95,47 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
     constexpr int S = KPW;         // PV key streams per 64-key block
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     StepState* st = a.st;
-    const int pos = st->pos[b];
-    const int L = pos + 1, cap = a.kv.capacity[b];
+    const int pos = *gbl(&st->pos[b]);
+    // (selects, not an indexed load: a runtime index would place the
+    // argument copy in scratch memory)
+    const int L = pos + 1, cap = b == 0 ? a.kv.capacity[0] : a.kv.capacity[1];
+    uint16_t* const kv_base = b == 0 ? a.kv.base[0] : a.kv.base[1];
     if (pos < 0 || L > cap) {
-        if (tid == 0 && wg == 0) atomicCAS(&st->error, 0, 1);
+        if (tid == 0 && wg == 0) set_error(&st->error, 1);
         return true;
     }
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const int W = (nb + a.bpw - 1) / a.bpw;
+    const int bpw = (nb + a.wgs - 1) / a.wgs;  // <= a.bpw, which sizes e_s
+    const int W = (nb + bpw - 1) / bpw;
     if (wg >= W) return true;
     const int G = a.heads / a.kv_heads;
-    const int blk0 = wg * a.bpw, blk1 = min(nb, blk0 + a.bpw), nbl = blk1 - blk0;
+    const int blk0 = wg * bpw, blk1 = min(nb, blk0 + bpw), nbl = blk1 - blk0;
     const int j0 = blk0 * kBlockKeys, j1 = min(L, blk1 * kBlockKeys), nk = j1 - j0;
-    const int estride = a.bpw * kBlockKeys;
+    const int estride = bpw * kBlockKeys;
     int* cnt = a.counters + ((size_t)b * a.kv_heads + g) * 4;
     const float* row = a.qkv + (size_t)b * a.qkv_stride;
-    uint16_t* Kc = a.kv.base[b] + kv_off(a.layer, 0, a.kv_heads, g, cap, 0, D);
-    uint16_t* Vc = a.kv.base[b] + kv_off(a.layer, 1, a.kv_heads, g, cap, 0, D);
+    uint16_t* Kc = kv_base + kv_off(a.layer, 0, a.kv_heads, g, cap, 0, D);
+    uint16_t* Vc = kv_base + kv_off(a.layer, 1, a.kv_heads, g, cap, 0, D);
     const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
 
     // ---- phase 0: queries (and the new key/value) -------------------------
-    for (int i = tid; i < G * D; i += NT) q_s[i / D][i % D] = row[(size_t)(g * G) * D + i];
+    for (int i = tid; i < G * D; i += NT) q_s[i / D][i % D] = ld_dev(row + (size_t)(g * G) * D + i);
     const bool owns_new = j1 == L && a.q_norm != nullptr;
     if (owns_new)
-        for (int d = tid; d < D; d += NT) k_s[d] = row[(size_t)(a.heads + g) * D + d];
+        for (int d = tid; d < D; d += NT) k_s[d] = ld_dev(row + (size_t)(a.heads + g) * D + d);
     __syncthreads();
     if (a.q_norm) {
         // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
         if (tid < G || (owns_new && tid == G)) {
             const float* v = tid < G ? q_s[tid] : k_s;
             float sum = -0.0f;
-            for (int d = 0; d < D; ++d) sum = sum + v[d] * v[d];
+            for (int d = 0; d < D; d += 16) {
+                float t[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) t[j] = v[d + j];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
+            }
             hscale[tid] = norm_scale_from_sum(sum, D, a.eps);
         }
         __syncthreads();
@@ -135,21 +148,21 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
             float* v = h < G ? q_s[h] : k_s;
             const float* gam = h < G ? a.q_norm : a.k_norm;
             const float s = hscale[h];
-            const float x0 = rb(rb(v[d] * s) * gam[d]);
-            const float x1 = rb(rb(v[d + half] * s) * gam[d + half]);
-            const float c = cs[d], si = sn[d];
+            const float x0 = rb(rb(v[d] * s) * gbl(gam)[d]);
+            const float x1 = rb(rb(v[d + half] * s) * gbl(gam)[d + half]);
+            const float c = gbl(cs)[d], si = gbl(sn)[d];
             const float y0 = rb(rb(x0 * c) - rb(x1 * si));
             const float y1 = rb(rb(x1 * c) + rb(x0 * si));
             v[d] = y0;
             v[d + half] = y1;
             if (h == G) {
-                Kc[(size_t)pos * D + d] = bf16_bits(y0);
-                Kc[(size_t)pos * D + d + half] = bf16_bits(y1);
+                gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
+                gblw(Kc)[(size_t)pos * D + d + half] = bf16_bits(y1);
             }
         }
         if (owns_new) {
             const float* vs = row + (size_t)(a.heads + a.kv_heads + g) * D;
-            for (int d = tid; d < D; d += NT) Vc[(size_t)pos * D + d] = bf16_bits(vs[d]);
+            for (int d = tid; d < D; d += NT) gblw(Vc)[(size_t)pos * D + d] = bf16_bits(ld_dev(vs + d));
         }
         __syncthreads();
     }
@@ -169,7 +182,7 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int j = base + r * KPW + kk;
-                kr[r] = j < j1 ? *reinterpret_cast<const uint4*>(Kc + (size_t)j * D + 8 * c)
+                kr[r] = j < j1 ? ldg4(Kc + (size_t)j * D + 8 * c)
                                : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
@@ -196,8 +209,9 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
             float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
-            if (lane == 0) a.bmax[hbase + (size_t)h * a.blk_stride + blk0 + bl] = m;
+            if (lane == 0) st_dev(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m);
         }
+        stores_done();
         __syncthreads();
         if (tid == 0) signal(&cnt[0]);
         if (!wait_for(&cnt[0], W, st)) return false;
@@ -208,7 +222,7 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
         for (int h = wave; h < G; h += NW) {
             const float* bm = a.bmax + hbase + (size_t)h * a.blk_stride;
             float m = -__builtin_huge_valf();
-            for (int i = lane; i < nb; i += 64) m = fmaxf(m, bm[i]);
+            for (int i = lane; i < nb; i += 64) m = fmaxf(m, ld_dev(bm + i));
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
             if (lane == 0) m_s[h] = m;
@@ -225,8 +239,9 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
             float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
-            if (lane == 0) a.bsum[hbase + (size_t)h * a.blk_stride + blk0 + bl] = v;
+            if (lane == 0) st_dev(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v);
         }
+        stores_done();
         __syncthreads();
         if (tid == 0) signal(&cnt[1]);
         if (!wait_for(&cnt[1], W, st)) return false;
@@ -234,11 +249,28 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
 
     // ---- phase 3: p = e / total, partial PV, merge by the last workgroup ---
     {
-        if (tid < G) {
-            const float* bs = a.bsum + hbase + (size_t)tid * a.blk_stride;
-            float tot = bs[0];
-            for (int i = 1; i < nb; ++i) tot = tot + bs[i];
-            t_s[tid] = tot;
+        // total = block sums added left to right; the sums are gathered into
+        // LDS by all threads first (a chain of dependent device loads would
+        // pay a memory round trip per block)
+        {
+            constexpr int CH = 128;
+            __shared__ float bs_s[MAXG][CH];
+            float tot = 0.0f;
+            for (int base = 0; base < nb; base += CH) {
+                const int n = min(CH, nb - base);
+                for (int i = tid; i < G * CH; i += NT) {
+                    const int h = i / CH, j = i % CH;
+                    if (j < n) bs_s[h][j] = ld_dev(a.bsum + hbase + (size_t)h * a.blk_stride + base + j);
+                }
+                __syncthreads();
+                if (tid < G) {
+                    int j = 0;
+                    if (base == 0) tot = bs_s[tid][j++];
+                    for (; j < n; ++j) tot = tot + bs_s[tid][j];
+                }
+                __syncthreads();
+            }
+            if (tid < G) t_s[tid] = tot;
         }
         __syncthreads();
         for (int i = tid; i < G * nk; i += NT) {
@@ -253,7 +285,7 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
 #pragma unroll
             for (int i = 0; i < kBlockKeys / S; ++i) {
                 const int j = jb + t + S * i;
-                vr[i] = j < L ? *reinterpret_cast<const uint4*>(Vc + (size_t)j * D + 8 * c)
+                vr[i] = j < L ? ldg4(Vc + (size_t)j * D + 8 * c)
                               : make_uint4(0, 0, 0, 0);
             }
             float acc[MAXG][8];
@@ -289,10 +321,11 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
                     if (h < G) {
                         float* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) dst[e] = acc[h][e];
+                        for (int e = 0; e < 8; ++e) st_dev(dst + e, acc[h][e]);
                     }
             }
         }
+        stores_done();
         __syncthreads();
         __shared__ int s_last;
         if (tid == 0) s_last = signal(&cnt[2]) == W - 1;
@@ -301,11 +334,19 @@ __device__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) 
         for (int i = tid; i < G * D; i += NT) {
             const int h = i / D, d = i % D;
             const float* pp = a.part + (hbase + (size_t)h * a.blk_stride) * D + d;
-            float o = pp[0];
-            for (int blk = 1; blk < nb; ++blk) o = o + pp[(size_t)blk * D];
-            a.out[(size_t)b * a.out_stride + (size_t)(g * G + h) * D + d] = rb(o);
+            // blocks added left to right; loads issued 16 at a time
+            float o = 0.0f;
+            for (int base = 0; base < nb; base += 16) {
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = base + j < nb ? ld_dev(pp + (size_t)(base + j) * D) : 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (base + j < nb) o = base + j == 0 ? v[j] : o + v[j];
+            }
+            st_dev(a.out + (size_t)b * a.out_stride + (size_t)(g * G + h) * D + d, rb(o));
         }
-        if (tid < 3) cnt[tid] = 0;
+        if (tid < 3) st_dev_i(&cnt[tid], 0);
     }
     return true;
 }

@@ -9,6 +9,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "dev_mem.h"
 #include "kernels.h"
 #include "y2_math.h"
 
@@ -39,7 +40,7 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ w, int row
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
         const int c = lane + 64 * it;
-        buf[it] = wr[c < nchunk ? c : 0];
+        buf[it] = ldg4(wr + (c < nchunk ? c : 0));
     }
 }
 
@@ -119,13 +120,15 @@ __device__ __forceinline__ void gemv_store(float* yp, float acc, float acc2) {
 // B = 2^-24 * 1.001 * sum_i t_i (n - i) on that chain's rounding error in f64
 // (each of the n-1 additions errs by at most 2^-24 of its partial sum); the
 // scale rb(1/sqrt(S/n + eps)) is monotone in S, so when both ends of
-// [E - B, E + B] give the same BF16 scale it is the chain's scale.  Otherwise
-// thread 0 runs the chain.
+// [E - B, E + B] give the same BF16 scale it is the chain's scale.  Every
+// thread evaluates that test on the same per-wave partials (so the outcome is
+// uniform); otherwise thread 0 runs the chain.
 template <int NT>
-__device__ float norm_scale_block(const float* xs, int n, float eps, int* fallbacks) {
+__device__ __forceinline__ float norm_scale_block(const float* xs, int n, float eps, int* fallbacks) {
     __shared__ double red_e[NT / 64], red_w[NT / 64];
     __shared__ float s_scale;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __syncthreads();  // a previous call's readers of red_e / red_w / s_scale are done
     double e_sum = 0.0, w_sum = 0.0;
     for (int i = tid; i < n; i += NT) {
         const float t = xs[i] * xs[i];
@@ -142,35 +145,37 @@ __device__ float norm_scale_block(const float* xs, int n, float eps, int* fallba
         red_w[wave] = w_sum;
     }
     __syncthreads();
+    double e = 0.0, w = 0.0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) {
+        e += red_e[i];
+        w += red_w[i];
+    }
+    if (e < 1e300 && w < 1e300) {
+        const double bound = w * 0x1.0p-24 * 1.001 + e * 4e-12;
+        const double lo = e - bound, hi = e + bound;
+        float lo_f = (float)lo, hi_f = (float)hi;
+        if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
+        if (lo_f < 0.0f) lo_f = 0.0f;
+        if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
+        const float s_a = norm_scale_from_sum(lo_f, n, eps);
+        const float s_b = norm_scale_from_sum(hi_f, n, eps);
+        if (hi_f <= 3.0e38f && s_a == s_b) return s_a;
+    }
     if (tid == 0) {
-        double e = 0.0, w = 0.0;
-        for (int i = 0; i < NT / 64; ++i) {
-            e += red_e[i];
-            w += red_w[i];
+        // the sequential chain itself; LDS reads batched ahead of the adds
+        float sum = -0.0f;
+        int i = 0;
+        for (; i + 16 <= n; i += 16) {
+            float t[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t[j] = xs[i + j];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
         }
-        float scale = 0.0f;
-        bool done = false;
-        if (e < 1e300 && w < 1e300) {
-            const double bound = w * 0x1.0p-24 * 1.001 + e * 4e-12;
-            const double lo = e - bound, hi = e + bound;
-            float lo_f = (float)lo, hi_f = (float)hi;
-            if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
-            if (lo_f < 0.0f) lo_f = 0.0f;
-            if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
-            const float s_a = norm_scale_from_sum(lo_f, n, eps);
-            const float s_b = norm_scale_from_sum(hi_f, n, eps);
-            if (hi_f <= 3.0e38f && s_a == s_b) {
-                scale = s_a;
-                done = true;
-            }
-        }
-        if (!done) {
-            float sum = -0.0f;
-            for (int i = 0; i < n; ++i) sum = sum + xs[i] * xs[i];
-            scale = norm_scale_from_sum(sum, n, eps);
-            if (fallbacks) atomicAdd(fallbacks, 1);
-        }
-        s_scale = scale;
+        for (; i < n; ++i) sum = sum + xs[i] * xs[i];
+        s_scale = norm_scale_from_sum(sum, n, eps);
+        if (fallbacks) add_dev(fallbacks, 1);
     }
     __syncthreads();
     return s_scale;

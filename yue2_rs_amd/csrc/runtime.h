@@ -40,11 +40,17 @@ struct Workspace {
     int32_t* bars = nullptr;      // two grid-barrier counters of the step kernel
     StepState* st = nullptr;
     int32_t* token_log = nullptr;
+    void* step_args = nullptr;  // device copy of the step kernel's arguments
+    void* step_host = nullptr;  // host copy of the same (StepArgs)
+    bool step_args_ready = false;
     int ensure(int rows, int max_blocks, const Yue2Config& c);
     // Clear the step state and every sync counter (stream-ordered).
     void reset(hipStream_t s) { launch_reset_state(s, st, counters, counter_n, bars, 2); }
     void release();
-    ~Workspace() { release(); }
+    Workspace() = default;
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    ~Workspace();
 };
 
 }  // namespace y2
@@ -83,6 +89,10 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
 // vocabulary head only); returns 1 when it cannot be used.
 int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
                        hipStream_t s, unsigned long long* trace = nullptr, int trace_slots = 0);
+// Upload the workspace's step kernel arguments (synchronous; call after
+// Workspace::ensure and before capturing a graph).  1 when the shape has no
+// step kernel.
+int prepare_step(Yue2Model* m, Workspace& w);
 void phase_range(int phase, int* start, int* end, int* stop);
 int phase_end_id(int phase);
 int check_phase_vocab(int phase, int vocab);

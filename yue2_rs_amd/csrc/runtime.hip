@@ -93,6 +93,7 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     const size_t o_part = cv.take<float>((size_t)rows * Hq * blk_stride * D);
     const size_t o_st = cv.take<StepState>(1);
     const size_t o_log = cv.take<int32_t>((size_t)log_cap);
+    const size_t o_args = cv.take<StepArgs>(1);
     hipError_t e = hipMalloc(&block, cv.offset);
     if (e != hipSuccess) {
         block = nullptr;
@@ -113,6 +114,9 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     part = reinterpret_cast<float*>(p + o_part);
     st = reinterpret_cast<StepState*>(p + o_st);
     token_log = reinterpret_cast<int32_t*>(p + o_log);
+    step_args = p + o_args;
+    step_args_ready = false;
+    if (!step_host) step_host = new StepArgs{};
     e = hipMemset(st, 0, sizeof(StepState));
     counter_n = rows * Hkv * 4;
     if (e == hipSuccess) e = hipMemset(counters, 0, sizeof(int32_t) * rows * Hkv * 4);
@@ -124,7 +128,14 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
 void Workspace::release() {
     if (block) (void)hipFree(block);
     block = nullptr;
+    step_args = nullptr;
+    step_args_ready = false;
     rows = max_blocks = 0;
+}
+
+Workspace::~Workspace() {
+    release();
+    delete static_cast<StepArgs*>(step_host);
 }
 
 // Enqueue one token step for `rows` batch rows reading ids/positions from the
@@ -197,11 +208,11 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
     return YUE2_OK;
 }
 
-int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
-                       hipStream_t s, unsigned long long* trace, int trace_slots) {
+int prepare_step(Yue2Model* m, Workspace& w) {
     const Yue2Config& c = m->c;
-    if (!trace && !m->step_kernel) return 1;
-    if ((head && phase != YUE2_PHASE_NONE) || !step_supported(c, rows, m->cus)) return 1;
+    const int rows = w.rows;
+    if (!step_supported(c, rows, m->cus)) return 1;
+    if (w.step_args_ready) return YUE2_OK;
     const int D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
     const int qw = Hq * D, qkvw = (Hq + 2 * Hkv) * D;
     StepArgs a{};
@@ -216,7 +227,6 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
     a.heads = Hq;
     a.kv_heads = Hkv;
     a.rows = rows;
-    a.head = head ? 1 : 0;
     a.eps = c.rms_norm_eps;
     a.x = w.x;
     a.qkv = w.qkv;
@@ -225,12 +235,9 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
     a.logits = w.logits;
     a.bars = w.bars;
     a.st = w.st;
-    a.trace = trace;
-    a.trace_slots = trace ? trace_slots : 0;
     AttnArgs& at = a.attn;
     at.qkv = w.qkv;
     at.qkv_stride = qkvw;
-    at.kv = kv;
     at.heads = Hq;
     at.kv_heads = Hkv;
     at.dim = D;
@@ -249,7 +256,26 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
     at.bpw = (w.max_blocks + at.wgs - 1) / at.wgs;
     at.counters = w.counters;
     at.st = w.st;
-    hipError_t e = launch_step(s, a, m->cus);
+    if (step_lds_bytes(a) > 128 * 1024) return 1;
+    hipError_t e = hipMemcpy(w.step_args, &a, sizeof(StepArgs), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "step arguments upload");
+    *reinterpret_cast<StepArgs*>(w.step_host) = a;
+    w.step_args_ready = true;
+    return YUE2_OK;
+}
+
+int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
+                       hipStream_t s, unsigned long long* trace, int trace_slots) {
+    if (!trace && !m->step_kernel) return 1;
+    if ((head && phase != YUE2_PHASE_NONE) || rows != w.rows || !step_supported(m->c, rows, m->cus)) return 1;
+    if (!w.step_args_ready) return fail(YUE2_ERR_DEVICE, "step kernel arguments not prepared");
+    StepCall call{};
+    call.kv = kv;
+    call.head = head ? 1 : 0;
+    call.trace = trace;
+    call.trace_slots = trace ? trace_slots : 0;
+    hipError_t e = launch_step(s, static_cast<const StepArgs*>(w.step_args),
+                               *reinterpret_cast<const StepArgs*>(w.step_host), call, m->cus);
     return e == hipSuccess ? YUE2_OK : hip_fail(e, "step kernel");
 }
 
@@ -531,6 +557,8 @@ extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* i
             return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
     const int blocks = (c->capacity + kBlockKeys - 1) / kBlockKeys;
     if (int rc = m->ws.ensure(1, blocks, m->c)) return rc;
+    if (m->step_kernel)
+        if (int rc = prepare_step(m, m->ws); rc < 0) return rc;
     KvView kv{};
     kv.base[0] = c->kv;
     kv.capacity[0] = c->capacity;
@@ -570,6 +598,7 @@ extern "C" int32_t yue2_hip_trace_step(Yue2Model* m, Yue2Cache* c, int32_t id, u
     if ((size_t)cap < n) return fail(YUE2_ERR_ARG, "stamp buffer too small");
     const int blocks = (c->capacity + kBlockKeys - 1) / kBlockKeys;
     if (int rc = m->ws.ensure(1, blocks, m->c)) return rc;
+    if (int rc = prepare_step(m, m->ws)) return rc < 0 ? rc : fail(YUE2_ERR_ARG, "no step kernel for this shape");
     unsigned long long* dev = nullptr;
     if (hipMalloc(&dev, n * sizeof(*dev)) != hipSuccess) return fail(YUE2_ERR_ALLOC, "trace buffer");
     KvView kv{};

@@ -4,23 +4,33 @@
 //
 // Why one kernel: each phase of the step (norm -> QKV -> attention -> O ->
 // norm -> gate/up -> down) depends on the complete output of the previous
-// one, so a kernel per phase pays a launch, a ramp-up and a drain for every
-// dependency -- about 5 us each, ~140 times per token.  Here one workgroup
-// per CU stays resident for the whole step.  Phases are separated by grid
-// barriers, and before arriving at a barrier every wave already requests the
-// weights of its first row of the next GEMV, so HBM keeps streaming while the
-// barrier and the next phase's RMSNorm resolve.
+// one.  A kernel per phase pays a launch, a ramp-up and a drain at every one
+// of those ~140 dependencies per token (about 7 us each on this part, the
+// same as a whole 16 MB read).  Here one workgroup per CU stays resident for
+// the whole step and phases are separated by grid barriers.
+//
+// Weight streaming: each wave walks its rows of a GEMV as a sequence of
+// items (SEG 16-byte chunks per lane of one row, both matrices for the
+// gate/up pair) through a ring of R register slots, so R-1 items are in
+// flight while one is multiplied.  Before arriving at a barrier every wave
+// already issues the first R-1 items of the next GEMV, so HBM keeps
+// streaming while the barrier, the staging and the RMSNorm resolve.
 //
 // Work split (n rows of a GEMV over G workgroups): workgroup w owns rows
-// [w*n/G, (w+1)*n/G); its 8 waves take every 8th row, double-buffered.  The
-// arithmetic of every row is the DOT order of dev_gemv.h, the attention is
-// dev_attn.h with one (kv head, row) group per G/(kv_heads*rows) workgroups,
-// so the results equal the per-phase kernels' bit for bit.
+// [w*n/G, (w+1)*n/G); its 8 waves take every 8th row.  Every row's
+// arithmetic is the DOT order of dev_gemv.h and the attention is dev_attn.h
+// with one (kv head, row) group per G/(kv_heads*rows) workgroups, so the
+// results equal the per-phase kernels' bit for bit.
 //
-// Barriers: a counter per launch (two, alternating with the launch sequence
-// number so the idle one can be cleared), bounded spins; a timeout sets the
-// device error and every workgroup leaves, so a launch always terminates.
-// The launch uses exactly one workgroup per CU, so all are co-resident.
+// Cross-workgroup data (x, q/k/v, attention output, SwiGLU activations) is
+// written and read with agent-scope relaxed atomics (sc1 accesses on gfx950,
+// coherent across the XCDs' L2s without write-back or invalidate).  A barrier
+// is: every thread completes its stores (s_waitcnt), workgroup barrier,
+// thread 0 adds to the launch's counter and spins on relaxed loads (bounded;
+// a timeout sets the device error and every workgroup leaves, so a launch
+// always terminates).  Two counters alternate with the launch sequence
+// number so the idle one can be cleared.  The launch uses exactly one
+// workgroup per CU, so all are co-resident.
 #include <algorithm>
 
 #include "dev_attn.h"
@@ -42,35 +52,30 @@ struct Tracer {
     unsigned long long* buf;
     int slots, slot;
     __device__ __forceinline__ void mark() {
-        if (buf && threadIdx.x == 0 && slot < slots) buf[(size_t)slot * gridDim.x + blockIdx.x] = wall_clock64();
+        if (buf && threadIdx.x == 0 && slot < slots) gblw(buf)[(size_t)slot * gridDim.x + blockIdx.x] = wall_clock64();
         ++slot;
     }
 };
 
-// Grid barrier number `epoch` of this launch.  Thread 0 arrives with a
-// release add (writes this XCD's dirty L2 lines back) and spins on relaxed
-// agent-scope loads, which read through to memory without touching the
-// caches; one acquire fence after the spin (L1/L2 invalidate) makes the other
-// workgroups' results visible, and the workgroup barrier passes that on.
-__device__ bool grid_sync(int* bar, int epoch, StepState* st, Tracer& tr) {
+// Grid barrier number `epoch` of this launch.  Callers have completed their
+// cross-workgroup stores (stores_done) before calling.
+__device__ __forceinline__ bool grid_sync(int* bar, int epoch, StepState* st, Tracer& tr) {
     __shared__ int s_ok;
     __syncthreads();
     tr.mark();
     if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(bar, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        add_dev(bar, 1);
         const int target = epoch * (int)gridDim.x;
         int ok = 1;
         unsigned spins = 0;
-        while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (++spins > (1u << 22) ||
-                __hip_atomic_load(&st->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                atomicCAS(&st->error, 0, kDevErrBarrier);
+        while (ld_dev_i(bar) < target) {
+            if (++spins > (1u << 22) || ld_dev_i(&st->error)) {
+                set_error(&st->error, kDevErrBarrier);
                 ok = 0;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         s_ok = ok;
     }
     tr.mark();
@@ -80,75 +85,209 @@ __device__ bool grid_sync(int* bar, int epoch, StepState* st, Tracer& tr) {
 
 __device__ __forceinline__ int part_lo(int n, int w, int parts) { return (int)(((long)n * w) / parts); }
 
-// Request this wave's first row of rows [r0, r1) (both matrices for a pair).
-// The load is unconditional (a wave without a row re-reads the range's last
-// row, or row 0 for an empty range) so the buffer is provably overwritten here
-// and holds no live values between phases.
-template <int IT, bool PAIR>
-__device__ __forceinline__ void prefetch_first(const uint16_t* w, const uint16_t* w2, int k, int r0,
-                                               int r1, uint4* buf) {
-    const int lane = threadIdx.x & 63;
-    const int row = max(min(r0 + (threadIdx.x >> 6), r1 - 1), 0);
-    load_row<IT>(w, row, k, lane, buf);
-    if constexpr (PAIR) load_row<IT>(w2, row, k, lane, buf + IT);
+// ---- GEMV through a register ring ------------------------------------------
+
+constexpr int seg_of(int it, int cap) {
+    int s = cap < it ? cap : it;
+    while (it % s) --s;
+    return s;
 }
 
-// Rows [r0, r1) of y = W xs with epilogue EPI; buf holds each wave's first row.
-template <int B, int EPI, int IT>
-__device__ __forceinline__ void gemv_rows(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
-                                          float* y, int y_stride, int r0, int r1, uint4* buf) {
-    constexpr bool PAIR = EPI == EPI_SWIGLU;
-    const int lane = threadIdx.x & 63;
-    int row = r0 + (threadIdx.x >> 6);
-    float acc[B], acc2[B];
-    if constexpr (IT > 8) {
-        // single buffer: one long row per wave is enough bytes in flight
-        while (row < r1) {
-            dot_rows<B, IT, PAIR>(xs, k, lane, buf, buf + IT, acc, acc2);
-            if (lane == 0)
-#pragma unroll
-                for (int b = 0; b < B; ++b) gemv_store<EPI>(y + (size_t)b * y_stride + row, acc[b], acc2[b]);
-            row += kStepWaves;
-            if (row < r1) {
-                load_row<IT>(w, row, k, lane, buf);
-                if constexpr (PAIR) load_row<IT>(w2, row, k, lane, buf + IT);
-            }
-        }
+// Item shape of a GEMV with IT chunks per lane per row.
+template <int IT, bool PAIR>
+struct Ring {
+    static constexpr int SEG = seg_of(IT, PAIR ? 2 : 4);  // chunks per lane per item
+    static constexpr int NSEG = IT / SEG;                 // items per row
+    static constexpr int R = PAIR ? 4 : 5;                // ring depth (items)
+    static constexpr int W = SEG * (PAIR ? 2 : 1);        // uint4 per item
+    static constexpr int SIZE = R * W;                    // uint4 of the ring
+};
+
+// The rows of this wave in [r0, r1) as items; item q of a wave is segment
+// q % NSEG of row r0 + wave + 8 * (q / NSEG).  Items past the last one (the
+// ring's look-ahead at the end of a GEMV) re-read the last item, and a wave
+// without rows reads row min(r0, n - 1): loads stay unconditional and in
+// bounds, and the re-reads hit in L2.
+template <int NSEG>
+__device__ __forceinline__ void item_at(int q, int Q, int r0, int n, int* row, int* seg) {
+    const int wave = threadIdx.x >> 6;
+    if (Q == 0) {
+        *row = min(r0, n - 1);
+        *seg = 0;
         return;
     }
-    uint4 nb[PAIR ? 2 * IT : IT];
-    while (row < r1) {
-        int next = row + kStepWaves;
-        if (next < r1) {
-            load_row<IT>(w, next, k, lane, nb);
-            if constexpr (PAIR) load_row<IT>(w2, next, k, lane, nb + IT);
-        }
-        dot_rows<B, IT, PAIR>(xs, k, lane, buf, buf + IT, acc, acc2);
-        if (lane == 0)
+    const int qq = min(q, Q - 1);
+    *row = r0 + wave + kStepWaves * (qq / NSEG);
+    *seg = qq % NSEG;
+}
+
+template <int SEG, bool PAIR>
+__device__ __forceinline__ void load_item(const uint16_t* w, const uint16_t* w2, int k, int row, int seg,
+                                          uint4* buf) {
+    const int lane = threadIdx.x & 63, nchunk = k >> 3;
+    const uint4* a = reinterpret_cast<const uint4*>(w + (size_t)row * k);
 #pragma unroll
-            for (int b = 0; b < B; ++b) gemv_store<EPI>(y + (size_t)b * y_stride + row, acc[b], acc2[b]);
-        row = next;
-        if (row >= r1) break;
-        next = row + kStepWaves;
-        if (next < r1) {
-            load_row<IT>(w, next, k, lane, buf);
-            if constexpr (PAIR) load_row<IT>(w2, next, k, lane, buf + IT);
-        }
-        dot_rows<B, IT, PAIR>(xs, k, lane, nb, nb + IT, acc, acc2);
-        if (lane == 0)
+    for (int it = 0; it < SEG; ++it) {
+        const int c = lane + 64 * (seg * SEG + it);
+        buf[it] = ldg4(a + (c < nchunk ? c : 0));
+    }
+    if constexpr (PAIR) {
+        const uint4* b = reinterpret_cast<const uint4*>(w2 + (size_t)row * k);
 #pragma unroll
-            for (int b = 0; b < B; ++b) gemv_store<EPI>(y + (size_t)b * y_stride + row, acc[b], acc2[b]);
-        row = next;
+        for (int it = 0; it < SEG; ++it) {
+            const int c = lane + 64 * (seg * SEG + it);
+            buf[SEG + it] = ldg4(b + (c < nchunk ? c : 0));
+        }
     }
 }
 
-// xs[b*k + i] = src[b*stride + i]
-template <int B>
+// Continue the DOT chains of batch rows b < B over one item (chunks of the
+// lane past the row end contribute fma(0, 0, acc) = acc).
+template <int B, int SEG, bool PAIR>
+__device__ __forceinline__ void dot_item(const float* xs, int k, int seg, const uint4* wv, float* acc,
+                                         float* acc2) {
+    const int lane = threadIdx.x & 63, nchunk = k >> 3;
+#pragma unroll
+    for (int it = 0; it < SEG; ++it) {
+        const int c = lane + 64 * (seg * SEG + it);
+        const bool ok = c < nchunk;
+        const int cc = ok ? c : 0;
+        float wf[8], wf2[8];
+        unpack_bf16x8(wv[it], wf);
+        if constexpr (PAIR) unpack_bf16x8(wv[SEG + it], wf2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            wf[e] = ok ? wf[e] : 0.0f;
+            if constexpr (PAIR) wf2[e] = ok ? wf2[e] : 0.0f;
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float4* xp = reinterpret_cast<const float4*>(xs + b * k + 8 * cc);
+            const float4 x0 = xp[0], x1 = xp[1];
+            float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[e] = ok ? xv[e] : 0.0f;
+            float s = acc[b];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = __builtin_fmaf(wf[e], xv[e], s);
+            acc[b] = s;
+            if constexpr (PAIR) {
+                float s2 = acc2[b];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s2 = __builtin_fmaf(wf2[e], xv[e], s2);
+                acc2[b] = s2;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Rows of the residual stream owned by one workgroup, staged in LDS before a
+// residual GEMV (a global load in the epilogue would retire behind every
+// weight load in flight and drain the ring).
+constexpr int kResRows = 64;
+
+// Output of one row (see gemv_store in dev_gemv.h) through an sc1 store;
+// res = the row's current residual value (EPI_RESID).
+template <int EPI>
+__device__ __forceinline__ void store_dev(float* yp, float acc, float acc2, float res) {
+    if constexpr (EPI == EPI_STORE) {
+        st_dev(yp, rb(acc));
+    } else if constexpr (EPI == EPI_RESID) {
+        st_dev(yp, rb(res + rb(acc)));
+    } else {
+        st_dev(yp, rb(silu_rb(rb(acc)) * rb(acc2)));
+    }
+}
+
+// Issue the first R-1 items of this wave's rows [r0, r1) into ring slots.
+template <int IT, bool PAIR>
+__device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t* w2, int k, int r0, int r1,
+                                              int n, uint4* ring) {
+    using C = Ring<IT, PAIR>;
+    const int wave = threadIdx.x >> 6, span = r1 - r0;
+    const int Q = (span > wave ? (span - wave + kStepWaves - 1) / kStepWaves : 0) * C::NSEG;
+#pragma unroll
+    for (int s = 0; s < C::R - 1; ++s) {
+        int row, seg;
+        item_at<C::NSEG>(s, Q, r0, n, &row, &seg);
+        load_item<C::SEG, PAIR>(w, w2, k, row, seg, ring + s * C::W);
+    }
+}
+
+// Rows [r0, r1) of y = W xs (xs: B staged rows of k floats in LDS) with
+// epilogue EPI; the ring holds the first R-1 items (prefetch_ring).  res:
+// for EPI_RESID, res[b * kResRows + (row - r0)] = y's current value (LDS).
+template <int B, int EPI, int IT>
+__device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
+                                          float* y, int y_stride, int r0, int r1, int n, uint4* ring,
+                                          const float* res = nullptr) {
+    constexpr bool PAIR = EPI == EPI_SWIGLU;
+    using C = Ring<IT, PAIR>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, span = r1 - r0;
+    const int Q = (span > wave ? (span - wave + kStepWaves - 1) / kStepWaves : 0) * C::NSEG;
+    float acc[B], acc2[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[b] = acc2[b] = 0.0f;
+    for (int q0 = 0; q0 < Q; q0 += C::R) {
+#pragma unroll
+        for (int s = 0; s < C::R; ++s) {
+            const int q = q0 + s;
+            if (q >= Q) break;
+            {
+                // refill the slot of item q - 1 with item q + R - 1
+                int row, seg;
+                item_at<C::NSEG>(q + C::R - 1, Q, r0, n, &row, &seg);
+                load_item<C::SEG, PAIR>(w, w2, k, row, seg, ring + ((s + C::R - 1) % C::R) * C::W);
+            }
+            const int seg = q % C::NSEG;
+            dot_item<B, C::SEG, PAIR>(xs, k, seg, ring + s * C::W, acc, acc2);
+            if (seg == C::NSEG - 1) {
+                const int row = r0 + wave + kStepWaves * (q / C::NSEG);
+#pragma unroll
+                for (int b = 0; b < B; ++b) {
+                    const float v = wave_sum_xor(acc[b]);
+                    const float v2 = PAIR ? wave_sum_xor(acc2[b]) : 0.0f;
+                    const float rv = EPI == EPI_RESID ? res[b * kResRows + (row - r0)] : 0.0f;
+                    if (lane == 0) store_dev<EPI>(y + (size_t)b * y_stride + row, v, v2, rv);
+                    acc[b] = acc2[b] = 0.0f;
+                }
+            }
+        }
+    }
+}
+
+// ---- staging and norms -----------------------------------------------------
+
+// xs[b*k + i] = src[b*stride + i] for b < B (N >= k / 512 loads per thread,
+// all issued before the LDS writes).
+template <int B, int N>
 __device__ __forceinline__ void stage(float* xs, const float* src, int stride, int k) {
+    float v[B][N];
 #pragma unroll
     for (int b = 0; b < B; ++b)
-        for (int i = threadIdx.x; i < k; i += kStepThreads) xs[b * k + i] = src[(size_t)b * stride + i];
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = threadIdx.x + j * kStepThreads;
+            v[b][j] = i < k ? ld_dev(src + (size_t)b * stride + i) : 0.0f;
+        }
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = threadIdx.x + j * kStepThreads;
+            if (i < k) xs[b * k + i] = v[b][j];
+        }
     __syncthreads();
+}
+
+// res[b * kResRows + r] = x[b * stride + r0 + r] for r < r1 - r0 (LDS); the
+// caller's next workgroup barrier publishes it.
+template <int B>
+__device__ __forceinline__ void stage_res(float* res, const float* x, int stride, int r0, int r1) {
+    const int n = r1 - r0;
+    for (int i = threadIdx.x; i < B * n; i += kStepThreads)
+        res[(i / n) * kResRows + i % n] = ld_dev(x + (size_t)(i / n) * stride + r0 + i % n);
 }
 
 // xs[b] = RMSNorm(xs[b]) with gammas g (Norm::apply, src/tensor.rs:1140-1157).
@@ -158,135 +297,201 @@ __device__ __forceinline__ void norm_rows(float* xs, int k, const float* g, floa
     for (int b = 0; b < B; ++b) {
         float* xb = xs + b * k;
         const float s = norm_scale_block<kStepThreads>(xb, k, eps, fallbacks);
-        for (int i = threadIdx.x; i < k; i += kStepThreads) xb[i] = rb(rb(xb[i] * s) * g[i]);
+        for (int i = threadIdx.x; i < k; i += kStepThreads) xb[i] = rb(rb(xb[i] * s) * gbl(g)[i]);
     }
     __syncthreads();
 }
 
+// ---- the kernel ------------------------------------------------------------
+
+typedef const __attribute__((address_space(4))) StepArgs* ArgsPtr;
+
+// The arguments through a pointer the compiler cannot follow from one phase
+// to the next: fields are re-read (scalar loads) in the phase that uses them
+// instead of being kept live, in scalar registers, across the whole launch.
+__device__ __forceinline__ ArgsPtr fresh(ArgsPtr p) {
+    asm volatile("" : "+s"(p));
+    return p;
+}
+
+// The attention arguments of layer l (field by field: a struct copy cannot
+// bind to the constant address space).
+__device__ __forceinline__ AttnArgs layer_attn(ArgsPtr a, const KvView& kv, int l) {
+    AttnArgs at;
+    at.qkv = a->attn.qkv;
+    at.qkv_stride = a->attn.qkv_stride;
+    at.kv = kv;
+    at.layer = l;
+    at.heads = a->attn.heads;
+    at.kv_heads = a->attn.kv_heads;
+    at.dim = a->attn.dim;
+    at.rows = a->attn.rows;
+    at.scale = a->attn.scale;
+    at.eps = a->attn.eps;
+    at.q_norm = a->layers[l].q_norm;
+    at.k_norm = a->layers[l].k_norm;
+    at.cos_t = a->attn.cos_t;
+    at.sin_t = a->attn.sin_t;
+    at.bmax = a->attn.bmax;
+    at.bsum = a->attn.bsum;
+    at.part = a->attn.part;
+    at.out = a->attn.out;
+    at.out_stride = a->attn.out_stride;
+    at.blk_stride = a->attn.blk_stride;
+    at.wgs = a->attn.wgs;
+    at.bpw = a->attn.bpw;
+    at.counters = a->attn.counters;
+    at.st = a->attn.st;
+    return at;
+}
+
 template <int B, int D, int ITH, int ITQ, int ITI>
-__global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs a) {
+__global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
     extern __shared__ float lds[];
-    constexpr int PMAX = std::max(std::max(2 * ITH, ITQ), ITI);
+    __shared__ float res_s[B * kResRows];
+    constexpr int RMAX = std::max(std::max(Ring<ITH, false>::SIZE, Ring<ITH, true>::SIZE),
+                                  std::max(Ring<ITQ, false>::SIZE, Ring<ITI, false>::SIZE));
+    const ArgsPtr args = (ArgsPtr)args_dev;
     const int tid = threadIdx.x, wg = blockIdx.x, nwg = gridDim.x;
-    StepState* st = a.st;
-    if (st->error) return;
-    const int seq = st->seq;
-    int* bar = a.bars + (seq & 1);
-    if (wg == 0 && tid == 0) a.bars[(seq + 1) & 1] = 0;
+    StepState* st = fresh(args)->st;
+    if (ld_dev_i(&st->error)) return;
+    const int seq = *gbl(&st->seq);
+    int* bar = fresh(args)->bars + (seq & 1);
+    if (wg == 0 && tid == 0) st_dev_i(fresh(args)->bars + ((seq + 1) & 1), 0);
     int epoch = 0;
-    const int H = a.hidden, I = a.intermediate, qw = a.heads * D;
-    const int qkvw = qw + 2 * a.kv_heads * D;
-    int* fallbacks = wg == 0 ? &st->norm_fallbacks : nullptr;
-    uint4 pre[PMAX];
-    Tracer tr{a.trace, a.trace_slots, 0};
+    uint4 ring[RMAX];
+    Tracer tr{call.trace, call.trace_slots, 0};
     tr.mark();
 
     // Embedding (src/model.rs:452-464): this workgroup's slice of x, and the
     // whole of x staged for the first norm.
-    for (int b = 0; b < B; ++b) {
-        const int id = st->ids[b];
-        if (id < 0 || id >= a.vocab) {
-            if (tid == 0) atomicCAS(&st->error, 0, 2);
-            return;
-        }
-    }
     {
-        const int lo = part_lo(H, wg, nwg), hi = part_lo(H, wg + 1, nwg);
+        ArgsPtr a = fresh(args);
+        const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
+        int ids[B];
         for (int b = 0; b < B; ++b) {
-            const uint16_t* e = a.embed + (size_t)st->ids[b] * H;
-            for (int i = lo + tid; i < hi; i += kStepThreads) a.x[(size_t)b * H + i] = bf16(e[i]);
+            ids[b] = *gbl(&st->ids[b]);
+            if (ids[b] < 0 || ids[b] >= a->vocab) {
+                if (tid == 0) set_error(&st->error, 2);
+                return;
+            }
         }
+        const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+        for (int b = 0; b < B; ++b) {
+            const auto* e = gbl(a->embed + (size_t)ids[b] * H);
+            for (int i = h0 + tid; i < h1; i += kStepThreads) st_dev(a->x + (size_t)b * H + i, bf16(e[i]));
+        }
+        stores_done();
+        prefetch_ring<ITH, false>(a->layers[0].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
+                                  part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+        for (int b = 0; b < B; ++b) {
+            const auto* e = gbl(a->embed + (size_t)ids[b] * H);
+            for (int i = tid; i < H; i += kStepThreads) lds[b * H + i] = bf16(e[i]);
+        }
+        __syncthreads();
     }
-    {
-        const int r0 = part_lo(qkvw, wg, nwg), r1 = part_lo(qkvw, wg + 1, nwg);
-        prefetch_first<ITH, false>(a.layers[0].wqkv, nullptr, H, r0, r1, pre);
-    }
-    for (int b = 0; b < B; ++b) {
-        const uint16_t* e = a.embed + (size_t)st->ids[b] * H;
-        for (int i = tid; i < H; i += kStepThreads) lds[b * H + i] = bf16(e[i]);
-    }
-    __syncthreads();
 
-    const int groups = a.kv_heads * B, wpg = nwg / groups;
-    const int group = wg / wpg, wg_in = wg % wpg;
-    for (int l = 0; l < a.layers_n; ++l) {
-        const LayerDev& Lw = a.layers[l];
+    const int layers_n = fresh(args)->layers_n;
+    for (int l = 0; l < layers_n; ++l) {
         // ---- input RMSNorm + fused QKV projection ----
-        if (l > 0) stage<B>(lds, a.x, H, H);
-        norm_rows<B>(lds, H, Lw.in_norm, a.eps, fallbacks);
-        tr.mark();
         {
-            const int r0 = part_lo(qkvw, wg, nwg), r1 = part_lo(qkvw, wg + 1, nwg);
-            gemv_rows<B, EPI_STORE, ITH>(Lw.wqkv, nullptr, lds, H, a.qkv, qkvw, r0, r1, pre);
+            ArgsPtr a = fresh(args);
+            const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
+            if (l > 0) stage<B, ITH>(lds, a->x, H, H);
+            norm_rows<B>(lds, H, a->layers[l].in_norm, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
+            tr.mark();
+            a = fresh(args);
+            gemv_ring<B, EPI_STORE, ITH>(a->layers[l].wqkv, nullptr, lds, H, a->qkv, qkvw, part_lo(qkvw, wg, nwg),
+                                         part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+            stores_done();
         }
         if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- QK-norm + RoPE + KV append + attention ----
         {
-            AttnArgs at = a.attn;
-            at.layer = l;
-            at.q_norm = Lw.q_norm;
-            at.k_norm = Lw.k_norm;
-            if (!attn_group<kStepThreads, D, 4>(at, wg_in, group % a.kv_heads, group / a.kv_heads, lds)) return;
-        }
-        {
-            const int r0 = part_lo(H, wg, nwg), r1 = part_lo(H, wg + 1, nwg);
-            prefetch_first<ITQ, false>(Lw.wo, nullptr, qw, r0, r1, pre);
+            ArgsPtr a = fresh(args);
+            const int groups = a->kv_heads * B, wpg = nwg / groups;
+            const int group = wg / wpg;
+            const AttnArgs at = layer_attn(a, call.kv, l);
+            if (!attn_group<kStepThreads, D, 4>(at, wg % wpg, group % at.kv_heads, group / at.kv_heads, lds))
+                return;
+            stores_done();
+            a = fresh(args);
+            const int H = a->hidden, qw = a->heads * D;
+            prefetch_ring<ITQ, false>(a->layers[l].wo, nullptr, qw, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg),
+                                      H, ring);
         }
         if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- O projection + residual ----
-        stage<B>(lds, a.att, qw, qw);
-        tr.mark();
         {
-            const int r0 = part_lo(H, wg, nwg), r1 = part_lo(H, wg + 1, nwg);
-            gemv_rows<B, EPI_RESID, ITQ>(Lw.wo, nullptr, lds, qw, a.x, H, r0, r1, pre);
-        }
-        {
-            const int r0 = part_lo(I, wg, nwg), r1 = part_lo(I, wg + 1, nwg);
-            prefetch_first<ITH, true>(Lw.wg, Lw.wu, H, r0, r1, pre);
+            ArgsPtr a = fresh(args);
+            const int H = a->hidden, qw = a->heads * D, I = a->intermediate;
+            stage_res<B>(res_s, a->x, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
+            stage<B, ITQ>(lds, a->att, qw, qw);
+            tr.mark();
+            a = fresh(args);
+            gemv_ring<B, EPI_RESID, ITQ>(a->layers[l].wo, nullptr, lds, qw, a->x, H, part_lo(H, wg, nwg),
+                                         part_lo(H, wg + 1, nwg), H, ring, res_s);
+            stores_done();
+            a = fresh(args);
+            prefetch_ring<ITH, true>(a->layers[l].wg, a->layers[l].wu, H, part_lo(I, wg, nwg),
+                                     part_lo(I, wg + 1, nwg), I, ring);
         }
         if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- post-attention RMSNorm + gate/up + SwiGLU ----
-        stage<B>(lds, a.x, H, H);
-        norm_rows<B>(lds, H, Lw.post_norm, a.eps, fallbacks);
-        tr.mark();
         {
-            const int r0 = part_lo(I, wg, nwg), r1 = part_lo(I, wg + 1, nwg);
-            gemv_rows<B, EPI_SWIGLU, ITH>(Lw.wg, Lw.wu, lds, H, a.act, I, r0, r1, pre);
-        }
-        {
-            const int r0 = part_lo(H, wg, nwg), r1 = part_lo(H, wg + 1, nwg);
-            prefetch_first<ITI, false>(Lw.wd, nullptr, I, r0, r1, pre);
+            ArgsPtr a = fresh(args);
+            const int H = a->hidden, I = a->intermediate;
+            stage<B, ITH>(lds, a->x, H, H);
+            norm_rows<B>(lds, H, a->layers[l].post_norm, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
+            tr.mark();
+            a = fresh(args);
+            gemv_ring<B, EPI_SWIGLU, ITH>(a->layers[l].wg, a->layers[l].wu, lds, H, a->act, I, part_lo(I, wg, nwg),
+                                          part_lo(I, wg + 1, nwg), I, ring);
+            stores_done();
+            a = fresh(args);
+            prefetch_ring<ITI, false>(a->layers[l].wd, nullptr, I, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg), H,
+                                      ring);
         }
         if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- down projection + residual ----
-        stage<B>(lds, a.act, I, I);
-        tr.mark();
         {
-            const int r0 = part_lo(H, wg, nwg), r1 = part_lo(H, wg + 1, nwg);
-            gemv_rows<B, EPI_RESID, ITI>(Lw.wd, nullptr, lds, I, a.x, H, r0, r1, pre);
-        }
-        if (l + 1 < a.layers_n) {
-            const int r0 = part_lo(qkvw, wg, nwg), r1 = part_lo(qkvw, wg + 1, nwg);
-            prefetch_first<ITH, false>(a.layers[l + 1].wqkv, nullptr, H, r0, r1, pre);
-        } else if (a.head) {
-            const int r0 = part_lo(a.vocab, wg, nwg), r1 = part_lo(a.vocab, wg + 1, nwg);
-            prefetch_first<ITH, false>(a.lm_head, nullptr, H, r0, r1, pre);
+            ArgsPtr a = fresh(args);
+            const int H = a->hidden, I = a->intermediate;
+            stage_res<B>(res_s, a->x, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
+            stage<B, ITI>(lds, a->act, I, I);
+            tr.mark();
+            a = fresh(args);
+            gemv_ring<B, EPI_RESID, ITI>(a->layers[l].wd, nullptr, lds, I, a->x, H, part_lo(H, wg, nwg),
+                                         part_lo(H, wg + 1, nwg), H, ring, res_s);
+            stores_done();
+            a = fresh(args);
+            const int qkvw = (a->heads + 2 * a->kv_heads) * D;
+            if (l + 1 < layers_n) {
+                prefetch_ring<ITH, false>(a->layers[l + 1].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
+                                          part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+            } else if (call.head) {
+                prefetch_ring<ITH, false>(a->lm_head, nullptr, H, part_lo(a->vocab, wg, nwg),
+                                          part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
+            }
         }
         if (!grid_sync(bar, ++epoch, st, tr)) return;
     }
     // ---- final norm + LM head (src/model.rs:465-468, 590) ----
-    if (a.head) {
-        stage<B>(lds, a.x, H, H);
-        norm_rows<B>(lds, H, a.final_norm, a.eps, nullptr);
-        const int r0 = part_lo(a.vocab, wg, nwg), r1 = part_lo(a.vocab, wg + 1, nwg);
-        gemv_rows<B, EPI_STORE, ITH>(a.lm_head, nullptr, lds, H, a.logits, a.vocab, r0, r1, pre);
+    if (call.head) {
+        ArgsPtr a = fresh(args);
+        const int H = a->hidden;
+        stage<B, ITH>(lds, a->x, H, H);
+        norm_rows<B>(lds, H, a->final_norm, a->eps, nullptr);
+        a = fresh(args);
+        gemv_ring<B, EPI_STORE, ITH>(a->lm_head, nullptr, lds, H, a->logits, a->vocab, part_lo(a->vocab, wg, nwg),
+                                     part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
     }
-    if (wg == 0 && tid == 0) st->seq = seq + 1;
+    if (wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
 }
 
 template <int B, int D, int ITH, int ITQ, int ITI>
-static hipError_t launch_step_t(hipStream_t s, const StepArgs& a, int nwg, size_t lds) {
-    step_kernel<B, D, ITH, ITQ, ITI><<<nwg, kStepThreads, lds, s>>>(a);
+static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCall& call, int nwg, size_t lds) {
+    step_kernel<B, D, ITH, ITQ, ITI><<<nwg, kStepThreads, lds, s>>>(dev, call);
     return hipGetLastError();
 }
 
@@ -298,22 +503,26 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const bool shape = (c.head_dim == 128 && ith == 6 && itq == 6 && iti == 16) ||
                        (c.head_dim == 64 && ith == 2 && itq == 2 && iti == 6);
     return shape && rows >= 1 && rows <= 2 && nwg % (c.num_key_value_heads * rows) == 0 &&
-           c.num_attention_heads / c.num_key_value_heads <= 4;
+           c.num_attention_heads / c.num_key_value_heads <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows;
 }
 
-hipError_t launch_step(hipStream_t s, const StepArgs& a, int nwg) {
+size_t step_lds_bytes(const StepArgs& a) {
     const int kmax = std::max(std::max(a.hidden, a.intermediate), a.heads * a.attn.dim);
     const int G = a.heads / a.kv_heads;
-    const size_t lds = std::max((size_t)a.rows * kmax, (size_t)G * a.attn.bpw * kBlockKeys) * sizeof(float);
+    return std::max((size_t)a.rows * kmax, (size_t)G * a.attn.bpw * kBlockKeys) * sizeof(float);
+}
+
+hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {
+    const size_t lds = step_lds_bytes(a);
     if (lds > 128 * 1024) return hipErrorInvalidValue;
     const int ith = (a.hidden / 8 + 63) / 64;
     if (a.attn.dim == 128 && ith == 6) {
-        if (a.rows == 1) return launch_step_t<1, 128, 6, 6, 16>(s, a, nwg, lds);
-        return launch_step_t<2, 128, 6, 6, 16>(s, a, nwg, lds);
+        if (a.rows == 1) return launch_step_t<1, 128, 6, 6, 16>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 128, 6, 6, 16>(s, dev, call, nwg, lds);
     }
     if (a.attn.dim == 64 && ith == 2) {
-        if (a.rows == 1) return launch_step_t<1, 64, 2, 2, 6>(s, a, nwg, lds);
-        return launch_step_t<2, 64, 2, 2, 6>(s, a, nwg, lds);
+        if (a.rows == 1) return launch_step_t<1, 64, 2, 2, 6>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 64, 2, 2, 6>(s, dev, call, nwg, lds);
     }
     return hipErrorInvalidValue;
 }

@@ -37,19 +37,38 @@
  *   RMSNorm sum    sequential f32 sum as the reference defines it
  *                  (src/tensor.rs:1144, 1160): no substitute needed.
  *
- * Parity pins (what checks each function; see tests/):
- *   round_bf16       closed form + exhaustive-in-sample check against numpy.
- *   y2o_expf         equals the correctly rounded exp on all sampled inputs
- *                    (numpy float64 exp rounded to f32) -- pins vvexpf and
- *                    f32::exp up to their own (unpublished) ulp behaviour.
- *   y2o_log1p        within 2 ulp of numpy log1p; the f32 cast equals.
- *   DOT / linear     one-hot inputs, small-integer exactness, f64 bound.
- *   norm             closed form on constant rows.
- *   rotary           position 0 is the identity.
- *   attention        the reference's own known-answer generator and
- *                    tolerance (src/tensor.rs:9-83) against f64.
- *   MT19937          std::mt19937 known answer (10000th draw of 5489).
- *   choose           brute force on small vocabularies, greedy closed form.
+ * Parity pins (what checks each function; tests/test_oracle_*.py):
+ *   y2o_round_bf16   nearest BF16 with ties to even, computed from the two
+ *                    BF16 neighbours in f64, on 90k bit patterns incl. ties.
+ *   y2o_expf         equals the correctly rounded exp (numpy float64 exp
+ *                    rounded once to f32) on 89k inputs incl. both range ends
+ *                    -- stands in for vvexpf and f32::exp, whose own ulp
+ *                    behaviour is unpublished (parity unpinned beyond that).
+ *   y2o_log1p        within 2 ulp of numpy log1p on the race's domain.
+ *   y2o_linear/DOT   one-hot inputs reproduce W's columns; small-integer
+ *                    operands give the exact integer product; random operands
+ *                    stay inside the f32 dot-product error bound of an f64
+ *                    product; a row alone equals the same row in a batch.
+ *   y2o_norm_*       constant rows in closed form; an input on which only a
+ *                    sequential f32 sum of squares gives the right BF16 scale.
+ *   y2o_rotary_*     position 0 is the identity; the table is rb(cos/sin) of
+ *                    p * theta^(-2i/d) within one BF16 step of f64 libm.
+ *   y2o_attention_row the reference's own known-answer generator and
+ *                    tolerance (src/tensor.rs:9-83) against f64; one key gives
+ *                    rb(V0); equal keys give rb(mean V) exactly.
+ *   y2o_cfg_mix      scale 1 / 0 give the conditional / unconditional row.
+ *   y2o_mt_*         std::mt19937 known answer (10000th draw of seed 5489),
+ *                    2000 draws equal numpy's RandomState for five seeds,
+ *                    uniform_f64 and discard from their definitions.
+ *   y2o_choose       greedy ties and no draw at T = 0; exactly 2V draws when
+ *                    sampling; race frequencies equal the softmax (5 sigma);
+ *                    top-p keeps the crossing token and 1 (legacy 3) protected
+ *                    ids; top-k keeps ties; penalty sign, powi and window;
+ *                    NaN/+inf rejected; ABC/semantic masks and min_tokens.
+ *   y2o_forward/generate  tests/golden/ fixtures (prefill logits digest, 64
+ *                    greedy ids, 32 sampled CFG ids) written by
+ *                    tests/golden/make_golden.py; chunked prefill equals the
+ *                    token-by-token step (the GPU tests run both).
  *   Accelerate's exact summation order, macOS libm cos/sin/powf and the real
  *   checkpoint's logits cannot be run here: parity with those is unpinned
  *   beyond the checks above.

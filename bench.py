@@ -119,8 +119,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--kernel-iters", type=int, default=112)
-    ap.add_argument("--step-kernel", type=int, default=0, choices=[0, 1],
-                    help="1: one persistent kernel per token instead of one kernel per phase")
+    ap.add_argument("--step-kernel", type=int, default=1, choices=[0, 1],
+                    help="1 (default): one persistent kernel per token; 0: one kernel per phase")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)",

@@ -219,9 +219,10 @@ void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t te
 int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
 /* Execution choice: run decode steps (yue2_hip_forward and decoders created
  * afterwards) through the persistent token-step kernel -- one launch per
- * token, grid barriers between phases -- instead of one kernel per phase.
- * Both produce the same bits.  Returns 1 when enabled, 0 when off or when
- * the model's shape has no step kernel. */
+ * token, workgroups exchanging tagged words instead of meeting at barriers
+ * -- or through one kernel per phase.  Both produce the same bits.  The
+ * step kernel is the default for shapes that have one.  Returns 1 when
+ * enabled, 0 when off or when the model's shape has no step kernel. */
 int32_t yue2_hip_model_set_step_kernel(Yue2Model *m, int32_t on);
 /* Diagnostics: RMSNorm guard fallbacks taken since the model was opened. */
 int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);

@@ -1,0 +1,365 @@
+// dev_flow.h -- tagged-word dataflow between the workgroups of the
+// persistent token-step kernel, and the decode attention written on it.
+//
+// Every value that one workgroup produces for others is stored as one
+// 64-bit word {tag: high 32 bits, value: low 32 bits} with a single
+// agent-scope atomic store (an sc1 dwordx2 store: written through to the
+// device-coherent level, and never observed half-written).  A consumer polls
+// the words it needs with agent-scope atomic loads until every tag equals the
+// tag it expects.  The data carries its own readiness, so there is no
+// barrier, no counter and no wait for store completion between dependent
+// phases: a dependency costs one store-to-load visibility.
+//
+// Tags: (epoch << 12) | (layer << 4) | kind, epoch = launch sequence + 1
+// (20 bits).  Each word is rewritten every launch; the state reset bumps the
+// sequence, so words left by an aborted launch can never match.  A buffer is
+// rewritten only after all its readers have consumed it: every rewrite
+// depends, through the step's own data dependencies, on outputs that each
+// reader produced after its read (x after down needs every workgroup's
+// SwiGLU output, which needs every workgroup to have read x after O, ...).
+//
+// All polls are bounded: on timeout (or once another workgroup has set the
+// device error) the poll sets the error and returns false, and the kernel
+// leaves, so every launch terminates.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "dev_mem.h"
+#include "kernels.h"
+#include "y2_math.h"
+
+namespace y2 {
+
+enum FlowKind { FK_EMB = 0, FK_QKV = 1, FK_ATT = 2, FK_XO = 3, FK_ACT = 4, FK_XD = 5, FK_BMAX = 6, FK_BSUM = 7,
+                FK_PART = 8 };
+constexpr int kDevErrFlow = 8;
+// Words a thread gathers in the attention merge (512 threads): a workgroup
+// merges ceil(G*D/W) outputs over nb <= W * bpw blocks, at most
+// G*D*bpw + nb <= 512 * 24 + 384 words for G*D <= 512 and bpw <= 24.
+constexpr int kMergePer = 26;
+
+__device__ __forceinline__ uint32_t flow_tag(uint32_t epoch, int layer, int kind) {
+    return (epoch << 12) | ((uint32_t)layer << 4) | (uint32_t)kind;
+}
+
+__device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
+    const uint64_t w = ((uint64_t)tag << 32) | (uint64_t)f2u(v);
+    __hip_atomic_store(gblw(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
+    return __hip_atomic_load(gblw(const_cast<uint64_t*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// dst[i] = value of the word addr(i), i < n, once its tag equals `tag` (dst in
+// LDS).  All NT threads of the block take part; n <= NT * MAXPER.  Returns
+// false (device error set) on timeout; the result is uniform over the block.
+template <int NT, int MAXPER, class Addr>
+__device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float* dst, StepState* st) {
+    __shared__ int s_fail;
+    const int tid = threadIdx.x;
+    // every thread has read the previous call's flag before it is reset, and
+    // the reset is visible before anyone can set it
+    __syncthreads();
+    if (tid == 0) s_fail = 0;
+    __syncthreads();
+    uint32_t pend = 0;
+#pragma unroll
+    for (int j = 0; j < MAXPER; ++j)
+        if (tid + j * NT < n) pend |= 1u << j;
+    unsigned rounds = 0;
+    while (pend) {
+        uint64_t w[MAXPER];
+#pragma unroll
+        for (int j = 0; j < MAXPER; ++j) w[j] = (pend >> j) & 1 ? ld_tag(addr(tid + j * NT)) : 0;
+#pragma unroll
+        for (int j = 0; j < MAXPER; ++j)
+            if (((pend >> j) & 1) && (uint32_t)(w[j] >> 32) == tag) {
+                dst[tid + j * NT] = u2f((uint32_t)w[j]);
+                pend &= ~(1u << j);
+            }
+        if (pend) {
+            ++rounds;
+            if ((rounds & 255) == 0 && (rounds > (1u << 20) || ld_dev_i(&st->error))) {
+                set_error(&st->error, kDevErrFlow);
+                s_fail = 1;  // benign race: every writer stores 1
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+    return s_fail == 0;
+}
+
+// The 2-D region src[r * stride + c], r < n / cols, c < cols, row-major.
+template <int NT, int MAXPER>
+__device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, size_t stride, uint32_t tag,
+                                       float* dst, StepState* st) {
+    return gather_at<NT, MAXPER>(
+        [=](int i) { return src + (size_t)(i / cols) * stride + i % cols; }, n, tag, dst, st);
+}
+
+// Arguments of one layer's attention in the step kernel.
+struct FlowAttn {
+    const uint64_t* qkv;  // tagged [rows][qkv_stride]: q heads, k heads, v heads
+    int qkv_stride;
+    uint16_t* kv_base;  // this batch row's cache: [layers][2][kv_heads][cap][dim] BF16
+    int cap, pos, layer, heads, kv_heads, blk_stride, att_stride, wpg;
+    float scale, eps;
+    const float *q_norm, *k_norm, *cos_t, *sin_t;
+    uint64_t *bmax, *bsum, *part;  // tagged [rows][heads][blk_stride] (part: x dim)
+    uint64_t* att;                 // tagged [rows][att_stride]
+    uint32_t epoch;
+    StepState* st;
+};
+
+// Workgroup wi (of wpg) of group (kv head g, batch row b): the same
+// arithmetic as attn_group in dev_attn.h (and so the same bits), with the
+// three group exchanges (block maxima, block sums, partial PV) as tagged
+// words and the final merge spread over the group's workgroups.  e_s: LDS
+// scratch of max(G * bpw * 64, merge) floats.  false: timeout (error set).
+template <int NT, int D, int MAXG>
+__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* e_s) {
+    constexpr int NW = NT / 64;
+    constexpr int CPL = D / 8;     // lanes per key row
+    constexpr int KPW = 64 / CPL;  // keys per wave load
+    constexpr int S = KPW;         // PV key streams per 64-key block
+    constexpr int MAXNB = 24576 / kBlockKeys;
+    __shared__ float q_s[MAXG][D];
+    __shared__ float k_s[D], v_s[D];
+    __shared__ float hscale[MAXG + 1];
+    __shared__ float m_s[MAXG], t_s[MAXG];
+    __shared__ float red_s[MAXG * MAXNB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    StepState* st = a.st;
+    const int pos = a.pos, L = pos + 1, cap = a.cap;
+    const int nb = (L + kBlockKeys - 1) / kBlockKeys;
+    const int bpw = (nb + a.wpg - 1) / a.wpg;
+    const int W = (nb + bpw - 1) / bpw;
+    if (wi >= W) return true;
+    const int G = a.heads / a.kv_heads;
+    const int blk0 = wi * bpw, blk1 = min(nb, blk0 + bpw), nbl = blk1 - blk0;
+    const int j0 = blk0 * kBlockKeys, j1 = min(L, blk1 * kBlockKeys), nk = j1 - j0;
+    const int estride = bpw * kBlockKeys;
+    const uint64_t* row = a.qkv + (size_t)b * a.qkv_stride;
+    uint16_t* Kc = a.kv_base + kv_off(a.layer, 0, a.kv_heads, g, cap, 0, D);
+    uint16_t* Vc = a.kv_base + kv_off(a.layer, 1, a.kv_heads, g, cap, 0, D);
+    const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
+    const bool owns_new = j1 == L;
+    const uint32_t t_qkv = flow_tag(a.epoch, a.layer, FK_QKV);
+
+    // ---- phase 0: queries (and the new key/value) -------------------------
+    if (!gather<NT, (MAXG * D + NT - 1) / NT>(row + (size_t)(g * G) * D, G * D, G * D, 0, t_qkv, &q_s[0][0], st))
+        return false;
+    if (owns_new) {
+        if (!gather<NT, 1>(row + (size_t)(a.heads + g) * D, D, D, 0, t_qkv, k_s, st)) return false;
+        if (!gather<NT, 1>(row + (size_t)(a.heads + a.kv_heads + g) * D, D, D, 0, t_qkv, v_s, st)) return false;
+    }
+    // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
+    if (tid < G || (owns_new && tid == G)) {
+        const float* v = tid < G ? q_s[tid] : k_s;
+        float sum = -0.0f;
+        for (int d = 0; d < D; d += 16) {
+            float t[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t[j] = v[d + j];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
+        }
+        hscale[tid] = norm_scale_from_sum(sum, D, a.eps);
+    }
+    __syncthreads();
+    {
+        const int half = D / 2;
+        const float* cs = a.cos_t + (size_t)pos * half;
+        const float* sn = a.sin_t + (size_t)pos * half;
+        const int pairs = (G + (owns_new ? 1 : 0)) * half;
+        for (int i = tid; i < pairs; i += NT) {
+            const int h = i / half, d = i % half;
+            float* v = h < G ? q_s[h] : k_s;
+            const float* gam = h < G ? a.q_norm : a.k_norm;
+            const float s = hscale[h];
+            const float x0 = rb(rb(v[d] * s) * gbl(gam)[d]);
+            const float x1 = rb(rb(v[d + half] * s) * gbl(gam)[d + half]);
+            const float c = gbl(cs)[d], si = gbl(sn)[d];
+            const float y0 = rb(rb(x0 * c) - rb(x1 * si));
+            const float y1 = rb(rb(x1 * c) + rb(x0 * si));
+            v[d] = y0;
+            v[d + half] = y1;
+            if (h == G) {
+                gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
+                gblw(Kc)[(size_t)pos * D + d + half] = bf16_bits(y1);
+            }
+        }
+        if (owns_new)
+            for (int d = tid; d < D; d += NT) gblw(Vc)[(size_t)pos * D + d] = bf16_bits(v_s[d]);
+        stores_done();  // the appended row is read back below by other waves
+        __syncthreads();
+    }
+
+    // ---- phase 1: scaled scores and block maxima ---------------------------
+    const uint32_t t_bmax = flow_tag(a.epoch, a.layer, FK_BMAX);
+    {
+        const int c = lane % CPL, kk = lane / CPL;
+        float qv[MAXG][8];
+#pragma unroll
+        for (int h = 0; h < MAXG; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qv[h][e] = h < G ? q_s[h][8 * c + e] : 0.0f;
+        constexpr int R = 8;
+        for (int base = j0 + wave * R * KPW; base < j1; base += NW * R * KPW) {
+            uint4 kr[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int j = base + r * KPW + kk;
+                kr[r] = j < j1 ? ldg4(Kc + (size_t)j * D + 8 * c) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int j = base + r * KPW + kk;
+                float kf[8];
+                unpack8a(kr[r], kf);
+#pragma unroll
+                for (int h = 0; h < MAXG; ++h) {
+                    if (h >= G) break;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
+#pragma unroll
+                    for (int s = CPL / 2; s >= 1; s >>= 1) acc = acc + __shfl_xor(acc, s, 64);
+                    if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
+                }
+            }
+        }
+        __syncthreads();
+        for (int i = wave; i < G * nbl; i += NW) {
+            const int h = i / nbl, bl = i % nbl;
+            const int jl = bl * kBlockKeys + lane;
+            float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            if (lane == 0) st_tag(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m, t_bmax);
+        }
+    }
+
+    // ---- phase 2: M, exp(s - M) and block sums -----------------------------
+    const uint32_t t_bsum = flow_tag(a.epoch, a.layer, FK_BSUM);
+    {
+        if (!gather<NT, (MAXG * MAXNB + NT - 1) / NT>(a.bmax + hbase, G * nb, nb, a.blk_stride, t_bmax, red_s, st))
+            return false;
+        for (int h = wave; h < G; h += NW) {
+            float m = -__builtin_huge_valf();
+            for (int i = lane; i < nb; i += 64) m = fmaxf(m, red_s[h * nb + i]);
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            if (lane == 0) m_s[h] = m;
+        }
+        __syncthreads();
+        for (int i = tid; i < G * nk; i += NT) {
+            const int h = i / nk, jl = i % nk;
+            e_s[h * estride + jl] = expf_cr(e_s[h * estride + jl] - m_s[h]);
+        }
+        __syncthreads();
+        for (int i = wave; i < G * nbl; i += NW) {
+            const int h = i / nbl, bl = i % nbl;
+            const int jl = bl * kBlockKeys + lane;
+            float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
+            if (lane == 0) st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v, t_bsum);
+        }
+    }
+
+    // ---- phase 3: total, p = e / total, partial PV -------------------------
+    const uint32_t t_part = flow_tag(a.epoch, a.layer, FK_PART);
+    {
+        if (!gather<NT, (MAXG * MAXNB + NT - 1) / NT>(a.bsum + hbase, G * nb, nb, a.blk_stride, t_bsum, red_s, st))
+            return false;
+        if (tid < G) {
+            // block sums added left to right
+            float tot = red_s[tid * nb];
+            for (int i = 1; i < nb; ++i) tot = tot + red_s[tid * nb + i];
+            t_s[tid] = tot;
+        }
+        __syncthreads();
+        for (int i = tid; i < G * nk; i += NT) {
+            const int h = i / nk, jl = i % nk;
+            e_s[h * estride + jl] = e_s[h * estride + jl] / t_s[h];
+        }
+        __syncthreads();
+        const int t = lane / CPL, c = lane % CPL;
+        for (int bl = wave; bl < nbl; bl += NW) {
+            const int jb = (blk0 + bl) * kBlockKeys;
+            uint4 vr[kBlockKeys / S];
+#pragma unroll
+            for (int i = 0; i < kBlockKeys / S; ++i) {
+                const int j = jb + t + S * i;
+                vr[i] = j < L ? ldg4(Vc + (size_t)j * D + 8 * c) : make_uint4(0, 0, 0, 0);
+            }
+            float acc[MAXG][8];
+#pragma unroll
+            for (int h = 0; h < MAXG; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kBlockKeys / S; ++i) {
+                const int jj = t + S * i;
+                if (jb + jj < L) {
+                    float vf[8];
+                    unpack8a(vr[i], vf);
+#pragma unroll
+                    for (int h = 0; h < MAXG; ++h) {
+                        if (h >= G) break;
+                        const float p = e_s[h * estride + bl * kBlockKeys + jj];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p, vf[e], acc[h][e]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 32; s >= CPL; s >>= 1)
+#pragma unroll
+                for (int h = 0; h < MAXG; ++h)
+                    if (h < G)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] + __shfl_xor(acc[h][e], s, 64);
+            if (t == 0) {
+#pragma unroll
+                for (int h = 0; h < MAXG; ++h)
+                    if (h < G) {
+                        uint64_t* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) st_tag(dst + e, acc[h][e], t_part);
+                    }
+            }
+        }
+    }
+
+    // ---- merge: workgroup wi adds the blocks of outputs [o0, o1) -----------
+    {
+        const int outs = G * D, chunk = (outs + W - 1) / W;
+        const int o0 = min(outs, wi * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
+        __syncthreads();  // e_s is reused below
+        // e_s[i * nb + k] = partial of block k for output o0 + i
+        const uint64_t* part = a.part + hbase * D;
+        const size_t hstride = (size_t)a.blk_stride * D;
+        const int nbm = nb;
+        if (!gather_at<NT, kMergePer>(
+                [=](int i) {
+                    const int o = o0 + i / nbm, k = i % nbm;
+                    return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
+                },
+                no * nb, t_part, e_s, st))
+            return false;
+        const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
+        for (int i = tid; i < no; i += NT) {
+            const float* pp = e_s + i * nb;
+            float o = pp[0];
+            for (int k = 1; k < nb; ++k) o = o + pp[k];  // blocks left to right
+            st_tag(a.att + (size_t)b * a.att_stride + (size_t)g * G * D + o0 + i, rb(o), t_att);
+        }
+    }
+    return true;
+}
+
+}  // namespace y2

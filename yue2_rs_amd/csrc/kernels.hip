@@ -238,6 +238,9 @@ __global__ void reset_state_kernel(StepState* st, int32_t* c0, int n0, int32_t* 
         st->error = 0;
         st->norm_fallbacks = 0;
         st->done = 0;
+        // a new launch sequence: words tagged by a launch that stopped on an
+        // error can never match the next launch's tags
+        st->seq += 2;
     }
     for (int i = threadIdx.x; i < n0; i += blockDim.x) c0[i] = 0;
     for (int i = threadIdx.x; i < n1; i += blockDim.x) c1[i] = 0;

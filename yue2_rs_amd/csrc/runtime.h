@@ -41,6 +41,7 @@ struct Workspace {
     StepState* st = nullptr;
     int32_t* token_log = nullptr;
     void* step_args = nullptr;  // device copy of the step kernel's arguments
+    void* flow_block = nullptr; // the step kernel's tagged-word buffers
     void* step_host = nullptr;  // host copy of the same (StepArgs)
     bool step_args_ready = false;
     int ensure(int rows, int max_blocks, const Yue2Config& c);
@@ -65,7 +66,7 @@ struct Yue2Model {
     std::vector<y2::LayerDev> layers;
     y2::LayerDev* layers_dev = nullptr;  // the same table in device memory (step kernel)
     int cus = 0;                         // compute units: workgroups of the step kernel
-    bool step_kernel = false;            // run decode steps through the persistent kernel
+    bool step_kernel = false;            // decode steps through the persistent kernel (default where supported)
     y2::Workspace ws;  // batch-1 workspace of the parity API
     int norm_fallbacks = 0;
 };

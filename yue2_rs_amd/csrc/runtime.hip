@@ -127,7 +127,9 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
 
 void Workspace::release() {
     if (block) (void)hipFree(block);
+    if (flow_block) (void)hipFree(flow_block);
     block = nullptr;
+    flow_block = nullptr;
     step_args = nullptr;
     step_args_ready = false;
     rows = max_blocks = 0;
@@ -214,49 +216,51 @@ int prepare_step(Yue2Model* m, Workspace& w) {
     if (!step_supported(c, rows, m->cus)) return 1;
     if (w.step_args_ready) return YUE2_OK;
     const int D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
-    const int qw = Hq * D, qkvw = (Hq + 2 * Hkv) * D;
+    const int H = c.hidden_size, I = c.intermediate_size;
+    const size_t qw = (size_t)Hq * D, qkvw = (size_t)(Hq + 2 * Hkv) * D;
     StepArgs a{};
     a.layers = m->layers_dev;
     a.embed = m->embed;
     a.lm_head = m->lm_head;
     a.final_norm = m->final_norm;
+    a.rope_cos = m->rope_cos;
+    a.rope_sin = m->rope_sin;
     a.layers_n = c.num_hidden_layers;
-    a.hidden = c.hidden_size;
-    a.intermediate = c.intermediate_size;
+    a.hidden = H;
+    a.intermediate = I;
     a.vocab = c.vocab_size;
     a.heads = Hq;
     a.kv_heads = Hkv;
+    a.head_dim = D;
     a.rows = rows;
+    a.blk_stride = w.blk_stride;
+    a.max_blocks = w.max_blocks;
     a.eps = c.rms_norm_eps;
-    a.x = w.x;
-    a.qkv = w.qkv;
-    a.att = w.att;
-    a.act = w.act;
+    a.scale = 1.0f / std::sqrt((float)D);
     a.logits = w.logits;
-    a.bars = w.bars;
     a.st = w.st;
-    AttnArgs& at = a.attn;
-    at.qkv = w.qkv;
-    at.qkv_stride = qkvw;
-    at.heads = Hq;
-    at.kv_heads = Hkv;
-    at.dim = D;
-    at.rows = rows;
-    at.scale = 1.0f / std::sqrt((float)D);
-    at.eps = c.rms_norm_eps;
-    at.cos_t = m->rope_cos;
-    at.sin_t = m->rope_sin;
-    at.bmax = w.bmax;
-    at.bsum = w.bsum;
-    at.part = w.part;
-    at.out = w.att;
-    at.out_stride = qw;
-    at.blk_stride = w.blk_stride;
-    at.wgs = m->cus / (Hkv * rows);
-    at.bpw = (w.max_blocks + at.wgs - 1) / at.wgs;
-    at.counters = w.counters;
-    at.st = w.st;
-    if (step_lds_bytes(a) > 128 * 1024) return 1;
+    if (step_lds_bytes(a, m->cus) > kStepLdsMax) return 1;
+    // tagged-word buffers, zero (= no tag) until first written
+    const size_t n_x = rows * (size_t)H, n_qkv = rows * qkvw, n_att = rows * qw, n_act = rows * (size_t)I;
+    const size_t n_blk = rows * (size_t)Hq * w.blk_stride, n_part = n_blk * D;
+    const size_t words = n_x + n_qkv + n_att + n_act + 2 * n_blk + n_part;
+    if (!w.flow_block) {
+        hipError_t e = hipMalloc(&w.flow_block, words * sizeof(uint64_t));
+        if (e != hipSuccess) {
+            w.flow_block = nullptr;
+            return hip_fail(e, "hipMalloc(step dataflow words)");
+        }
+        e = hipMemset(w.flow_block, 0, words * sizeof(uint64_t));
+        if (e != hipSuccess) return hip_fail(e, "hipMemset(step dataflow words)");
+    }
+    uint64_t* p = static_cast<uint64_t*>(w.flow_block);
+    a.tx = p;
+    a.tqkv = a.tx + n_x;
+    a.tatt = a.tqkv + n_qkv;
+    a.tact = a.tatt + n_att;
+    a.tbmax = a.tact + n_act;
+    a.tbsum = a.tbmax + n_blk;
+    a.tpart = a.tbsum + n_blk;
     hipError_t e = hipMemcpy(w.step_args, &a, sizeof(StepArgs), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "step arguments upload");
     *reinterpret_cast<StepArgs*>(w.step_host) = a;
@@ -487,6 +491,8 @@ extern "C" Yue2Model* yue2_hip_model_open(const Yue2Config* c, const uint16_t* e
         yue2_hip_model_free(m);
         return nullptr;
     }
+    // the persistent step kernel is the default where the shape has one
+    m->step_kernel = step_supported(m->c, 1, m->cus);
     return m;
 }
 

@@ -15,11 +15,15 @@ struct StepArgs {
     const uint16_t* embed;
     const uint16_t* lm_head;
     const float* final_norm;
-    int layers_n, hidden, intermediate, vocab, heads, kv_heads, rows;
-    float eps;
-    float *x, *qkv, *att, *act, *logits;
-    int* bars;               // two grid-barrier counters, zero at first use
-    AttnArgs attn;           // kv, layer and norms are filled in per call / per layer
+    const float *rope_cos, *rope_sin;  // [positions][head_dim / 2]
+    int layers_n, hidden, intermediate, vocab, heads, kv_heads, head_dim, rows;
+    int blk_stride, max_blocks;
+    float eps, scale;
+    float* logits;  // [rows][vocab]
+    // tagged words (dev_flow.h): x, q/k/v, attention output, SwiGLU output,
+    // attention block maxima / sums [rows][heads][blk_stride] and partial PV
+    // [rows][heads][blk_stride][head_dim]
+    uint64_t *tx, *tqkv, *tatt, *tact, *tbmax, *tbsum, *tpart;
     StepState* st;
 };
 
@@ -31,14 +35,17 @@ struct StepCall {
     unsigned long long* trace;  // optional wall-clock stamps, kTraceSlotsPerLayer per layer + 1
 };
 
-// Trace slots: one at the start, then per layer the start of each GEMV (4)
-// and the arrival at / departure from each grid barrier (5 x 2).
-constexpr int kTraceSlotsPerLayer = 14;
+// Trace slots: one at the start, then per layer: QKV start, QKV end,
+// attention end, O start, O end, gate/up start, gate/up end, down start,
+// down end.
+constexpr int kTraceSlotsPerLayer = 9;
 
 // True when a compiled step kernel covers this shape on nwg workgroups.
 bool step_supported(const Yue2Config& c, int rows, int nwg);
-// Dynamic LDS bytes of the step kernel for these arguments.
-size_t step_lds_bytes(const StepArgs& a);
+// Dynamic LDS bytes of the step kernel for these arguments on nwg
+// workgroups; launches need at most kStepLdsMax.
+constexpr size_t kStepLdsMax = 128 * 1024;
+size_t step_lds_bytes(const StepArgs& a, int nwg);
 hipError_t launch_step(hipStream_t s, const StepArgs* dev_args, const StepArgs& host_args,
                        const StepCall& call, int nwg);
 

@@ -7,33 +7,30 @@
 // one.  A kernel per phase pays a launch, a ramp-up and a drain at every one
 // of those ~140 dependencies per token (about 7 us each on this part, the
 // same as a whole 16 MB read).  Here one workgroup per CU stays resident for
-// the whole step and phases are separated by grid barriers.
+// the whole step.
+//
+// Dependencies between workgroups are dataflow, not barriers: every value a
+// workgroup produces for others (q/k/v, attention output, x after O and after
+// down, SwiGLU activations, the attention block statistics and partials) is a
+// tagged 64-bit word (dev_flow.h), and its consumers poll for it.  A
+// workgroup starts on the next phase as soon as the inputs it needs exist.
 //
 // Weight streaming: each wave walks its rows of a GEMV as a sequence of
 // items (SEG 16-byte chunks per lane of one row, both matrices for the
 // gate/up pair) through a ring of R register slots, so R-1 items are in
-// flight while one is multiplied.  Before arriving at a barrier every wave
-// already issues the first R-1 items of the next GEMV, so HBM keeps
-// streaming while the barrier, the staging and the RMSNorm resolve.
+// flight while one is multiplied.  Before polling for the next phase's
+// inputs every wave already issues the first R-1 items of the next GEMV.
 //
 // Work split (n rows of a GEMV over G workgroups): workgroup w owns rows
 // [w*n/G, (w+1)*n/G); its 8 waves take every 8th row.  Every row's
-// arithmetic is the DOT order of dev_gemv.h and the attention is dev_attn.h
-// with one (kv head, row) group per G/(kv_heads*rows) workgroups, so the
-// results equal the per-phase kernels' bit for bit.
-//
-// Cross-workgroup data (x, q/k/v, attention output, SwiGLU activations) is
-// written and read with agent-scope relaxed atomics (sc1 accesses on gfx950,
-// coherent across the XCDs' L2s without write-back or invalidate).  A barrier
-// is: every thread completes its stores (s_waitcnt), workgroup barrier,
-// thread 0 adds to the launch's counter and spins on relaxed loads (bounded;
-// a timeout sets the device error and every workgroup leaves, so a launch
-// always terminates).  Two counters alternate with the launch sequence
-// number so the idle one can be cleared.  The launch uses exactly one
-// workgroup per CU, so all are co-resident.
+// arithmetic is the DOT order of dev_gemv.h, and the attention is the same
+// arithmetic as dev_attn.h, so the results equal the per-phase kernels' bit
+// for bit.  The launch uses exactly one workgroup per CU, so all are
+// co-resident (every wait is bounded all the same).
 #include <algorithm>
 
 #include "dev_attn.h"
+#include "dev_flow.h"
 #include "dev_gemv.h"
 #include "kernels.h"
 #include "runtime.h"
@@ -43,7 +40,6 @@ namespace y2 {
 
 constexpr int kStepThreads = 512;
 constexpr int kStepWaves = kStepThreads / 64;
-constexpr int kDevErrBarrier = 7;
 
 // Optional trace: thread 0 of each workgroup stamps the device wall clock
 // (100 MHz) into trace[slot * gridDim.x + workgroup]; slots past the buffer
@@ -56,32 +52,6 @@ struct Tracer {
         ++slot;
     }
 };
-
-// Grid barrier number `epoch` of this launch.  Callers have completed their
-// cross-workgroup stores (stores_done) before calling.
-__device__ __forceinline__ bool grid_sync(int* bar, int epoch, StepState* st, Tracer& tr) {
-    __shared__ int s_ok;
-    __syncthreads();
-    tr.mark();
-    if (threadIdx.x == 0) {
-        add_dev(bar, 1);
-        const int target = epoch * (int)gridDim.x;
-        int ok = 1;
-        unsigned spins = 0;
-        while (ld_dev_i(bar) < target) {
-            if (++spins > (1u << 22) || ld_dev_i(&st->error)) {
-                set_error(&st->error, kDevErrBarrier);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        s_ok = ok;
-    }
-    tr.mark();
-    __syncthreads();
-    return s_ok != 0;
-}
 
 __device__ __forceinline__ int part_lo(int n, int w, int parts) { return (int)(((long)n * w) / parts); }
 
@@ -187,17 +157,22 @@ __device__ __forceinline__ void dot_item(const float* xs, int k, int seg, const 
 // weight load in flight and drain the ring).
 constexpr int kResRows = 64;
 
-// Output of one row (see gemv_store in dev_gemv.h) through an sc1 store;
-// res = the row's current residual value (EPI_RESID).
+// Output of one row (see gemv_store in dev_gemv.h) as a tagged word, or as
+// a plain float (y_tag == 0: the LM head, read by the next kernel); res =
+// the row's current residual value (EPI_RESID).
 template <int EPI>
-__device__ __forceinline__ void store_dev(float* yp, float acc, float acc2, float res) {
+__device__ __forceinline__ void store_out(float* y, uint64_t* ty, size_t i, uint32_t tag, float acc, float acc2,
+                                          float res) {
+    float v;
     if constexpr (EPI == EPI_STORE) {
-        st_dev(yp, rb(acc));
+        v = rb(acc);
     } else if constexpr (EPI == EPI_RESID) {
-        st_dev(yp, rb(res + rb(acc)));
+        v = rb(res + rb(acc));
     } else {
-        st_dev(yp, rb(silu_rb(rb(acc)) * rb(acc2)));
+        v = rb(silu_rb(rb(acc)) * rb(acc2));
     }
+    if (ty) st_tag(ty + i, v, tag);
+    else gblw(y)[i] = v;
 }
 
 // Issue the first R-1 items of this wave's rows [r0, r1) into ring slots.
@@ -216,12 +191,13 @@ __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t*
 }
 
 // Rows [r0, r1) of y = W xs (xs: B staged rows of k floats in LDS) with
-// epilogue EPI; the ring holds the first R-1 items (prefetch_ring).  res:
-// for EPI_RESID, res[b * kResRows + (row - r0)] = y's current value (LDS).
+// epilogue EPI, written as tagged words to ty (or as floats to y when ty is
+// null); the ring holds the first R-1 items (prefetch_ring).  res: for
+// EPI_RESID, res[b * (r1 - r0) + (row - r0)] = the row's current value (LDS).
 template <int B, int EPI, int IT>
 __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
-                                          float* y, int y_stride, int r0, int r1, int n, uint4* ring,
-                                          const float* res = nullptr) {
+                                          float* y, uint64_t* ty, uint32_t tag, int y_stride, int r0, int r1,
+                                          int n, uint4* ring, const float* res = nullptr) {
     constexpr bool PAIR = EPI == EPI_SWIGLU;
     using C = Ring<IT, PAIR>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, span = r1 - r0;
@@ -248,8 +224,8 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
                 for (int b = 0; b < B; ++b) {
                     const float v = wave_sum_xor(acc[b]);
                     const float v2 = PAIR ? wave_sum_xor(acc2[b]) : 0.0f;
-                    const float rv = EPI == EPI_RESID ? res[b * kResRows + (row - r0)] : 0.0f;
-                    if (lane == 0) store_dev<EPI>(y + (size_t)b * y_stride + row, v, v2, rv);
+                    const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
+                    if (lane == 0) store_out<EPI>(y, ty, (size_t)b * y_stride + row, tag, v, v2, rv);
                     acc[b] = acc2[b] = 0.0f;
                 }
             }
@@ -259,35 +235,19 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
 
 // ---- staging and norms -----------------------------------------------------
 
-// xs[b*k + i] = src[b*stride + i] for b < B (N >= k / 512 loads per thread,
-// all issued before the LDS writes).
+// xs[b * k + i] = word tx[b * k + i] with the given tag, for b < B, i < k.
 template <int B, int N>
-__device__ __forceinline__ void stage(float* xs, const float* src, int stride, int k) {
-    float v[B][N];
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-        for (int j = 0; j < N; ++j) {
-            const int i = threadIdx.x + j * kStepThreads;
-            v[b][j] = i < k ? ld_dev(src + (size_t)b * stride + i) : 0.0f;
-        }
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-        for (int j = 0; j < N; ++j) {
-            const int i = threadIdx.x + j * kStepThreads;
-            if (i < k) xs[b * k + i] = v[b][j];
-        }
-    __syncthreads();
+__device__ __forceinline__ bool stage(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
+    return gather<kStepThreads, B * N>(tx, B * k, B * k, 0, tag, xs, st);
 }
 
-// res[b * kResRows + r] = x[b * stride + r0 + r] for r < r1 - r0 (LDS); the
-// caller's next workgroup barrier publishes it.
+// res[b * n + r] = word tx[b * stride + r0 + r], r < n = r1 - r0 (n <= kResRows).
 template <int B>
-__device__ __forceinline__ void stage_res(float* res, const float* x, int stride, int r0, int r1) {
+__device__ __forceinline__ bool stage_res(float* res, const uint64_t* tx, int stride, int r0, int r1, uint32_t tag,
+                                          StepState* st) {
     const int n = r1 - r0;
-    for (int i = threadIdx.x; i < B * n; i += kStepThreads)
-        res[(i / n) * kResRows + i % n] = ld_dev(x + (size_t)(i / n) * stride + r0 + i % n);
+    return gather_at<kStepThreads, 1>([=](int i) { return tx + (size_t)(i / n) * stride + r0 + i % n; }, B * n,
+                                      tag, res, st);
 }
 
 // xs[b] = RMSNorm(xs[b]) with gammas g (Norm::apply, src/tensor.rs:1140-1157).
@@ -314,35 +274,35 @@ __device__ __forceinline__ ArgsPtr fresh(ArgsPtr p) {
     return p;
 }
 
-// The attention arguments of layer l (field by field: a struct copy cannot
-// bind to the constant address space).
-__device__ __forceinline__ AttnArgs layer_attn(ArgsPtr a, const KvView& kv, int l) {
-    AttnArgs at;
-    at.qkv = a->attn.qkv;
-    at.qkv_stride = a->attn.qkv_stride;
-    at.kv = kv;
-    at.layer = l;
-    at.heads = a->attn.heads;
-    at.kv_heads = a->attn.kv_heads;
-    at.dim = a->attn.dim;
-    at.rows = a->attn.rows;
-    at.scale = a->attn.scale;
-    at.eps = a->attn.eps;
-    at.q_norm = a->layers[l].q_norm;
-    at.k_norm = a->layers[l].k_norm;
-    at.cos_t = a->attn.cos_t;
-    at.sin_t = a->attn.sin_t;
-    at.bmax = a->attn.bmax;
-    at.bsum = a->attn.bsum;
-    at.part = a->attn.part;
-    at.out = a->attn.out;
-    at.out_stride = a->attn.out_stride;
-    at.blk_stride = a->attn.blk_stride;
-    at.wgs = a->attn.wgs;
-    at.bpw = a->attn.bpw;
-    at.counters = a->attn.counters;
-    at.st = a->attn.st;
-    return at;
+// The attention arguments of layer l for batch row b (field by field: a
+// struct copy cannot bind to the constant address space).
+__device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int b, int l, uint32_t epoch,
+                                               int wpg, int D) {
+    FlowAttn f;
+    f.qkv = a->tqkv;
+    f.qkv_stride = (a->heads + 2 * a->kv_heads) * D;
+    f.kv_base = b == 0 ? kv.base[0] : kv.base[1];  // selects: no indexed struct copy
+    f.cap = b == 0 ? kv.capacity[0] : kv.capacity[1];
+    f.pos = *gbl(&a->st->pos[b]);
+    f.layer = l;
+    f.heads = a->heads;
+    f.kv_heads = a->kv_heads;
+    f.blk_stride = a->blk_stride;
+    f.att_stride = a->heads * D;
+    f.wpg = wpg;
+    f.scale = a->scale;
+    f.eps = a->eps;
+    f.q_norm = a->layers[l].q_norm;
+    f.k_norm = a->layers[l].k_norm;
+    f.cos_t = a->rope_cos;
+    f.sin_t = a->rope_sin;
+    f.bmax = a->tbmax;
+    f.bsum = a->tbsum;
+    f.part = a->tpart;
+    f.att = a->tatt;
+    f.epoch = epoch;
+    f.st = a->st;
+    return f;
 }
 
 template <int B, int D, int ITH, int ITQ, int ITI>
@@ -356,15 +316,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     StepState* st = fresh(args)->st;
     if (ld_dev_i(&st->error)) return;
     const int seq = *gbl(&st->seq);
-    int* bar = fresh(args)->bars + (seq & 1);
-    if (wg == 0 && tid == 0) st_dev_i(fresh(args)->bars + ((seq + 1) & 1), 0);
-    int epoch = 0;
+    const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
     uint4 ring[RMAX];
     Tracer tr{call.trace, call.trace_slots, 0};
     tr.mark();
 
-    // Embedding (src/model.rs:452-464): this workgroup's slice of x, and the
-    // whole of x staged for the first norm.
+    // Embedding (src/model.rs:452-464): this workgroup's slice of x as tagged
+    // words (its own residual rows), and the whole of x staged for the first
+    // norm straight from the table.
     {
         ArgsPtr a = fresh(args);
         const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
@@ -377,11 +336,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             }
         }
         const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+        const uint32_t t_emb = flow_tag(epoch, 0, FK_EMB);
         for (int b = 0; b < B; ++b) {
             const auto* e = gbl(a->embed + (size_t)ids[b] * H);
-            for (int i = h0 + tid; i < h1; i += kStepThreads) st_dev(a->x + (size_t)b * H + i, bf16(e[i]));
+            for (int i = h0 + tid; i < h1; i += kStepThreads) st_tag(a->tx + (size_t)b * H + i, bf16(e[i]), t_emb);
         }
-        stores_done();
         prefetch_ring<ITH, false>(a->layers[0].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
                                   part_lo(qkvw, wg + 1, nwg), qkvw, ring);
         for (int b = 0; b < B; ++b) {
@@ -397,73 +356,79 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
-            if (l > 0) stage<B, ITH>(lds, a->x, H, H);
+            if (l > 0 && !stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
+            a = fresh(args);
             norm_rows<B>(lds, H, a->layers[l].in_norm, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH>(a->layers[l].wqkv, nullptr, lds, H, a->qkv, qkvw, part_lo(qkvw, wg, nwg),
+            gemv_ring<B, EPI_STORE, ITH>(a->layers[l].wqkv, nullptr, lds, H, nullptr, a->tqkv,
+                                         flow_tag(epoch, l, FK_QKV), qkvw, part_lo(qkvw, wg, nwg),
                                          part_lo(qkvw, wg + 1, nwg), qkvw, ring);
-            stores_done();
+            tr.mark();
         }
-        if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- QK-norm + RoPE + KV append + attention ----
         {
             ArgsPtr a = fresh(args);
             const int groups = a->kv_heads * B, wpg = nwg / groups;
-            const int group = wg / wpg;
-            const AttnArgs at = layer_attn(a, call.kv, l);
-            if (!attn_group<kStepThreads, D, 4>(at, wg % wpg, group % at.kv_heads, group / at.kv_heads, lds))
-                return;
-            stores_done();
+            const int group = wg / wpg, kvh = a->kv_heads;
+            const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D);
+            if (!attn_flow<kStepThreads, D, 4>(fa, wg % wpg, group % kvh, group / kvh, lds)) return;
+            tr.mark();
             a = fresh(args);
             const int H = a->hidden, qw = a->heads * D;
             prefetch_ring<ITQ, false>(a->layers[l].wo, nullptr, qw, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg),
                                       H, ring);
         }
-        if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- O projection + residual ----
         {
             ArgsPtr a = fresh(args);
-            const int H = a->hidden, qw = a->heads * D, I = a->intermediate;
-            stage_res<B>(res_s, a->x, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
-            stage<B, ITQ>(lds, a->att, qw, qw);
+            const int H = a->hidden, qw = a->heads * D;
+            const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+            if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l > 0 ? l - 1 : 0, l > 0 ? FK_XD : FK_EMB),
+                              st))
+                return;
+            a = fresh(args);
+            if (!stage<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITQ>(a->layers[l].wo, nullptr, lds, qw, a->x, H, part_lo(H, wg, nwg),
-                                         part_lo(H, wg + 1, nwg), H, ring, res_s);
-            stores_done();
+            gemv_ring<B, EPI_RESID, ITQ>(a->layers[l].wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
+                                         H, h0, h1, H, ring, res_s);
+            tr.mark();
             a = fresh(args);
+            const int I = a->intermediate;
             prefetch_ring<ITH, true>(a->layers[l].wg, a->layers[l].wu, H, part_lo(I, wg, nwg),
                                      part_lo(I, wg + 1, nwg), I, ring);
         }
-        if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- post-attention RMSNorm + gate/up + SwiGLU ----
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
-            stage<B, ITH>(lds, a->x, H, H);
+            if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
+            a = fresh(args);
             norm_rows<B>(lds, H, a->layers[l].post_norm, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_SWIGLU, ITH>(a->layers[l].wg, a->layers[l].wu, lds, H, a->act, I, part_lo(I, wg, nwg),
-                                          part_lo(I, wg + 1, nwg), I, ring);
-            stores_done();
+            gemv_ring<B, EPI_SWIGLU, ITH>(a->layers[l].wg, a->layers[l].wu, lds, H, nullptr, a->tact,
+                                          flow_tag(epoch, l, FK_ACT), I, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg),
+                                          I, ring);
+            tr.mark();
             a = fresh(args);
             prefetch_ring<ITI, false>(a->layers[l].wd, nullptr, I, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg), H,
                                       ring);
         }
-        if (!grid_sync(bar, ++epoch, st, tr)) return;
         // ---- down projection + residual ----
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
-            stage_res<B>(res_s, a->x, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
-            stage<B, ITI>(lds, a->act, I, I);
+            const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+            if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l, FK_XO), st)) return;
+            a = fresh(args);
+            if (!stage<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITI>(a->layers[l].wd, nullptr, lds, I, a->x, H, part_lo(H, wg, nwg),
-                                         part_lo(H, wg + 1, nwg), H, ring, res_s);
-            stores_done();
+            gemv_ring<B, EPI_RESID, ITI>(a->layers[l].wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
+                                         H, h0, h1, H, ring, res_s);
+            tr.mark();
             a = fresh(args);
             const int qkvw = (a->heads + 2 * a->kv_heads) * D;
             if (l + 1 < layers_n) {
@@ -474,18 +439,20 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                                           part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
             }
         }
-        if (!grid_sync(bar, ++epoch, st, tr)) return;
     }
     // ---- final norm + LM head (src/model.rs:465-468, 590) ----
     if (call.head) {
         ArgsPtr a = fresh(args);
         const int H = a->hidden;
-        stage<B, ITH>(lds, a->x, H, H);
+        if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, layers_n - 1, FK_XD), st)) return;
+        a = fresh(args);
         norm_rows<B>(lds, H, a->final_norm, a->eps, nullptr);
         a = fresh(args);
-        gemv_ring<B, EPI_STORE, ITH>(a->lm_head, nullptr, lds, H, a->logits, a->vocab, part_lo(a->vocab, wg, nwg),
-                                     part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
+        gemv_ring<B, EPI_STORE, ITH>(a->lm_head, nullptr, lds, H, a->logits, nullptr, 0, a->vocab,
+                                     part_lo(a->vocab, wg, nwg), part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
     }
+    // The next launch's epoch.  Workgroup 0 cannot get here before every
+    // workgroup has read seq: its final input needs every workgroup's output.
     if (wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
 }
 
@@ -502,25 +469,35 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const int iti = (c.intermediate_size / 8 + 63) / 64;
     const bool shape = (c.head_dim == 128 && ith == 6 && itq == 6 && iti == 16) ||
                        (c.head_dim == 64 && ith == 2 && itq == 2 && iti == 6);
-    return shape && rows >= 1 && rows <= 2 && nwg % (c.num_key_value_heads * rows) == 0 &&
-           c.num_attention_heads / c.num_key_value_heads <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows;
+    if (!shape || rows < 1 || rows > 2 || nwg % (c.num_key_value_heads * rows) != 0) return false;
+    const int G = c.num_attention_heads / c.num_key_value_heads;
+    const int wpg = nwg / (c.num_key_value_heads * rows);
+    const int max_blocks = (c.max_position_embeddings + kBlockKeys - 1) / kBlockKeys;
+    const int bpw = (max_blocks + wpg - 1) / wpg;
+    return G <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows && max_blocks <= 24576 / kBlockKeys &&
+           G * c.head_dim * bpw + max_blocks <= kStepThreads * kMergePer;
 }
 
-size_t step_lds_bytes(const StepArgs& a) {
-    const int kmax = std::max(std::max(a.hidden, a.intermediate), a.heads * a.attn.dim);
-    const int G = a.heads / a.kv_heads;
-    return std::max((size_t)a.rows * kmax, (size_t)G * a.attn.bpw * kBlockKeys) * sizeof(float);
+size_t step_lds_bytes(const StepArgs& a, int nwg) {
+    const int kmax = std::max(std::max(a.hidden, a.intermediate), a.heads * a.head_dim);
+    const int G = a.heads / a.kv_heads, wpg = nwg / (a.kv_heads * a.rows);
+    const int bpw = (a.max_blocks + wpg - 1) / wpg;
+    // staged GEMV inputs; attention scores of G heads over bpw blocks; the
+    // attention merge (outputs x blocks)
+    const size_t floats = std::max(std::max((size_t)a.rows * kmax, (size_t)G * bpw * kBlockKeys),
+                                   (size_t)G * a.head_dim * bpw + a.max_blocks);
+    return floats * sizeof(float);
 }
 
 hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {
-    const size_t lds = step_lds_bytes(a);
-    if (lds > 128 * 1024) return hipErrorInvalidValue;
+    const size_t lds = step_lds_bytes(a, nwg);
+    if (lds > kStepLdsMax) return hipErrorInvalidValue;
     const int ith = (a.hidden / 8 + 63) / 64;
-    if (a.attn.dim == 128 && ith == 6) {
+    if (a.head_dim == 128 && ith == 6) {
         if (a.rows == 1) return launch_step_t<1, 128, 6, 6, 16>(s, dev, call, nwg, lds);
         return launch_step_t<2, 128, 6, 6, 16>(s, dev, call, nwg, lds);
     }
-    if (a.attn.dim == 64 && ith == 2) {
+    if (a.head_dim == 64 && ith == 2) {
         if (a.rows == 1) return launch_step_t<1, 64, 2, 2, 6>(s, dev, call, nwg, lds);
         return launch_step_t<2, 64, 2, 2, 6>(s, dev, call, nwg, lds);
     }

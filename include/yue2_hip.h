@@ -240,11 +240,12 @@ int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t ite
  * through the persistent token-step kernel (appends to the cache like
  * yue2_hip_forward, computes no logits), recording the device wall clock
  * (100 MHz) per workgroup: stamps[s * wgs + w] for slot s = 0 at the start,
- * then per layer 14 slots -- QKV start, arrive, depart (QKV barrier),
- * arrive, depart (attention barrier), O start, arrive, depart, gate/up
- * start, arrive, depart, down start, arrive, depart.  cap = entries
- * available in stamps; *wgs and *slots receive the trace shape.
- * YUE2_ERR_ARG when the shape has no step kernel or cap is too small. */
+ * then per layer 15 slots -- QKV start, QKV end, attention: queries gathered,
+ * new key appended, block maxima stored, maxima gathered, sums gathered,
+ * partials stored, attention end; O start, O end, gate/up start, gate/up
+ * end, down start, down end.  cap = entries available in stamps; *wgs and
+ * *slots receive the trace shape.  YUE2_ERR_ARG when the shape has no step
+ * kernel or cap is too small. */
 int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, int32_t id, uint64_t *stamps, int32_t cap,
                             int32_t *wgs, int32_t *slots);
 

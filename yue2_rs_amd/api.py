@@ -274,8 +274,8 @@ class Model:
     def trace_step(self, token: int, cache: "Cache") -> np.ndarray:
         """One decode step through the persistent step kernel with phase
         stamps: uint64 array [slot, workgroup] of the device wall clock
-        (100 MHz); slot 0 = start, then 14 per layer (see yue2_hip.h)."""
-        cap = (1 + 14 * self.config.num_hidden_layers) * 1024
+        (100 MHz); slot 0 = start, then 15 per layer (see yue2_hip.h)."""
+        cap = (1 + 15 * self.config.num_hidden_layers) * 1024
         out = np.zeros(cap, dtype=np.uint64)
         wgs, slots = C.c_int32(0), C.c_int32(0)
         _check(lib().yue2_hip_trace_step(self._h, cache._h, int(token), _ptr(out), cap,

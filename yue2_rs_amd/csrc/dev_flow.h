@@ -77,15 +77,14 @@ __device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float*
                 dst[tid + j * NT] = u2f((uint32_t)w[j]);
                 pend &= ~(1u << j);
             }
-        if (pend) {
-            ++rounds;
-            if ((rounds & 255) == 0 && (rounds > (1u << 20) || ld_dev_i(&st->error))) {
-                set_error(&st->error, kDevErrFlow);
-                s_fail = 1;  // benign race: every writer stores 1
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
+        if (!pend) break;
+        ++rounds;
+        if ((rounds & 255) == 0 && (rounds > (1u << 20) || ld_dev_i(&st->error))) {
+            set_error(&st->error, kDevErrFlow);
+            s_fail = 1;  // benign race: every writer stores 1
+            break;
         }
+        __builtin_amdgcn_s_sleep(1);
     }
     __syncthreads();
     return s_fail == 0;
@@ -95,8 +94,8 @@ __device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float*
 template <int NT, int MAXPER>
 __device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, size_t stride, uint32_t tag,
                                        float* dst, StepState* st) {
-    return gather_at<NT, MAXPER>(
-        [=](int i) { return src + (size_t)(i / cols) * stride + i % cols; }, n, tag, dst, st);
+    return gather_at<NT, MAXPER>([=](int i) { return src + (size_t)(i / cols) * stride + i % cols; }, n, tag, dst,
+                                 st);
 }
 
 // Arguments of one layer's attention in the step kernel.
@@ -118,8 +117,8 @@ struct FlowAttn {
 // three group exchanges (block maxima, block sums, partial PV) as tagged
 // words and the final merge spread over the group's workgroups.  e_s: LDS
 // scratch of max(G * bpw * 64, merge) floats.  false: timeout (error set).
-template <int NT, int D, int MAXG>
-__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* e_s) {
+template <int NT, int D, int MAXG, class Mark>
+__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* e_s, Mark&& mark) {
     constexpr int NW = NT / 64;
     constexpr int CPL = D / 8;     // lanes per key row
     constexpr int KPW = 64 / CPL;  // keys per wave load
@@ -136,7 +135,10 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
     const int bpw = (nb + a.wpg - 1) / a.wpg;
     const int W = (nb + bpw - 1) / bpw;
-    if (wi >= W) return true;
+    if (wi >= W) {
+        for (int i = 0; i < 6; ++i) mark();  // keep the trace slots aligned
+        return true;
+    }
     const int G = a.heads / a.kv_heads;
     const int blk0 = wi * bpw, blk1 = min(nb, blk0 + bpw), nbl = blk1 - blk0;
     const int j0 = blk0 * kBlockKeys, j1 = min(L, blk1 * kBlockKeys), nk = j1 - j0;
@@ -151,6 +153,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     // ---- phase 0: queries (and the new key/value) -------------------------
     if (!gather<NT, (MAXG * D + NT - 1) / NT>(row + (size_t)(g * G) * D, G * D, G * D, 0, t_qkv, &q_s[0][0], st))
         return false;
+    mark();
     if (owns_new) {
         if (!gather<NT, 1>(row + (size_t)(a.heads + g) * D, D, D, 0, t_qkv, k_s, st)) return false;
         if (!gather<NT, 1>(row + (size_t)(a.heads + a.kv_heads + g) * D, D, D, 0, t_qkv, v_s, st)) return false;
@@ -196,6 +199,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         stores_done();  // the appended row is read back below by other waves
         __syncthreads();
     }
+    mark();
 
     // ---- phase 1: scaled scores and block maxima ---------------------------
     const uint32_t t_bmax = flow_tag(a.epoch, a.layer, FK_BMAX);
@@ -241,12 +245,14 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             if (lane == 0) st_tag(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m, t_bmax);
         }
     }
+    mark();
 
     // ---- phase 2: M, exp(s - M) and block sums -----------------------------
     const uint32_t t_bsum = flow_tag(a.epoch, a.layer, FK_BSUM);
     {
         if (!gather<NT, (MAXG * MAXNB + NT - 1) / NT>(a.bmax + hbase, G * nb, nb, a.blk_stride, t_bmax, red_s, st))
             return false;
+        mark();
         for (int h = wave; h < G; h += NW) {
             float m = -__builtin_huge_valf();
             for (int i = lane; i < nb; i += 64) m = fmaxf(m, red_s[h * nb + i]);
@@ -275,6 +281,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     {
         if (!gather<NT, (MAXG * MAXNB + NT - 1) / NT>(a.bsum + hbase, G * nb, nb, a.blk_stride, t_bsum, red_s, st))
             return false;
+        mark();
         if (tid < G) {
             // block sums added left to right
             float tot = red_s[tid * nb];
@@ -335,6 +342,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         }
     }
 
+    mark();
     // ---- merge: workgroup wi adds the blocks of outputs [o0, o1) -----------
     {
         const int outs = G * D, chunk = (outs + W - 1) / W;

@@ -36,9 +36,10 @@ struct StepCall {
 };
 
 // Trace slots: one at the start, then per layer: QKV start, QKV end,
-// attention end, O start, O end, gate/up start, gate/up end, down start,
-// down end.
-constexpr int kTraceSlotsPerLayer = 9;
+// six inside the attention (queries gathered, new key appended, block maxima
+// stored, maxima gathered, sums gathered, partials stored), attention end,
+// O start, O end, gate/up start, gate/up end, down start, down end.
+constexpr int kTraceSlotsPerLayer = 15;
 
 // True when a compiled step kernel covers this shape on nwg workgroups.
 bool step_supported(const Yue2Config& c, int rows, int nwg);

@@ -194,6 +194,8 @@ __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t*
 // epilogue EPI, written as tagged words to ty (or as floats to y when ty is
 // null); the ring holds the first R-1 items (prefetch_ring).  res: for
 // EPI_RESID, res[b * (r1 - r0) + (row - r0)] = the row's current value (LDS).
+// (Writing the new value back to res here instead of re-reading it later
+// measured slower: the GEMVs of the whole kernel lost about half their rate.)
 template <int B, int EPI, int IT>
 __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
                                           float* y, uint64_t* ty, uint32_t tag, int y_stride, int r0, int r1,
@@ -224,8 +226,10 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
                 for (int b = 0; b < B; ++b) {
                     const float v = wave_sum_xor(acc[b]);
                     const float v2 = PAIR ? wave_sum_xor(acc2[b]) : 0.0f;
-                    const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
-                    if (lane == 0) store_out<EPI>(y, ty, (size_t)b * y_stride + row, tag, v, v2, rv);
+                    if (lane == 0) {
+                        const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
+                        store_out<EPI>(y, ty, (size_t)b * y_stride + row, tag, v, v2, rv);
+                    }
                     acc[b] = acc2[b] = 0.0f;
                 }
             }
@@ -238,10 +242,19 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
 // xs[b * k + i] = word tx[b * k + i] with the given tag, for b < B, i < k.
 template <int B, int N>
 __device__ __forceinline__ bool stage(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
-    return gather<kStepThreads, B * N>(tx, B * k, B * k, 0, tag, xs, st);
+    if constexpr (B * N <= 16) {
+        return gather<kStepThreads, B * N>(tx, B * k, B * k, 0, tag, xs, st);
+    } else {
+        // one row at a time: 16 words in flight per thread at most
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            if (!gather<kStepThreads, N>(tx + (size_t)b * k, k, k, 0, tag, xs + b * k, st)) return false;
+        return true;
+    }
 }
 
-// res[b * n + r] = word tx[b * stride + r0 + r], r < n = r1 - r0 (n <= kResRows).
+// res[b * n + r] = word tx[b * stride + r0 + r], r < n = r1 - r0 (n <= kResRows):
+// this workgroup's own rows of x, which it wrote itself.
 template <int B>
 __device__ __forceinline__ bool stage_res(float* res, const uint64_t* tx, int stride, int r0, int r1, uint32_t tag,
                                           StepState* st) {
@@ -250,14 +263,29 @@ __device__ __forceinline__ bool stage_res(float* res, const uint64_t* tx, int st
                                       tag, res, st);
 }
 
-// xs[b] = RMSNorm(xs[b]) with gammas g (Norm::apply, src/tensor.rs:1140-1157).
-template <int B>
-__device__ __forceinline__ void norm_rows(float* xs, int k, const float* g, float eps, int* fallbacks) {
+// gam[j] = g[tid + 512 j] (0 past k): a norm's gammas, loaded ahead.
+template <int N>
+__device__ __forceinline__ void load_gamma(const float* g, int k, float* gam) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const int i = threadIdx.x + j * kStepThreads;
+        gam[j] = i < k ? gbl(g)[i] : 0.0f;
+    }
+}
+
+// xs[b] = RMSNorm(xs[b]) (Norm::apply, src/tensor.rs:1140-1157) with the
+// gammas of load_gamma.
+template <int B, int N>
+__device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, float eps, int* fallbacks) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
         float* xb = xs + b * k;
         const float s = norm_scale_block<kStepThreads>(xb, k, eps, fallbacks);
-        for (int i = threadIdx.x; i < k; i += kStepThreads) xb[i] = rb(rb(xb[i] * s) * gbl(g)[i]);
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = threadIdx.x + j * kStepThreads;
+            if (i < k) xb[i] = rb(rb(xb[i] * s) * gam[j]);
+        }
     }
     __syncthreads();
 }
@@ -308,7 +336,7 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
 template <int B, int D, int ITH, int ITQ, int ITI>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
     extern __shared__ float lds[];
-    __shared__ float res_s[B * kResRows];
+    __shared__ float res_s[B * kResRows];  // this workgroup's rows of x (residual)
     constexpr int RMAX = std::max(std::max(Ring<ITH, false>::SIZE, Ring<ITH, true>::SIZE),
                                   std::max(Ring<ITQ, false>::SIZE, Ring<ITI, false>::SIZE));
     const ArgsPtr args = (ArgsPtr)args_dev;
@@ -318,12 +346,13 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     const int seq = *gbl(&st->seq);
     const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
     uint4 ring[RMAX];
+    float gam[ITH];
     Tracer tr{call.trace, call.trace_slots, 0};
     tr.mark();
 
-    // Embedding (src/model.rs:452-464): this workgroup's slice of x as tagged
-    // words (its own residual rows), and the whole of x staged for the first
-    // norm straight from the table.
+    // Embedding (src/model.rs:452-464): this workgroup's rows of x as tagged
+    // words (its residual rows for the first O projection), and the whole of
+    // x staged for the first norm, straight from the table.
     {
         ArgsPtr a = fresh(args);
         const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
@@ -335,16 +364,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 return;
             }
         }
+        load_gamma<ITH>(a->layers[0].in_norm, H, gam);
+        prefetch_ring<ITH, false>(a->layers[0].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
+                                  part_lo(qkvw, wg + 1, nwg), qkvw, ring);
         const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
         const uint32_t t_emb = flow_tag(epoch, 0, FK_EMB);
         for (int b = 0; b < B; ++b) {
             const auto* e = gbl(a->embed + (size_t)ids[b] * H);
             for (int i = h0 + tid; i < h1; i += kStepThreads) st_tag(a->tx + (size_t)b * H + i, bf16(e[i]), t_emb);
-        }
-        prefetch_ring<ITH, false>(a->layers[0].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
-                                  part_lo(qkvw, wg + 1, nwg), qkvw, ring);
-        for (int b = 0; b < B; ++b) {
-            const auto* e = gbl(a->embed + (size_t)ids[b] * H);
             for (int i = tid; i < H; i += kStepThreads) lds[b * H + i] = bf16(e[i]);
         }
         __syncthreads();
@@ -356,9 +383,16 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
-            if (l > 0 && !stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
+            if (l > 0) {
+                // this layer's gammas and first weights go out before the wait
+                load_gamma<ITH>(a->layers[l].in_norm, H, gam);
+                prefetch_ring<ITH, false>(a->layers[l].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
+                                          part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+                a = fresh(args);
+                if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
+            }
             a = fresh(args);
-            norm_rows<B>(lds, H, a->layers[l].in_norm, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
+            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
             gemv_ring<B, EPI_STORE, ITH>(a->layers[l].wqkv, nullptr, lds, H, nullptr, a->tqkv,
@@ -372,18 +406,17 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int groups = a->kv_heads * B, wpg = nwg / groups;
             const int group = wg / wpg, kvh = a->kv_heads;
             const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D);
-            if (!attn_flow<kStepThreads, D, 4>(fa, wg % wpg, group % kvh, group / kvh, lds)) return;
+            if (!attn_flow<kStepThreads, D, 4>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
+                return;
             tr.mark();
-            a = fresh(args);
-            const int H = a->hidden, qw = a->heads * D;
-            prefetch_ring<ITQ, false>(a->layers[l].wo, nullptr, qw, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg),
-                                      H, ring);
         }
         // ---- O projection + residual ----
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qw = a->heads * D;
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+            prefetch_ring<ITQ, false>(a->layers[l].wo, nullptr, qw, h0, h1, H, ring);
+            a = fresh(args);
             if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l > 0 ? l - 1 : 0, l > 0 ? FK_XD : FK_EMB),
                               st))
                 return;
@@ -394,33 +427,32 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             gemv_ring<B, EPI_RESID, ITQ>(a->layers[l].wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
-            a = fresh(args);
-            const int I = a->intermediate;
-            prefetch_ring<ITH, true>(a->layers[l].wg, a->layers[l].wu, H, part_lo(I, wg, nwg),
-                                     part_lo(I, wg + 1, nwg), I, ring);
         }
         // ---- post-attention RMSNorm + gate/up + SwiGLU ----
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
+            load_gamma<ITH>(a->layers[l].post_norm, H, gam);
+            prefetch_ring<ITH, true>(a->layers[l].wg, a->layers[l].wu, H, part_lo(I, wg, nwg),
+                                     part_lo(I, wg + 1, nwg), I, ring);
+            a = fresh(args);
             if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
             a = fresh(args);
-            norm_rows<B>(lds, H, a->layers[l].post_norm, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
+            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
             gemv_ring<B, EPI_SWIGLU, ITH>(a->layers[l].wg, a->layers[l].wu, lds, H, nullptr, a->tact,
                                           flow_tag(epoch, l, FK_ACT), I, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg),
                                           I, ring);
             tr.mark();
-            a = fresh(args);
-            prefetch_ring<ITI, false>(a->layers[l].wd, nullptr, I, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg), H,
-                                      ring);
         }
         // ---- down projection + residual ----
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+            prefetch_ring<ITI, false>(a->layers[l].wd, nullptr, I, h0, h1, H, ring);
+            a = fresh(args);
             if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l, FK_XO), st)) return;
             a = fresh(args);
             if (!stage<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
@@ -429,27 +461,22 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             gemv_ring<B, EPI_RESID, ITI>(a->layers[l].wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
-            a = fresh(args);
-            const int qkvw = (a->heads + 2 * a->kv_heads) * D;
-            if (l + 1 < layers_n) {
-                prefetch_ring<ITH, false>(a->layers[l + 1].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
-                                          part_lo(qkvw, wg + 1, nwg), qkvw, ring);
-            } else if (call.head) {
-                prefetch_ring<ITH, false>(a->lm_head, nullptr, H, part_lo(a->vocab, wg, nwg),
-                                          part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
-            }
         }
     }
     // ---- final norm + LM head (src/model.rs:465-468, 590) ----
     if (call.head) {
         ArgsPtr a = fresh(args);
         const int H = a->hidden;
+        const int v0 = part_lo(a->vocab, wg, nwg), v1 = part_lo(a->vocab, wg + 1, nwg);
+        load_gamma<ITH>(a->final_norm, H, gam);
+        prefetch_ring<ITH, false>(a->lm_head, nullptr, H, v0, v1, a->vocab, ring);
+        a = fresh(args);
         if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, layers_n - 1, FK_XD), st)) return;
         a = fresh(args);
-        norm_rows<B>(lds, H, a->final_norm, a->eps, nullptr);
+        norm_rows<B, ITH>(lds, H, gam, a->eps, nullptr);
         a = fresh(args);
-        gemv_ring<B, EPI_STORE, ITH>(a->lm_head, nullptr, lds, H, a->logits, nullptr, 0, a->vocab,
-                                     part_lo(a->vocab, wg, nwg), part_lo(a->vocab, wg + 1, nwg), a->vocab, ring);
+        gemv_ring<B, EPI_STORE, ITH>(a->lm_head, nullptr, lds, H, a->logits, nullptr, 0, a->vocab, v0, v1, a->vocab,
+                                     ring);
     }
     // The next launch's epoch.  Workgroup 0 cannot get here before every
     // workgroup has read seq: its final input needs every workgroup's output.

@@ -112,18 +112,37 @@ struct FlowAttn {
     StepState* st;
 };
 
-// Workgroup wi (of wpg) of group (kv head g, batch row b): the same
-// arithmetic as attn_group in dev_attn.h (and so the same bits), with the
-// three group exchanges (block maxima, block sums, partial PV) as tagged
-// words and the final merge spread over the group's workgroups.  e_s: LDS
-// scratch of max(G * bpw * 64, merge) floats.  false: timeout (error set).
+// K/V blocks staged in LDS at a time by the attention (64 keys each).
+constexpr int kAttnChunk = 3;
+
+// Dynamic LDS bytes attn_flow needs: staged K and V chunks, the scores of G
+// heads over bpw blocks (the merge reuses the K/V region).
+__host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
+    return (size_t)2 * kAttnChunk * kBlockKeys * D * sizeof(uint16_t) + (size_t)G * bpw * kBlockKeys * sizeof(float);
+}
+
+// Workgroup wi (of wpg) of group (kv head g, batch row b): the arithmetic of
+// attn_group in dev_attn.h (so the same bits), with the three group
+// exchanges (block maxima, block sums, partial PV) as tagged words and the
+// final merge spread over the group's workgroups.  Latency is what limits a
+// decode attention at a few thousand keys, so:
+//  - the workgroup's first K and V blocks and the RoPE / QK-norm constants
+//    are requested before it waits for its queries;
+//  - K and V go through LDS (kAttnChunk blocks at a time), and the owner of
+//    the newest key uses its freshly computed row from there, so the cache
+//    append needs no completion wait;
+//  - PV runs one (block, head) item per wave.
+// lds: attn_flow_lds(G, D, bpw) bytes.  false: timeout (error set).
 template <int NT, int D, int MAXG, class Mark>
-__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* e_s, Mark&& mark) {
+__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark) {
     constexpr int NW = NT / 64;
     constexpr int CPL = D / 8;     // lanes per key row
-    constexpr int KPW = 64 / CPL;  // keys per wave load
+    constexpr int KPW = 64 / CPL;  // keys per wave pass
     constexpr int S = KPW;         // PV key streams per 64-key block
     constexpr int MAXNB = 24576 / kBlockKeys;
+    constexpr int BLK_U4 = kBlockKeys * D / 8;           // uint4 per staged block
+    constexpr int PER = (kAttnChunk * BLK_U4 + NT - 1) / NT;  // uint4 per thread per chunk
+    constexpr int HALF = D / 2;
     __shared__ float q_s[MAXG][D];
     __shared__ float k_s[D], v_s[D];
     __shared__ float hscale[MAXG + 1];
@@ -149,15 +168,49 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
     const bool owns_new = j1 == L;
     const uint32_t t_qkv = flow_tag(a.epoch, a.layer, FK_QKV);
+    uint4* Ks = reinterpret_cast<uint4*>(lds);  // [kAttnChunk * 64][D / 8]
+    uint4* Vs = Ks + kAttnChunk * BLK_U4;
+    float* e_s = reinterpret_cast<float*>(Vs + kAttnChunk * BLK_U4);
 
-    // ---- phase 0: queries (and the new key/value) -------------------------
+    // staged-chunk loads: rows [c0 * 64, ...) of this workgroup's keys; rows
+    // past L are not read (their slots are never used)
+    auto load_chunk = [&](const uint16_t* base, int cb, uint4* r) {
+        const int nrow = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT, key = u / (D / 8), part = u % (D / 8);
+            r[i] = key < nrow ? ldg4(base + (size_t)(j0 + cb * kBlockKeys + key) * D + 8 * part)
+                              : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_chunk = [&](uint4* dst, const uint4* r) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (tid + i * NT < kAttnChunk * BLK_U4) dst[tid + i * NT] = r[i];
+    };
+
+    // ---- phase 0: early requests, queries, new key/value --------------------
+    uint4 kr[PER], vr[PER];
+    load_chunk(Kc, 0, kr);
+    load_chunk(Vc, 0, vr);
+    // RoPE / QK-norm constants of the (head, d) pair this thread rotates
+    const int pairs = (G + (owns_new ? 1 : 0)) * HALF;
+    float c_cos = 0.0f, c_sin = 0.0f, c_g0 = 0.0f, c_g1 = 0.0f;
+    if (tid < pairs) {
+        const int h = tid / HALF, d = tid % HALF;
+        const float* gam = h < G ? a.q_norm : a.k_norm;
+        c_g0 = gbl(gam)[d];
+        c_g1 = gbl(gam)[d + HALF];
+        c_cos = gbl(a.cos_t + (size_t)pos * HALF)[d];
+        c_sin = gbl(a.sin_t + (size_t)pos * HALF)[d];
+    }
     if (!gather<NT, (MAXG * D + NT - 1) / NT>(row + (size_t)(g * G) * D, G * D, G * D, 0, t_qkv, &q_s[0][0], st))
         return false;
-    mark();
     if (owns_new) {
         if (!gather<NT, 1>(row + (size_t)(a.heads + g) * D, D, D, 0, t_qkv, k_s, st)) return false;
         if (!gather<NT, 1>(row + (size_t)(a.heads + a.kv_heads + g) * D, D, D, 0, t_qkv, v_s, st)) return false;
     }
+    mark();
     // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
     if (tid < G || (owns_new && tid == G)) {
         const float* v = tid < G ? q_s[tid] : k_s;
@@ -171,34 +224,38 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         }
         hscale[tid] = norm_scale_from_sum(sum, D, a.eps);
     }
+    store_chunk(Ks, kr);
+    store_chunk(Vs, vr);
     __syncthreads();
-    {
-        const int half = D / 2;
-        const float* cs = a.cos_t + (size_t)pos * half;
-        const float* sn = a.sin_t + (size_t)pos * half;
-        const int pairs = (G + (owns_new ? 1 : 0)) * half;
-        for (int i = tid; i < pairs; i += NT) {
-            const int h = i / half, d = i % half;
-            float* v = h < G ? q_s[h] : k_s;
-            const float* gam = h < G ? a.q_norm : a.k_norm;
-            const float s = hscale[h];
-            const float x0 = rb(rb(v[d] * s) * gbl(gam)[d]);
-            const float x1 = rb(rb(v[d + half] * s) * gbl(gam)[d + half]);
-            const float c = gbl(cs)[d], si = gbl(sn)[d];
-            const float y0 = rb(rb(x0 * c) - rb(x1 * si));
-            const float y1 = rb(rb(x1 * c) + rb(x0 * si));
-            v[d] = y0;
-            v[d + half] = y1;
-            if (h == G) {
-                gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
-                gblw(Kc)[(size_t)pos * D + d + half] = bf16_bits(y1);
+    // rotate-half RoPE (src/model.rs:151-168); the new key and value go to the
+    // cache for later steps and straight into the staged chunk for this one
+    if (tid < pairs) {
+        const int h = tid / HALF, d = tid % HALF;
+        float* v = h < G ? q_s[h] : k_s;
+        const float s = hscale[h];
+        const float x0 = rb(rb(v[d] * s) * c_g0);
+        const float x1 = rb(rb(v[d + HALF] * s) * c_g1);
+        const float y0 = rb(rb(x0 * c_cos) - rb(x1 * c_sin));
+        const float y1 = rb(rb(x1 * c_cos) + rb(x0 * c_sin));
+        v[d] = y0;
+        v[d + HALF] = y1;
+        if (h == G) {
+            gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
+            gblw(Kc)[(size_t)pos * D + d + HALF] = bf16_bits(y1);
+            if (pos - j0 < kAttnChunk * kBlockKeys) {
+                uint16_t* kl = reinterpret_cast<uint16_t*>(Ks) + (size_t)(pos - j0) * D;
+                kl[d] = bf16_bits(y0);
+                kl[d + HALF] = bf16_bits(y1);
             }
         }
-        if (owns_new)
-            for (int d = tid; d < D; d += NT) gblw(Vc)[(size_t)pos * D + d] = bf16_bits(v_s[d]);
-        stores_done();  // the appended row is read back below by other waves
-        __syncthreads();
     }
+    if (owns_new)
+        for (int d = tid; d < D; d += NT) {
+            const uint16_t bits = bf16_bits(v_s[d]);
+            gblw(Vc)[(size_t)pos * D + d] = bits;
+            if (pos - j0 < kAttnChunk * kBlockKeys) reinterpret_cast<uint16_t*>(Vs)[(size_t)(pos - j0) * D + d] = bits;
+        }
+    __syncthreads();
     mark();
 
     // ---- phase 1: scaled scores and block maxima ---------------------------
@@ -210,19 +267,25 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         for (int h = 0; h < MAXG; ++h)
 #pragma unroll
             for (int e = 0; e < 8; ++e) qv[h][e] = h < G ? q_s[h][8 * c + e] : 0.0f;
-        constexpr int R = 8;
-        for (int base = j0 + wave * R * KPW; base < j1; base += NW * R * KPW) {
-            uint4 kr[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int j = base + r * KPW + kk;
-                kr[r] = j < j1 ? ldg4(Kc + (size_t)j * D + 8 * c) : make_uint4(0, 0, 0, 0);
+        for (int cb = 0; cb < nbl; cb += kAttnChunk) {
+            if (cb > 0) {
+                // a later chunk (long contexts): stage it, then patch the new key
+                __syncthreads();
+                load_chunk(Kc, cb, kr);
+                store_chunk(Ks, kr);
+                __syncthreads();
+                const int kp = pos - j0 - cb * kBlockKeys;
+                if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
+                    for (int d = tid; d < D; d += NT)
+                        reinterpret_cast<uint16_t*>(Ks)[(size_t)kp * D + d] = bf16_bits(k_s[d]);
+                __syncthreads();
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int j = base + r * KPW + kk;
+            const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
+            for (int kg = wave; kg * KPW < keys; kg += NW) {
+                const int kl = kg * KPW + kk;  // key within the chunk
+                const int j = j0 + cb * kBlockKeys + kl;
                 float kf[8];
-                unpack8a(kr[r], kf);
+                unpack8a(Ks[(size_t)kl * (D / 8) + c], kf);
 #pragma unroll
                 for (int h = 0; h < MAXG; ++h) {
                     if (h >= G) break;
@@ -230,7 +293,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
 #pragma unroll
-                    for (int s = CPL / 2; s >= 1; s >>= 1) acc = acc + __shfl_xor(acc, s, 64);
+                    for (int s2 = CPL / 2; s2 >= 1; s2 >>= 1) acc = acc + __shfl_xor(acc, s2, 64);
                     if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
                 }
             }
@@ -241,7 +304,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             const int jl = bl * kBlockKeys + lane;
             float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
 #pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            for (int s2 = 32; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2, 64));
             if (lane == 0) st_tag(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m, t_bmax);
         }
     }
@@ -257,7 +320,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             float m = -__builtin_huge_valf();
             for (int i = lane; i < nb; i += 64) m = fmaxf(m, red_s[h * nb + i]);
 #pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            for (int s2 = 32; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2, 64));
             if (lane == 0) m_s[h] = m;
         }
         __syncthreads();
@@ -271,7 +334,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             const int jl = bl * kBlockKeys + lane;
             float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
 #pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
+            for (int s2 = 32; s2 >= 1; s2 >>= 1) v = v + __shfl_xor(v, s2, 64);
             if (lane == 0) st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v, t_bsum);
         }
     }
@@ -295,60 +358,57 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         }
         __syncthreads();
         const int t = lane / CPL, c = lane % CPL;
-        for (int bl = wave; bl < nbl; bl += NW) {
-            const int jb = (blk0 + bl) * kBlockKeys;
-            uint4 vr[kBlockKeys / S];
-#pragma unroll
-            for (int i = 0; i < kBlockKeys / S; ++i) {
-                const int j = jb + t + S * i;
-                vr[i] = j < L ? ldg4(Vc + (size_t)j * D + 8 * c) : make_uint4(0, 0, 0, 0);
+        for (int cb = 0; cb < nbl; cb += kAttnChunk) {
+            if (cb > 0) {
+                __syncthreads();
+                load_chunk(Vc, cb, vr);
+                store_chunk(Vs, vr);
+                __syncthreads();
+                const int kp = pos - j0 - cb * kBlockKeys;
+                if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
+                    for (int d = tid; d < D; d += NT)
+                        reinterpret_cast<uint16_t*>(Vs)[(size_t)kp * D + d] = bf16_bits(v_s[d]);
+                __syncthreads();
             }
-            float acc[MAXG][8];
+            const int cblocks = min(kAttnChunk, nbl - cb);
+            // one (block, head) item per wave
+            for (int it = wave; it < cblocks * G; it += NW) {
+                const int bc = it / G, h = it % G, bl = cb + bc;
+                const int jb = (blk0 + bl) * kBlockKeys;
+                float acc[8];
 #pragma unroll
-            for (int h = 0; h < MAXG; ++h)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
-#pragma unroll
-            for (int i = 0; i < kBlockKeys / S; ++i) {
-                const int jj = t + S * i;
-                if (jb + jj < L) {
-                    float vf[8];
-                    unpack8a(vr[i], vf);
-#pragma unroll
-                    for (int h = 0; h < MAXG; ++h) {
-                        if (h >= G) break;
+                for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll 4
+                for (int i = 0; i < kBlockKeys / S; ++i) {
+                    const int jj = t + S * i;
+                    if (jb + jj < L) {
+                        float vf[8];
+                        unpack8a(Vs[(size_t)(bc * kBlockKeys + jj) * (D / 8) + c], vf);
                         const float p = e_s[h * estride + bl * kBlockKeys + jj];
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p, vf[e], acc[h][e]);
+                        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
                     }
                 }
-            }
 #pragma unroll
-            for (int s = 32; s >= CPL; s >>= 1)
+                for (int s2 = 32; s2 >= CPL; s2 >>= 1)
 #pragma unroll
-                for (int h = 0; h < MAXG; ++h)
-                    if (h < G)
+                    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], s2, 64);
+                // the S stream lanes hold the same sums: each stores 8 / S of them
+                uint64_t* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] + __shfl_xor(acc[h][e], s, 64);
-            if (t == 0) {
-#pragma unroll
-                for (int h = 0; h < MAXG; ++h)
-                    if (h < G) {
-                        uint64_t* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) st_tag(dst + e, acc[h][e], t_part);
-                    }
+                for (int e = 0; e < 8; ++e)
+                    if (e % S == t) st_tag(dst + e, acc[e], t_part);
             }
         }
     }
-
     mark();
+
     // ---- merge: workgroup wi adds the blocks of outputs [o0, o1) -----------
     {
         const int outs = G * D, chunk = (outs + W - 1) / W;
         const int o0 = min(outs, wi * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
-        __syncthreads();  // e_s is reused below
-        // e_s[i * nb + k] = partial of block k for output o0 + i
+        __syncthreads();  // the K/V region is reused below
+        float* m_buf = lds;  // [no][nb]: partial of block k for output o0 + i
         const uint64_t* part = a.part + hbase * D;
         const size_t hstride = (size_t)a.blk_stride * D;
         const int nbm = nb;
@@ -357,11 +417,11 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                     const int o = o0 + i / nbm, k = i % nbm;
                     return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
                 },
-                no * nb, t_part, e_s, st))
+                no * nb, t_part, m_buf, st))
             return false;
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
         for (int i = tid; i < no; i += NT) {
-            const float* pp = e_s + i * nb;
+            const float* pp = m_buf + i * nb;
             float o = pp[0];
             for (int k = 1; k < nb; ++k) o = o + pp[k];  // blocks left to right
             st_tag(a.att + (size_t)b * a.att_stride + (size_t)g * G * D + o0 + i, rb(o), t_att);

@@ -509,11 +509,9 @@ size_t step_lds_bytes(const StepArgs& a, int nwg) {
     const int kmax = std::max(std::max(a.hidden, a.intermediate), a.heads * a.head_dim);
     const int G = a.heads / a.kv_heads, wpg = nwg / (a.kv_heads * a.rows);
     const int bpw = (a.max_blocks + wpg - 1) / wpg;
-    // staged GEMV inputs; attention scores of G heads over bpw blocks; the
-    // attention merge (outputs x blocks)
-    const size_t floats = std::max(std::max((size_t)a.rows * kmax, (size_t)G * bpw * kBlockKeys),
-                                   (size_t)G * a.head_dim * bpw + a.max_blocks);
-    return floats * sizeof(float);
+    // staged GEMV inputs; the attention (staged K/V chunks + scores; its
+    // merge reuses the K/V region)
+    return std::max((size_t)a.rows * kmax * sizeof(float), attn_flow_lds(G, a.head_dim, bpw));
 }
 
 hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {

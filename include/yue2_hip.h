@@ -191,6 +191,16 @@ void yue2_hip_decoder_free(Yue2Decoder *d);
 int32_t yue2_hip_decoder_run(Yue2Decoder *d, const float *first_logits, int32_t steps,
                              int32_t *tokens, float *step_ms);
 
+/* sampling::choose (src/sampling.rs:103-215) on the device for one row of
+ * logits (already CFG-mixed).  history / history_len: the ids generated so
+ * far, of which the last penalty_window set the repetition penalty; step
+ * gates the end token by min_tokens; draws: the 2 * vocab MT19937 outputs
+ * the call consumes, in stream order (may be NULL when temperature is 0).
+ * *id receives the chosen id.  Returns YUE2_OK or a negative Yue2Error. */
+int32_t yue2_hip_choose(const float *logits, int32_t vocab, const Yue2Sampling *sampling,
+                        const int32_t *history, int32_t history_len, int32_t step,
+                        int32_t phase, int32_t legacy, const uint32_t *draws, int32_t *id);
+
 /* sampling::generate (src/sampling.rs:222-294) on the device. */
 int32_t yue2_hip_generate(Yue2Model *m, const int32_t *prefix, int32_t prefix_len,
                           const Yue2Sampling *sampling, uint64_t seed, int32_t phase,

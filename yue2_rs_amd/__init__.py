@@ -5,9 +5,9 @@ The compute path is libyue2_hip.so (hand-written HIP kernels, C ABI in
 include/yue2_hip.h); this package binds it with ctypes.
 """
 from .api import (PHASE_ABC, PHASE_NONE, PHASE_SEMANTIC, Cache, Checkpoint, Config, Decoder,
-                  Generated, LayerWeights, Model, Sampling, Yue2Error, available, generate, lib,
-                  synchronize)
+                  Generated, LayerWeights, Model, Sampling, Yue2Error, available, choose, generate,
+                  lib, synchronize)
 
 __all__ = ["PHASE_ABC", "PHASE_NONE", "PHASE_SEMANTIC", "Cache", "Checkpoint", "Config", "Decoder",
-           "Generated", "LayerWeights", "Model", "Sampling", "Yue2Error", "available", "generate",
-           "lib", "synchronize"]
+           "Generated", "LayerWeights", "Model", "Sampling", "Yue2Error", "available", "choose",
+           "generate", "lib", "synchronize"]

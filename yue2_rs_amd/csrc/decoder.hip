@@ -32,6 +32,7 @@ struct Yue2Decoder {
     SampleArgs sa{};
     MtState* mt = nullptr;
     uint32_t* streams = nullptr;
+    void* cand = nullptr;  // chunked choose(): candidate lists and chunk totals
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
     hipGraph_t graph = nullptr;
@@ -83,6 +84,7 @@ static void decoder_release(Yue2Decoder* d) {
     if (d->side) (void)hipStreamDestroy(d->side);
     if (d->mt) (void)hipFree(d->mt);
     if (d->streams) (void)hipFree(d->streams);
+    if (d->cand) (void)hipFree(d->cand);
     d->w.release();
 }
 
@@ -127,6 +129,12 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
             e = hipMemcpy(d->mt, &host, sizeof(MtState), hipMemcpyHostToDevice);
         }
     }
+    const int mode = sampling ? 1 : 0;
+    const float temp = sampling ? sampling->temperature : 0.0f;
+    const int list = choose_list_len(V, mode, temp, sampling ? sampling->top_k : 1);
+    const int chunks = (V + kChooseChunk - 1) / kChooseChunk;
+    if (rc == YUE2_OK && e == hipSuccess && list > 0)
+        e = hipMalloc(&d->cand, sizeof(uint64_t) * (size_t)chunks * list + sizeof(int2) * chunks);
     if (rc == YUE2_OK && e == hipSuccess) e = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);
     if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->fork, hipEventDisableTiming);
     if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->join, hipEventDisableTiming);
@@ -141,13 +149,21 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     a.scores = d->w.mixed;
     a.stream[0] = d->streams;
     a.stream[1] = d->streams ? d->streams + 2 * (size_t)V : nullptr;
+    a.history = d->w.token_log;
+    a.hist_len = -1;
     a.token_log = d->w.token_log;
     a.st = d->w.st;
     a.rows = d->rows;
     a.vocab = V;
     a.phase = phase;
     a.end_id = phase_end_id(phase);
-    a.mode = sampling ? 1 : 0;
+    a.mode = mode;
+    if (d->cand) {
+        a.cand = static_cast<uint64_t*>(d->cand);
+        a.meta = reinterpret_cast<int2*>(a.cand + (size_t)chunks * list);
+        a.chunks = chunks;
+        a.list = list;
+    }
     a.cfg_scale = scale;
     a.legacy = legacy;
     if (sampling) {
@@ -344,6 +360,87 @@ extern "C" int32_t yue2_hip_decoder_time_kernel(Yue2Decoder* d, int32_t kernel, 
     (void)hipEventDestroy(b1);
     (void)hipFree(tmp);
     return rc;
+}
+
+// sampling::choose (src/sampling.rs:103-215) for one row of logits.
+extern "C" int32_t yue2_hip_choose(const float* logits, int32_t vocab, const Yue2Sampling* sampling,
+                                   const int32_t* history, int32_t history_len, int32_t step,
+                                   int32_t phase, int32_t legacy, const uint32_t* draws,
+                                   int32_t* id) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!logits || !id || vocab < 1 || history_len < 0 || step < 0 || (history_len > 0 && !history))
+        return fail(YUE2_ERR_ARG, "bad choose arguments");
+    if (int rc = validate_sampling(sampling)) return rc;
+    if (int rc = check_phase_vocab(phase, vocab)) return rc;
+    const bool rng = sampling->temperature != 0.0f;
+    if (rng && !draws) return fail(YUE2_ERR_ARG, "choose needs 2 * vocab draws");
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 HIP device");
+    const size_t V = vocab;
+    const int list = choose_list_len(vocab, 1, sampling->temperature, sampling->top_k);
+    const int chunks = (vocab + kChooseChunk - 1) / kChooseChunk;
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = at;
+        at = (at + bytes + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_st = take(sizeof(StepState)), o_logits = take(sizeof(float) * V);
+    const size_t o_scores = take(sizeof(float) * V), o_draws = take(rng ? sizeof(uint32_t) * 2 * V : 0);
+    const size_t o_hist = take(sizeof(int32_t) * std::max(history_len, 1));
+    const size_t o_cand = take(list > 0 ? sizeof(uint64_t) * (size_t)chunks * list : 0);
+    const size_t o_meta = take(list > 0 ? sizeof(int2) * chunks : 0);
+    char* p = nullptr;
+    hipError_t e = hipMalloc(&p, at);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(choose)");
+    hipStream_t s = nullptr;
+    StepState st{};
+    st.step = step;
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMemcpyAsync(p + o_st, &st, sizeof(st), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(p + o_logits, logits, sizeof(float) * V, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && rng)
+        e = hipMemcpyAsync(p + o_draws, draws, sizeof(uint32_t) * 2 * V, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && history_len > 0)
+        e = hipMemcpyAsync(p + o_hist, history, sizeof(int32_t) * history_len, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) {
+        SampleArgs a{};
+        a.logits = reinterpret_cast<const float*>(p + o_logits);
+        a.scores = reinterpret_cast<float*>(p + o_scores);
+        a.stream[0] = a.stream[1] = rng ? reinterpret_cast<const uint32_t*>(p + o_draws) : nullptr;
+        a.history = reinterpret_cast<const int32_t*>(p + o_hist);
+        a.hist_len = history_len;
+        a.token_log = nullptr;
+        a.st = reinterpret_cast<StepState*>(p + o_st);
+        a.rows = 1;
+        a.vocab = vocab;
+        a.phase = phase;
+        a.end_id = phase_end_id(phase);
+        a.mode = 1;
+        a.cfg_scale = 1.0f;
+        a.temperature = sampling->temperature;
+        a.top_p = sampling->top_p;
+        a.top_k = sampling->top_k;
+        a.repetition_penalty = sampling->repetition_penalty;
+        a.window = sampling->penalty_window;
+        a.min_tokens = sampling->min_tokens;
+        a.legacy = legacy;
+        if (list > 0) {
+            a.cand = reinterpret_cast<uint64_t*>(p + o_cand);
+            a.meta = reinterpret_cast<int2*>(p + o_meta);
+            a.chunks = chunks;
+            a.list = list;
+        }
+        launch_choose(s, a);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(&st, p + o_st, sizeof(st), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (s) (void)hipStreamDestroy(s);
+    (void)hipFree(p);
+    if (e != hipSuccess) return hip_fail(e, "choose");
+    if (int rc = step_error(st)) return rc;
+    *id = st.ids[0];
+    return YUE2_OK;
 }
 
 extern "C" int32_t yue2_hip_generate(Yue2Model* m, const int32_t* prefix, int32_t prefix_len,

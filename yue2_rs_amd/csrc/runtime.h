@@ -98,6 +98,8 @@ void phase_range(int phase, int* start, int* end, int* stop);
 int phase_end_id(int phase);
 int check_phase_vocab(int phase, int vocab);
 int read_step_error(Workspace& w, hipStream_t s);
+// The error a step state carries (YUE2_OK when none), with its message set.
+int step_error(const StepState& st);
 
 // Small state kernels (kernels.hip).
 void launch_fill(hipStream_t s, float* p, size_t n, float v);

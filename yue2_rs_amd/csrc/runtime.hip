@@ -314,6 +314,10 @@ int read_step_error(Workspace& w, hipStream_t s) {
     hipError_t e = hipMemcpyAsync(&st, w.st, sizeof(StepState), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(e, "step state readback");
+    return step_error(st);
+}
+
+int step_error(const StepState& st) {
     if (st.error == 1) return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
     if (st.error == 2) return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
     if (st.error == 3) return fail(YUE2_ERR_EMPTY, "Empty sampling distribution");

@@ -1,13 +1,26 @@
 // sampler.hip -- on-device CFG mix, choose() and the MT19937 stream.
 //
-// One workgroup selects the next token from the LM-head logits so that only
-// the token id leaves the device.  It follows src/sampling.rs:103-215 step by
-// step: phase mask, repetition penalty, validity check, greedy argmax or
-// temperature, top-k with ties kept at the threshold, top-p with a
-// sequential f32 cumulative sum, renormalisation and the exponential race
-// p / -ln(1 - u) in id order.  The race reads its uniforms from the token's
-// block of 2 * vocab MT19937 outputs, which choose() consumes whatever the
-// logits are, so the block is generated ahead by mt_generate_kernel.
+// choose() follows src/sampling.rs:103-215 step by step: phase mask,
+// repetition penalty, validity check, greedy argmax or temperature, top-k
+// with ties kept at the threshold, top-p with a sequential f32 cumulative
+// sum, renormalisation and the exponential race p / -ln(1 - u) in id order.
+// The race reads its uniforms from the token's block of 2 * vocab MT19937
+// outputs, which choose() consumes whatever the logits are, so the block is
+// generated ahead by mt_generate_kernel.
+//
+// Chunked path: score_kernel, one workgroup per kChooseChunk vocabulary
+// entries, applies the mix, mask, penalty and temperature and sorts its chunk
+// by (score descending, id ascending), keeping the first min(top_k, chunk)
+// entries.  Every entry of the global top-k is within its own chunk's top-k,
+// so finish_kernel (one workgroup) finds the top-k threshold by radix select
+// over at most chunks * top_k keys.  Only a chunk whose list was cut short
+// and ends at the threshold can hold further survivors (entries equal to the
+// threshold); those chunks are rescanned.  Sort, top-p, renormalisation and
+// the race then run over the survivors alone.
+// Single-workgroup path: choose_kernel does the same over the whole
+// vocabulary; it serves top-k values the chunked lists cannot hold.
+#include <algorithm>
+
 #include "kernels.h"
 #include "runtime.h"
 #include "sampler.h"
@@ -16,6 +29,8 @@
 namespace y2 {
 
 constexpr int kSurvivorMax = 2048;
+constexpr int kWindowMax = 128;  // penalty_window is at most 100
+static_assert(kChooseChunk == 1024, "finish_kernel rescans one chunk with its 1024 threads");
 
 __device__ __forceinline__ uint32_t ukey(float f) { return (uint32_t)total_key(f) ^ 0x80000000u; }
 __device__ __forceinline__ float from_ukey(uint32_t k) {
@@ -26,6 +41,20 @@ __device__ __forceinline__ bool is_finite(float v) {
     return (f2u(v) & 0x7f800000u) != 0x7f800000u;
 }
 __device__ __forceinline__ float cast(float x, int legacy) { return legacy ? rb(x) : x; }
+
+// Order key of entry i with score v: ascending keys run through the scores
+// in descending total order, ties by ascending id (src/sampling.rs:170, 174).
+__device__ __forceinline__ uint64_t order_key(float v, int i) {
+    return ((uint64_t)(~ukey(v)) << 32) | (uint32_t)i;
+}
+__device__ __forceinline__ float key_value(uint64_t k) { return from_ukey(~(uint32_t)(k >> 32)); }
+
+__device__ __forceinline__ uint64_t kmin(uint64_t a, uint64_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
 
 // compiler-rt __powisf2, which Rust's f32::powi calls for a run-time exponent.
 __device__ float powi_f32(float a, int b) {
@@ -59,15 +88,153 @@ __device__ void bitonic_sort(uint64_t* v, int n) {
     }
 }
 
+// CFG mix (src/sampling.rs:261-266) and phase mask (:116-129) of entry i.
+__device__ __forceinline__ float mixed_score(const SampleArgs& a, int i, int step) {
+    const float c = a.logits[i];
+    float v = c;
+    if (a.rows == 2) {
+        const float u = a.logits[(size_t)a.vocab + i];
+        v = rb(u + rb(a.cfg_scale * rb(c - u)));
+    }
+    bool in = true;
+    if (a.phase == YUE2_PHASE_ABC) in = i < kEod;
+    else if (a.phase == YUE2_PHASE_SEMANTIC) in = i >= kCodecOffset && i < kCodecOffset + kCodecSize;
+    if (a.phase != YUE2_PHASE_NONE && i == a.end_id && step >= a.min_tokens) in = true;
+    return (a.mode == 0 || in) ? v : -__builtin_huge_valf();
+}
+
+// The penalty window: the last penalty_window history ids (:130-131), into
+// ids; returns their number.  Ends with a barrier.
+__device__ int load_window(const SampleArgs& a, int step, int32_t* ids) {
+    int wn = 0;
+    if (a.mode == 1) {
+        const int len = a.hist_len >= 0 ? a.hist_len : step;
+        const int from = len > a.window ? len - a.window : 0;
+        wn = len - from;
+        for (int i = threadIdx.x; i < wn; i += blockDim.x) ids[i] = a.history[from + i];
+    }
+    __syncthreads();
+    return wn;
+}
+
+// Repetition penalty (:132-144) on the ids in [lo, lo + n), whose scores are
+// vals[id - lo]: the first occurrence of each id in the window applies
+// alpha^count.  Needs blockDim.x >= wn; ends with a barrier.
+__device__ void apply_penalty(const SampleArgs& a, const int32_t* ids, int wn, float* vals, int lo,
+                              int n) {
+    const int t = threadIdx.x;
+    if (t < wn) {
+        const int id = ids[t];
+        if (id >= lo && id < lo + n) {
+            bool first = true;
+            for (int j = 0; j < t; ++j) first &= ids[j] != id;
+            if (first) {
+                int count = 0;
+                for (int j = t; j < wn; ++j) count += ids[j] == id;
+                const float alpha = cast(powi_f32(a.repetition_penalty, count), a.legacy);
+                const float s = vals[id - lo];
+                vals[id - lo] = cast(s < 0.0f ? s * alpha : s / alpha, a.legacy);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The chosen id becomes every row's next input; it is logged at [step] and
+// ends the phase when it is the end token.
+__device__ void publish(const SampleArgs& a, int step, int32_t id) {
+    StepState* st = a.st;
+    for (int b = 0; b < a.rows; ++b) st->ids[b] = id;
+    if (a.token_log) a.token_log[step] = id;
+    if (a.phase != YUE2_PHASE_NONE && id == a.end_id) st->done = 1;
+}
+
+// Steps 6-8 over the n <= kSurvivorMax survivors, given as order keys in
+// surv (scores in sc): sort by score descending and id ascending (:174),
+// top-p (:175-190) and renormalisation (:191-197) as sequential f32 sums,
+// then the exponential race in id order (:198-214), whose uniforms are
+// stream positions 2 id and 2 id + 1 of this token's block.  Returns the
+// chosen id in every thread.
+__device__ int32_t race_tail(const SampleArgs& a, int step, const float* sc, uint64_t* surv,
+                             float* e_val, int n, int* s_kept, int* s_sel) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    int n2 = 2;
+    while (n2 < n) n2 <<= 1;
+    for (int i = n + tid; i < n2; i += nt) surv[i] = ~0ull;
+    __syncthreads();
+    bitonic_sort(surv, n2);
+    const float max = sc[(int32_t)(surv[0] & 0xffffffffu)];
+    for (int i = tid; i < n; i += nt) e_val[i] = expf_cr(sc[(int32_t)(surv[i] & 0xffffffffu)] - max);
+    __syncthreads();
+    if (tid == 0) {
+        int kept = n;
+        if (a.top_p < 1.0f) {
+            float sum = -0.0f;
+            for (int i = 0; i < n; ++i) sum = sum + e_val[i];
+            float cumulative = 0.0f;
+            const int protect = a.legacy ? 3 : 1;
+            kept = 0;
+            for (int i = 0; i < n; ++i) {
+                const float p = cast(e_val[i] / sum, a.legacy);
+                cumulative += p;
+                const float prior = cast(cast(cumulative, a.legacy) - p, a.legacy);
+                if (prior <= a.top_p || i < protect) {
+                    surv[kept] = surv[i];
+                    e_val[kept] = e_val[i];
+                    ++kept;
+                }
+            }
+        }
+        float sum = -0.0f;
+        for (int i = 0; i < kept; ++i) sum = sum + e_val[i];
+        for (int i = 0; i < kept; ++i) {
+            const float p = cast(e_val[i] / sum, a.legacy);
+            surv[i] = ((uint64_t)(surv[i] & 0xffffffffu) << 32) | f2u(p);
+        }
+        *s_kept = kept;
+    }
+    __syncthreads();
+    const int kept = *s_kept;
+    int k2 = 2;
+    while (k2 < kept) k2 <<= 1;
+    for (int i = kept + tid; i < k2; i += nt) surv[i] = ~0ull;
+    __syncthreads();
+    bitonic_sort(surv, k2);
+    const uint32_t* stream = a.stream[step & 1];
+    for (int i = tid; i < kept; i += nt) {
+        const uint32_t id = (uint32_t)(surv[i] >> 32);
+        const float p = u2f((uint32_t)(surv[i] & 0xffffffffu));
+        const uint64_t hi = stream[2 * (size_t)id], lo = stream[2 * (size_t)id + 1];
+        const double u = (double)(((hi << 32) | lo) & ((1ull << 53) - 1)) / 9007199254740992.0;
+        const float noise = cast((float)(-log1p_d(-u)), a.legacy);
+        e_val[i] = cast(p / noise, a.legacy);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float best = -__builtin_huge_valf();
+        int32_t selected = 0;
+        for (int i = 0; i < kept; ++i) {
+            if (e_val[i] > best) {
+                best = e_val[i];
+                selected = (int32_t)(surv[i] >> 32);
+            }
+        }
+        *s_sel = selected;
+    }
+    __syncthreads();
+    return *s_sel;
+}
+
+// Single-workgroup choose() over the whole vocabulary.
 __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
     __shared__ uint64_t surv[kSurvivorMax];
     __shared__ float e_val[kSurvivorMax];
     __shared__ uint32_t hist[256];
-    __shared__ int32_t window_ids[128];
-    __shared__ int32_t s_count, s_bad, s_selected, s_kept;
+    __shared__ int32_t window_ids[kWindowMax];
+    __shared__ int32_t s_count, s_bad, s_sel, s_kept;
     __shared__ uint32_t s_prefix;
     __shared__ int32_t s_remaining;
-    __shared__ int32_t red_key[16], red_idx[16];
+    __shared__ uint64_t red[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     StepState* st = a.st;
     if (st->error || st->done) return;
@@ -78,45 +245,14 @@ __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
         s_bad = 0;
         s_kept = 0;
     }
-    // 1. CFG mix (src/sampling.rs:261-266) and phase mask (:116-129).
-    for (int i = tid; i < V; i += 1024) {
-        const float c = a.logits[i];
-        float v = c;
-        if (a.rows == 2) {
-            const float u = a.logits[(size_t)V + i];
-            v = rb(u + rb(a.cfg_scale * rb(c - u)));
-        }
-        bool in = true;
-        if (a.phase == YUE2_PHASE_ABC) in = i < kEod;
-        else if (a.phase == YUE2_PHASE_SEMANTIC) in = i >= kCodecOffset && i < kCodecOffset + kCodecSize;
-        if (a.phase != YUE2_PHASE_NONE && i == a.end_id && step >= a.min_tokens) in = true;
-        sc[i] = (a.mode == 0 || in) ? v : -__builtin_huge_valf();
-    }
-    __syncthreads();
-    // 2. Repetition penalty over the last penalty_window generated ids
-    //    (:130-144).  The first occurrence of each id applies alpha^count.
-    if (a.mode == 1) {
-        const int from = step > a.window ? step - a.window : 0;
-        const int wn = step - from;
-        for (int i = tid; i < wn; i += 1024) window_ids[i] = a.token_log[from + i];
-        __syncthreads();
-        if (tid < wn) {
-            const int id = window_ids[tid];
-            bool first = true;
-            for (int j = 0; j < tid; ++j) first &= window_ids[j] != id;
-            if (first) {
-                int count = 0;
-                for (int j = tid; j < wn; ++j) count += window_ids[j] == id;
-                const float alpha = cast(powi_f32(a.repetition_penalty, count), a.legacy);
-                const float s = sc[id];
-                sc[id] = cast(s < 0.0f ? s * alpha : s / alpha, a.legacy);
-            }
-        }
-        __syncthreads();
-    }
+    // 1-2. mix, mask and repetition penalty
+    for (int i = tid; i < V; i += 1024) sc[i] = mixed_score(a, i, step);
+    const int wn = load_window(a, step, window_ids);
+    if (a.mode == 1) apply_penalty(a, window_ids, wn, sc, 0, V);
     // 3. NaN / +inf check (:145-147), then greedy or temperature (:148-161).
     const bool greedy = a.mode == 0 || a.temperature == 0.0f;
-    int32_t bk = INT32_MIN, bi = INT32_MAX, local_count = 0;
+    uint64_t best = ~0ull;
+    int local_count = 0;
     for (int i = tid; i < V; i += 1024) {
         float v = sc[i];
         if (v != v || v == __builtin_huge_valf()) s_bad = 1;
@@ -126,26 +262,13 @@ __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
         }
         if (is_finite(v)) {
             ++local_count;
-            const int32_t k = total_key(v);
-            if (k > bk) {
-                bk = k;
-                bi = i;
-            }
+            best = kmin(best, order_key(v, i));
         }
     }
     atomicAdd(&s_count, local_count);
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-        const int32_t ok = __shfl_xor(bk, s, 64), oi = __shfl_xor(bi, s, 64);
-        if (ok > bk || (ok == bk && oi < bi)) {
-            bk = ok;
-            bi = oi;
-        }
-    }
-    if (lane == 0) {
-        red_key[wave] = bk;
-        red_idx[wave] = bi;
-    }
+    for (int s = 32; s >= 1; s >>= 1) best = kmin(best, shfl_xor64(best, s));
+    if (lane == 0) red[wave] = best;
     __syncthreads();
     if (a.mode == 1 && s_bad) {
         if (tid == 0) atomicCAS(&st->error, 0, 4);
@@ -155,16 +278,10 @@ __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
         if (tid == 0) atomicCAS(&st->error, 0, 3);
         return;
     }
+    int32_t selected;
     if (greedy) {
-        if (tid == 0) {
-            for (int w = 1; w < 16; ++w)
-                if (red_key[w] > bk || (red_key[w] == bk && red_idx[w] < bi)) {
-                    bk = red_key[w];
-                    bi = red_idx[w];
-                }
-            s_selected = bi;
-        }
-        __syncthreads();
+        for (int w = 0; w < 16; ++w) best = kmin(best, red[w]);
+        selected = (int32_t)(best & 0xffffffffu);
     } else {
         // 4. top-k threshold: the element of rank min(k-1, n-1) in
         //    descending total order, by radix select on the order keys.
@@ -206,7 +323,7 @@ __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
             const float v = sc[i];
             if (is_finite(v) && v >= threshold) {
                 const int at = atomicAdd(&s_count, 1);
-                if (at < kSurvivorMax) surv[at] = ((uint64_t)(~ukey(v)) << 32) | (uint32_t)i;
+                if (at < kSurvivorMax) surv[at] = order_key(v, i);
             }
         }
         __syncthreads();
@@ -215,81 +332,262 @@ __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
             if (tid == 0) atomicCAS(&st->error, 0, 5);
             return;
         }
-        int n2 = 2;
-        while (n2 < n) n2 <<= 1;
-        for (int i = n + tid; i < n2; i += 1024) surv[i] = ~0ull;
-        __syncthreads();
-        // 6. Sort by score descending, id ascending (:174).
-        bitonic_sort(surv, n2);
-        const float max = sc[(int32_t)(surv[0] & 0xffffffffu)];
-        for (int i = tid; i < n; i += 1024) e_val[i] = expf_cr(sc[(int32_t)(surv[i] & 0xffffffffu)] - max);
-        __syncthreads();
-        // 7. top-p (:175-190) and renormalisation (:191-197), sequential f32.
-        if (tid == 0) {
-            int kept = n;
-            if (a.top_p < 1.0f) {
-                float sum = -0.0f;
-                for (int i = 0; i < n; ++i) sum = sum + e_val[i];
-                float cumulative = 0.0f;
-                const int protect = a.legacy ? 3 : 1;
-                kept = 0;
-                for (int i = 0; i < n; ++i) {
-                    const float p = cast(e_val[i] / sum, a.legacy);
-                    cumulative += p;
-                    const float prior = cast(cast(cumulative, a.legacy) - p, a.legacy);
-                    if (prior <= a.top_p || i < protect) {
-                        surv[kept] = surv[i];
-                        e_val[kept] = e_val[i];
-                        ++kept;
-                    }
-                }
-            }
-            float sum = -0.0f;
-            for (int i = 0; i < kept; ++i) sum = sum + e_val[i];
-            for (int i = 0; i < kept; ++i) {
-                const float p = cast(e_val[i] / sum, a.legacy);
-                surv[i] = ((uint64_t)(surv[i] & 0xffffffffu) << 32) | f2u(p);
-            }
-            s_kept = kept;
-        }
-        __syncthreads();
-        const int kept = s_kept;
-        int k2 = 2;
-        while (k2 < kept) k2 <<= 1;
-        for (int i = kept + tid; i < k2; i += 1024) surv[i] = ~0ull;
-        __syncthreads();
-        // 8. Exponential race in id order (:198-214): uniforms at stream
-        //    positions 2 id and 2 id + 1 of this token's block.
-        bitonic_sort(surv, k2);
-        const uint32_t* stream = a.stream[step & 1];
-        for (int i = tid; i < kept; i += 1024) {
-            const uint32_t id = (uint32_t)(surv[i] >> 32);
-            const float p = u2f((uint32_t)(surv[i] & 0xffffffffu));
-            const uint64_t hi = stream[2 * (size_t)id], lo = stream[2 * (size_t)id + 1];
-            const double u = (double)(((hi << 32) | lo) & ((1ull << 53) - 1)) / 9007199254740992.0;
-            const float noise = cast((float)(-log1p_d(-u)), a.legacy);
-            e_val[i] = cast(p / noise, a.legacy);
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float best = -__builtin_huge_valf();
-            int32_t selected = 0;
-            for (int i = 0; i < kept; ++i) {
-                if (e_val[i] > best) {
-                    best = e_val[i];
-                    selected = (int32_t)(surv[i] >> 32);
-                }
-            }
-            s_selected = selected;
-        }
-        __syncthreads();
+        selected = race_tail(a, step, sc, surv, e_val, n, &s_kept, &s_sel);
     }
+    if (tid == 0) publish(a, step, selected);
+}
+
+// Chunked path, part 1: one workgroup of 256 threads per kChooseChunk
+// entries.  Writes the tempered scores (for the survivors' exponentials and
+// rescans), the chunk's {finite entries, invalid-logit flag} and its first
+// `list` order keys (greedy: list 1, the chunk's best entry).
+__global__ __launch_bounds__(256) void score_kernel(const SampleArgs a) {
+    constexpr int PER = kChooseChunk / 256;
+    __shared__ float vals[kChooseChunk];
+    __shared__ uint64_t keys[kChooseChunk];
+    __shared__ int32_t window_ids[kWindowMax];
+    __shared__ int32_t s_finite, s_bad;
+    __shared__ uint64_t s_best[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const StepState* st = a.st;
+    if (st->error || st->done) return;
+    const int V = a.vocab, step = st->step, c = blockIdx.x, lo = c * kChooseChunk;
     if (tid == 0) {
-        const int32_t id = s_selected;
-        for (int b = 0; b < a.rows; ++b) st->ids[b] = id;
-        a.token_log[step] = id;
-        if (a.phase != YUE2_PHASE_NONE && id == a.end_id) st->done = 1;
+        s_finite = 0;
+        s_bad = 0;
     }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int j = tid + 256 * e, i = lo + j;
+        vals[j] = i < V ? mixed_score(a, i, step) : -__builtin_huge_valf();
+    }
+    const int wn = load_window(a, step, window_ids);
+    if (a.mode == 1) apply_penalty(a, window_ids, wn, vals, lo, min(kChooseChunk, V - lo));
+    const bool greedy = a.mode == 0 || a.temperature == 0.0f;
+    int fin = 0, bad = 0;
+    uint64_t best = ~0ull;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int j = tid + 256 * e, i = lo + j;
+        float v = vals[j];
+        uint64_t key = ~0ull;
+        if (i < V) {
+            if (v != v || v == __builtin_huge_valf()) bad = 1;
+            if (!greedy) {
+                if (a.temperature != 1.0f) v = cast(v / a.temperature, a.legacy);
+                a.scores[i] = v;
+            }
+            if (is_finite(v)) {
+                ++fin;
+                key = order_key(v, i);
+            }
+        }
+        if (greedy) best = kmin(best, key);
+        else keys[j] = key;
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        fin += __shfl_xor(fin, s, 64);
+        bad |= __shfl_xor(bad, s, 64);
+        if (greedy) best = kmin(best, shfl_xor64(best, s));
+    }
+    if (lane == 0) {
+        atomicAdd(&s_finite, fin);
+        if (bad) atomicOr(&s_bad, 1);
+        s_best[wave] = best;
+    }
+    __syncthreads();
+    if (greedy) {
+        if (tid == 0) {
+            for (int w = 1; w < 4; ++w) best = kmin(best, s_best[w]);
+            a.cand[c] = kmin(best, s_best[0]);
+            a.meta[c] = make_int2(s_finite, s_bad);
+        }
+        return;
+    }
+    bitonic_sort(keys, kChooseChunk);
+    const int n = min(a.list, s_finite);
+    for (int j = tid; j < n; j += 256) a.cand[(size_t)c * a.list + j] = keys[j];
+    if (tid == 0) a.meta[c] = make_int2(s_finite, s_bad);
+}
+
+// Chunked path, part 2: one workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void finish_kernel(const SampleArgs a) {
+    constexpr int PER = kChooseCandMax / 1024;
+    __shared__ int32_t off[kChooseChunksMax + 1];
+    __shared__ int32_t rescan[kChooseChunksMax];
+    __shared__ uint64_t rescan_last[kChooseChunksMax];
+    __shared__ uint64_t surv[kSurvivorMax];
+    __shared__ float e_val[kSurvivorMax];
+    __shared__ uint32_t hist[256];
+    __shared__ int32_t wsum[16];
+    __shared__ uint64_t red[16];
+    __shared__ int32_t s_count, s_bad, s_n, s_nres, s_kept, s_sel, s_remaining;
+    __shared__ uint32_t s_prefix;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    StepState* st = a.st;
+    if (st->error || st->done) return;
+    const int V = a.vocab, step = st->step, nch = a.chunks, L = a.list;
+    if (tid == 0) {
+        s_count = 0;
+        s_bad = 0;
+        s_n = 0;
+        s_nres = 0;
+    }
+    // chunk totals, one chunk per thread, and the offsets of the lists
+    // concatenated in chunk order (off[nch] = their total length)
+    int fin = 0, bad = 0;
+    if (tid < nch) {
+        const int2 m = a.meta[tid];
+        fin = m.x;
+        bad = m.y;
+    }
+    const int nc = min(L, fin);
+    int incl = nc;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    if (fin) atomicAdd(&s_count, fin);
+    if (bad) atomicOr(&s_bad, 1);
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    if (tid <= nch) off[tid] = base + incl - nc;
+    __syncthreads();
+    if (a.mode == 1 && s_bad) {
+        if (tid == 0) atomicCAS(&st->error, 0, 4);
+        return;
+    }
+    const int count = s_count;
+    if (count == 0) {
+        if (tid == 0) atomicCAS(&st->error, 0, 3);
+        return;
+    }
+    if (a.mode == 0 || a.temperature == 0.0f) {
+        uint64_t best = fin > 0 ? a.cand[tid] : ~0ull;
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) best = kmin(best, shfl_xor64(best, s));
+        if (lane == 0) red[wave] = best;
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 0; w < 16; ++w) best = kmin(best, red[w]);
+            publish(a, step, (int32_t)(best & 0xffffffffu));
+        }
+        return;
+    }
+    // candidates: entry i of the concatenation lies in the last chunk whose
+    // offset is <= i
+    const int T = off[nch];
+    uint64_t mine[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int i = tid + 1024 * q;
+        mine[q] = ~0ull;
+        if (i < T) {
+            int lo = 0, hi = nch;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (off[mid] <= i) lo = mid;
+                else hi = mid;
+            }
+            mine[q] = a.cand[(size_t)lo * L + (i - off[lo])];
+        }
+    }
+    // top-k threshold: rank min(k-1, n-1) in descending order, by radix
+    // select over the candidates' score keys
+    if (tid == 0) {
+        s_prefix = 0;
+        s_remaining = min(a.top_k - 1, count - 1);
+    }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        const uint32_t prefix = s_prefix;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (tid + 1024 * q >= T) continue;
+            const uint32_t k = ~(uint32_t)(mine[q] >> 32);
+            if (shift == 24 || (k >> (shift + 8)) == (prefix >> (shift + 8)))
+                atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // lane l holds bins 255 - 4 l .. 252 - 4 l, in descending order
+            uint32_t h[4];
+            int t = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h[q] = hist[255 - 4 * lane - q];
+                t += (int)h[q];
+            }
+            int above = t;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int u = __shfl_up(above, d, 64);
+                if (lane >= d) above += u;
+            }
+            above -= t;  // entries in higher bins than this lane's
+            const int remaining = s_remaining;
+            if (remaining >= above && remaining < above + t) {
+                int cum = above;
+                for (int q = 0; q < 4; ++q) {
+                    if (cum + (int)h[q] > remaining) {
+                        s_prefix = prefix | ((uint32_t)(255 - 4 * lane - q) << shift);
+                        s_remaining = remaining - cum;
+                        break;
+                    }
+                    cum += (int)h[q];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    const float threshold = from_ukey(s_prefix);
+    // survivors (:173): listed entries >= threshold ...
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        if (tid + 1024 * q >= T) continue;
+        if (key_value(mine[q]) >= threshold) {
+            const int at = atomicAdd(&s_n, 1);
+            if (at < kSurvivorMax) surv[at] = mine[q];
+        }
+    }
+    // ... and, from chunks whose list was cut at an entry equal to the
+    // threshold, the entries after that one in order that equal it too
+    if (tid < nch && fin > L) {
+        const uint64_t last = a.cand[(size_t)tid * L + L - 1];
+        if (key_value(last) >= threshold) {
+            const int r = atomicAdd(&s_nres, 1);
+            rescan[r] = tid;
+            rescan_last[r] = last;
+        }
+    }
+    __syncthreads();
+    const int nres = s_nres;
+    for (int r = 0; r < nres; ++r) {
+        const int i = rescan[r] * kChooseChunk + tid;
+        if (i < V) {
+            const float v = a.scores[i];
+            if (is_finite(v) && v >= threshold) {
+                const uint64_t k = order_key(v, i);
+                if (k > rescan_last[r]) {
+                    const int at = atomicAdd(&s_n, 1);
+                    if (at < kSurvivorMax) surv[at] = k;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int n = s_n;
+    if (n > kSurvivorMax) {
+        if (tid == 0) atomicCAS(&st->error, 0, 5);
+        return;
+    }
+    const int32_t selected = race_tail(a, step, a.scores, surv, e_val, n, &s_kept, &s_sel);
+    if (tid == 0) publish(a, step, selected);
 }
 
 // MT19937 block generation (src/sampling.rs:15-55).  The twist of 624 words
@@ -355,7 +653,22 @@ __global__ __launch_bounds__(256) void mt_generate_kernel(MtState* mt, uint32_t*
     if (tid == 0) mt->next = next;
 }
 
-void launch_choose(hipStream_t s, const SampleArgs& a) { choose_kernel<<<1, 1024, 0, s>>>(a); }
+int choose_list_len(int vocab, int mode, float temperature, int top_k) {
+    const int chunks = (vocab + kChooseChunk - 1) / kChooseChunk;
+    if (chunks < 1 || chunks >= kChooseChunksMax) return 0;
+    const int list = (mode == 0 || temperature == 0.0f) ? 1 : std::min(top_k, kChooseChunk);
+    if (list < 1 || (size_t)chunks * list > (size_t)kChooseCandMax) return 0;
+    return list;
+}
+
+void launch_choose(hipStream_t s, const SampleArgs& a) {
+    if (a.cand) {
+        score_kernel<<<a.chunks, 256, 0, s>>>(a);
+        finish_kernel<<<1, 1024, 0, s>>>(a);
+    } else {
+        choose_kernel<<<1, 1024, 0, s>>>(a);
+    }
+}
 
 void launch_mt_generate(hipStream_t s, MtState* mt, uint32_t* out0, uint32_t* out1, size_t count,
                         const StepState* st, int ahead) {

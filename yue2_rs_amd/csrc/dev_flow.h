@@ -90,12 +90,34 @@ __device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float*
     return s_fail == 0;
 }
 
+// Division by a run-time d >= 1 of numerators i < 2^32 / d: floor(i / d) =
+// umulhi(i, ceil(2^32 / d)) (the rounding error of the multiplier stays
+// below 1/d), d = 1 passed through.  The division itself would be ~40
+// instructions at every use.
+struct FastDiv {
+    uint32_t d, m;
+    __device__ __forceinline__ explicit FastDiv(int dd) : d((uint32_t)dd), m(0xFFFFFFFFu / (uint32_t)dd + 1u) {}
+    __device__ __forceinline__ int div(int i) const { return d == 1 ? i : (int)__umulhi((uint32_t)i, m); }
+    __device__ __forceinline__ int mod(int i) const { return i - div(i) * (int)d; }
+};
+
+// The contiguous words src[0, n).
+template <int NT, int MAXPER>
+__device__ __forceinline__ bool gather_flat(const uint64_t* src, int n, uint32_t tag, float* dst, StepState* st) {
+    return gather_at<NT, MAXPER>([=](int i) { return src + i; }, n, tag, dst, st);
+}
+
 // The 2-D region src[r * stride + c], r < n / cols, c < cols, row-major.
 template <int NT, int MAXPER>
 __device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, size_t stride, uint32_t tag,
                                        float* dst, StepState* st) {
-    return gather_at<NT, MAXPER>([=](int i) { return src + (size_t)(i / cols) * stride + i % cols; }, n, tag, dst,
-                                 st);
+    const FastDiv fc(cols);
+    return gather_at<NT, MAXPER>(
+        [=](int i) {
+            const int r = fc.div(i);
+            return src + (size_t)r * stride + (i - r * cols);
+        },
+        n, tag, dst, st);
 }
 
 // Arguments of one layer's attention in the step kernel.
@@ -204,11 +226,11 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         c_cos = gbl(a.cos_t + (size_t)pos * HALF)[d];
         c_sin = gbl(a.sin_t + (size_t)pos * HALF)[d];
     }
-    if (!gather<NT, (MAXG * D + NT - 1) / NT>(row + (size_t)(g * G) * D, G * D, G * D, 0, t_qkv, &q_s[0][0], st))
+    if (!gather_flat<NT, (MAXG * D + NT - 1) / NT>(row + (size_t)(g * G) * D, G * D, t_qkv, &q_s[0][0], st))
         return false;
     if (owns_new) {
-        if (!gather<NT, 1>(row + (size_t)(a.heads + g) * D, D, D, 0, t_qkv, k_s, st)) return false;
-        if (!gather<NT, 1>(row + (size_t)(a.heads + a.kv_heads + g) * D, D, D, 0, t_qkv, v_s, st)) return false;
+        if (!gather_flat<NT, 1>(row + (size_t)(a.heads + g) * D, D, t_qkv, k_s, st)) return false;
+        if (!gather_flat<NT, 1>(row + (size_t)(a.heads + a.kv_heads + g) * D, D, t_qkv, v_s, st)) return false;
     }
     mark();
     // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
@@ -411,10 +433,10 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         float* m_buf = lds;  // [no][nb]: partial of block k for output o0 + i
         const uint64_t* part = a.part + hbase * D;
         const size_t hstride = (size_t)a.blk_stride * D;
-        const int nbm = nb;
+        const FastDiv fnb(nb);
         if (!gather_at<NT, kMergePer>(
                 [=](int i) {
-                    const int o = o0 + i / nbm, k = i % nbm;
+                    const int r = fnb.div(i), o = o0 + r, k = i - r * (int)fnb.d;
                     return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
                 },
                 no * nb, t_part, m_buf, st))

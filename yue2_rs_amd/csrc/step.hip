@@ -41,19 +41,25 @@ namespace y2 {
 constexpr int kStepThreads = 512;
 constexpr int kStepWaves = kStepThreads / 64;
 
-// Optional trace: thread 0 of each workgroup stamps the device wall clock
-// (100 MHz) into trace[slot * gridDim.x + workgroup]; slots past the buffer
-// are dropped.
+// Trace of the traced instantiation: thread 0 of each workgroup stamps the
+// device wall clock (100 MHz) into trace[slot * gridDim.x + workgroup];
+// slots past the buffer are dropped.  The untraced kernel has no code for it.
+template <bool ON>
 struct Tracer {
     unsigned long long* buf;
     int slots, slot;
     __device__ __forceinline__ void mark() {
-        if (buf && threadIdx.x == 0 && slot < slots) gblw(buf)[(size_t)slot * gridDim.x + blockIdx.x] = wall_clock64();
-        ++slot;
+        if constexpr (ON) {
+            if (threadIdx.x == 0 && slot < slots) gblw(buf)[(size_t)slot * gridDim.x + blockIdx.x] = wall_clock64();
+            ++slot;
+        }
     }
 };
 
-__device__ __forceinline__ int part_lo(int n, int w, int parts) { return (int)(((long)n * w) / parts); }
+// First row of part w of n rows split over `parts` (n * parts < 2^32).
+__device__ __forceinline__ int part_lo(int n, int w, int parts) {
+    return (int)((uint32_t)n * (uint32_t)w / (uint32_t)parts);
+}
 
 // ---- GEMV through a register ring ------------------------------------------
 
@@ -91,7 +97,9 @@ __device__ __forceinline__ void item_at(int q, int Q, int r0, int n, int* row, i
     *seg = qq % NSEG;
 }
 
-template <int SEG, bool PAIR>
+// MASK: k may be short of 64 * 8 * IT (the lane's chunks past the row end
+// are read at chunk 0 and masked); without it k is exactly that.
+template <int SEG, bool PAIR, bool MASK>
 __device__ __forceinline__ void load_item(const uint16_t* w, const uint16_t* w2, int k, int row, int seg,
                                           uint4* buf) {
     const int lane = threadIdx.x & 63, nchunk = k >> 3;
@@ -99,28 +107,28 @@ __device__ __forceinline__ void load_item(const uint16_t* w, const uint16_t* w2,
 #pragma unroll
     for (int it = 0; it < SEG; ++it) {
         const int c = lane + 64 * (seg * SEG + it);
-        buf[it] = ldg4(a + (c < nchunk ? c : 0));
+        buf[it] = ldg4(a + (!MASK || c < nchunk ? c : 0));
     }
     if constexpr (PAIR) {
         const uint4* b = reinterpret_cast<const uint4*>(w2 + (size_t)row * k);
 #pragma unroll
         for (int it = 0; it < SEG; ++it) {
             const int c = lane + 64 * (seg * SEG + it);
-            buf[SEG + it] = ldg4(b + (c < nchunk ? c : 0));
+            buf[SEG + it] = ldg4(b + (!MASK || c < nchunk ? c : 0));
         }
     }
 }
 
 // Continue the DOT chains of batch rows b < B over one item (chunks of the
 // lane past the row end contribute fma(0, 0, acc) = acc).
-template <int B, int SEG, bool PAIR>
+template <int B, int SEG, bool PAIR, bool MASK>
 __device__ __forceinline__ void dot_item(const float* xs, int k, int seg, const uint4* wv, float* acc,
                                          float* acc2) {
     const int lane = threadIdx.x & 63, nchunk = k >> 3;
 #pragma unroll
     for (int it = 0; it < SEG; ++it) {
         const int c = lane + 64 * (seg * SEG + it);
-        const bool ok = c < nchunk;
+        const bool ok = !MASK || c < nchunk;
         const int cc = ok ? c : 0;
         float wf[8], wf2[8];
         unpack_bf16x8(wv[it], wf);
@@ -176,7 +184,7 @@ __device__ __forceinline__ void store_out(float* y, uint64_t* ty, size_t i, uint
 }
 
 // Issue the first R-1 items of this wave's rows [r0, r1) into ring slots.
-template <int IT, bool PAIR>
+template <int IT, bool PAIR, bool MASK = false>
 __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t* w2, int k, int r0, int r1,
                                               int n, uint4* ring) {
     using C = Ring<IT, PAIR>;
@@ -186,7 +194,7 @@ __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t*
     for (int s = 0; s < C::R - 1; ++s) {
         int row, seg;
         item_at<C::NSEG>(s, Q, r0, n, &row, &seg);
-        load_item<C::SEG, PAIR>(w, w2, k, row, seg, ring + s * C::W);
+        load_item<C::SEG, PAIR, MASK>(w, w2, k, row, seg, ring + s * C::W);
     }
 }
 
@@ -196,7 +204,7 @@ __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t*
 // EPI_RESID, res[b * (r1 - r0) + (row - r0)] = the row's current value (LDS).
 // (Writing the new value back to res here instead of re-reading it later
 // measured slower: the GEMVs of the whole kernel lost about half their rate.)
-template <int B, int EPI, int IT>
+template <int B, int EPI, int IT, bool MASK = false>
 __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
                                           float* y, uint64_t* ty, uint32_t tag, int y_stride, int r0, int r1,
                                           int n, uint4* ring, const float* res = nullptr) {
@@ -216,10 +224,10 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
                 // refill the slot of item q - 1 with item q + R - 1
                 int row, seg;
                 item_at<C::NSEG>(q + C::R - 1, Q, r0, n, &row, &seg);
-                load_item<C::SEG, PAIR>(w, w2, k, row, seg, ring + ((s + C::R - 1) % C::R) * C::W);
+                load_item<C::SEG, PAIR, MASK>(w, w2, k, row, seg, ring + ((s + C::R - 1) % C::R) * C::W);
             }
             const int seg = q % C::NSEG;
-            dot_item<B, C::SEG, PAIR>(xs, k, seg, ring + s * C::W, acc, acc2);
+            dot_item<B, C::SEG, PAIR, MASK>(xs, k, seg, ring + s * C::W, acc, acc2);
             if (seg == C::NSEG - 1) {
                 const int row = r0 + wave + kStepWaves * (q / C::NSEG);
 #pragma unroll
@@ -243,12 +251,12 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
 template <int B, int N>
 __device__ __forceinline__ bool stage(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
     if constexpr (B * N <= 16) {
-        return gather<kStepThreads, B * N>(tx, B * k, B * k, 0, tag, xs, st);
+        return gather_flat<kStepThreads, B * N>(tx, B * k, tag, xs, st);
     } else {
         // one row at a time: 16 words in flight per thread at most
 #pragma unroll
         for (int b = 0; b < B; ++b)
-            if (!gather<kStepThreads, N>(tx + (size_t)b * k, k, k, 0, tag, xs + b * k, st)) return false;
+            if (!gather_flat<kStepThreads, N>(tx + (size_t)b * k, k, tag, xs + b * k, st)) return false;
         return true;
     }
 }
@@ -259,18 +267,17 @@ template <int B>
 __device__ __forceinline__ bool stage_res(float* res, const uint64_t* tx, int stride, int r0, int r1, uint32_t tag,
                                           StepState* st) {
     const int n = r1 - r0;
-    return gather_at<kStepThreads, 1>([=](int i) { return tx + (size_t)(i / n) * stride + r0 + i % n; }, B * n,
-                                      tag, res, st);
+    return gather<kStepThreads, 1>(tx + r0, B * n, n, stride, tag, res, st);
 }
 
-// gam[j] = g[tid + 512 j] (0 past k): a norm's gammas, loaded ahead.
+// gam[j] = g[tid + 512 j] for tid + 512 j < k: a norm's gammas, loaded
+// ahead.  The loads are unconditional (entries past k re-read g[k - 1] and
+// are never used): a conditional load would make the compiler wait for it,
+// and so for everything issued before it, where the branches join.
 template <int N>
 __device__ __forceinline__ void load_gamma(const float* g, int k, float* gam) {
 #pragma unroll
-    for (int j = 0; j < N; ++j) {
-        const int i = threadIdx.x + j * kStepThreads;
-        gam[j] = i < k ? gbl(g)[i] : 0.0f;
-    }
+    for (int j = 0; j < N; ++j) gam[j] = gbl(g)[min((int)threadIdx.x + j * kStepThreads, k - 1)];
 }
 
 // xs[b] = RMSNorm(xs[b]) (Norm::apply, src/tensor.rs:1140-1157) with the
@@ -293,6 +300,13 @@ __device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, fl
 // ---- the kernel ------------------------------------------------------------
 
 typedef const __attribute__((address_space(4))) StepArgs* ArgsPtr;
+typedef const __attribute__((address_space(4))) LayerDev* LayerPtr;
+
+// Layer l's weight and norm pointers through the constant address space:
+// scalar loads, which wait on nothing but themselves.  (A generic pointer
+// would be read with a vector load, and on this architecture the wait for a
+// vector load also waits for every store and load issued before it.)
+__device__ __forceinline__ LayerPtr layer_at(ArgsPtr a, int l) { return (LayerPtr)a->layers + l; }
 
 // The arguments through a pointer the compiler cannot follow from one phase
 // to the next: fields are re-read (scalar loads) in the phase that uses them
@@ -320,8 +334,8 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
     f.wpg = wpg;
     f.scale = a->scale;
     f.eps = a->eps;
-    f.q_norm = a->layers[l].q_norm;
-    f.k_norm = a->layers[l].k_norm;
+    f.q_norm = layer_at(a, l)->q_norm;
+    f.k_norm = layer_at(a, l)->k_norm;
     f.cos_t = a->rope_cos;
     f.sin_t = a->rope_sin;
     f.bmax = a->tbmax;
@@ -333,7 +347,9 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
     return f;
 }
 
-template <int B, int D, int ITH, int ITQ, int ITI>
+// MASKI: the intermediate size is short of 512 * ITI (the down projection's
+// rows are masked); TRACE: the traced instantiation.
+template <int B, int D, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
     extern __shared__ float lds[];
     __shared__ float res_s[B * kResRows];  // this workgroup's rows of x (residual)
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
     uint4 ring[RMAX];
     float gam[ITH];
-    Tracer tr{call.trace, call.trace_slots, 0};
+    Tracer<TRACE> tr{call.trace, call.trace_slots, 0};
     tr.mark();
 
     // Embedding (src/model.rs:452-464): this workgroup's rows of x as tagged
@@ -364,8 +380,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 return;
             }
         }
-        load_gamma<ITH>(a->layers[0].in_norm, H, gam);
-        prefetch_ring<ITH, false>(a->layers[0].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
+        load_gamma<ITH>(layer_at(a, 0)->in_norm, H, gam);
+        prefetch_ring<ITH, false>(layer_at(a, 0)->wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
                                   part_lo(qkvw, wg + 1, nwg), qkvw, ring);
         const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
         const uint32_t t_emb = flow_tag(epoch, 0, FK_EMB);
@@ -385,9 +401,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
             if (l > 0) {
                 // this layer's gammas and first weights go out before the wait
-                load_gamma<ITH>(a->layers[l].in_norm, H, gam);
-                prefetch_ring<ITH, false>(a->layers[l].wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
-                                          part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+                load_gamma<ITH>(layer_at(a, l)->in_norm, H, gam);
+                prefetch_ring<ITH, false>(layer_at(a, l)->wqkv, nullptr, H, part_lo(qkvw, wg, nwg), part_lo(qkvw, wg + 1, nwg), qkvw, ring);
                 a = fresh(args);
                 if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
             }
@@ -395,9 +410,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH>(a->layers[l].wqkv, nullptr, lds, H, nullptr, a->tqkv,
-                                         flow_tag(epoch, l, FK_QKV), qkvw, part_lo(qkvw, wg, nwg),
-                                         part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+            gemv_ring<B, EPI_STORE, ITH>(layer_at(a, l)->wqkv, nullptr, lds, H, nullptr, a->tqkv,
+                                         flow_tag(epoch, l, FK_QKV), qkvw, part_lo(qkvw, wg, nwg), part_lo(qkvw, wg + 1, nwg), qkvw, ring);
             tr.mark();
         }
         // ---- QK-norm + RoPE + KV append + attention ----
@@ -415,7 +429,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qw = a->heads * D;
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
-            prefetch_ring<ITQ, false>(a->layers[l].wo, nullptr, qw, h0, h1, H, ring);
+            prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l > 0 ? l - 1 : 0, l > 0 ? FK_XD : FK_EMB),
                               st))
@@ -424,7 +438,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             if (!stage<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITQ>(a->layers[l].wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
+            gemv_ring<B, EPI_RESID, ITQ>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
         }
@@ -432,16 +446,15 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
-            load_gamma<ITH>(a->layers[l].post_norm, H, gam);
-            prefetch_ring<ITH, true>(a->layers[l].wg, a->layers[l].wu, H, part_lo(I, wg, nwg),
-                                     part_lo(I, wg + 1, nwg), I, ring);
+            load_gamma<ITH>(layer_at(a, l)->post_norm, H, gam);
+            prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg), I, ring);
             a = fresh(args);
             if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
             a = fresh(args);
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_SWIGLU, ITH>(a->layers[l].wg, a->layers[l].wu, lds, H, nullptr, a->tact,
+            gemv_ring<B, EPI_SWIGLU, ITH>(layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact,
                                           flow_tag(epoch, l, FK_ACT), I, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg),
                                           I, ring);
             tr.mark();
@@ -451,14 +464,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
-            prefetch_ring<ITI, false>(a->layers[l].wd, nullptr, I, h0, h1, H, ring);
+            prefetch_ring<ITI, false, MASKI>(layer_at(a, l)->wd, nullptr, I, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l, FK_XO), st)) return;
             a = fresh(args);
             if (!stage<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITI>(a->layers[l].wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
+            gemv_ring<B, EPI_RESID, ITI, MASKI>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
         }
@@ -483,9 +496,12 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     if (wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
 }
 
-template <int B, int D, int ITH, int ITQ, int ITI>
+template <int B, int D, int ITH, int ITQ, int ITI, bool MASKI>
 static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCall& call, int nwg, size_t lds) {
-    step_kernel<B, D, ITH, ITQ, ITI><<<nwg, kStepThreads, lds, s>>>(dev, call);
+    if (call.trace)
+        step_kernel<B, D, ITH, ITQ, ITI, MASKI, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
+    else
+        step_kernel<B, D, ITH, ITQ, ITI, MASKI, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
     return hipGetLastError();
 }
 
@@ -494,8 +510,11 @@ static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCa
 bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const int ith = (c.hidden_size / 8 + 63) / 64, itq = (c.num_attention_heads * c.head_dim / 8 + 63) / 64;
     const int iti = (c.intermediate_size / 8 + 63) / 64;
-    const bool shape = (c.head_dim == 128 && ith == 6 && itq == 6 && iti == 16) ||
-                       (c.head_dim == 64 && ith == 2 && itq == 2 && iti == 6);
+    // hidden and heads * head_dim exactly 512 * IT (their GEMVs are unmasked)
+    const bool exact = c.hidden_size == 512 * ith && c.num_attention_heads * c.head_dim == 512 * itq;
+    // (the head_dim-128 kernel also takes the intermediate size as exactly 512 * 16)
+    const bool shape = exact && ((c.head_dim == 128 && ith == 6 && itq == 6 && c.intermediate_size == 512 * 16) ||
+                                 (c.head_dim == 64 && ith == 2 && itq == 2 && iti == 6));
     if (!shape || rows < 1 || rows > 2 || nwg % (c.num_key_value_heads * rows) != 0) return false;
     const int G = c.num_attention_heads / c.num_key_value_heads;
     const int wpg = nwg / (c.num_key_value_heads * rows);
@@ -518,13 +537,13 @@ hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, co
     const size_t lds = step_lds_bytes(a, nwg);
     if (lds > kStepLdsMax) return hipErrorInvalidValue;
     const int ith = (a.hidden / 8 + 63) / 64;
-    if (a.head_dim == 128 && ith == 6) {
-        if (a.rows == 1) return launch_step_t<1, 128, 6, 6, 16>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 128, 6, 6, 16>(s, dev, call, nwg, lds);
+    if (a.head_dim == 128 && ith == 6 && a.intermediate == 512 * 16) {
+        if (a.rows == 1) return launch_step_t<1, 128, 6, 6, 16, false>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 128, 6, 6, 16, false>(s, dev, call, nwg, lds);
     }
     if (a.head_dim == 64 && ith == 2) {
-        if (a.rows == 1) return launch_step_t<1, 64, 2, 2, 6>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 64, 2, 2, 6>(s, dev, call, nwg, lds);
+        if (a.rows == 1) return launch_step_t<1, 64, 2, 2, 6, true>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 64, 2, 2, 6, true>(s, dev, call, nwg, lds);
     }
     return hipErrorInvalidValue;
 }

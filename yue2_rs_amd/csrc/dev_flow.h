@@ -37,6 +37,8 @@ constexpr int kDevErrFlow = 8;
 // merges ceil(G*D/W) outputs over nb <= W * bpw blocks, at most
 // G*D*bpw + nb <= 512 * 24 + 384 words for G*D <= 512 and bpw <= 24.
 constexpr int kMergePer = 26;
+// Words per thread in one gather pass of the merge.
+constexpr int kMergeBatch = 8;
 
 __device__ __forceinline__ uint32_t flow_tag(uint32_t epoch, int layer, int kind) {
     return (epoch << 12) | ((uint32_t)layer << 4) | (uint32_t)kind;
@@ -434,13 +436,18 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         const uint64_t* part = a.part + hbase * D;
         const size_t hstride = (size_t)a.blk_stride * D;
         const FastDiv fnb(nb);
-        if (!gather_at<NT, kMergePer>(
-                [=](int i) {
-                    const int r = fnb.div(i), o = o0 + r, k = i - r * (int)fnb.d;
-                    return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
-                },
-                no * nb, t_part, m_buf, st))
-            return false;
+        // in passes of at most kMergeBatch words per thread: one pass at
+        // short contexts, and the unrolled poll stays small
+        for (int p0 = 0; p0 < no * nb; p0 += NT * kMergeBatch) {
+            if (!gather_at<NT, kMergeBatch>(
+                    [=](int i) {
+                        i += p0;
+                        const int r = fnb.div(i), o = o0 + r, k = i - r * (int)fnb.d;
+                        return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
+                    },
+                    min(no * nb - p0, NT * kMergeBatch), t_part, m_buf + p0, st))
+                return false;
+        }
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
         for (int i = tid; i < no; i += NT) {
             const float* pp = m_buf + i * nb;

@@ -22,9 +22,16 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4 w, float* f) {
     f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
 }
 
+// v summed over the wave by the xor butterfly 32, 16, ..., 1.  Steps below
+// 32 stay inside 32-lane halves, where ds_swizzle's bit mode (and 0x1f,
+// xor m) is the exchange without an address computation.
 __device__ __forceinline__ float wave_sum_xor(float v) {
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
+    v = v + __shfl_xor(v, 32, 64);
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (16 << 10)));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (8 << 10)));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (4 << 10)));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (2 << 10)));
+    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (1 << 10)));
     return v;
 }
 
@@ -158,8 +165,13 @@ __device__ __forceinline__ float norm_scale_block(const float* xs, int n, float 
         if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
         if (lo_f < 0.0f) lo_f = 0.0f;
         if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
-        const float s_a = norm_scale_from_sum(lo_f, n, eps);
-        const float s_b = norm_scale_from_sum(hi_f, n, eps);
+        float s_a = 0.0f, s_b = 0.0f;
+#pragma unroll 1
+        for (int t = 0; t < 2; ++t) {  // one copy of the scale arithmetic
+            const float v = norm_scale_from_sum(t ? hi_f : lo_f, n, eps);
+            if (t) s_b = v;
+            else s_a = v;
+        }
         if (hi_f <= 3.0e38f && s_a == s_b) return s_a;
     }
     if (tid == 0) {

@@ -284,8 +284,8 @@ __device__ __forceinline__ void load_gamma(const float* g, int k, float* gam) {
 // gammas of load_gamma.
 template <int B, int N>
 __device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, float eps, int* fallbacks) {
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
+#pragma unroll 1
+    for (int b = 0; b < B; ++b) {  // one copy of the code for both rows
         float* xb = xs + b * k;
         const float s = norm_scale_block<kStepThreads>(xb, k, eps, fallbacks);
 #pragma unroll

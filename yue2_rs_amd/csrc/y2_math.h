@@ -20,10 +20,13 @@ Y2_HD double u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
 
 // round_bf16 of src/tensor.rs:645-652: round to nearest even at bit 16,
 // NaN becomes a quiet NaN with the payload's top bits.
+// Both results are formed and one selected: no branch (this is inlined at
+// every rounding of the decode step).
 Y2_HD float rb(float v) {
-    uint32_t b = f2u(v);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return u2f((b & 0xffff0000u) | 0x00400000u);
-    return u2f((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
+    const uint32_t b = f2u(v);
+    const uint32_t nan = (b & 0xffff0000u) | 0x00400000u;
+    const uint32_t rne = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+    return u2f((b & 0x7fffffffu) > 0x7f800000u ? nan : rne);
 }
 // BF16 bits of a value that is already BF16-exact.
 Y2_HD uint16_t bf16_bits(float v) { return (uint16_t)(f2u(v) >> 16); }

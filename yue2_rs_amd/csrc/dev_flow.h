@@ -167,8 +167,9 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     constexpr int BLK_U4 = kBlockKeys * D / 8;           // uint4 per staged block
     constexpr int PER = (kAttnChunk * BLK_U4 + NT - 1) / NT;  // uint4 per thread per chunk
     constexpr int HALF = D / 2;
-    __shared__ float q_s[MAXG][D];
-    __shared__ float k_s[D], v_s[D];
+    // the group's queries, then (owner of the new key) its key and value rows
+    __shared__ float qkv_s[(MAXG + 2) * D];
+    float(*q_s)[D] = reinterpret_cast<float(*)[D]>(qkv_s);
     __shared__ float hscale[MAXG + 1];
     __shared__ float m_s[MAXG], t_s[MAXG];
     __shared__ float red_s[MAXG * MAXNB];
@@ -192,6 +193,8 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
     const bool owns_new = j1 == L;
     const uint32_t t_qkv = flow_tag(a.epoch, a.layer, FK_QKV);
+    float* k_s = qkv_s + G * D;
+    float* v_s = k_s + D;
     uint4* Ks = reinterpret_cast<uint4*>(lds);  // [kAttnChunk * 64][D / 8]
     uint4* Vs = Ks + kAttnChunk * BLK_U4;
     float* e_s = reinterpret_cast<float*>(Vs + kAttnChunk * BLK_U4);
@@ -228,11 +231,16 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         c_cos = gbl(a.cos_t + (size_t)pos * HALF)[d];
         c_sin = gbl(a.sin_t + (size_t)pos * HALF)[d];
     }
-    if (!gather_flat<NT, (MAXG * D + NT - 1) / NT>(row + (size_t)(g * G) * D, G * D, t_qkv, &q_s[0][0], st))
-        return false;
-    if (owns_new) {
-        if (!gather_flat<NT, 1>(row + (size_t)(a.heads + g) * D, D, t_qkv, k_s, st)) return false;
-        if (!gather_flat<NT, 1>(row + (size_t)(a.heads + a.kv_heads + g) * D, D, t_qkv, v_s, st)) return false;
+    {
+        // one gather for all three: a single wait
+        const int nq = G * D;
+        const uint64_t* qsrc = row + (size_t)(g * G) * D;
+        const uint64_t* ksrc = row + (size_t)(a.heads + g) * D;
+        const uint64_t* vsrc = row + (size_t)(a.heads + a.kv_heads + g) * D;
+        if (!gather_at<NT, ((MAXG + 2) * D + NT - 1) / NT>(
+                [=](int i) { return i < nq ? qsrc + i : (i < nq + D ? ksrc + (i - nq) : vsrc + (i - nq - D)); },
+                nq + (owns_new ? 2 * D : 0), t_qkv, qkv_s, st))
+            return false;
     }
     mark();
     // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).

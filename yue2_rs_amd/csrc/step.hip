@@ -230,15 +230,21 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
             dot_item<B, C::SEG, PAIR, MASK>(xs, k, seg, ring + s * C::W, acc, acc2);
             if (seg == C::NSEG - 1) {
                 const int row = r0 + wave + kStepWaves * (q / C::NSEG);
+                float v[B], v2[B];
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
-                    const float v = wave_sum_xor(acc[b]);
-                    const float v2 = PAIR ? wave_sum_xor(acc2[b]) : 0.0f;
-                    if (lane == 0) {
-                        const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
-                        store_out<EPI>(y, ty, (size_t)b * y_stride + row, tag, v, v2, rv);
-                    }
+                    v[b] = wave_sum_xor(acc[b]);
+                    v2[b] = PAIR ? wave_sum_xor(acc2[b]) : 0.0f;
                     acc[b] = acc2[b] = 0.0f;
+                }
+                if (lane == 0) {
+                    // one copy of the epilogue for the batch rows
+#pragma unroll 1
+                    for (int b = 0; b < B; ++b) {
+                        const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
+                        store_out<EPI>(y, ty, (size_t)b * y_stride + row, tag, b == 0 ? v[0] : v[B - 1],
+                                       b == 0 ? v2[0] : v2[B - 1], rv);
+                    }
                 }
             }
         }

@@ -248,7 +248,8 @@ int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t ite
 
 /* Diagnostics: one decode step of token `id` at the cache's next position
  * through the persistent token-step kernel (appends to the cache like
- * yue2_hip_forward, computes no logits), recording the device wall clock
+ * yue2_hip_forward, computes no logits; with `c2` non-NULL, a batch-2 step
+ * of the same id over both caches), recording the device wall clock
  * (100 MHz) per workgroup: stamps[s * wgs + w] for slot s = 0 at the start,
  * then per layer 15 slots -- QKV start, QKV end, attention: queries gathered,
  * new key appended, block maxima stored, maxima gathered, sums gathered,
@@ -256,8 +257,8 @@ int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t ite
  * end, down start, down end.  cap = entries available in stamps; *wgs and
  * *slots receive the trace shape.  YUE2_ERR_ARG when the shape has no step
  * kernel or cap is too small. */
-int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, int32_t id, uint64_t *stamps, int32_t cap,
-                            int32_t *wgs, int32_t *slots);
+int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, Yue2Cache *c2, int32_t id, uint64_t *stamps,
+                            int32_t cap, int32_t *wgs, int32_t *slots);
 
 #ifdef __cplusplus
 }

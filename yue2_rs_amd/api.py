@@ -114,7 +114,7 @@ def lib() -> C.CDLL:
         "yue2_hip_selftest_math": (i32, [i32, vp, vp, sz]),
         "yue2_hip_norm_fallbacks": (i32, [vp]),
         "yue2_hip_decoder_time_kernel": (i32, [vp, i32, i32, vp, vp]),
-        "yue2_hip_trace_step": (i32, [vp, vp, i32, vp, i32, vp, vp]),
+        "yue2_hip_trace_step": (i32, [vp, vp, vp, i32, vp, i32, vp, vp]),
         "yue2_hip_model_set_step_kernel": (i32, [vp, i32]),
     }
     for name, (res, args) in sig.items():
@@ -272,15 +272,16 @@ class Model:
     def norm_fallbacks(self) -> int:
         return int(lib().yue2_hip_norm_fallbacks(self._h))
 
-    def trace_step(self, token: int, cache: "Cache") -> np.ndarray:
+    def trace_step(self, token: int, cache: "Cache", cache2: Optional["Cache"] = None) -> np.ndarray:
         """One decode step through the persistent step kernel with phase
         stamps: uint64 array [slot, workgroup] of the device wall clock
-        (100 MHz); slot 0 = start, then 15 per layer (see yue2_hip.h)."""
+        (100 MHz); slot 0 = start, then 15 per layer (see yue2_hip.h).
+        cache2: a batch-2 step over both caches."""
         cap = (1 + 15 * self.config.num_hidden_layers) * 1024
         out = np.zeros(cap, dtype=np.uint64)
         wgs, slots = C.c_int32(0), C.c_int32(0)
-        _check(lib().yue2_hip_trace_step(self._h, cache._h, int(token), _ptr(out), cap,
-                                         C.byref(wgs), C.byref(slots)))
+        _check(lib().yue2_hip_trace_step(self._h, cache._h, None if cache2 is None else cache2._h, int(token),
+                                         _ptr(out), cap, C.byref(wgs), C.byref(slots)))
         return out[: slots.value * wgs.value].reshape(slots.value, wgs.value)
 
 

@@ -594,38 +594,49 @@ extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* i
     return YUE2_OK;
 }
 
-extern "C" int32_t yue2_hip_trace_step(Yue2Model* m, Yue2Cache* c, int32_t id, uint64_t* stamps,
+extern "C" int32_t yue2_hip_trace_step(Yue2Model* m, Yue2Cache* c, Yue2Cache* c2, int32_t id, uint64_t* stamps,
                                        int32_t cap, int32_t* wgs, int32_t* slots) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
-    if (!m || !c || !stamps || !wgs || !slots || c->m != m)
+    if (!m || !c || !stamps || !wgs || !slots || c->m != m || (c2 && (c2->m != m || c2 == c)))
         return fail(YUE2_ERR_ARG, "null model, cache or output");
-    if (!step_supported(m->c, 1, m->cus)) return fail(YUE2_ERR_ARG, "no step kernel for this shape");
-    if (c->length + 1 > c->capacity || c->length + 1 > m->c.max_position_embeddings)
-        return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    const int rows = c2 ? 2 : 1;
+    Yue2Cache* cs[2] = {c, c2};
+    if (!step_supported(m->c, rows, m->cus)) return fail(YUE2_ERR_ARG, "no step kernel for this shape");
+    int cap_max = 0;
+    for (int b = 0; b < rows; ++b) {
+        if (cs[b]->length + 1 > cs[b]->capacity || cs[b]->length + 1 > m->c.max_position_embeddings)
+            return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+        cap_max = std::max(cap_max, cs[b]->capacity);
+    }
     if (id < 0 || id >= m->c.vocab_size) return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
     const int nb = 1 + kTraceSlotsPerLayer * m->c.num_hidden_layers;
     const size_t n = (size_t)nb * m->cus;
     if ((size_t)cap < n) return fail(YUE2_ERR_ARG, "stamp buffer too small");
-    const int blocks = (c->capacity + kBlockKeys - 1) / kBlockKeys;
-    if (int rc = m->ws.ensure(1, blocks, m->c)) return rc;
-    if (int rc = prepare_step(m, m->ws)) return rc < 0 ? rc : fail(YUE2_ERR_ARG, "no step kernel for this shape");
+    // a workspace of its own for batch 2 (the model's serves batch-1 forwards)
+    Workspace w2;
+    Workspace& w = rows == 1 ? m->ws : w2;
+    const int blocks = (cap_max + kBlockKeys - 1) / kBlockKeys;
+    if (int rc = w.ensure(rows, blocks, m->c)) return rc;
+    if (int rc = prepare_step(m, w)) return rc < 0 ? rc : fail(YUE2_ERR_ARG, "no step kernel for this shape");
     unsigned long long* dev = nullptr;
     if (hipMalloc(&dev, n * sizeof(*dev)) != hipSuccess) return fail(YUE2_ERR_ALLOC, "trace buffer");
     KvView kv{};
-    kv.base[0] = c->kv;
-    kv.capacity[0] = c->capacity;
+    for (int b = 0; b < rows; ++b) {
+        kv.base[b] = cs[b]->kv;
+        kv.capacity[b] = cs[b]->capacity;
+    }
     hipStream_t s = m->stream;
-    m->ws.reset(s);
-    launch_set_state(s, m->ws.st, 1, c->length, 0, id, 0);
-    int rc = enqueue_step_fused(m, m->ws, kv, 1, false, YUE2_PHASE_NONE, s, dev, nb);
-    if (rc == 0) rc = read_step_error(m->ws, s);
+    w.reset(s);
+    launch_set_state(s, w.st, rows, c->length, rows > 1 ? c2->length : 0, id, rows > 1 ? id : 0);
+    int rc = enqueue_step_fused(m, w, kv, rows, false, YUE2_PHASE_NONE, s, dev, nb);
+    if (rc == 0) rc = read_step_error(w, s);
     if (rc == 0) {
         hipError_t e = hipMemcpy(stamps, dev, n * sizeof(*dev), hipMemcpyDeviceToHost);
         if (e != hipSuccess) rc = hip_fail(e, "trace readback");
     }
     (void)hipFree(dev);
     if (rc) return rc;
-    c->length += 1;
+    for (int b = 0; b < rows; ++b) cs[b]->length += 1;
     *wgs = m->cus;
     *slots = nb;
     return YUE2_OK;

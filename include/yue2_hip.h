@@ -240,7 +240,8 @@ int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);
 /* Diagnostics: time one of the decoder's own kernels with HIP events on the
  * decoder's stream, cycling through the layers so that no launch finds its
  * weights in the last-level cache.  kernel: 0 gate/up GEMV with the SwiGLU
- * epilogue, 1 down GEMV, 2 fused QKV GEMV, 3 O GEMV, 4 LM-head GEMV.
+ * epilogue, 1 down GEMV, 2 fused QKV GEMV, 3 O GEMV, 4 LM-head GEMV, 5 the
+ * persistent step kernel (whole token, at the decoder's current position).
  * avg_ms = mean launch duration; bytes = algorithmic HBM bytes per launch.
  * The decoder must have run at least one step. */
 int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t iters, float *avg_ms,

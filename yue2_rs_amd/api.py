@@ -337,11 +337,12 @@ class Decoder:
         n = _check(lib().yue2_hip_decoder_run(self._h, _ptr(fl), steps, _ptr(tokens), _ptr(ms)))
         return tokens[:n], (ms[:n] if timing else None)
 
-    KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "o": 3, "lm_head": 4}
+    KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "o": 3, "lm_head": 4, "step": 5}
 
     def time_kernel(self, kernel: str, iters: int = 112):
         """(mean launch ms, algorithmic bytes per launch) of one of the
-        decoder's GEMV kernels, timed with HIP events on its stream."""
+        decoder's kernels (a per-phase GEMV, or "step": the persistent
+        step kernel), timed with HIP events on its stream."""
         ms, by = C.c_float(0), C.c_double(0)
         _check(lib().yue2_hip_decoder_time_kernel(self._h, self.KERNELS[kernel], iters, C.byref(ms),
                                                   C.byref(by)))

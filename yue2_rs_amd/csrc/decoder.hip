@@ -19,6 +19,7 @@
 #include "kernels.h"
 #include "runtime.h"
 #include "sampler.h"
+#include "step.h"
 #include "y2_math.h"
 
 using namespace y2;
@@ -306,14 +307,59 @@ static int choose_only(Yue2Decoder* d, const float* first_logits, int32_t* token
     return read_tokens(d, d->steps_done, 1, token);
 }
 
+// The persistent step kernel of this decoder, launched `iters` times at the
+// decoder's current position (every launch recomputes the same token: it
+// rewrites the same K/V slots and logits, and the state is not advanced).
+// bytes: every weight once, each row's K/V over its current context plus
+// the new position, the embedding rows.
+static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double* bytes) {
+    Yue2Model* m = d->m;
+    const Yue2Config& c = m->c;
+    if (!m->step_kernel || !step_supported(c, d->rows, m->cus))
+        return fail(YUE2_ERR_ARG, "the decoder does not run the step kernel");
+    const double H = c.hidden_size, D = c.head_dim, I = c.intermediate_size, V = c.vocab_size;
+    const double q = c.num_attention_heads * D, kv = c.num_key_value_heads * D, L = c.num_hidden_layers;
+    const double weights = L * (2.0 * (H * (q + 2.0 * kv) + q * H + 3.0 * H * I) + 4.0 * (2.0 * H + 2.0 * D)) +
+                           2.0 * V * H + 4.0 * H;
+    double kvb = 0.0;
+    for (int b = 0; b < d->rows; ++b)
+        kvb += L * 2.0 * kv * 2.0 * (d->caches[b]->length + 1) + 2.0 * H;
+    hipStream_t s = m->stream;
+    hipEvent_t b0, b1;
+    if (hipEventCreate(&b0) != hipSuccess) return fail(YUE2_ERR_DEVICE, "hipEventCreate");
+    if (hipEventCreate(&b1) != hipSuccess) {
+        (void)hipEventDestroy(b0);
+        return fail(YUE2_ERR_DEVICE, "hipEventCreate");
+    }
+    int rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);  // untimed
+    if (rc == YUE2_OK) (void)hipEventRecord(b0, s);
+    for (int i = 0; i < iters && rc == YUE2_OK; ++i) rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+    if (rc == YUE2_OK) {
+        (void)hipEventRecord(b1, s);
+        hipError_t e = hipEventSynchronize(b1);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, b0, b1);
+        if (e != hipSuccess) rc = hip_fail(e, "step kernel timing");
+        *avg_ms = ms / (float)iters;
+        *bytes = weights + kvb;
+    } else if (rc > 0) {
+        rc = fail(YUE2_ERR_ARG, "the decoder does not run the step kernel");
+    }
+    if (rc == YUE2_OK) rc = read_step_error(d->w, s);
+    (void)hipEventDestroy(b0);
+    (void)hipEventDestroy(b1);
+    return rc;
+}
+
 extern "C" int32_t yue2_hip_decoder_time_kernel(Yue2Decoder* d, int32_t kernel, int32_t iters,
                                                 float* avg_ms, double* bytes) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
-    if (!d || !avg_ms || !bytes || iters <= 0 || kernel < 0 || kernel > 4)
+    if (!d || !avg_ms || !bytes || iters <= 0 || kernel < 0 || kernel > 5)
         return fail(YUE2_ERR_ARG, "bad kernel timing request");
     if (!d->started) return fail(YUE2_ERR_ARG, "decoder has not run");
     Yue2Model* m = d->m;
     const Yue2Config& c = m->c;
+    if (kernel == 5) return time_step_kernel(d, iters, avg_ms, bytes);
     const int H = c.hidden_size, D = c.head_dim, I = c.intermediate_size, V = c.vocab_size;
     const int qw = c.num_attention_heads * D, qkvw = qw + 2 * c.num_key_value_heads * D;
     const int rows = d->rows, L = c.num_hidden_layers;

@@ -399,27 +399,36 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         __syncthreads();
     }
 
+    // Layers, then (when the call asks for logits) one more pass of the
+    // norm + GEMV head with the final norm and the LM head: one copy of that
+    // code serves both (the per-layer code has to fit the instruction cache).
     const int layers_n = fresh(args)->layers_n;
-    for (int l = 0; l < layers_n; ++l) {
-        // ---- input RMSNorm + fused QKV projection ----
+    const int passes = layers_n + (call.head ? 1 : 0);
+    for (int l = 0; l < passes; ++l) {
+        const bool last = l == layers_n;
+        // ---- input RMSNorm + fused QKV projection (final norm + LM head) ----
         {
             ArgsPtr a = fresh(args);
-            const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
+            const int lc = min(l, layers_n - 1);  // layer pointers are never read past the table
+            const int H = a->hidden, n = last ? a->vocab : (a->heads + 2 * a->kv_heads) * D;
+            const uint16_t* w = last ? a->lm_head : layer_at(a, lc)->wqkv;
+            const int r0 = part_lo(n, wg, nwg), r1 = part_lo(n, wg + 1, nwg);
             if (l > 0) {
-                // this layer's gammas and first weights go out before the wait
-                load_gamma<ITH>(layer_at(a, l)->in_norm, H, gam);
-                prefetch_ring<ITH, false>(layer_at(a, l)->wqkv, nullptr, H, part_lo(qkvw, wg, nwg), part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+                // the gammas and first weights go out before the wait
+                load_gamma<ITH>(last ? a->final_norm : layer_at(a, lc)->in_norm, H, gam);
+                prefetch_ring<ITH, false>(w, nullptr, H, r0, r1, n, ring);
                 a = fresh(args);
                 if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
             }
             a = fresh(args);
-            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
+            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH>(layer_at(a, l)->wqkv, nullptr, lds, H, nullptr, a->tqkv,
-                                         flow_tag(epoch, l, FK_QKV), qkvw, part_lo(qkvw, wg, nwg), part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+            gemv_ring<B, EPI_STORE, ITH>(w, nullptr, lds, H, last ? a->logits : nullptr, last ? nullptr : a->tqkv,
+                                         flow_tag(epoch, l, FK_QKV), n, r0, r1, n, ring);
             tr.mark();
         }
+        if (last) break;
         // ---- QK-norm + RoPE + KV append + attention ----
         {
             ArgsPtr a = fresh(args);
@@ -481,21 +490,6 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
         }
-    }
-    // ---- final norm + LM head (src/model.rs:465-468, 590) ----
-    if (call.head) {
-        ArgsPtr a = fresh(args);
-        const int H = a->hidden;
-        const int v0 = part_lo(a->vocab, wg, nwg), v1 = part_lo(a->vocab, wg + 1, nwg);
-        load_gamma<ITH>(a->final_norm, H, gam);
-        prefetch_ring<ITH, false>(a->lm_head, nullptr, H, v0, v1, a->vocab, ring);
-        a = fresh(args);
-        if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, layers_n - 1, FK_XD), st)) return;
-        a = fresh(args);
-        norm_rows<B, ITH>(lds, H, gam, a->eps, nullptr);
-        a = fresh(args);
-        gemv_ring<B, EPI_STORE, ITH>(a->lm_head, nullptr, lds, H, a->logits, nullptr, 0, a->vocab, v0, v1, a->vocab,
-                                     ring);
     }
     // The next launch's epoch.  Workgroup 0 cannot get here before every
     // workgroup has read seq: its final input needs every workgroup's output.

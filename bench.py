@@ -20,6 +20,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -76,6 +77,21 @@ def measure(y2, model, caches, first, sampling, scale, warmup, steps, c):
         "hbm_roofline_frac": step_bytes(c, rows, mean_ctx) / (wall / steps) / HBM_PEAK,
         "bytes_per_step": step_bytes(c, rows, mean_ctx),
     }
+
+
+def measured_traffic(context):
+    """HBM bytes per launch of the CFG step kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated against a plain copy),
+    when they were measured at this context; otherwise None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "step_kernel_3b_cfg_traffic.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    vals = dict(re.findall(r"^(traffic_bytes_per_launch|context): (\d+)$", text, re.M))
+    if int(vals.get("context", -1)) != context:
+        return None
+    return int(vals["traffic_bytes_per_launch"])
 
 
 def cpu_baseline(ckpt, c, prompt_len, scale, sampling, threads, budget_s, max_steps):
@@ -168,10 +184,11 @@ def main() -> int:
     # stream at the end of the timed run's context.
     step_ms, step_b = d2.time_kernel("step", args.kernel_iters)
     achieved = step_b / (step_ms * 1e-3) / 1e9
+    context = c_pos.length
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(achieved / 8000.0, 4), "traffic": None,
+                "frac": round(achieved / 8000.0, 4), "traffic": measured_traffic(context),
                 "kernel": "step_kernel<2, 128, 6, 6, 16> (whole CFG batch-2 token: 28 layers + LM head)",
-                "launch_ms": round(step_ms, 5), "bytes_per_launch": int(step_b)}
+                "launch_ms": round(step_ms, 5), "bytes_per_launch": int(step_b), "context": context}
     # the per-phase GEMV kernels of the phase-kernel path, for reference
     others = {}
     for name in ("gate_up", "down", "qkv", "o", "lm_head"):

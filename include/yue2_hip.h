@@ -261,6 +261,23 @@ int32_t yue2_hip_decoder_time_kernel(Yue2Decoder *d, int32_t kernel, int32_t ite
 int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, Yue2Cache *c2, int32_t id, uint64_t *stamps,
                             int32_t cap, int32_t *wgs, int32_t *slots);
 
+/* Microbenchmarks against the HBM roofline (device-resident inputs; each
+ * timed launch reads another copy of its operands, so the 256 MB Infinity
+ * Cache cannot serve repeats).
+ * yue2_hip_bench_gemv: the BF16 GEMV y = W x (W [n x k], `rows` batch rows,
+ * FP32 accumulation, rounded output) over `copies` weight copies; *avg_ms =
+ * mean launch time over `iters` launches, *bytes = n k 2 + rows k 2 +
+ * rows n 4 (the weights, BF16 inputs and f32 outputs).
+ * yue2_hip_bench_attention: the split-KV decode attention of one layer (24
+ * query heads, 8 KV heads, head_dim 128, QK-norm + RoPE + KV append
+ * included) for `rows` rows whose new token attends `context` positions,
+ * cycling over `layers` distinct layer caches; *bytes = rows 4096 context
+ * (the K and V rows read).  Both return 0 or a negative Yue2Error. */
+int32_t yue2_hip_bench_gemv(int32_t n, int32_t k, int32_t rows, int32_t copies, int32_t iters, float *avg_ms,
+                            double *bytes);
+int32_t yue2_hip_bench_attention(int32_t context, int32_t rows, int32_t layers, int32_t iters, float *avg_ms,
+                                 double *bytes);
+
 #ifdef __cplusplus
 }
 #endif

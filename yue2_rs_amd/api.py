@@ -116,6 +116,8 @@ def lib() -> C.CDLL:
         "yue2_hip_decoder_time_kernel": (i32, [vp, i32, i32, vp, vp]),
         "yue2_hip_trace_step": (i32, [vp, vp, vp, i32, vp, i32, vp, vp]),
         "yue2_hip_model_set_step_kernel": (i32, [vp, i32]),
+        "yue2_hip_bench_gemv": (i32, [i32, i32, i32, i32, i32, vp, vp]),
+        "yue2_hip_bench_attention": (i32, [i32, i32, i32, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

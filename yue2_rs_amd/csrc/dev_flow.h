@@ -24,6 +24,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "dev_attn.h"
 #include "dev_mem.h"
 #include "kernels.h"
 #include "y2_math.h"

@@ -3,56 +3,45 @@
 // with the RMSNorm that produces its input (Norm::apply, :1140-1157).
 //
 // Layout and schedule (gfx950):
-//  * one 512-thread workgroup per CU; workgroup g owns a contiguous range of
-//    weight rows, and its 8 waves take every 8th row of that range;
-//  * a wave owns one row at a time: lane l streams chunks l, l+64, ... of the
-//    row with 128-bit loads (8 BF16 values) and keeps one f32 fma chain, then
-//    the 64 lanes combine by an xor butterfly -- exactly the DOT order, so any
-//    batch row equals the batch-1 result;
-//  * the first row's weights are requested before the input vector is staged,
-//    and row r+8 is requested while row r is computed (double buffering), so
-//    each CU keeps ~100 KB of weight reads in flight;
-//  * the input rows are staged once per workgroup in LDS (f32).  With a norm
+//  * one 512-thread workgroup per CU; workgroup g owns the contiguous rows
+//    [g n / G, (g + 1) n / G) and its 8 waves take every 8th row of them;
+//  * a wave walks its rows as items through the register ring of dev_ring.h
+//    (R-1 items of 16-byte loads in flight, ~100 KB per CU): lane l streams
+//    chunks l, l+64, ... of a row and keeps one f32 fma chain, then the 64
+//    lanes combine by an xor butterfly -- exactly the DOT order, so any batch
+//    row equals the batch-1 result;
+//  * the ring's first items are requested before the input vector is staged;
+//  * the input rows are staged once per workgroup in LDS (f32), and for a
+//    residual epilogue the workgroup's own output rows as well.  With a norm
 //    prologue the workgroup computes the RMSNorm scale itself (guarded, see
 //    norm_scale_block) and stages rb(rb(x * s) * gamma).
 #include <algorithm>
 
 #include "dev_gemv.h"
+#include "dev_ring.h"
 #include "kernels.h"
 #include "y2_math.h"
 
 namespace y2 {
 
-constexpr int kGemvThreads = 512;
-constexpr int kGemvWaves = kGemvThreads / 64;
+constexpr int kGemvThreads = kRingThreads;
 
-template <int B, int EPI, int IT>
-__device__ __forceinline__ void compute_row(const GemvArgs& a, const float* xs, int row, int lane,
-                                            const uint4* wv, const uint4* wv2) {
-    float acc[B], acc2[B];
-    dot_rows<B, IT, EPI == EPI_SWIGLU>(xs, a.k, lane, wv, wv2, acc, acc2);
-    if (lane == 0) {
-#pragma unroll
-        for (int b = 0; b < B; ++b) gemv_store<EPI>(a.y + (size_t)b * a.y_stride + row, acc[b], acc2[b]);
-    }
-}
-
+// IT chunks of 8 per lane cover k (k <= 512 IT); chunks past k are masked.
 template <int B, int EPI, int IT, bool NORM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs a) {
-    extern __shared__ float xs[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int k = a.k;
-    const int per = (a.n + gridDim.x - 1) / gridDim.x;
-    const int r0 = blockIdx.x * per, r1 = min(a.n, r0 + per);
-    constexpr int IT2 = EPI == EPI_SWIGLU ? IT : 1;
-    uint4 bufA[IT], bufA2[IT2], bufB[IT], bufB2[IT2];
-    int row = r0 + wave;
-    if (row < r1) {
-        load_row<IT>(a.w, row, k, lane, bufA);
-        if constexpr (EPI == EPI_SWIGLU) load_row<IT>(a.w2, row, k, lane, bufA2);
-    }
+    extern __shared__ float xs[];  // [B][k] inputs, then [B][kResRows] residual rows
+    constexpr bool PAIR = EPI == EPI_SWIGLU;
+    const int tid = threadIdx.x, k = a.k, n = a.n;
+    const int r0 = part_lo(n, blockIdx.x, gridDim.x), r1 = part_lo(n, blockIdx.x + 1, gridDim.x);
+    uint4 ring[Ring<IT, PAIR>::SIZE];
+    prefetch_ring<IT, PAIR, true>(a.w, a.w2, k, r0, r1, n, ring);
     for (int b = 0; b < B; ++b)
         for (int i = tid; i < k; i += kGemvThreads) xs[b * k + i] = a.x[(size_t)b * a.x_stride + i];
+    float* res = xs + B * k;
+    if constexpr (EPI == EPI_RESID) {
+        const int span = r1 - r0;
+        if (tid < B * span) res[tid] = a.y[(size_t)(tid / span) * a.y_stride + r0 + tid % span];
+    }
     __syncthreads();
     if constexpr (NORM) {
         for (int b = 0; b < B; ++b) {
@@ -63,23 +52,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs a) {
         }
         __syncthreads();
     }
-    while (row < r1) {
-        int next = row + kGemvWaves;
-        if (next < r1) {
-            load_row<IT>(a.w, next, k, lane, bufB);
-            if constexpr (EPI == EPI_SWIGLU) load_row<IT>(a.w2, next, k, lane, bufB2);
-        }
-        compute_row<B, EPI, IT>(a, xs, row, lane, bufA, bufA2);
-        row = next;
-        if (row >= r1) break;
-        next = row + kGemvWaves;
-        if (next < r1) {
-            load_row<IT>(a.w, next, k, lane, bufA);
-            if constexpr (EPI == EPI_SWIGLU) load_row<IT>(a.w2, next, k, lane, bufA2);
-        }
-        compute_row<B, EPI, IT>(a, xs, row, lane, bufB, bufB2);
-        row = next;
-    }
+    gemv_ring<B, EPI, IT, true>(a.w, a.w2, xs, k, a.y, nullptr, 0, a.y_stride, r0, r1, n, ring, res);
 }
 
 static int g_cus = 0;
@@ -97,8 +70,10 @@ static int cu_count() {
 template <int B, int EPI, bool NORM>
 static hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a) {
     const int iters = (a.k / 8 + 63) / 64;
-    const int blocks = std::max(1, std::min(cu_count(), (a.n + kGemvWaves - 1) / kGemvWaves));
-    const size_t lds = (size_t)B * a.k * sizeof(float);
+    const int blocks = std::max(1, std::min(cu_count(), a.n));
+    // a residual epilogue stages the workgroup's output rows (at most kResRows)
+    if (EPI == EPI_RESID && (a.n + blocks - 1) / blocks > kResRows) return hipErrorInvalidValue;
+    const size_t lds = (size_t)B * (a.k + kResRows) * sizeof(float);
 #define Y2_GEMV_CASE(N)                                                       \
     if (iters <= N) {                                                         \
         gemv_kernel<B, EPI, N, NORM><<<blocks, kGemvThreads, lds, s>>>(a);    \

@@ -8,7 +8,7 @@
 
 namespace y2 {
 
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 512;
 
 template <int D, int MAXG>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs a) {
@@ -35,8 +35,10 @@ hipError_t launch_attention(hipStream_t s, const AttnArgs& a) {
     const int G = a.heads / a.kv_heads;
     if (G < 1 || G > 8 || a.heads % a.kv_heads) return hipErrorInvalidValue;
     if (a.wgs * a.kv_heads * a.rows > 1024) return hipErrorInvalidValue;
+    // the block statistics are gathered for at most 384 blocks (24576 keys)
+    if (a.wgs * a.bpw > 24576 / kBlockKeys && a.blk_stride > 24576 / kBlockKeys) return hipErrorInvalidValue;
     const dim3 grid(a.wgs, a.kv_heads, a.rows);
-    const size_t lds = (size_t)G * a.bpw * kBlockKeys * sizeof(float);
+    const size_t lds = attn_group_lds(G, a.dim, a.wgs, a.bpw);
     if (lds > 96 * 1024) return hipErrorInvalidValue;
     const bool small = G <= 4;
     switch (a.dim) {

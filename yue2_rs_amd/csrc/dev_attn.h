@@ -78,11 +78,23 @@ __device__ __forceinline__ bool wait_for(int* cnt, int target, StepState* st) {
     return s_ok != 0;
 }
 
+// Block counts up to which the last workgroup of a group merges every output
+// (one round of loads); beyond, each workgroup merges a share after one more
+// group barrier.
+constexpr int kMergeLastMax = 32;
+
+// LDS bytes attn_group needs: the scores of G heads over bpw blocks and the
+// group's block sums, later the merge's [outputs][blocks] partials.
+__host__ __device__ constexpr size_t attn_group_lds(int G, int D, int wgs, int bpw) {
+    const size_t scores = (size_t)G * bpw * kBlockKeys + (size_t)G * wgs * bpw, merge = ((size_t)G * D + wgs) * bpw;
+    return (scores > merge ? scores : merge) * sizeof(float);
+}
+
 // One workgroup's share of the attention of kv head g, batch row b: the
 // workgroup handles 64-key blocks [wg * bpw, (wg + 1) * bpw) of that head.
 // G = heads / kv_heads <= MAXG query heads share the K/V rows.  e_s: LDS
-// scratch of G * bpw * 64 floats.  Returns false when a group sync timed out
-// (the device error is set).
+// scratch of attn_group_lds(G, D, wgs, bpw) bytes.  Returns false when a
+// group sync timed out (the device error is set).
 template <int NT, int D, int MAXG>
 __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int b, float* e_s) {
     constexpr int NW = NT / 64;
@@ -221,8 +233,13 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
     {
         for (int h = wave; h < G; h += NW) {
             const float* bm = a.bmax + hbase + (size_t)h * a.blk_stride;
-            float m = -__builtin_huge_valf();
-            for (int i = lane; i < nb; i += 64) m = fmaxf(m, ld_dev(bm + i));
+            // every block maximum of the head requested at once (nb <= 384)
+            float v[6];
+#pragma unroll
+            for (int u = 0; u < 6; ++u) v[u] = lane + 64 * u < nb ? ld_dev(bm + lane + 64 * u) : -__builtin_huge_valf();
+            float m = v[0];
+#pragma unroll
+            for (int u = 1; u < 6; ++u) m = fmaxf(m, v[u]);
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
             if (lane == 0) m_s[h] = m;
@@ -253,24 +270,23 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
         // LDS by all threads first (a chain of dependent device loads would
         // pay a memory round trip per block)
         {
-            constexpr int CH = 128;
-            __shared__ float bs_s[MAXG][CH];
-            float tot = 0.0f;
-            for (int base = 0; base < nb; base += CH) {
-                const int n = min(CH, nb - base);
-                for (int i = tid; i < G * CH; i += NT) {
-                    const int h = i / CH, j = i % CH;
-                    if (j < n) bs_s[h][j] = ld_dev(a.bsum + hbase + (size_t)h * a.blk_stride + base + j);
-                }
-                __syncthreads();
-                if (tid < G) {
-                    int j = 0;
-                    if (base == 0) tot = bs_s[tid][j++];
-                    for (; j < n; ++j) tot = tot + bs_s[tid][j];
-                }
-                __syncthreads();
+            float* bs = e_s + G * estride;  // [G][nb] block sums, after the scores
+            const int total = G * nb;        // <= 8 * 384 = 6 * 512
+            float v[6];
+#pragma unroll
+            for (int u = 0; u < 6; ++u) {
+                const int i = tid + u * NT, h = i / nb, j = i - h * nb;
+                v[u] = i < total ? ld_dev(a.bsum + hbase + (size_t)h * a.blk_stride + j) : 0.0f;
             }
-            if (tid < G) t_s[tid] = tot;
+#pragma unroll
+            for (int u = 0; u < 6; ++u)
+                if (tid + u * NT < total) bs[tid + u * NT] = v[u];
+            __syncthreads();
+            if (tid < G) {
+                float tot = bs[tid * nb];
+                for (int j = 1; j < nb; ++j) tot = tot + bs[tid * nb + j];
+                t_s[tid] = tot;
+            }
         }
         __syncthreads();
         for (int i = tid; i < G * nk; i += NT) {
@@ -327,26 +343,66 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
         }
         stores_done();
         __syncthreads();
-        __shared__ int s_last;
-        if (tid == 0) s_last = signal(&cnt[2]) == W - 1;
-        __syncthreads();
-        if (!s_last) return true;
-        for (int i = tid; i < G * D; i += NT) {
-            const int h = i / D, d = i % D;
-            const float* pp = a.part + (hbase + (size_t)h * a.blk_stride) * D + d;
-            // blocks added left to right; loads issued 16 at a time
-            float o = 0.0f;
-            for (int base = 0; base < nb; base += 16) {
-                float v[16];
+        if (nb <= kMergeLastMax) {
+            // short contexts: the last workgroup through merges every output
+            __shared__ int s_last;
+            if (tid == 0) s_last = signal(&cnt[2]) == W - 1;
+            __syncthreads();
+            if (!s_last) return true;
+            for (int i = tid; i < G * D; i += NT) {
+                const int h = i / D, d = i % D;
+                const float* pp = a.part + (hbase + (size_t)h * a.blk_stride) * D + d;
+                float v[kMergeLastMax];
 #pragma unroll
-                for (int j = 0; j < 16; ++j) v[j] = base + j < nb ? ld_dev(pp + (size_t)(base + j) * D) : 0.0f;
+                for (int j = 0; j < kMergeLastMax; ++j) v[j] = j < nb ? ld_dev(pp + (size_t)j * D) : 0.0f;
+                float o = v[0];
 #pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (base + j < nb) o = base + j == 0 ? v[j] : o + v[j];
+                for (int j = 1; j < kMergeLastMax; ++j)
+                    if (j < nb) o = o + v[j];  // blocks left to right
+                st_dev(a.out + (size_t)b * a.out_stride + (size_t)(g * G + h) * D + d, rb(o));
             }
-            st_dev(a.out + (size_t)b * a.out_stride + (size_t)(g * G + h) * D + d, rb(o));
+            if (tid < 3) st_dev_i(&cnt[tid], 0);
+            return true;
         }
-        if (tid < 3) st_dev_i(&cnt[tid], 0);
+        if (tid == 0) signal(&cnt[2]);
+        if (!wait_for(&cnt[2], W, st)) return false;
+        // longer contexts: workgroup wg adds the blocks (left to right) of the outputs
+        // [o0, o1) of the group.  Its partials are first gathered into LDS by
+        // all threads, 16 requests per thread in flight: a chain of dependent
+        // device loads would pay a memory round trip per block.
+        const int outs = G * D, chunk = (outs + W - 1) / W;
+        const int o0 = min(outs, wg * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
+        float* mb = e_s;  // [no][nb]; the scores are no longer needed
+        const float* part = a.part + hbase * D;
+        const int total = no * nb;
+        for (int base = 0; base < total; base += 16 * NT) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int i = base + tid + u * NT;
+                float x = 0.0f;
+                if (i < total) {
+                    const int r = i / nb, k = i - r * nb, o = o0 + r;
+                    x = ld_dev(part + ((size_t)(o / D) * a.blk_stride + k) * D + o % D);
+                }
+                v[u] = x;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (base + tid + u * NT < total) mb[base + tid + u * NT] = v[u];
+        }
+        __syncthreads();
+        for (int i = tid; i < no; i += NT) {
+            const float* pp = mb + i * nb;
+            float o = pp[0];
+            for (int k = 1; k < nb; ++k) o = o + pp[k];
+            st_dev(a.out + (size_t)b * a.out_stride + (size_t)(g * G) * D + o0 + i, rb(o));
+        }
+        __syncthreads();
+        // the last workgroup through clears the group's counters for the
+        // next launch (every workgroup has passed all of its waits)
+        if (tid == 0 && signal(&cnt[3]) == W - 1)
+            for (int c = 0; c < 4; ++c) st_dev_i(&cnt[c], 0);
     }
     return true;
 }

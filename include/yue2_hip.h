@@ -224,8 +224,11 @@ void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t te
                              float stddev, int32_t threads);
 
 /* Diagnostics: evaluate a device math routine elementwise on host arrays
- * (which: 0 exp f32, 1 log1p f64, 2 round_bf16, 3 SiLU).  Returns 0 or a
- * negative Yue2Error. */
+ * (which: 0 exp f32, 1 log1p f64, 2 round_bf16, 3 SiLU), or, per 64-lane
+ * wave of f32 inputs (n a multiple of 256), a lane exchange: 4-9 the value of
+ * lane ^ 1, 2, 4, 8, 16, 32; the xor-butterfly sums over distances 32..1
+ * (10 ALU exchanges, 11 __shfl_xor), 8..1 (12, 13) and 32..16 (14, 15); 16
+ * the max over 32..1.  Returns 0 or a negative Yue2Error. */
 int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
 /* Execution choice: run decode steps (yue2_hip_forward and decoders created
  * afterwards) through the persistent token-step kernel -- one launch per

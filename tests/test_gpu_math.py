@@ -61,3 +61,21 @@ def test_round_and_silu_match_oracle(gpu):
     ref = (g / (np.float32(1.0) + e)).astype(np.float32)
     want = np.array([L.y2o_round_bf16(float(v)) for v in ref], dtype=np.float32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_lane_exchanges_are_exact(gpu):
+    """The ALU lane exchanges (DPP, permlane swaps) read lane ^ m exactly, and
+    the xor butterflies built on them give the same bits as __shfl_xor ones
+    (the DOT order, attention score, PV stream and block sums all use them)."""
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.normal(0, 1, 64 * 1023).astype(np.float32),
+                        np.tile(np.array([1e30, -1e30, 1e-30, -0.0, 0.0, 3.0, -3.0, 1.0], np.float32), 8)])
+    lanes = np.arange(x.size) % 64
+    base = np.arange(x.size) - lanes
+    for j, m in enumerate([1, 2, 4, 8, 16, 32]):
+        got = _device(4 + j, x)
+        assert np.array_equal(got.view(np.uint32), x[base + (lanes ^ m)].view(np.uint32)), m
+    for new, old in [(10, 11), (12, 13), (14, 15)]:
+        assert np.array_equal(_device(new, x).view(np.uint32), _device(old, x).view(np.uint32)), new
+    mx = _device(16, x).reshape(-1, 64)
+    assert np.array_equal(mx, np.repeat(x.reshape(-1, 64).max(axis=1, keepdims=True), 64, axis=1))

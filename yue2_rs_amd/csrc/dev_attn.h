@@ -208,8 +208,7 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
                     float acc = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
-#pragma unroll
-                    for (int s = CPL / 2; s >= 1; s >>= 1) acc = acc + __shfl_xor(acc, s, 64);
+acc = xor_sum<CPL / 2>(acc);
                     if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
                 }
             }
@@ -219,8 +218,7 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+m = xor_max<32>(m);
             if (lane == 0) st_dev(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m);
         }
         stores_done();
@@ -240,8 +238,7 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
             float m = v[0];
 #pragma unroll
             for (int u = 1; u < 6; ++u) m = fmaxf(m, v[u]);
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+m = xor_max<32>(m);
             if (lane == 0) m_s[h] = m;
         }
         __syncthreads();
@@ -254,8 +251,7 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) v = v + __shfl_xor(v, s, 64);
+v = xor_sum<32>(v);
             if (lane == 0) st_dev(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v);
         }
         stores_done();
@@ -325,12 +321,10 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
                 }
             }
 #pragma unroll
-            for (int s = 32; s >= CPL; s >>= 1)
+            for (int h = 0; h < MAXG; ++h)
+                if (h < G)
 #pragma unroll
-                for (int h = 0; h < MAXG; ++h)
-                    if (h < G)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[h][e] = acc[h][e] + __shfl_xor(acc[h][e], s, 64);
+                    for (int e = 0; e < 8; ++e) acc[h][e] = xor_sum<32, CPL>(acc[h][e]);
             if (t == 0) {
 #pragma unroll
                 for (int h = 0; h < MAXG; ++h)

@@ -325,8 +325,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                     float acc = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
-#pragma unroll
-                    for (int s2 = CPL / 2; s2 >= 1; s2 >>= 1) acc = acc + __shfl_xor(acc, s2, 64);
+acc = xor_sum<CPL / 2>(acc);
                     if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
                 }
             }
@@ -336,8 +335,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
-#pragma unroll
-            for (int s2 = 32; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2, 64));
+m = xor_max<32>(m);
             if (lane == 0) st_tag(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m, t_bmax);
         }
     }
@@ -352,8 +350,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         for (int h = wave; h < G; h += NW) {
             float m = -__builtin_huge_valf();
             for (int i = lane; i < nb; i += 64) m = fmaxf(m, red_s[h * nb + i]);
-#pragma unroll
-            for (int s2 = 32; s2 >= 1; s2 >>= 1) m = fmaxf(m, __shfl_xor(m, s2, 64));
+m = xor_max<32>(m);
             if (lane == 0) m_s[h] = m;
         }
         __syncthreads();
@@ -366,8 +363,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
-#pragma unroll
-            for (int s2 = 32; s2 >= 1; s2 >>= 1) v = v + __shfl_xor(v, s2, 64);
+v = xor_sum<32>(v);
             if (lane == 0) st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v, t_bsum);
         }
     }
@@ -423,9 +419,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                     }
                 }
 #pragma unroll
-                for (int s2 = 32; s2 >= CPL; s2 >>= 1)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], s2, 64);
+                for (int e = 0; e < 8; ++e) acc[e] = xor_sum<32, CPL>(acc[e]);
                 // the S stream lanes hold the same sums: each stores 8 / S of them
                 uint64_t* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
 #pragma unroll

@@ -22,18 +22,9 @@ __device__ __forceinline__ void unpack_bf16x8(const uint4 w, float* f) {
     f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
 }
 
-// v summed over the wave by the xor butterfly 32, 16, ..., 1.  Steps below
-// 32 stay inside 32-lane halves, where ds_swizzle's bit mode (and 0x1f,
-// xor m) is the exchange without an address computation.
-__device__ __forceinline__ float wave_sum_xor(float v) {
-    v = v + __shfl_xor(v, 32, 64);
-    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (16 << 10)));
-    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (8 << 10)));
-    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (4 << 10)));
-    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (2 << 10)));
-    v = v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (1 << 10)));
-    return v;
-}
+// v summed over the wave by the xor butterfly 32, 16, ..., 1 (ALU lane
+// exchanges, dev_mem.h).
+__device__ __forceinline__ float wave_sum_xor(float v) { return xor_sum<32>(v); }
 
 // Request the IT chunks that `lane` owns in weight row `row` (k BF16 per row).
 // Loads are unconditional so the compiler can keep them in flight across the
@@ -142,11 +133,8 @@ __device__ __forceinline__ float norm_scale_block(const float* xs, int n, float 
         e_sum += (double)t;
         w_sum += (double)t * (double)(n - i);
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-        e_sum += __shfl_xor(e_sum, s, 64);
-        w_sum += __shfl_xor(w_sum, s, 64);
-    }
+    e_sum = xor_sum<32>(e_sum);
+    w_sum = xor_sum<32>(w_sum);
     if (lane == 0) {
         red_e[wave] = e_sum;
         red_w[wave] = w_sum;

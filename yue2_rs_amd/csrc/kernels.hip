@@ -14,6 +14,7 @@
 // Rows of a batch never interact, so a CFG batch-2 row equals a batch-1 row.
 #include <algorithm>
 
+#include "dev_mem.h"
 #include "kernels.h"
 #include "y2_math.h"
 
@@ -171,8 +172,43 @@ __global__ void advance_kernel(StepState* st, int rows) {
     }
 }
 
+// The xor butterflies through __shfl_xor (LDS crossbar): the reference the
+// selftest holds the ALU lane exchanges of dev_mem.h to.
+template <int HI, int LO>
+__device__ __forceinline__ float shfl_sum(float v) {
+#pragma unroll
+    for (int s = HI; s >= LO; s >>= 1) v = v + __shfl_xor(v, s, 64);
+    return v;
+}
+
+// Lane-exchange checks (which >= 4, whole waves: n % 256 == 0).
+__device__ float lane_selftest(int which, float v) {
+    switch (which) {
+        case 4: return xor_lane<1>(v);
+        case 5: return xor_lane<2>(v);
+        case 6: return xor_lane<4>(v);
+        case 7: return xor_lane<8>(v);
+        case 8: return xor_lane<16>(v);
+        case 9: return xor_lane<32>(v);
+        case 10: return xor_sum<32>(v);
+        case 11: return shfl_sum<32, 1>(v);
+        case 12: return xor_sum<8>(v);
+        case 13: return shfl_sum<8, 1>(v);
+        case 14: return xor_sum<32, 16>(v);
+        case 15: return shfl_sum<32, 16>(v);
+        case 16: return xor_max<32>(v);
+        default: return 0.0f;
+    }
+}
+
 __global__ void math_selftest_kernel(int which, const void* in, void* out, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (which >= 4) {
+        // every lane of the wave takes part in the exchange
+        const float v = static_cast<const float*>(in)[i];
+        static_cast<float*>(out)[i] = lane_selftest(which, v);
+        return;
+    }
     if (i >= n) return;
     if (which == 0) static_cast<float*>(out)[i] = expf_cr(static_cast<const float*>(in)[i]);
     else if (which == 1) static_cast<double*>(out)[i] = log1p_d(static_cast<const double*>(in)[i]);

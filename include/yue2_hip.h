@@ -275,11 +275,16 @@ int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, Yue2Cache *c2, int32_t i
  * query heads, 8 KV heads, head_dim 128, QK-norm + RoPE + KV append
  * included) for `rows` rows whose new token attends `context` positions,
  * cycling over `layers` distinct layer caches; *bytes = rows 4096 context
- * (the K and V rows read).  Both return 0 or a negative Yue2Error. */
+ * (the K and V rows read).
+ * yue2_hip_bench_copy: hipMemcpyAsync of `bytes` (a multiple of 256) from
+ * one device buffer to another, once untimed and then `iters` times;
+ * *avg_ms = mean time per copy (each reads and writes `bytes`).
+ * All three return 0 or a negative Yue2Error. */
 int32_t yue2_hip_bench_gemv(int32_t n, int32_t k, int32_t rows, int32_t copies, int32_t iters, float *avg_ms,
                             double *bytes);
 int32_t yue2_hip_bench_attention(int32_t context, int32_t rows, int32_t layers, int32_t iters, float *avg_ms,
                                  double *bytes);
+int32_t yue2_hip_bench_copy(int64_t bytes, int32_t iters, float *avg_ms);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,12 @@ float y2o_round_bf16(float v) {
 }
 #define rb y2o_round_bf16
 
+/* y2o_round_bf16 over bit patterns (no float passes through a call, so
+ * signalling NaNs keep their payload): out[i] = bits of rb(bits in[i]). */
+void y2o_round_bf16_bits(const uint32_t *in, uint32_t *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = f2u(rb(u2f(in[i])));
+}
+
 float y2o_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
 
 /*

@@ -143,6 +143,7 @@ void y2o_set_threads(int n);
 int y2o_get_threads(void);
 
 float y2o_round_bf16(float v);
+void y2o_round_bf16_bits(const uint32_t *in, uint32_t *out, size_t n);
 float y2o_bf16_to_f32(uint16_t b);
 float y2o_expf(float x);
 double y2o_log1p(double x);

@@ -68,6 +68,7 @@ def lib() -> C.CDLL:
         sig = {
             "y2o_set_threads": (None, [i32]),
             "y2o_round_bf16": (f32, [f32]),
+            "y2o_round_bf16_bits": (None, [vp, vp, C.c_size_t]),
             "y2o_expf": (f32, [f32]),
             "y2o_log1p": (f64, [f64]),
             "y2o_dot_bf16": (f32, [vp, vp, i32]),

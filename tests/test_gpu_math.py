@@ -63,6 +63,21 @@ def test_round_and_silu_match_oracle(gpu):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_round_matches_oracle_on_every_bit_pattern(gpu):
+    """The device rounding (the gfx950 BF16 conversion instruction) equals the
+    oracle's round_bf16 on all 2^32 f32 bit patterns: ties, denormals,
+    infinities, quiet and signalling NaNs of both signs."""
+    L = O.lib()
+    chunk = 1 << 28
+    for c in range(1 << 32 >> 28):
+        bits = np.arange(c * chunk, (c + 1) * chunk, dtype=np.uint64).astype(np.uint32)
+        got = _device(2, bits.view(np.float32)).view(np.uint32)
+        want = np.empty_like(bits)
+        L.y2o_round_bf16_bits(bits.ctypes.data, want.ctypes.data, bits.size)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, [(hex(int(bits[i])), hex(int(got[i])), hex(int(want[i]))) for i in bad[:8]]
+
+
 def test_lane_exchanges_are_exact(gpu):
     """The ALU lane exchanges (DPP, permlane swaps) read lane ^ m exactly, and
     the xor butterflies built on them give the same bits as __shfl_xor ones

@@ -93,3 +93,23 @@ def test_log1p_within_two_ulp():
     assert err.max() <= 2.0, float(xs[int(np.argmax(err))])
     assert f(0.0) == 0.0
     assert f(-1.0) == float("-inf")
+
+
+def test_round_bf16_bits_matches_scalar_and_keeps_nan_payload():
+    """The array form rounds like the scalar one, and signalling NaNs come back
+    quiet with their sign and top payload bits."""
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2 ** 32, size=20000, dtype=np.uint64).astype(np.uint32)
+    bits = np.concatenate([bits, np.array([0x7F800001, 0xFF800001, 0x7FA12345, 0xFFBFFFFF, 0x7FC00000,
+                                           0x7F800000, 0xFF800000, 0x00008000, 0x00018000, 0x7F7F8000],
+                                          dtype=np.uint32)])
+    out = np.empty_like(bits)
+    L = O.lib()
+    L.y2o_round_bf16_bits(bits.ctypes.data, out.ctypes.data, bits.size)
+    nan = (bits & 0x7FFFFFFF) > 0x7F800000
+    assert np.array_equal(out[nan], (bits[nan] & 0xFFFF0000) | 0x00400000)
+    for b, o in zip(bits[~nan][:4000], out[~nan][:4000]):
+        assert int(np.float32(L.y2o_round_bf16(float(np.uint32(b).view(np.float32)))).view(np.uint32)) == int(o)
+    # ties to even: 0x00008000 -> 0, 0x00018000 -> 0x00020000; the largest
+    # finite value's tie rounds to infinity
+    assert list(out[-3:]) == [0, 0x00020000, 0x7F800000]

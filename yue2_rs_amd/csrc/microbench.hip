@@ -1,6 +1,8 @@
 // microbench.hip -- device-resident microbenchmarks of the decode kernels
-// against the HBM roofline: the BF16 GEMV family at the 3B layer shapes and
-// the split-KV decode attention over growing contexts.  Inputs live in HBM
+// against the HBM roofline: the BF16 GEMV family at the 3B layer shapes,
+// the split-KV decode attention over growing contexts, and a plain
+// device-to-device copy (the practical HBM rate and the calibration workload
+// of the traffic counters).  Inputs live in HBM
 // before timing; each launch reads a different copy of its operands (more
 // than the 256 MB Infinity Cache in total), so repeats are not served from
 // the cache.  Times are HIP events around the launches on one stream.
@@ -60,6 +62,31 @@ struct Events {
 }  // namespace y2
 
 using namespace y2;
+
+extern "C" int32_t yue2_hip_bench_copy(int64_t bytes, int32_t iters, float* avg_ms) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!avg_ms || bytes <= 0 || bytes % 256 || iters < 1) return fail(YUE2_ERR_ARG, "bad copy benchmark request");
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no usable gfx950 device");
+    DevBufs m;
+    void* src = m.alloc((size_t)bytes);
+    void* dst = m.alloc((size_t)bytes);
+    if (!src || !dst) return fail(YUE2_ERR_ALLOC, "copy benchmark buffers");
+    hipStream_t s = nullptr;
+    fill_bf16(s, static_cast<uint16_t*>(src), (size_t)bytes / 2, 11, 1.0f);
+    Events ev;
+    if (!ev.ok()) return fail(YUE2_ERR_DEVICE, "hipEventCreate");
+    hipError_t e = hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipEventRecord(ev.a, s);
+    for (int i = 0; i < iters && e == hipSuccess; ++i)
+        e = hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipEventRecord(ev.b, s);
+    if (e == hipSuccess) e = hipEventSynchronize(ev.b);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.a, ev.b);
+    if (e != hipSuccess) return hip_fail(e, "copy benchmark");
+    *avg_ms = ms / (float)iters;
+    return YUE2_OK;
+}
 
 extern "C" int32_t yue2_hip_bench_gemv(int32_t n, int32_t k, int32_t rows, int32_t copies, int32_t iters,
                                        float* avg_ms, double* bytes) {

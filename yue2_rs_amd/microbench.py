@@ -7,12 +7,15 @@ Attention (split-KV GQA decode, 24 query / 8 KV heads, head_dim 128, QK-norm,
 RoPE at the position and the KV append included) at contexts 1024, 4096,
 16384 and 24576, batch 1 and 2, over 28 distinct layer caches; bytes per
 layer-call = b 4096 L (the K and V rows).
+Copy: a plain 256 MiB device-to-device hipMemcpy, the practical HBM rate
+(bytes = read + written) and the calibration workload of the FETCH_SIZE /
+WRITE_SIZE counters.
 
 Every timed launch reads another copy of its operands (more than 512 MB in
 total), so the 256 MB Infinity Cache cannot serve repeats.  One JSON line per
 case on stdout.
 
-    python -m yue2_rs_amd.microbench [gemv|attention|all]
+    python -m yue2_rs_amd.microbench [gemv|attention|copy|all]
 """
 from __future__ import annotations
 
@@ -45,6 +48,14 @@ def attention(context: int, rows: int, layers: int = 28, iters: int = 112) -> di
             "bytes": int(by.value), "GB_s": round(gbs, 1), "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
 
 
+def copy(nbytes: int = 256 * 2**20, iters: int = 20) -> dict:
+    ms = C.c_float(0)
+    _check(lib().yue2_hip_bench_copy(nbytes, iters, C.byref(ms)))
+    gbs = 2 * nbytes / (ms.value * 1e-3) / 1e9
+    return {"bytes": nbytes, "copy_us": round(ms.value * 1e3, 2), "GB_s": round(gbs, 1),
+            "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
+
+
 def main(argv=None) -> int:
     what = (argv or sys.argv[1:] or ["all"])[0]
     if not available():
@@ -58,6 +69,8 @@ def main(argv=None) -> int:
         for L in CONTEXTS:
             for rows in (1, 2):
                 print(json.dumps({"bench": "attention", **attention(L, rows)}), flush=True)
+    if what in ("copy", "all"):
+        print(json.dumps({"bench": "copy", **copy()}), flush=True)
     return 0
 
 

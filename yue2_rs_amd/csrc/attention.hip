@@ -12,7 +12,7 @@ constexpr int kAttnThreads = 512;
 
 template <int D, int MAXG>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs a) {
-    extern __shared__ float e_s[];  // [G][bpw * 64]
+    extern __shared__ __align__(16) float e_s[];  // [G][bpw * 64]
     attn_group<kAttnThreads, D, MAXG>(a, blockIdx.x, blockIdx.y, blockIdx.z, e_s);
 }
 

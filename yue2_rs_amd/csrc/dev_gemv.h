@@ -112,73 +112,93 @@ __device__ __forceinline__ void gemv_store(float* yp, float acc, float acc2) {
     }
 }
 
-// RMSNorm scale of xs[0..n) (LDS), all NT threads of the block participating.
+// RMSNorm scales of B rows xs[b * n .. b * n + n) (LDS); all NT threads of
+// the block take part, entering together right after a block barrier, and
+// each gets scale[b] for every row.
 // The reference sums the squares in one sequential f32 chain
 // (src/tensor.rs:1144).  The block computes the exact sum E and the bound
 // B = 2^-24 * 1.001 * sum_i t_i (n - i) on that chain's rounding error in f64
 // (each of the n-1 additions errs by at most 2^-24 of its partial sum); the
 // scale rb(1/sqrt(S/n + eps)) is monotone in S, so when both ends of
-// [E - B, E + B] give the same BF16 scale it is the chain's scale.  Every
-// thread evaluates that test on the same per-wave partials (so the outcome is
-// uniform); otherwise thread 0 runs the chain.
-template <int NT>
-__device__ __forceinline__ float norm_scale_block(const float* xs, int n, float eps, int* fallbacks) {
-    __shared__ double red_e[NT / 64], red_w[NT / 64];
-    __shared__ float s_scale;
+// [E - B, E + B] give the same BF16 scale it is the chain's scale.  Lane
+// 2b + e of every wave evaluates end e of row b (all ends at once), and the
+// outcome is read back from those lanes, so it is uniform over the block.
+// A row that is not decided that way gets the chain itself, run by lane 0 of
+// wave b (the rows' chains on different SIMDs at once).
+template <int NT, int B>
+__device__ __forceinline__ void norm_scales_block(const float* xs, int n, float eps, int* fallbacks, float* scale) {
+    static_assert(B <= NT / 64 && 2 * B <= 64, "one wave per fallback chain");
+    constexpr int NW = NT / 64;
+    __shared__ double red_e[B][NW], red_w[B][NW];
+    __shared__ float s_scale[B];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __syncthreads();  // a previous call's readers of red_e / red_w / s_scale are done
-    double e_sum = 0.0, w_sum = 0.0;
+    double e_sum[B], w_sum[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) e_sum[b] = w_sum[b] = 0.0;
     for (int i = tid; i < n; i += NT) {
-        const float t = xs[i] * xs[i];
-        e_sum += (double)t;
-        w_sum += (double)t * (double)(n - i);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float t = xs[b * n + i] * xs[b * n + i];
+            e_sum[b] += (double)t;
+            w_sum[b] += (double)t * (double)(n - i);
+        }
     }
-    e_sum = xor_sum<32>(e_sum);
-    w_sum = xor_sum<32>(w_sum);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        e_sum[b] = xor_sum<32>(e_sum[b]);
+        w_sum[b] = xor_sum<32>(w_sum[b]);
+    }
     if (lane == 0) {
-        red_e[wave] = e_sum;
-        red_w[wave] = w_sum;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            red_e[b][wave] = e_sum[b];
+            red_w[b][wave] = w_sum[b];
+        }
     }
     __syncthreads();
+    const int q = lane % (2 * B), row = q >> 1;
     double e = 0.0, w = 0.0;
 #pragma unroll
-    for (int i = 0; i < NT / 64; ++i) {
-        e += red_e[i];
-        w += red_w[i];
+    for (int i = 0; i < NW; ++i) {
+        e += red_e[row][i];
+        w += red_w[row][i];
     }
-    if (e < 1e300 && w < 1e300) {
-        const double bound = w * 0x1.0p-24 * 1.001 + e * 4e-12;
-        const double lo = e - bound, hi = e + bound;
-        float lo_f = (float)lo, hi_f = (float)hi;
-        if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
-        if (lo_f < 0.0f) lo_f = 0.0f;
-        if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
-        float s_a = 0.0f, s_b = 0.0f;
-#pragma unroll 1
-        for (int t = 0; t < 2; ++t) {  // one copy of the scale arithmetic
-            const float v = norm_scale_from_sum(t ? hi_f : lo_f, n, eps);
-            if (t) s_b = v;
-            else s_a = v;
-        }
-        if (hi_f <= 3.0e38f && s_a == s_b) return s_a;
+    const double bound = w * 0x1.0p-24 * 1.001 + e * 4e-12;
+    const double lo = e - bound, hi = e + bound;
+    float lo_f = (float)lo, hi_f = (float)hi;
+    if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
+    if (lo_f < 0.0f) lo_f = 0.0f;
+    if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
+    const float sv = norm_scale_from_sum((q & 1) ? hi_f : lo_f, n, eps);
+    const bool decided = e < 1e300 && w < 1e300 && hi_f <= 3.0e38f && sv == xor_lane<1>(sv);
+    unsigned okmask = 0;  // bit b: row b's scale decided
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        scale[b] = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(sv), 2 * b));
+        okmask |= (unsigned)__builtin_amdgcn_readlane(decided ? 1 : 0, 2 * b) << b;
     }
-    if (tid == 0) {
-        // the sequential chain itself; LDS reads batched ahead of the adds
+    if (okmask == (1u << B) - 1u) return;
+    if (wave < B && lane == 0 && !((okmask >> wave) & 1u)) {
+        // the sequential chain itself (row `wave`); LDS reads batched ahead
+        // of the adds
+        const float* x = xs + wave * n;
         float sum = -0.0f;
         int i = 0;
         for (; i + 16 <= n; i += 16) {
             float t[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) t[j] = xs[i + j];
+            for (int j = 0; j < 16; ++j) t[j] = x[i + j];
 #pragma unroll
             for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
         }
-        for (; i < n; ++i) sum = sum + xs[i] * xs[i];
-        s_scale = norm_scale_from_sum(sum, n, eps);
+        for (; i < n; ++i) sum = sum + x[i] * x[i];
+        s_scale[wave] = norm_scale_from_sum(sum, n, eps);
         if (fallbacks) add_dev(fallbacks, 1);
     }
     __syncthreads();
-    return s_scale;
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+        if (!((okmask >> b) & 1u)) scale[b] = s_scale[b];
 }
 
 }  // namespace y2

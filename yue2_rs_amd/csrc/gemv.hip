@@ -14,7 +14,7 @@
 //  * the input rows are staged once per workgroup in LDS (f32), and for a
 //    residual epilogue the workgroup's own output rows as well.  With a norm
 //    prologue the workgroup computes the RMSNorm scale itself (guarded, see
-//    norm_scale_block) and stages rb(rb(x * s) * gamma).
+//    norm_scales_block) and stages rb(rb(x * s) * gamma).
 #include <algorithm>
 
 #include "dev_gemv.h"
@@ -29,7 +29,9 @@ constexpr int kGemvThreads = kRingThreads;
 // IT chunks of 8 per lane cover k (k <= 512 IT); chunks past k are masked.
 template <int B, int EPI, int IT, bool NORM>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs a) {
-    extern __shared__ float xs[];  // [B][k] inputs, then [B][kResRows] residual rows
+    // 16-byte aligned whatever the static LDS before it: the staged rows are
+    // read as float4 (a misaligned 16-byte LDS read is split and slow)
+    extern __shared__ __align__(16) float xs[];  // [B][k] inputs, then [B][kResRows] residual rows
     constexpr bool PAIR = EPI == EPI_SWIGLU;
     const int tid = threadIdx.x, k = a.k, n = a.n;
     const int r0 = part_lo(n, blockIdx.x, gridDim.x), r1 = part_lo(n, blockIdx.x + 1, gridDim.x);
@@ -44,12 +46,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs a) {
     }
     __syncthreads();
     if constexpr (NORM) {
-        for (int b = 0; b < B; ++b) {
-            float* xb = xs + b * k;
-            const float s = norm_scale_block<kGemvThreads>(
-                xb, k, a.eps, (blockIdx.x == 0 && a.st) ? &a.st->norm_fallbacks : nullptr);
-            for (int i = tid; i < k; i += kGemvThreads) xb[i] = rb(rb(xb[i] * s) * a.gamma[i]);
-        }
+        float s[B];
+        norm_scales_block<kGemvThreads, B>(xs, k, a.eps, (blockIdx.x == 0 && a.st) ? &a.st->norm_fallbacks : nullptr,
+                                           s);
+        for (int b = 0; b < B; ++b)
+            for (int i = tid; i < k; i += kGemvThreads) xs[b * k + i] = rb(rb(xs[b * k + i] * s[b]) * a.gamma[i]);
         __syncthreads();
     }
     gemv_ring<B, EPI, IT, true>(a.w, a.w2, xs, k, a.y, nullptr, 0, a.y_stride, r0, r1, n, ring, res);

@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
                                                       const float* __restrict__ gamma,
                                                       float* __restrict__ out, int out_stride,
                                                       int n, float eps, StepState* st) {
-    extern __shared__ float xs[];
+    extern __shared__ __align__(16) float xs[];
     __shared__ double red_e[4], red_w[4];
     __shared__ float s_scale;
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

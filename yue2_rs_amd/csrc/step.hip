@@ -92,19 +92,19 @@ __device__ __forceinline__ void load_gamma(const float* g, int k, float* gam) {
 }
 
 // xs[b] = RMSNorm(xs[b]) (Norm::apply, src/tensor.rs:1140-1157) with the
-// gammas of load_gamma.
+// gammas of load_gamma; the rows' scales are decided together.  Entered
+// right after a block barrier.
 template <int B, int N>
 __device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, float eps, int* fallbacks) {
-#pragma unroll 1
-    for (int b = 0; b < B; ++b) {  // one copy of the code for both rows
-        float* xb = xs + b * k;
-        const float s = norm_scale_block<kStepThreads>(xb, k, eps, fallbacks);
+    float s[B];
+    norm_scales_block<kStepThreads, B>(xs, k, eps, fallbacks, s);
+#pragma unroll
+    for (int b = 0; b < B; ++b)
 #pragma unroll
         for (int j = 0; j < N; ++j) {
             const int i = threadIdx.x + j * kStepThreads;
-            if (i < k) xb[i] = rb(rb(xb[i] * s) * gam[j]);
+            if (i < k) xs[b * k + i] = rb(rb(xs[b * k + i] * s[b]) * gam[j]);
         }
-    }
     __syncthreads();
 }
 
@@ -162,7 +162,10 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
 // rows are masked); TRACE: the traced instantiation.
 template <int B, int D, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
-    extern __shared__ float lds[];
+    // 16-byte aligned whatever the static LDS before it: staged inputs and K/V
+    // chunks are read with 16-byte LDS reads, which are split and slow when
+    // misaligned
+    extern __shared__ __align__(16) float lds[];
     __shared__ float res_s[B * kResRows];  // this workgroup's rows of x (residual)
     constexpr int RMAX = std::max(std::max(Ring<ITH, false>::SIZE, Ring<ITH, true>::SIZE),
                                   std::max(Ring<ITQ, false>::SIZE, Ring<ITI, false>::SIZE));

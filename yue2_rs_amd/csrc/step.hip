@@ -72,13 +72,15 @@ __device__ __forceinline__ bool stage(float* xs, const uint64_t* tx, int k, uint
     }
 }
 
-// res[b * n + r] = word tx[b * stride + r0 + r], r < n = r1 - r0 (n <= kResRows):
-// this workgroup's own rows of x, which it wrote itself.
+// res[b * n + r] = xs[b * k + h0 + r], r < n = h1 - h0 <= kResRows: this
+// workgroup's rows of the residual stream, taken from the staged x before it
+// is normalised, for the residual epilogue of the next O or down projection
+// (whose rows [h0, h1) are this workgroup's).  The norm's first barrier
+// orders these reads before its writes to xs.
 template <int B>
-__device__ __forceinline__ bool stage_res(float* res, const uint64_t* tx, int stride, int r0, int r1, uint32_t tag,
-                                          StepState* st) {
-    const int n = r1 - r0;
-    return gather<kStepThreads, 1>(tx + r0, B * n, n, stride, tag, res, st);
+__device__ __forceinline__ void copy_res(float* res, const float* xs, int k, int h0, int h1) {
+    const int n = h1 - h0, t = threadIdx.x;
+    if (t < B * n) res[t] = xs[(t / n) * k + h0 + t % n];
 }
 
 // gam[j] = g[tid + 512 j] for tid + 512 j < k: a norm's gammas, loaded
@@ -180,9 +182,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     Tracer<TRACE> tr{call.trace, call.trace_slots, 0};
     tr.mark();
 
-    // Embedding (src/model.rs:452-464): this workgroup's rows of x as tagged
-    // words (its residual rows for the first O projection), and the whole of
-    // x staged for the first norm, straight from the table.
+    // Embedding (src/model.rs:452-464): the whole of x staged for the first
+    // norm, straight from the table.
     {
         ArgsPtr a = fresh(args);
         const int H = a->hidden, qkvw = (a->heads + 2 * a->kv_heads) * D;
@@ -197,11 +198,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         load_gamma<ITH>(layer_at(a, 0)->in_norm, H, gam);
         prefetch_ring<ITH, false>(layer_at(a, 0)->wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
                                   part_lo(qkvw, wg + 1, nwg), qkvw, ring);
-        const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
-        const uint32_t t_emb = flow_tag(epoch, 0, FK_EMB);
         for (int b = 0; b < B; ++b) {
             const auto* e = gbl(a->embed + (size_t)ids[b] * H);
-            for (int i = h0 + tid; i < h1; i += kStepThreads) st_tag(a->tx + (size_t)b * H + i, bf16(e[i]), t_emb);
             for (int i = tid; i < H; i += kStepThreads) lds[b * H + i] = bf16(e[i]);
         }
         __syncthreads();
@@ -228,6 +226,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 a = fresh(args);
                 if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
             }
+            // this workgroup's rows of x: the residual of the O projection
+            if (!last) copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
             a = fresh(args);
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr);
             tr.mark();
@@ -254,10 +254,6 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
             prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
             a = fresh(args);
-            if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l > 0 ? l - 1 : 0, l > 0 ? FK_XD : FK_EMB),
-                              st))
-                return;
-            a = fresh(args);
             if (!stage<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
@@ -273,6 +269,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg), I, ring);
             a = fresh(args);
             if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
+            // this workgroup's rows of x: the residual of the down projection
+            copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
             a = fresh(args);
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
@@ -288,8 +286,6 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int H = a->hidden, I = a->intermediate;
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
             prefetch_ring<ITI, false, MASKI>(layer_at(a, l)->wd, nullptr, I, h0, h1, H, ring);
-            a = fresh(args);
-            if (!stage_res<B>(res_s, a->tx, H, h0, h1, flow_tag(epoch, l, FK_XO), st)) return;
             a = fresh(args);
             if (!stage<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
             tr.mark();

@@ -45,19 +45,26 @@ __device__ __forceinline__ uint32_t flow_tag(uint32_t epoch, int layer, int kind
     return (epoch << 12) | ((uint32_t)layer << 4) | (uint32_t)kind;
 }
 
-__device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) {
-    const uint64_t w = ((uint64_t)tag << 32) | (uint64_t)f2u(v);
+// A word's 32 value bits hold one f32, or (a packed word) two BF16-exact
+// values: batch row 0 in the low half, row 1 in the high half.
+__device__ __forceinline__ void st_tag_bits(uint64_t* p, uint32_t bits, uint32_t tag) {
+    const uint64_t w = ((uint64_t)tag << 32) | (uint64_t)bits;
     __hip_atomic_store(gblw(p), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_tag(uint64_t* p, float v, uint32_t tag) { st_tag_bits(p, f2u(v), tag); }
+__device__ __forceinline__ uint32_t pack_rows(float row0, float row1) {
+    return (f2u(row0) >> 16) | (f2u(row1) & 0xffff0000u);
 }
 __device__ __forceinline__ uint64_t ld_tag(const uint64_t* p) {
     return __hip_atomic_load(gblw(const_cast<uint64_t*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// dst[i] = value of the word addr(i), i < n, once its tag equals `tag` (dst in
-// LDS).  All NT threads of the block take part; n <= NT * MAXPER.  Returns
-// false (device error set) on timeout; the result is uniform over the block.
-template <int NT, int MAXPER, class Addr>
-__device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float* dst, StepState* st) {
+// put(i, value bits of the word addr(i)), i < n, once its tag equals `tag`
+// (put writes LDS).  All NT threads of the block take part; n <= NT * MAXPER.
+// Returns false (device error set) on timeout; the result is uniform over the
+// block.
+template <int NT, int MAXPER, class Addr, class Put>
+__device__ __forceinline__ bool gather_put(Addr addr, int n, uint32_t tag, Put put, StepState* st) {
     __shared__ int s_fail;
     const int tid = threadIdx.x;
     // every thread has read the previous call's flag before it is reset, and
@@ -77,7 +84,7 @@ __device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float*
 #pragma unroll
         for (int j = 0; j < MAXPER; ++j)
             if (((pend >> j) & 1) && (uint32_t)(w[j] >> 32) == tag) {
-                dst[tid + j * NT] = u2f((uint32_t)w[j]);
+                put(tid + j * NT, (uint32_t)w[j]);
                 pend &= ~(1u << j);
             }
         if (!pend) break;
@@ -91,6 +98,12 @@ __device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float*
     }
     __syncthreads();
     return s_fail == 0;
+}
+
+// dst[i] = value of the word addr(i) (one f32 per word), i < n.
+template <int NT, int MAXPER, class Addr>
+__device__ __forceinline__ bool gather_at(Addr addr, int n, uint32_t tag, float* dst, StepState* st) {
+    return gather_put<NT, MAXPER>(addr, n, tag, [=](int i, uint32_t bits) { dst[i] = u2f(bits); }, st);
 }
 
 // Division by a run-time d >= 1 of numerators i < 2^32 / d: floor(i / d) =
@@ -110,6 +123,18 @@ __device__ __forceinline__ bool gather_flat(const uint64_t* src, int n, uint32_t
     return gather_at<NT, MAXPER>([=](int i) { return src + i; }, n, tag, dst, st);
 }
 
+// Packed words src[0, k): dst[i] = row 0's value of word i, dst[k + i] = row
+// 1's.
+template <int NT, int MAXPER>
+__device__ __forceinline__ bool gather_pair(const uint64_t* src, int k, uint32_t tag, float* dst, StepState* st) {
+    return gather_put<NT, MAXPER>([=](int i) { return src + i; }, k, tag,
+                                  [=](int i, uint32_t bits) {
+                                      dst[i] = bf16_lo(bits);
+                                      dst[k + i] = bf16_hi(bits);
+                                  },
+                                  st);
+}
+
 // The 2-D region src[r * stride + c], r < n / cols, c < cols, row-major.
 template <int NT, int MAXPER>
 __device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, size_t stride, uint32_t tag,
@@ -125,8 +150,11 @@ __device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, siz
 
 // Arguments of one layer's attention in the step kernel.
 struct FlowAttn {
-    const uint64_t* qkv;  // tagged [rows][qkv_stride]: q heads, k heads, v heads
+    // tagged q heads, k heads, v heads: [rows][qkv_stride] words, or (packed)
+    // [qkv_stride] words holding both batch rows
+    const uint64_t* qkv;
     int qkv_stride;
+    bool packed;
     uint16_t* kv_base;  // this batch row's cache: [layers][2][kv_heads][cap][dim] BF16
     int cap, pos, layer, heads, kv_heads, blk_stride, att_stride, wpg;
     float scale, eps;
@@ -188,7 +216,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     const int blk0 = wi * bpw, blk1 = min(nb, blk0 + bpw), nbl = blk1 - blk0;
     const int j0 = blk0 * kBlockKeys, j1 = min(L, blk1 * kBlockKeys), nk = j1 - j0;
     const int estride = bpw * kBlockKeys;
-    const uint64_t* row = a.qkv + (size_t)b * a.qkv_stride;
+    const uint64_t* row = a.qkv + (a.packed ? 0 : (size_t)b * a.qkv_stride);
     uint16_t* Kc = a.kv_base + kv_off(a.layer, 0, a.kv_heads, g, cap, 0, D);
     uint16_t* Vc = a.kv_base + kv_off(a.layer, 1, a.kv_heads, g, cap, 0, D);
     const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
@@ -238,9 +266,13 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         const uint64_t* qsrc = row + (size_t)(g * G) * D;
         const uint64_t* ksrc = row + (size_t)(a.heads + g) * D;
         const uint64_t* vsrc = row + (size_t)(a.heads + a.kv_heads + g) * D;
-        if (!gather_at<NT, ((MAXG + 2) * D + NT - 1) / NT>(
+        // this batch row's half of a packed word
+        const int shift = a.packed ? (b ? 0 : 16) : 0;
+        const uint32_t keep = a.packed ? 0xffff0000u : 0xffffffffu;
+        if (!gather_put<NT, ((MAXG + 2) * D + NT - 1) / NT>(
                 [=](int i) { return i < nq ? qsrc + i : (i < nq + D ? ksrc + (i - nq) : vsrc + (i - nq - D)); },
-                nq + (owns_new ? 2 * D : 0), t_qkv, qkv_s, st))
+                nq + (owns_new ? 2 * D : 0), t_qkv,
+                [=](int i, uint32_t bits) { qkv_s[i] = u2f((bits << shift) & keep); }, st))
             return false;
     }
     mark();

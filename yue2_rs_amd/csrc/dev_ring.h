@@ -125,24 +125,19 @@ __device__ __forceinline__ void dot_item(const float* xs, int k, int seg, const 
 // weight load in flight and drain the ring).
 constexpr int kResRows = 64;
 
-// Output of one row (see gemv_store in dev_gemv.h) as a tagged word, or as
-// a plain float (y_tag == 0: the LM head, read by the next kernel); res =
-// the row's current residual value (EPI_RESID).
+// Output value of one row (see gemv_store in dev_gemv.h); res = the row's
+// current residual value (EPI_RESID).
 template <int EPI>
-__device__ __forceinline__ void store_out(float* y, uint64_t* ty, size_t i, uint32_t tag, float acc, float acc2,
-                                          float res) {
-    float v;
+__device__ __forceinline__ float out_value(float acc, float acc2, float res) {
     if constexpr (EPI == EPI_RAW) {
-        v = acc;
+        return acc;
     } else if constexpr (EPI == EPI_STORE) {
-        v = rb(acc);
+        return rb(acc);
     } else if constexpr (EPI == EPI_RESID) {
-        v = rb(res + rb(acc));
+        return rb(res + rb(acc));
     } else {
-        v = rb(silu_rb(rb(acc)) * rb(acc2));
+        return rb(silu_rb(rb(acc)) * rb(acc2));
     }
-    if (ty) st_tag(ty + i, v, tag);
-    else gblw(y)[i] = v;
 }
 
 // Issue the first R-1 items of this wave's rows [r0, r1) into ring slots.
@@ -164,9 +159,11 @@ __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t*
 // epilogue EPI, written as tagged words to ty (or as floats to y when ty is
 // null); the ring holds the first R-1 items (prefetch_ring).  res: for
 // EPI_RESID, res[b * (r1 - r0) + (row - r0)] = the row's current value (LDS).
+// PACK (B == 2, the outputs BF16-exact): one packed word per row holds both
+// batch rows (ty[row]); y_stride then only applies to y.
 // (Writing the new value back to res here instead of re-reading it later
 // measured slower: the GEMVs of the whole kernel lost about half their rate.)
-template <int B, int EPI, int IT, bool MASK = false>
+template <int B, int EPI, int IT, bool MASK = false, bool PACK = false>
 __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
                                           float* y, uint64_t* ty, uint32_t tag, int y_stride, int r0, int r1,
                                           int n, uint4* ring, const float* res = nullptr) {
@@ -200,12 +197,23 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
                     acc[b] = acc2[b] = 0.0f;
                 }
                 if (lane == 0) {
-                    // one copy of the epilogue for the batch rows
+                    if (PACK && ty) {
+                        static_assert(!PACK || B == 2, "packed words hold two batch rows");
+                        float o[B];
+#pragma unroll
+                        for (int b = 0; b < B; ++b)
+                            o[b] = out_value<EPI>(v[b], v2[b], EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f);
+                        st_tag_bits(ty + row, pack_rows(o[0], o[B - 1]), tag);
+                    } else {
+                        // one copy of the epilogue for the batch rows
 #pragma unroll 1
-                    for (int b = 0; b < B; ++b) {
-                        const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
-                        store_out<EPI>(y, ty, (size_t)b * y_stride + row, tag, b == 0 ? v[0] : v[B - 1],
-                                       b == 0 ? v2[0] : v2[B - 1], rv);
+                        for (int b = 0; b < B; ++b) {
+                            const float rv = EPI == EPI_RESID ? res[b * span + (row - r0)] : 0.0f;
+                            const float o = out_value<EPI>(b == 0 ? v[0] : v[B - 1], b == 0 ? v2[0] : v2[B - 1], rv);
+                            const size_t i = (size_t)b * y_stride + row;
+                            if (ty) st_tag(ty + i, o, tag);
+                            else gblw(y)[i] = o;
+                        }
                     }
                 }
             }

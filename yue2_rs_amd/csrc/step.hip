@@ -58,17 +58,28 @@ struct Tracer {
 
 // ---- staging and norms -----------------------------------------------------
 
-// xs[b * k + i] = word tx[b * k + i] with the given tag, for b < B, i < k.
+// Batch rows of x, the SwiGLU activations and q/k/v are BF16-exact, so with
+// two rows one packed word carries both (half the words to poll).
+template <int B>
+constexpr bool kPack = B == 2;
+
+// xs[b * k + i] = word tx[b * k + i] with the given tag, for b < B, i < k
+// (words of one f32 each).
 template <int B, int N>
 __device__ __forceinline__ bool stage(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
-    if constexpr (B * N <= 16) {
-        return gather_flat<kStepThreads, B * N>(tx, B * k, tag, xs, st);
+    static_assert(B * N <= 16, "at most 16 words per thread in flight");
+    return gather_flat<kStepThreads, B * N>(tx, B * k, tag, xs, st);
+}
+
+// xs[b * k + i] = row b's value of x-like words tx (packed for two rows,
+// else tx[b * k + i]), i < k.
+template <int B, int N>
+__device__ __forceinline__ bool stage_rows(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
+    if constexpr (kPack<B>) {
+        static_assert(N <= 16, "at most 16 words per thread in flight");
+        return gather_pair<kStepThreads, N>(tx, k, tag, xs, st);
     } else {
-        // one row at a time: 16 words in flight per thread at most
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-            if (!gather_flat<kStepThreads, N>(tx + (size_t)b * k, k, tag, xs + b * k, st)) return false;
-        return true;
+        return stage<B, N>(xs, tx, k, tag, st);
     }
 }
 
@@ -132,10 +143,11 @@ __device__ __forceinline__ ArgsPtr fresh(ArgsPtr p) {
 // The attention arguments of layer l for batch row b (field by field: a
 // struct copy cannot bind to the constant address space).
 __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int b, int l, uint32_t epoch,
-                                               int wpg, int D) {
+                                               int wpg, int D, bool packed) {
     FlowAttn f;
     f.qkv = a->tqkv;
     f.qkv_stride = (a->heads + 2 * a->kv_heads) * D;
+    f.packed = packed;
     f.kv_base = b == 0 ? kv.base[0] : kv.base[1];  // selects: no indexed struct copy
     f.cap = b == 0 ? kv.capacity[0] : kv.capacity[1];
     f.pos = *gbl(&a->st->pos[b]);
@@ -224,7 +236,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 load_gamma<ITH>(last ? a->final_norm : layer_at(a, lc)->in_norm, H, gam);
                 prefetch_ring<ITH, false>(w, nullptr, H, r0, r1, n, ring);
                 a = fresh(args);
-                if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
+                if (!stage_rows<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
             }
             // this workgroup's rows of x: the residual of the O projection
             if (!last) copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
@@ -232,7 +244,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH>(w, nullptr, lds, H, last ? a->logits : nullptr, last ? nullptr : a->tqkv,
+            gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(w, nullptr, lds, H, last ? a->logits : nullptr, last ? nullptr : a->tqkv,
                                          flow_tag(epoch, l, FK_QKV), n, r0, r1, n, ring);
             tr.mark();
         }
@@ -242,7 +254,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int groups = a->kv_heads * B, wpg = nwg / groups;
             const int group = wg / wpg, kvh = a->kv_heads;
-            const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D);
+            const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
             if (!attn_flow<kStepThreads, D, 4>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
                 return;
             tr.mark();
@@ -257,7 +269,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             if (!stage<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITQ>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
+            gemv_ring<B, EPI_RESID, ITQ, false, kPack<B>>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
         }
@@ -268,14 +280,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             load_gamma<ITH>(layer_at(a, l)->post_norm, H, gam);
             prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg), I, ring);
             a = fresh(args);
-            if (!stage<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
+            if (!stage_rows<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
             // this workgroup's rows of x: the residual of the down projection
             copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
             a = fresh(args);
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_SWIGLU, ITH>(layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact,
+            gemv_ring<B, EPI_SWIGLU, ITH, false, kPack<B>>(layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact,
                                           flow_tag(epoch, l, FK_ACT), I, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg),
                                           I, ring);
             tr.mark();
@@ -287,10 +299,10 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
             prefetch_ring<ITI, false, MASKI>(layer_at(a, l)->wd, nullptr, I, h0, h1, H, ring);
             a = fresh(args);
-            if (!stage<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
+            if (!stage_rows<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITI, MASKI>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
+            gemv_ring<B, EPI_RESID, ITI, MASKI, kPack<B>>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
                                          H, h0, h1, H, ring, res_s);
             tr.mark();
         }

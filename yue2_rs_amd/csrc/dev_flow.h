@@ -197,7 +197,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     constexpr int PER = (kAttnChunk * BLK_U4 + NT - 1) / NT;  // uint4 per thread per chunk
     constexpr int HALF = D / 2;
     // the group's queries, then (owner of the new key) its key and value rows
-    __shared__ float qkv_s[(MAXG + 2) * D];
+    __shared__ __align__(16) float qkv_s[(MAXG + 2) * D];  // read as float4 in the scores
     float(*q_s)[D] = reinterpret_cast<float(*)[D]>(qkv_s);
     __shared__ float hscale[MAXG + 1];
     __shared__ float m_s[MAXG], t_s[MAXG];
@@ -324,14 +324,18 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     mark();
 
     // ---- phase 1: scaled scores and block maxima ---------------------------
+    // The DOT order of a score (one fma chain per 8-dim chunk, then the xor
+    // butterfly over the chunks, largest distance first): lane c of a
+    // SCPL-lane key group keeps the chains of chunks c, c + SCPL, ... and
+    // adds them in-lane in the butterfly's order (its distances of SCPL and
+    // more), then the group's lanes finish with the distances below SCPL.
     const uint32_t t_bmax = flow_tag(a.epoch, a.layer, FK_BMAX);
     {
-        const int c = lane % CPL, kk = lane / CPL;
-        float qv[MAXG][8];
-#pragma unroll
-        for (int h = 0; h < MAXG; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qv[h][e] = h < G ? q_s[h][8 * c + e] : 0.0f;
+        constexpr int SCPL = 4;              // lanes per key
+        constexpr int NCH = D / 8 / SCPL;    // chains per lane
+        constexpr int SKPW = 64 / SCPL;      // keys per wave pass
+        static_assert(NCH >= 1 && (NCH & (NCH - 1)) == 0, "chains per lane");
+        const int c = lane % SCPL, kk = lane / SCPL;
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
                 // a later chunk (long contexts): stage it, then patch the new key
@@ -346,18 +350,31 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                 __syncthreads();
             }
             const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
-            for (int kg = wave; kg * KPW < keys; kg += NW) {
-                const int kl = kg * KPW + kk;  // key within the chunk
+            for (int kg = wave; kg * SKPW < keys; kg += NW) {
+                const int kl = kg * SKPW + kk;  // key within the chunk (rows past `keys` are never stored)
                 const int j = j0 + cb * kBlockKeys + kl;
-                float kf[8];
-                unpack8a(Ks[(size_t)kl * (D / 8) + c], kf);
+                float kf[NCH][8];
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) unpack8a(Ks[(size_t)kl * (D / 8) + c + SCPL * i], kf[i]);
 #pragma unroll
                 for (int h = 0; h < MAXG; ++h) {
                     if (h >= G) break;
-                    float acc = 0.0f;
+                    float ch[NCH];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[h][e], kf[e], acc);
-acc = xor_sum<CPL / 2>(acc);
+                    for (int i = 0; i < NCH; ++i) {
+                        const float4* qp = reinterpret_cast<const float4*>(q_s[h] + 8 * (c + SCPL * i));
+                        const float4 q0 = qp[0], q1 = qp[1];
+                        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[e], kf[i][e], acc);
+                        ch[i] = acc;
+                    }
+#pragma unroll
+                    for (int m = NCH / 2; m >= 1; m /= 2)
+#pragma unroll
+                        for (int i = 0; i < m; ++i) ch[i] = ch[i] + ch[i + m];
+                    const float acc = xor_sum<SCPL / 2>(ch[0]);
                     if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
                 }
             }

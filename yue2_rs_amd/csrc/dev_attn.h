@@ -305,19 +305,19 @@ v = xor_sum<32>(v);
             for (int h = 0; h < MAXG; ++h)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+            // no branch per key: keys past the context have zero V rows and
+            // p = 0, and fma(0, 0, acc) = acc (a chain from +0 is never -0)
 #pragma unroll
             for (int i = 0; i < kBlockKeys / S; ++i) {
                 const int jj = t + S * i;
-                if (jb + jj < L) {
-                    float vf[8];
-                    unpack8a(vr[i], vf);
+                float vf[8];
+                unpack8a(vr[i], vf);
 #pragma unroll
-                    for (int h = 0; h < MAXG; ++h) {
-                        if (h >= G) break;
-                        const float p = e_s[h * estride + bl * kBlockKeys + jj];
+                for (int h = 0; h < MAXG; ++h) {
+                    if (h >= G) break;
+                    const float p = jb + jj < L ? e_s[h * estride + bl * kBlockKeys + jj] : 0.0f;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p, vf[e], acc[h][e]);
-                    }
+                    for (int e = 0; e < 8; ++e) acc[h][e] = __builtin_fmaf(p, vf[e], acc[h][e]);
                 }
             }
 #pragma unroll

@@ -403,8 +403,9 @@ m = xor_max<32>(m);
             if (lane == 0) m_s[h] = m;
         }
         __syncthreads();
+        const FastDiv fnk(nk);
         for (int i = tid; i < G * nk; i += NT) {
-            const int h = i / nk, jl = i % nk;
+            const int h = fnk.div(i), jl = i - h * nk;
             e_s[h * estride + jl] = expf_cr(e_s[h * estride + jl] - m_s[h]);
         }
         __syncthreads();
@@ -430,8 +431,9 @@ v = xor_sum<32>(v);
             t_s[tid] = tot;
         }
         __syncthreads();
+        const FastDiv fnk(nk);
         for (int i = tid; i < G * nk; i += NT) {
-            const int h = i / nk, jl = i % nk;
+            const int h = fnk.div(i), jl = i - h * nk;
             e_s[h * estride + jl] = e_s[h * estride + jl] / t_s[h];
         }
         __syncthreads();
@@ -456,16 +458,18 @@ v = xor_sum<32>(v);
                 float acc[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+                // no branch per key, so the LDS reads of several keys are in
+                // flight at once: keys past the context have zero V rows
+                // (staged so) and p = 0, and fma(0, 0, acc) = acc (a chain
+                // from +0 is never -0)
 #pragma unroll 4
                 for (int i = 0; i < kBlockKeys / S; ++i) {
                     const int jj = t + S * i;
-                    if (jb + jj < L) {
-                        float vf[8];
-                        unpack8a(Vs[(size_t)(bc * kBlockKeys + jj) * (D / 8) + c], vf);
-                        const float p = e_s[h * estride + bl * kBlockKeys + jj];
+                    float vf[8];
+                    unpack8a(Vs[(size_t)(bc * kBlockKeys + jj) * (D / 8) + c], vf);
+                    const float p = jb + jj < L ? e_s[h * estride + bl * kBlockKeys + jj] : 0.0f;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
-                    }
+                    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
                 }
 #pragma unroll
                 for (int e = 0; e < 8; ++e) acc[e] = xor_sum<32, CPL>(acc[e]);

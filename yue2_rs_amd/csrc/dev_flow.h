@@ -148,6 +148,23 @@ __device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, siz
         n, tag, dst, st);
 }
 
+// v[0] + v[1] + ... + v[n-1] (n >= 1) added left to right, the LDS reads
+// issued eight at a time ahead of their adds (a loop of read-then-add would
+// wait out the LDS latency at every element).
+__device__ __forceinline__ float sum_left_to_right(const float* v, int n) {
+    float s = v[0];
+    int k = 1;
+    for (; k + 8 <= n; k += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = v[k + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = s + t[j];
+    }
+    for (; k < n; ++k) s = s + v[k];
+    return s;
+}
+
 // Arguments of one layer's attention in the step kernel.
 struct FlowAttn {
     // tagged q heads, k heads, v heads: [rows][qkv_stride] words, or (packed)
@@ -184,25 +201,30 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 //  - K and V go through LDS (kAttnChunk blocks at a time), and the owner of
 //    the newest key uses its freshly computed row from there, so the cache
 //    append needs no completion wait;
-//  - PV runs one (block, head) item per wave.
-// lds: attn_flow_lds(G, D, bpw) bytes.  false: timeout (error set).
-template <int NT, int D, int MAXG, class Mark>
+//  - PV runs one (block, half of the dims) item per wave, for all heads.
+// G = heads / kv_heads, the query heads of a group (the host checks that the
+// launch's shape has this G).  lds: attn_flow_lds(G, D, bpw) bytes.  false:
+// timeout (error set).
+template <int NT, int D, int G, class Mark>
 __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark) {
     constexpr int NW = NT / 64;
-    constexpr int CPL = D / 8;     // lanes per key row
-    constexpr int KPW = 64 / CPL;  // keys per wave pass
-    constexpr int S = KPW;         // PV key streams per 64-key block
+    constexpr int S = 512 / D;     // PV key streams per 64-key block
     constexpr int MAXNB = 24576 / kBlockKeys;
     constexpr int BLK_U4 = kBlockKeys * D / 8;           // uint4 per staged block
     constexpr int PER = (kAttnChunk * BLK_U4 + NT - 1) / NT;  // uint4 per thread per chunk
     constexpr int HALF = D / 2;
     // the group's queries, then (owner of the new key) its key and value rows
-    __shared__ __align__(16) float qkv_s[(MAXG + 2) * D];  // read as float4 in the scores
+    __shared__ __align__(16) float qkv_s[(G + 2) * D];  // read as float4 in the scores
     float(*q_s)[D] = reinterpret_cast<float(*)[D]>(qkv_s);
-    __shared__ float hscale[MAXG + 1];
-    __shared__ float m_s[MAXG], t_s[MAXG];
-    __shared__ float red_s[MAXG * MAXNB];
+    __shared__ float hscale[G + 1];
+    __shared__ float m_s[G], t_s[G];
+    __shared__ float red_s[G * MAXNB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The group size through an opaque copy outside the PV: with the count
+    // known, the compiler keeps more of the attention's per-head values live
+    // across the layer loop than the kernel has registers for (it spills).
+    int Gq = G;
+    asm volatile("" : "+s"(Gq));
     StepState* st = a.st;
     const int pos = a.pos, L = pos + 1, cap = a.cap;
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
@@ -212,17 +234,16 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         for (int i = 0; i < 6; ++i) mark();  // keep the trace slots aligned
         return true;
     }
-    const int G = a.heads / a.kv_heads;
     const int blk0 = wi * bpw, blk1 = min(nb, blk0 + bpw), nbl = blk1 - blk0;
     const int j0 = blk0 * kBlockKeys, j1 = min(L, blk1 * kBlockKeys), nk = j1 - j0;
     const int estride = bpw * kBlockKeys;
     const uint64_t* row = a.qkv + (a.packed ? 0 : (size_t)b * a.qkv_stride);
     uint16_t* Kc = a.kv_base + kv_off(a.layer, 0, a.kv_heads, g, cap, 0, D);
     uint16_t* Vc = a.kv_base + kv_off(a.layer, 1, a.kv_heads, g, cap, 0, D);
-    const size_t hbase = ((size_t)b * a.heads + (size_t)g * G) * a.blk_stride;
+    const size_t hbase = ((size_t)b * a.heads + (size_t)g * Gq) * a.blk_stride;
     const bool owns_new = j1 == L;
     const uint32_t t_qkv = flow_tag(a.epoch, a.layer, FK_QKV);
-    float* k_s = qkv_s + G * D;
+    float* k_s = qkv_s + Gq * D;
     float* v_s = k_s + D;
     uint4* Ks = reinterpret_cast<uint4*>(lds);  // [kAttnChunk * 64][D / 8]
     uint4* Vs = Ks + kAttnChunk * BLK_U4;
@@ -250,11 +271,11 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     load_chunk(Kc, 0, kr);
     load_chunk(Vc, 0, vr);
     // RoPE / QK-norm constants of the (head, d) pair this thread rotates
-    const int pairs = (G + (owns_new ? 1 : 0)) * HALF;
+    const int pairs = (Gq + (owns_new ? 1 : 0)) * HALF;
     float c_cos = 0.0f, c_sin = 0.0f, c_g0 = 0.0f, c_g1 = 0.0f;
     if (tid < pairs) {
         const int h = tid / HALF, d = tid % HALF;
-        const float* gam = h < G ? a.q_norm : a.k_norm;
+        const float* gam = h < Gq ? a.q_norm : a.k_norm;
         c_g0 = gbl(gam)[d];
         c_g1 = gbl(gam)[d + HALF];
         c_cos = gbl(a.cos_t + (size_t)pos * HALF)[d];
@@ -262,14 +283,14 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     }
     {
         // one gather for all three: a single wait
-        const int nq = G * D;
-        const uint64_t* qsrc = row + (size_t)(g * G) * D;
+        const int nq = Gq * D;
+        const uint64_t* qsrc = row + (size_t)(g * Gq) * D;
         const uint64_t* ksrc = row + (size_t)(a.heads + g) * D;
         const uint64_t* vsrc = row + (size_t)(a.heads + a.kv_heads + g) * D;
         // this batch row's half of a packed word
         const int shift = a.packed ? (b ? 0 : 16) : 0;
         const uint32_t keep = a.packed ? 0xffff0000u : 0xffffffffu;
-        if (!gather_put<NT, ((MAXG + 2) * D + NT - 1) / NT>(
+        if (!gather_put<NT, ((G + 2) * D + NT - 1) / NT>(
                 [=](int i) { return i < nq ? qsrc + i : (i < nq + D ? ksrc + (i - nq) : vsrc + (i - nq - D)); },
                 nq + (owns_new ? 2 * D : 0), t_qkv,
                 [=](int i, uint32_t bits) { qkv_s[i] = u2f((bits << shift) & keep); }, st))
@@ -277,8 +298,8 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     }
     mark();
     // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
-    if (tid < G || (owns_new && tid == G)) {
-        const float* v = tid < G ? q_s[tid] : k_s;
+    if (tid < Gq || (owns_new && tid == Gq)) {
+        const float* v = tid < Gq ? q_s[tid] : k_s;
         float sum = -0.0f;
         for (int d = 0; d < D; d += 16) {
             float t[16];
@@ -296,7 +317,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     // cache for later steps and straight into the staged chunk for this one
     if (tid < pairs) {
         const int h = tid / HALF, d = tid % HALF;
-        float* v = h < G ? q_s[h] : k_s;
+        float* v = h < Gq ? q_s[h] : k_s;
         const float s = hscale[h];
         const float x0 = rb(rb(v[d] * s) * c_g0);
         const float x1 = rb(rb(v[d + HALF] * s) * c_g1);
@@ -304,7 +325,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         const float y1 = rb(rb(x1 * c_cos) + rb(x0 * c_sin));
         v[d] = y0;
         v[d + HALF] = y1;
-        if (h == G) {
+        if (h == Gq) {
             gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
             gblw(Kc)[(size_t)pos * D + d + HALF] = bf16_bits(y1);
             if (pos - j0 < kAttnChunk * kBlockKeys) {
@@ -357,8 +378,8 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
 #pragma unroll
                 for (int i = 0; i < NCH; ++i) unpack8a(Ks[(size_t)kl * (D / 8) + c + SCPL * i], kf[i]);
 #pragma unroll
-                for (int h = 0; h < MAXG; ++h) {
-                    if (h >= G) break;
+                for (int h = 0; h < G; ++h) {
+                    if (h >= Gq) break;
                     float ch[NCH];
 #pragma unroll
                     for (int i = 0; i < NCH; ++i) {
@@ -380,7 +401,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             }
         }
         __syncthreads();
-        for (int i = wave; i < G * nbl; i += NW) {
+        for (int i = wave; i < Gq * nbl; i += NW) {
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
@@ -393,10 +414,10 @@ m = xor_max<32>(m);
     // ---- phase 2: M, exp(s - M) and block sums -----------------------------
     const uint32_t t_bsum = flow_tag(a.epoch, a.layer, FK_BSUM);
     {
-        if (!gather<NT, (MAXG * MAXNB + NT - 1) / NT>(a.bmax + hbase, G * nb, nb, a.blk_stride, t_bmax, red_s, st))
+        if (!gather<NT, (G * MAXNB + NT - 1) / NT>(a.bmax + hbase, Gq * nb, nb, a.blk_stride, t_bmax, red_s, st))
             return false;
         mark();
-        for (int h = wave; h < G; h += NW) {
+        for (int h = wave; h < Gq; h += NW) {
             float m = -__builtin_huge_valf();
             for (int i = lane; i < nb; i += 64) m = fmaxf(m, red_s[h * nb + i]);
 m = xor_max<32>(m);
@@ -404,12 +425,12 @@ m = xor_max<32>(m);
         }
         __syncthreads();
         const FastDiv fnk(nk);
-        for (int i = tid; i < G * nk; i += NT) {
+        for (int i = tid; i < Gq * nk; i += NT) {
             const int h = fnk.div(i), jl = i - h * nk;
             e_s[h * estride + jl] = expf_cr(e_s[h * estride + jl] - m_s[h]);
         }
         __syncthreads();
-        for (int i = wave; i < G * nbl; i += NW) {
+        for (int i = wave; i < Gq * nbl; i += NW) {
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
@@ -421,23 +442,36 @@ v = xor_sum<32>(v);
     // ---- phase 3: total, p = e / total, partial PV -------------------------
     const uint32_t t_part = flow_tag(a.epoch, a.layer, FK_PART);
     {
-        if (!gather<NT, (MAXG * MAXNB + NT - 1) / NT>(a.bsum + hbase, G * nb, nb, a.blk_stride, t_bsum, red_s, st))
+        if (!gather<NT, (G * MAXNB + NT - 1) / NT>(a.bsum + hbase, Gq * nb, nb, a.blk_stride, t_bsum, red_s, st))
             return false;
         mark();
-        if (tid < G) {
-            // block sums added left to right
-            float tot = red_s[tid * nb];
-            for (int i = 1; i < nb; ++i) tot = tot + red_s[tid * nb + i];
-            t_s[tid] = tot;
+        if (tid < Gq) t_s[tid] = sum_left_to_right(red_s + tid * nb, nb);  // block sums
+        __syncthreads();
+        // p = e / total into the K region (the scores are done with it), in
+        // stream order: p_s[h * estride + bl * 64 + t * KPS + i] is p of key
+        // t + S * i of block bl, so a lane reads four keys of its stream at
+        // once.  Keys past the context get p = 0.
+        constexpr int KPS = kBlockKeys / S;  // keys per stream
+        float* p_s = reinterpret_cast<float*>(Ks);
+        {
+            const int span = nbl * kBlockKeys;
+            const FastDiv fsp(span);
+            for (int i = tid; i < Gq * span; i += NT) {
+                const int h = fsp.div(i), jl = i - h * span;
+                const int jj = jl & (kBlockKeys - 1);
+                const float pv = jl < nk ? e_s[h * estride + jl] / t_s[h] : 0.0f;
+                p_s[h * estride + (jl - jj) + (jj % S) * KPS + jj / S] = pv;
+            }
         }
         __syncthreads();
-        const FastDiv fnk(nk);
-        for (int i = tid; i < G * nk; i += NT) {
-            const int h = fnk.div(i), jl = i - h * nk;
-            e_s[h * estride + jl] = e_s[h * estride + jl] / t_s[h];
-        }
-        __syncthreads();
-        const int t = lane / CPL, c = lane % CPL;
+        // PV: one (block, half of the dims) item per wave, all G heads at
+        // once (V read and unpacked once for them).  Lane (t, c): stream t,
+        // dims d0 .. d0 + 3.  The chains are branch-free: keys past the
+        // context have zero V rows (staged so) and p = 0, and fma(0, 0, acc)
+        // = acc (a chain from +0 is never -0).
+        constexpr int LPS = 64 / S;  // lanes per stream
+        static_assert(LPS * 4 * 2 == D, "two 4-dim parts per lane group");
+        const int t = lane / LPS, c = lane % LPS;
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
                 __syncthreads();
@@ -451,33 +485,48 @@ v = xor_sum<32>(v);
                 __syncthreads();
             }
             const int cblocks = min(kAttnChunk, nbl - cb);
-            // one (block, head) item per wave
-            for (int it = wave; it < cblocks * G; it += NW) {
-                const int bc = it / G, h = it % G, bl = cb + bc;
-                const int jb = (blk0 + bl) * kBlockKeys;
-                float acc[8];
+            for (int it = wave; it < cblocks * 2; it += NW) {
+                const int bc = it >> 1, bl = cb + bc, d0 = (it & 1) * (D / 2) + 4 * c;
+                const uint16_t* vrow = reinterpret_cast<const uint16_t*>(Vs) + (size_t)(bc * kBlockKeys + t) * D + d0;
+                const float* pp = p_s + bl * kBlockKeys + t * KPS;
+                float acc[G][4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-                // no branch per key, so the LDS reads of several keys are in
-                // flight at once: keys past the context have zero V rows
-                // (staged so) and p = 0, and fma(0, 0, acc) = acc (a chain
-                // from +0 is never -0)
-#pragma unroll 4
-                for (int i = 0; i < kBlockKeys / S; ++i) {
-                    const int jj = t + S * i;
-                    float vf[8];
-                    unpack8a(Vs[(size_t)(bc * kBlockKeys + jj) * (D / 8) + c], vf);
-                    const float p = jb + jj < L ? e_s[h * estride + bl * kBlockKeys + jj] : 0.0f;
+                for (int h = 0; h < G; ++h)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
+                    for (int e = 0; e < 4; ++e) acc[h][e] = 0.0f;
+#pragma unroll 1
+                for (int i0 = 0; i0 < KPS; i0 += 4) {
+                    // four keys' V and the G heads' p requested together
+                    uint2 w[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const uint2*>(vrow + (size_t)S * (i0 + u) * D);
+                    float4 p4[G];
+#pragma unroll
+                    for (int h = 0; h < G; ++h)
+                        p4[h] = *reinterpret_cast<const float4*>(pp + h * estride + i0);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float vf[4] = {bf16_lo(w[u].x), bf16_hi(w[u].x), bf16_lo(w[u].y), bf16_hi(w[u].y)};
+#pragma unroll
+                        for (int h = 0; h < G; ++h) {
+                            const float pv = u == 0 ? p4[h].x : u == 1 ? p4[h].y : u == 2 ? p4[h].z : p4[h].w;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pv, vf[e], acc[h][e]);
+                        }
+                    }
                 }
+                // streams combined in the butterfly order (distances S/2 .. 1
+                // between streams = lane distances 32 .. LPS); the S stream
+                // lanes then hold the same sums and each stores its share
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] = xor_sum<32, CPL>(acc[e]);
-                // the S stream lanes hold the same sums: each stores 8 / S of them
-                uint64_t* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
+                for (int h = 0; h < G; ++h) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (e % S == t) st_tag(dst + e, acc[e], t_part);
+                    for (int e = 0; e < 4; ++e) {
+                        const float v = xor_sum<32, LPS>(acc[h][e]);
+                        if ((h * 4 + e) % S == t)
+                            st_tag(a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + d0 + e, v, t_part);
+                    }
+                }
             }
         }
     }
@@ -485,7 +534,7 @@ v = xor_sum<32>(v);
 
     // ---- merge: workgroup wi adds the blocks of outputs [o0, o1) -----------
     {
-        const int outs = G * D, chunk = (outs + W - 1) / W;
+        const int outs = Gq * D, chunk = (outs + W - 1) / W;
         const int o0 = min(outs, wi * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
         __syncthreads();  // the K/V region is reused below
         float* m_buf = lds;  // [no][nb]: partial of block k for output o0 + i
@@ -506,10 +555,8 @@ v = xor_sum<32>(v);
         }
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
         for (int i = tid; i < no; i += NT) {
-            const float* pp = m_buf + i * nb;
-            float o = pp[0];
-            for (int k = 1; k < nb; ++k) o = o + pp[k];  // blocks left to right
-            st_tag(a.att + (size_t)b * a.att_stride + (size_t)g * G * D + o0 + i, rb(o), t_att);
+            const float o = sum_left_to_right(m_buf + i * nb, nb);  // blocks left to right
+            st_tag(a.att + (size_t)b * a.att_stride + (size_t)g * Gq * D + o0 + i, rb(o), t_att);
         }
     }
     return true;

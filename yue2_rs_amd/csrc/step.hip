@@ -172,9 +172,10 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
     return f;
 }
 
-// MASKI: the intermediate size is short of 512 * ITI (the down projection's
-// rows are masked); TRACE: the traced instantiation.
-template <int B, int D, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE>
+// G: query heads per KV head; MASKI: the intermediate size is short of
+// 512 * ITI (the down projection's rows are masked); TRACE: the traced
+// instantiation.
+template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
     // 16-byte aligned whatever the static LDS before it: staged inputs and K/V
     // chunks are read with 16-byte LDS reads, which are split and slow when
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int groups = a->kv_heads * B, wpg = nwg / groups;
             const int group = wg / wpg, kvh = a->kv_heads;
             const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
-            if (!attn_flow<kStepThreads, D, 4>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
+            if (!attn_flow<kStepThreads, D, G>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
                 return;
             tr.mark();
         }
@@ -312,32 +313,38 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     if (wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
 }
 
-template <int B, int D, int ITH, int ITQ, int ITI, bool MASKI>
+template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
 static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCall& call, int nwg, size_t lds) {
     if (call.trace)
-        step_kernel<B, D, ITH, ITQ, ITI, MASKI, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
     else
-        step_kernel<B, D, ITH, ITQ, ITI, MASKI, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
     return hipGetLastError();
 }
 
-// Shapes with a compiled step kernel: {head_dim, iterations for hidden,
-// for heads*head_dim, for intermediate}.
+// Shapes with a compiled step kernel: {head_dim, query heads per KV head,
+// iterations for hidden, for heads*head_dim, for intermediate}.
 bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const int ith = (c.hidden_size / 8 + 63) / 64, itq = (c.num_attention_heads * c.head_dim / 8 + 63) / 64;
     const int iti = (c.intermediate_size / 8 + 63) / 64;
     // hidden and heads * head_dim exactly 512 * IT (their GEMVs are unmasked)
     const bool exact = c.hidden_size == 512 * ith && c.num_attention_heads * c.head_dim == 512 * itq;
-    // (the head_dim-128 kernel also takes the intermediate size as exactly 512 * 16)
-    const bool shape = exact && ((c.head_dim == 128 && ith == 6 && itq == 6 && c.intermediate_size == 512 * 16) ||
-                                 (c.head_dim == 64 && ith == 2 && itq == 2 && iti == 6));
+    // (the head_dim-128 kernel also takes the intermediate size as exactly 512 * 16,
+    // and each kernel one group size)
+    const int G = c.num_key_value_heads > 0 ? c.num_attention_heads / c.num_key_value_heads : 0;
+    const bool grouped = G * c.num_key_value_heads == c.num_attention_heads;
+    const bool shape =
+        exact && grouped &&
+        ((c.head_dim == 128 && G == 3 && ith == 6 && itq == 6 && c.intermediate_size == 512 * 16) ||
+         (c.head_dim == 64 && G == 4 && ith == 2 && itq == 2 && iti == 6));
     if (!shape || rows < 1 || rows > 2 || nwg % (c.num_key_value_heads * rows) != 0) return false;
-    const int G = c.num_attention_heads / c.num_key_value_heads;
     const int wpg = nwg / (c.num_key_value_heads * rows);
     const int max_blocks = (c.max_position_embeddings + kBlockKeys - 1) / kBlockKeys;
     const int bpw = (max_blocks + wpg - 1) / wpg;
+    // the attention's p (G x bpw blocks of f32) is staged in its K region
     return G <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows && max_blocks <= 24576 / kBlockKeys &&
-           G * c.head_dim * bpw + max_blocks <= kStepThreads * kMergePer;
+           G * c.head_dim * bpw + max_blocks <= kStepThreads * kMergePer &&
+           G * bpw * kBlockKeys * 4 <= kAttnChunk * kBlockKeys * c.head_dim * 2;
 }
 
 size_t step_lds_bytes(const StepArgs& a, int nwg) {
@@ -352,14 +359,14 @@ size_t step_lds_bytes(const StepArgs& a, int nwg) {
 hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {
     const size_t lds = step_lds_bytes(a, nwg);
     if (lds > kStepLdsMax) return hipErrorInvalidValue;
-    const int ith = (a.hidden / 8 + 63) / 64;
-    if (a.head_dim == 128 && ith == 6 && a.intermediate == 512 * 16) {
-        if (a.rows == 1) return launch_step_t<1, 128, 6, 6, 16, false>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 128, 6, 6, 16, false>(s, dev, call, nwg, lds);
+    const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
+    if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16) {
+        if (a.rows == 1) return launch_step_t<1, 128, 3, 6, 6, 16, false>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 128, 3, 6, 6, 16, false>(s, dev, call, nwg, lds);
     }
-    if (a.head_dim == 64 && ith == 2) {
-        if (a.rows == 1) return launch_step_t<1, 64, 2, 2, 6, true>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 64, 2, 2, 6, true>(s, dev, call, nwg, lds);
+    if (a.head_dim == 64 && G == 4 && ith == 2) {
+        if (a.rows == 1) return launch_step_t<1, 64, 4, 2, 2, 6, true>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 64, 4, 2, 2, 6, true>(s, dev, call, nwg, lds);
     }
     return hipErrorInvalidValue;
 }

@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include "dev_attn.h"
+#include "dev_gemv.h"
 #include "dev_mem.h"
 #include "kernels.h"
 #include "y2_math.h"
@@ -217,7 +218,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     __shared__ __align__(16) float qkv_s[(G + 2) * D];  // read as float4 in the scores
     float(*q_s)[D] = reinterpret_cast<float(*)[D]>(qkv_s);
     __shared__ float hscale[G + 1];
-    __shared__ float m_s[G], t_s[G];
+    __shared__ float t_s[G];
     __shared__ float red_s[G * MAXNB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // The group size through an opaque copy outside the PV: with the count
@@ -297,18 +298,12 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             return false;
     }
     mark();
-    // Norm::heads: sequential sum of squares per head (src/tensor.rs:1160).
-    if (tid < Gq || (owns_new && tid == Gq)) {
-        const float* v = tid < Gq ? q_s[tid] : k_s;
-        float sum = -0.0f;
-        for (int d = 0; d < D; d += 16) {
-            float t[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) t[j] = v[d + j];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
-        }
-        hscale[tid] = norm_scale_from_sum(sum, D, a.eps);
+    // Norm::heads (src/tensor.rs:1160): the scale of the sequential sum of
+    // squares per head, decided by a whole wave per head (wave Gq: the new key)
+    static_assert(G + 1 <= NW, "one wave per head norm");
+    if (wave < Gq + (owns_new ? 1 : 0)) {
+        const float s = norm_scale_wave(wave < Gq ? q_s[wave] : k_s, D, a.eps);
+        if (lane == 0) hscale[wave] = s;
     }
     store_chunk(Ks, kr);
     store_chunk(Vs, vr);
@@ -417,24 +412,21 @@ m = xor_max<32>(m);
         if (!gather<NT, (G * MAXNB + NT - 1) / NT>(a.bmax + hbase, Gq * nb, nb, a.blk_stride, t_bmax, red_s, st))
             return false;
         mark();
-        for (int h = wave; h < Gq; h += NW) {
-            float m = -__builtin_huge_valf();
-            for (int i = lane; i < nb; i += 64) m = fmaxf(m, red_s[h * nb + i]);
-m = xor_max<32>(m);
-            if (lane == 0) m_s[h] = m;
-        }
-        __syncthreads();
-        const FastDiv fnk(nk);
-        for (int i = tid; i < Gq * nk; i += NT) {
-            const int h = fnk.div(i), jl = i - h * nk;
-            e_s[h * estride + jl] = expf_cr(e_s[h * estride + jl] - m_s[h]);
-        }
-        __syncthreads();
+        // exp(s - M) and the block sums in one pass, one (head, block) item
+        // per wave; each wave takes its head's M from the gathered block
+        // maxima itself, so no barrier separates the steps
         for (int i = wave; i < Gq * nbl; i += NW) {
             const int h = i / nbl, bl = i % nbl;
+            float m = -__builtin_huge_valf();
+            for (int k = lane; k < nb; k += 64) m = fmaxf(m, red_s[h * nb + k]);
+            m = xor_max<32>(m);
             const int jl = bl * kBlockKeys + lane;
-            float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
-v = xor_sum<32>(v);
+            float v = 0.0f;  // keys past the context add +0
+            if (jl < nk) {
+                v = expf_cr(e_s[h * estride + jl] - m);
+                e_s[h * estride + jl] = v;
+            }
+            v = xor_sum<32>(v);
             if (lane == 0) st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v, t_bsum);
         }
     }

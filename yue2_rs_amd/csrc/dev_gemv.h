@@ -112,6 +112,64 @@ __device__ __forceinline__ void gemv_store(float* yp, float acc, float acc2) {
     }
 }
 
+// The scale rb(1/sqrt(S/n + eps)) at one end (hi: the upper) of the interval
+// [E - B, E + B] that holds the sequential f32 chain's sum of squares, given
+// the exact sum E and the weighted sum W of norm_scales_block (B = 2^-24 *
+// 1.001 * W + E * 4e-12, the last term for the f64 rounding of E and W).
+// Returns whether the interval is finite; *scale gets that end's scale.
+__device__ __forceinline__ bool norm_scale_end(double e, double w, int n, float eps, bool hi_end, float* scale) {
+    const double bound = w * 0x1.0p-24 * 1.001 + e * 4e-12;
+    const double lo = e - bound, hi = e + bound;
+    float lo_f = (float)lo, hi_f = (float)hi;
+    if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
+    if (lo_f < 0.0f) lo_f = 0.0f;
+    if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
+    *scale = norm_scale_from_sum(hi_end ? hi_f : lo_f, n, eps);
+    return e < 1e300 && w < 1e300 && hi_f <= 3.0e38f;
+}
+
+// The sequential chain itself: rb(1/sqrt(sum/n + eps)) with sum = x[0]^2 +
+// x[1]^2 + ... from -0 in f32 (src/tensor.rs:1144, 1160); LDS reads batched
+// ahead of the adds.
+__device__ __forceinline__ float norm_scale_chain(const float* x, int n, float eps) {
+    float sum = -0.0f;
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        float t[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) t[j] = x[i + j];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
+    }
+    for (; i < n; ++i) sum = sum + x[i] * x[i];
+    return norm_scale_from_sum(sum, n, eps);
+}
+
+// RMSNorm scale of n values v[0..n) (LDS) computed by one whole wave, the
+// same decision as norm_scales_block (lanes 0 and 1 evaluate the two ends);
+// lane 0 runs the chain when the interval does not decide it.  Uniform over
+// the wave.
+__device__ __forceinline__ float norm_scale_wave(const float* v, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    double e = 0.0, w = 0.0;
+    for (int i = lane; i < n; i += 64) {
+        const float t = v[i] * v[i];
+        e += (double)t;
+        w += (double)t * (double)(n - i);
+    }
+    e = xor_sum<32>(e);
+    w = xor_sum<32>(w);
+    float sv;
+    const bool finite = norm_scale_end(e, w, n, eps, lane & 1, &sv);
+    const float other = xor_lane<1>(sv);  // the other end's scale (every lane takes part)
+    const bool decided = finite && sv == other;
+    if (__builtin_amdgcn_readfirstlane(decided ? 1 : 0))
+        return u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)f2u(sv)));
+    float s = 0.0f;
+    if (lane == 0) s = norm_scale_chain(v, n, eps);
+    return u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)f2u(s)));
+}
+
 // RMSNorm scales of B rows xs[b * n .. b * n + n) (LDS); all NT threads of
 // the block take part, entering together right after a block barrier, and
 // each gets scale[b] for every row.
@@ -163,14 +221,10 @@ __device__ __forceinline__ void norm_scales_block(const float* xs, int n, float 
         e += red_e[row][i];
         w += red_w[row][i];
     }
-    const double bound = w * 0x1.0p-24 * 1.001 + e * 4e-12;
-    const double lo = e - bound, hi = e + bound;
-    float lo_f = (float)lo, hi_f = (float)hi;
-    if ((double)lo_f > lo) lo_f = lo_f > 0.0f ? u2f(f2u(lo_f) - 1u) : 0.0f;
-    if (lo_f < 0.0f) lo_f = 0.0f;
-    if ((double)hi_f < hi) hi_f = u2f(f2u(hi_f) + 1u);
-    const float sv = norm_scale_from_sum((q & 1) ? hi_f : lo_f, n, eps);
-    const bool decided = e < 1e300 && w < 1e300 && hi_f <= 3.0e38f && sv == xor_lane<1>(sv);
+    float sv;
+    const bool finite = norm_scale_end(e, w, n, eps, q & 1, &sv);
+    const float other = xor_lane<1>(sv);  // the other end's scale (every lane takes part)
+    const bool decided = finite && sv == other;
     unsigned okmask = 0;  // bit b: row b's scale decided
 #pragma unroll
     for (int b = 0; b < B; ++b) {
@@ -179,20 +233,7 @@ __device__ __forceinline__ void norm_scales_block(const float* xs, int n, float 
     }
     if (okmask == (1u << B) - 1u) return;
     if (wave < B && lane == 0 && !((okmask >> wave) & 1u)) {
-        // the sequential chain itself (row `wave`); LDS reads batched ahead
-        // of the adds
-        const float* x = xs + wave * n;
-        float sum = -0.0f;
-        int i = 0;
-        for (; i + 16 <= n; i += 16) {
-            float t[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) t[j] = x[i + j];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) sum = sum + t[j] * t[j];
-        }
-        for (; i < n; ++i) sum = sum + x[i] * x[i];
-        s_scale[wave] = norm_scale_from_sum(sum, n, eps);
+        s_scale[wave] = norm_scale_chain(xs + wave * n, n, eps);  // row `wave`
         if (fallbacks) add_dev(fallbacks, 1);
     }
     __syncthreads();

@@ -170,37 +170,36 @@ __device__ __forceinline__ float norm_scale_wave(const float* v, int n, float ep
     return u2f((uint32_t)__builtin_amdgcn_readfirstlane((int)f2u(s)));
 }
 
-// RMSNorm scales of B rows xs[b * n .. b * n + n) (LDS); all NT threads of
-// the block take part, entering together right after a block barrier, and
-// each gets scale[b] for every row.
-// The reference sums the squares in one sequential f32 chain
-// (src/tensor.rs:1144).  The block computes the exact sum E and the bound
-// B = 2^-24 * 1.001 * sum_i t_i (n - i) on that chain's rounding error in f64
-// (each of the n-1 additions errs by at most 2^-24 of its partial sum); the
-// scale rb(1/sqrt(S/n + eps)) is monotone in S, so when both ends of
-// [E - B, E + B] give the same BF16 scale it is the chain's scale.  Lane
-// 2b + e of every wave evaluates end e of row b (all ends at once), and the
-// outcome is read back from those lanes, so it is uniform over the block.
-// A row that is not decided that way gets the chain itself, run by lane 0 of
-// wave b (the rows' chains on different SIMDs at once).
+// One value's share of the sums of norm_scales_block: t = x * x (f32, as in
+// the chain), E += t and W += t * (n - i) in f64, for element i of n.
+__device__ __forceinline__ void norm_partial_add(double& e, double& w, float x, int i, int n) {
+    const float t = x * x;
+    e += (double)t;
+    w += (double)t * (double)(n - i);
+}
+
+// This thread's shares of E and W for B rows: elements tid, tid + NT, ...
 template <int NT, int B>
-__device__ __forceinline__ void norm_scales_block(const float* xs, int n, float eps, int* fallbacks, float* scale) {
+__device__ __forceinline__ void norm_partials(const float* xs, int n, double* e_sum, double* w_sum) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) e_sum[b] = w_sum[b] = 0.0;
+    for (int i = threadIdx.x; i < n; i += NT) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) norm_partial_add(e_sum[b], w_sum[b], xs[b * n + i], i, n);
+    }
+}
+
+// norm_scales_block from each thread's shares of E and W (any split of the
+// elements over the threads, in any order: the bound's f64 term covers it);
+// e_sum and w_sum are consumed.
+template <int NT, int B>
+__device__ __forceinline__ void norm_scales_from(double* e_sum, double* w_sum, const float* xs, int n, float eps,
+                                                 int* fallbacks, float* scale) {
     static_assert(B <= NT / 64 && 2 * B <= 64, "one wave per fallback chain");
     constexpr int NW = NT / 64;
     __shared__ double red_e[B][NW], red_w[B][NW];
     __shared__ float s_scale[B];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    double e_sum[B], w_sum[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) e_sum[b] = w_sum[b] = 0.0;
-    for (int i = tid; i < n; i += NT) {
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const float t = xs[b * n + i] * xs[b * n + i];
-            e_sum[b] += (double)t;
-            w_sum[b] += (double)t * (double)(n - i);
-        }
-    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int b = 0; b < B; ++b) {
         e_sum[b] = xor_sum<32>(e_sum[b]);
@@ -240,6 +239,26 @@ __device__ __forceinline__ void norm_scales_block(const float* xs, int n, float 
 #pragma unroll
     for (int b = 0; b < B; ++b)
         if (!((okmask >> b) & 1u)) scale[b] = s_scale[b];
+}
+
+// RMSNorm scales of B rows xs[b * n .. b * n + n) (LDS); all NT threads of
+// the block take part, entering together right after a block barrier, and
+// each gets scale[b] for every row.
+// The reference sums the squares in one sequential f32 chain
+// (src/tensor.rs:1144).  The block computes the exact sum E and the bound
+// B = 2^-24 * 1.001 * sum_i t_i (n - i) on that chain's rounding error in f64
+// (each of the n-1 additions errs by at most 2^-24 of its partial sum); the
+// scale rb(1/sqrt(S/n + eps)) is monotone in S, so when both ends of
+// [E - B, E + B] give the same BF16 scale it is the chain's scale.  Lane
+// 2b + e of every wave evaluates end e of row b (all ends at once), and the
+// outcome is read back from those lanes, so it is uniform over the block.
+// A row that is not decided that way gets the chain itself, run by lane 0 of
+// wave b (the rows' chains on different SIMDs at once).
+template <int NT, int B>
+__device__ __forceinline__ void norm_scales_block(const float* xs, int n, float eps, int* fallbacks, float* scale) {
+    double e_sum[B], w_sum[B];
+    norm_partials<NT, B>(xs, n, e_sum, w_sum);
+    norm_scales_from<NT, B>(e_sum, w_sum, xs, n, eps, fallbacks, scale);
 }
 
 }  // namespace y2

@@ -83,6 +83,32 @@ __device__ __forceinline__ bool stage_rows(float* xs, const uint64_t* tx, int k,
     }
 }
 
+// stage_rows for x ahead of its RMSNorm, plus each thread's shares of the
+// norm's sums.  With packed words (two rows) the shares are added as the
+// words arrive (over the elements this thread stages, in arrival order), so
+// the norm needs no pass over LDS of its own; for one row a separate pass
+// measured faster (the added live registers cost the batch-1 kernel more).
+template <int B, int N>
+__device__ __forceinline__ bool stage_x(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st,
+                                        double* e_sum, double* w_sum) {
+    if constexpr (kPack<B>) {
+        static_assert(N <= 16, "at most 16 words per thread in flight");
+#pragma unroll
+        for (int b = 0; b < B; ++b) e_sum[b] = w_sum[b] = 0.0;
+        return gather_put<kStepThreads, N>([=](int i) { return tx + i; }, k, tag,
+                                           [&](int i, uint32_t bits) {
+                                               const float x0 = bf16_lo(bits), x1 = bf16_hi(bits);
+                                               xs[i] = x0;
+                                               xs[k + i] = x1;
+                                               norm_partial_add(e_sum[0], w_sum[0], x0, i, k);
+                                               norm_partial_add(e_sum[B - 1], w_sum[B - 1], x1, i, k);
+                                           },
+                                           st);
+    } else {
+        return stage_rows<B, N>(xs, tx, k, tag, st);  // norm_rows adds the shares
+    }
+}
+
 // res[b * n + r] = xs[b * k + h0 + r], r < n = h1 - h0 <= kResRows: this
 // workgroup's rows of the residual stream, taken from the staged x before it
 // is normalised, for the residual epilogue of the next O or down projection
@@ -105,12 +131,15 @@ __device__ __forceinline__ void load_gamma(const float* g, int k, float* gam) {
 }
 
 // xs[b] = RMSNorm(xs[b]) (Norm::apply, src/tensor.rs:1140-1157) with the
-// gammas of load_gamma; the rows' scales are decided together.  Entered
-// right after a block barrier.
+// gammas of load_gamma; the rows' scales are decided together from each
+// thread's shares of the sums (stage_x's with packed words, else added here).
+// Entered right after a block barrier.
 template <int B, int N>
-__device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, float eps, int* fallbacks) {
+__device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, float eps, int* fallbacks,
+                                          double* e_sum, double* w_sum) {
     float s[B];
-    norm_scales_block<kStepThreads, B>(xs, k, eps, fallbacks, s);
+    if constexpr (!kPack<B>) norm_partials<kStepThreads, B>(xs, k, e_sum, w_sum);
+    norm_scales_from<kStepThreads, B>(e_sum, w_sum, xs, k, eps, fallbacks, s);
 #pragma unroll
     for (int b = 0; b < B; ++b)
 #pragma unroll
@@ -192,6 +221,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
     uint4 ring[RMAX];
     float gam[ITH];
+    double e_sum[B], w_sum[B];  // this thread's shares of the next RMSNorm's sums
     Tracer<TRACE> tr{call.trace, call.trace_slots, 0};
     tr.mark();
 
@@ -237,12 +267,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 load_gamma<ITH>(last ? a->final_norm : layer_at(a, lc)->in_norm, H, gam);
                 prefetch_ring<ITH, false>(w, nullptr, H, r0, r1, n, ring);
                 a = fresh(args);
-                if (!stage_rows<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st)) return;
+                if (!stage_x<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st, e_sum, w_sum)) return;
+            } else if constexpr (kPack<B>) {
+                norm_partials<kStepThreads, B>(lds, H, e_sum, w_sum);  // x from the embedding
             }
             // this workgroup's rows of x: the residual of the O projection
             if (!last) copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
             a = fresh(args);
-            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr);
+            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
             gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(w, nullptr, lds, H, last ? a->logits : nullptr, last ? nullptr : a->tqkv,
@@ -281,11 +313,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             load_gamma<ITH>(layer_at(a, l)->post_norm, H, gam);
             prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg), I, ring);
             a = fresh(args);
-            if (!stage_rows<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st)) return;
+            if (!stage_x<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st, e_sum, w_sum)) return;
             // this workgroup's rows of x: the residual of the down projection
             copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
             a = fresh(args);
-            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr);
+            norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
             gemv_ring<B, EPI_SWIGLU, ITH, false, kPack<B>>(layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact,

@@ -149,6 +149,22 @@ __device__ void publish(const SampleArgs& a, int step, int32_t id) {
     if (a.phase != YUE2_PHASE_NONE && id == a.end_id) st->done = 1;
 }
 
+// v[0] + v[1] + ... + v[n-1] in f32 from -0, in order (n >= 0); the LDS
+// reads go out eight at a time ahead of their adds.
+__device__ __forceinline__ float seq_sum(const float* v, int n) {
+    float s = -0.0f;
+    int k = 0;
+    for (; k + 8 <= n; k += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = v[k + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = s + t[j];
+    }
+    for (; k < n; ++k) s = s + v[k];
+    return s;
+}
+
 // Steps 6-8 over the n <= kSurvivorMax survivors, given as order keys in
 // surv (scores in sc): sort by score descending and id ascending (:174),
 // top-p (:175-190) and renormalisation (:191-197) as sequential f32 sums,
@@ -166,35 +182,62 @@ __device__ int32_t race_tail(const SampleArgs& a, int step, const float* sc, uin
     const float max = sc[(int32_t)(surv[0] & 0xffffffffu)];
     for (int i = tid; i < n; i += nt) e_val[i] = expf_cr(sc[(int32_t)(surv[i] & 0xffffffffu)] - max);
     __syncthreads();
+    // The sums and the cumulative pass are sequential (in sorted order, as in
+    // the reference); the divisions are independent and run on all threads.
+    __shared__ float p_s[kSurvivorMax];
+    __shared__ float s_sum;
+    const bool nucleus = a.top_p < 1.0f;
+    if (nucleus) {
+        if (tid == 0) s_sum = seq_sum(e_val, n);
+        __syncthreads();
+        const float sum = s_sum;
+        for (int i = tid; i < n; i += nt) p_s[i] = cast(e_val[i] / sum, a.legacy);
+        __syncthreads();
+    }
     if (tid == 0) {
         int kept = n;
-        if (a.top_p < 1.0f) {
-            float sum = -0.0f;
-            for (int i = 0; i < n; ++i) sum = sum + e_val[i];
+        if (nucleus) {
             float cumulative = 0.0f;
             const int protect = a.legacy ? 3 : 1;
             kept = 0;
-            for (int i = 0; i < n; ++i) {
-                const float p = cast(e_val[i] / sum, a.legacy);
-                cumulative += p;
-                const float prior = cast(cast(cumulative, a.legacy) - p, a.legacy);
-                if (prior <= a.top_p || i < protect) {
-                    surv[kept] = surv[i];
-                    e_val[kept] = e_val[i];
-                    ++kept;
+            // entries read eight at a time ahead of the sequential pass (the
+            // compaction writes index kept <= i, never a later entry)
+            for (int i0 = 0; i0 < n; i0 += 8) {
+                float pv[8], ev[8];
+                uint64_t sv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = min(i0 + j, n - 1);
+                    pv[j] = p_s[i];
+                    ev[j] = e_val[i];
+                    sv[j] = surv[i];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (i0 + j >= n) break;
+                    cumulative += pv[j];
+                    const float prior = cast(cast(cumulative, a.legacy) - pv[j], a.legacy);
+                    if (prior <= a.top_p || i0 + j < protect) {
+                        surv[kept] = sv[j];
+                        e_val[kept] = ev[j];
+                        ++kept;
+                    }
                 }
             }
         }
-        float sum = -0.0f;
-        for (int i = 0; i < kept; ++i) sum = sum + e_val[i];
-        for (int i = 0; i < kept; ++i) {
-            const float p = cast(e_val[i] / sum, a.legacy);
-            surv[i] = ((uint64_t)(surv[i] & 0xffffffffu) << 32) | f2u(p);
-        }
+        s_sum = seq_sum(e_val, kept);
         *s_kept = kept;
     }
     __syncthreads();
     const int kept = *s_kept;
+    {
+        const float sum = s_sum;
+        for (int i = tid; i < kept; i += nt) {
+            const float p = cast(e_val[i] / sum, a.legacy);
+            surv[i] = ((uint64_t)(surv[i] & 0xffffffffu) << 32) | f2u(p);
+        }
+    }
+    __syncthreads();
     int k2 = 2;
     while (k2 < kept) k2 <<= 1;
     for (int i = kept + tid; i < k2; i += nt) surv[i] = ~0ull;
@@ -211,12 +254,24 @@ __device__ int32_t race_tail(const SampleArgs& a, int step, const float* sc, uin
     }
     __syncthreads();
     if (tid == 0) {
+        // the first maximum in id order; entries read eight at a time
         float best = -__builtin_huge_valf();
         int32_t selected = 0;
-        for (int i = 0; i < kept; ++i) {
-            if (e_val[i] > best) {
-                best = e_val[i];
-                selected = (int32_t)(surv[i] >> 32);
+        for (int i0 = 0; i0 < kept; i0 += 8) {
+            float ev[8];
+            uint64_t sv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = min(i0 + j, kept - 1);
+                ev[j] = e_val[i];
+                sv[j] = surv[i];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (i0 + j < kept && ev[j] > best) {
+                    best = ev[j];
+                    selected = (int32_t)(sv[j] >> 32);
+                }
             }
         }
         *s_sel = selected;

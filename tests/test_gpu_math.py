@@ -94,3 +94,36 @@ def test_lane_exchanges_are_exact(gpu):
         assert np.array_equal(_device(new, x).view(np.uint32), _device(old, x).view(np.uint32)), new
     mx = _device(16, x).reshape(-1, 64)
     assert np.array_equal(mx, np.repeat(x.reshape(-1, 64).max(axis=1, keepdims=True), 64, axis=1))
+
+
+def test_wave_norm_scale_matches_chain_near_rounding_boundaries(gpu):
+    """The wave-level RMSNorm decision (the QK head norms) equals the oracle's
+    sequential chain, also for vectors whose sum of squares puts the scale
+    next to a BF16 rounding boundary, where the exact-interval test cannot
+    decide and the device runs the chain itself."""
+    rng = np.random.default_rng(11)
+    n, eps = 64, np.float32(1e-6)
+    vecs = []
+    # scales just around BF16 midpoints: S = n (1 / m^2 - eps)
+    for _ in range(2048):
+        e = rng.integers(-6, 7)
+        mant = rng.integers(128, 256)
+        lo = np.float32(mant * 2.0 ** (e - 7))
+        hi = np.float32((mant + 1) * 2.0 ** (e - 7))
+        mid = (float(lo) + float(hi)) / 2.0
+        S = n * (1.0 / mid ** 2 - float(eps))
+        if S <= 0:
+            continue
+        x = np.sqrt(S / n) * (1.0 + 0.05 * rng.standard_normal(n))
+        x *= np.sqrt(S / np.sum(x * x))
+        vecs.append(x.astype(np.float32))
+    # ordinary vectors of assorted magnitudes
+    while len(vecs) % 4 or len(vecs) < 4096:
+        vecs.append((rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32))
+    x = np.concatenate(vecs).astype(np.float32)
+    got = _device(17, x).reshape(-1, n)
+    assert np.all(got == got[:, :1]), "the scale is uniform over the wave"
+    L = O.lib()
+    want = np.array([L.y2o_norm_scale(v.ctypes.data, n, float(eps)) for v in x.reshape(-1, n)], dtype=np.float32)
+    bad = np.nonzero(got[:, 0].view(np.uint32) != want.view(np.uint32))[0]
+    assert bad.size == 0, [(int(i), float(got[i, 0]), float(want[i])) for i in bad[:5]]

@@ -14,6 +14,7 @@
 // Rows of a batch never interact, so a CFG batch-2 row equals a batch-1 row.
 #include <algorithm>
 
+#include "dev_gemv.h"
 #include "dev_mem.h"
 #include "kernels.h"
 #include "y2_math.h"
@@ -203,6 +204,13 @@ __device__ float lane_selftest(int which, float v) {
 
 __global__ void math_selftest_kernel(int which, const void* in, void* out, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (which == 17) {
+        // the RMSNorm scale of each 64-value vector (eps 1e-6), decided by the
+        // wave as the head norms are; every lane stores it
+        const float* vec = static_cast<const float*>(in) + (i & ~(size_t)63);
+        static_cast<float*>(out)[i] = norm_scale_wave(vec, 64, 1e-6f);
+        return;
+    }
     if (which >= 4) {
         // every lane of the wave takes part in the exchange
         const float v = static_cast<const float*>(in)[i];

@@ -229,8 +229,10 @@ void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t te
  * lane ^ 1, 2, 4, 8, 16, 32; the xor-butterfly sums over distances 32..1
  * (10 ALU exchanges, 11 __shfl_xor), 8..1 (12, 13) and 32..16 (14, 15); 16
  * the max over 32..1; 17 the RMSNorm scale (eps 1e-6) of each consecutive
- * 64-value vector, decided by one wave (stored on all 64 of its outputs).
- * Returns 0 or a negative Yue2Error. */
+ * 64-value vector, decided by one wave (stored on all 64 of its outputs);
+ * 18 the RMSNorm scales of the two 128-value rows of each 256-value block,
+ * decided together by a 256-thread block (each row's outputs hold its
+ * scale).  Returns 0 or a negative Yue2Error. */
 int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
 /* Execution choice: run decode steps (yue2_hip_forward and decoders created
  * afterwards) through the persistent token-step kernel -- one launch per

@@ -96,6 +96,45 @@ def test_lane_exchanges_are_exact(gpu):
     assert np.array_equal(mx, np.repeat(x.reshape(-1, 64).max(axis=1, keepdims=True), 64, axis=1))
 
 
+def _near_boundary_rows(rng, count, n, eps):
+    """Rows whose sum of squares puts the RMSNorm scale at a BF16 rounding
+    midpoint (S = n (1 / m^2 - eps)), so the exact-interval test is undecided."""
+    rows = []
+    while len(rows) < count:
+        e = rng.integers(-6, 7)
+        mant = rng.integers(128, 256)
+        mid = (mant * 2.0 ** (e - 7) + (mant + 1) * 2.0 ** (e - 7)) / 2.0
+        S = n * (1.0 / mid ** 2 - float(eps))
+        if S <= 0:
+            continue
+        x = np.sqrt(S / n) * (1.0 + 0.05 * rng.standard_normal(n))
+        x *= np.sqrt(S / np.sum(x * x))
+        rows.append(x.astype(np.float32))
+    return rows
+
+
+def test_block_norm_scales_match_chain_near_rounding_boundaries(gpu):
+    """The block-wide two-row RMSNorm decision (every layer's norms) equals
+    the oracle's sequential chain for each row: rows at BF16 rounding
+    midpoints (the fallback chains, one per row, on different waves), ordinary
+    rows, and pairs mixing the two."""
+    rng = np.random.default_rng(12)
+    n, eps = 128, np.float32(1e-6)
+    near = _near_boundary_rows(rng, 1024, n, eps)
+    ordinary = [(rng.standard_normal(n) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32) for _ in range(1024)]
+    rows = []
+    for i in range(1024):  # near/near, near/ordinary, ordinary/near, ordinary/ordinary
+        k = i % 4
+        rows += [near[i] if k in (0, 1) else ordinary[i], near[i] if k in (0, 2) else ordinary[(i + 1) % 1024]]
+    x = np.concatenate(rows).astype(np.float32)
+    got = _device(18, x).reshape(-1, n)
+    L = O.lib()
+    want = np.array([L.y2o_norm_scale(v.ctypes.data, n, float(eps)) for v in x.reshape(-1, n)], dtype=np.float32)
+    assert np.all(got == got[:, :1])
+    bad = np.nonzero(got[:, 0].view(np.uint32) != want.view(np.uint32))[0]
+    assert bad.size == 0, [(int(i), float(got[i, 0]), float(want[i])) for i in bad[:5]]
+
+
 def test_wave_norm_scale_matches_chain_near_rounding_boundaries(gpu):
     """The wave-level RMSNorm decision (the QK head norms) equals the oracle's
     sequential chain, also for vectors whose sum of squares puts the scale

@@ -211,6 +211,16 @@ __global__ void math_selftest_kernel(int which, const void* in, void* out, size_
         static_cast<float*>(out)[i] = norm_scale_wave(vec, 64, 1e-6f);
         return;
     }
+    if (which == 18) {
+        // the RMSNorm scales (eps 1e-6) of the two 128-value rows of each
+        // 256-value block, decided together by the block as the step
+        // kernel's norms are; each row's threads store its scale
+        const float* rows = static_cast<const float*>(in) + (size_t)blockIdx.x * 256;
+        float sc[2];
+        norm_scales_block<256, 2>(rows, 128, 1e-6f, nullptr, sc);
+        static_cast<float*>(out)[i] = threadIdx.x < 128 ? sc[0] : sc[1];
+        return;
+    }
     if (which >= 4) {
         // every lane of the wave takes part in the exchange
         const float v = static_cast<const float*>(in)[i];

@@ -659,7 +659,7 @@ extern "C" int32_t yue2_hip_synchronize(void) {
 extern "C" int32_t yue2_hip_selftest_math(int32_t which, const void* in, void* out, size_t n) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 device");
-    if (which < 0 || which > 17 || !in || !out || (which >= 4 && n % 256 != 0))
+    if (which < 0 || which > 18 || !in || !out || (which >= 4 && n % 256 != 0))
         return fail(YUE2_ERR_ARG, "bad selftest request");
     const size_t elem = which == 1 ? sizeof(double) : sizeof(float);
     void *din = nullptr, *dout = nullptr;

@@ -1,5 +1,6 @@
 """Device math routines equal the oracle's bit for bit (exp, log1p,
-round_bf16, SiLU), on random and special inputs."""
+round_bf16 on every f32 bit pattern, SiLU, the ALU lane exchanges, and the
+RMSNorm scale decisions next to BF16 rounding boundaries)."""
 import ctypes as C
 
 import numpy as np

@@ -166,6 +166,14 @@ void yue2_hip_model_free(Yue2Model *m);
 Yue2Cache *yue2_hip_cache_new(Yue2Model *m, int32_t capacity);
 void yue2_hip_cache_free(Yue2Cache *c);
 int32_t yue2_hip_cache_length(const Yue2Cache *c);
+/* The device context of a cache from its host K/V mirror (Cache's key/value,
+ * src/model.rs:276-306), as the reference's Metal bridge fills its device
+ * context from the mirror (contextEntry, src/metal.m:633-666): key and value
+ * hold, per layer, `stride` rows of kv_heads * head_dim BF16-exact f32 values
+ * (layer l starts at l * stride rows); rows [0, length) are loaded and the
+ * cache length becomes `length`.  Returns 0 or a negative Yue2Error. */
+int32_t yue2_hip_cache_load(Yue2Cache *c, const float *key, const float *value, int32_t length,
+                            int32_t stride);
 
 /* Model::forward_phase (src/model.rs:465-477): run n ids through the model,
  * appending to the cache; write the logits of the last row (vocab_size f32,
@@ -190,6 +198,10 @@ void yue2_hip_decoder_free(Yue2Decoder *d);
  * steps run (it stops at the phase's end token) or a negative Yue2Error. */
 int32_t yue2_hip_decoder_run(Yue2Decoder *d, const float *first_logits, int32_t steps,
                              int32_t *tokens, float *step_ms);
+/* The logits the decoder's next choose() reads (src/sampling.rs:261-267
+ * before the mix): rows x vocab f32, the conditional row first; after a run
+ * they are the last step's forward outputs.  The decoder must have run. */
+int32_t yue2_hip_decoder_logits(Yue2Decoder *d, float *out);
 
 /* sampling::choose (src/sampling.rs:103-215) on the device for one row of
  * logits (already CFG-mixed).  history / history_len: the ids generated so

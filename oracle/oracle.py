@@ -186,6 +186,14 @@ class Cache:
         base = layer * c.capacity * c.width
         return np.ctypeslib.as_array(c.value, shape=(c.layers * c.capacity * c.width,))[base:base + n].reshape(c.length, c.width)
 
+    def arrays(self):
+        """(key, value) views of the whole mirror, each [layers, capacity, width]."""
+        c = self.ptr.contents
+        shape = (c.layers, c.capacity, c.width)
+        n = c.layers * c.capacity * c.width
+        return (np.ctypeslib.as_array(c.key, shape=(n,)).reshape(shape),
+                np.ctypeslib.as_array(c.value, shape=(n,)).reshape(shape))
+
     def fill_random(self, length: int, seed: int) -> None:
         """Give the cache `length` positions of BF16-exact N(0, 1) keys and
         values (for timing a step at a given context without a prefill)."""

@@ -101,11 +101,13 @@ def lib() -> C.CDLL:
         "yue2_hip_cache_new": (vp, [vp, i32]),
         "yue2_hip_cache_free": (None, [vp]),
         "yue2_hip_cache_length": (i32, [vp]),
+        "yue2_hip_cache_load": (i32, [vp, vp, vp, i32, i32]),
         "yue2_hip_forward": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_prefill": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_decoder_new": (vp, [vp, vp, vp, vp, u64, i32, f32, i32]),
         "yue2_hip_decoder_free": (None, [vp]),
         "yue2_hip_decoder_run": (i32, [vp, vp, i32, vp, vp]),
+        "yue2_hip_decoder_logits": (i32, [vp, vp]),
         "yue2_hip_generate": (i32, [vp, vp, i32, vp, u64, i32, vp, i32, f32, i32, vp, vp, vp]),
         "yue2_hip_choose": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, vp, vp]),
         "yue2_hip_last_error": (C.c_char_p, []),
@@ -302,6 +304,16 @@ class Cache:
     def length(self) -> int:
         return int(lib().yue2_hip_cache_length(self._h))
 
+    def load(self, key: np.ndarray, value: np.ndarray, length: int) -> None:
+        """Fill the device context from a host K/V mirror (per layer, rows of
+        kv_heads * head_dim BF16-exact f32): key/value shaped [layers, stride,
+        width] with stride >= length; the cache length becomes `length`."""
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        if k.shape != v.shape or k.ndim != 3:
+            raise ValueError("key and value must both be [layers, stride, width]")
+        _check(lib().yue2_hip_cache_load(self._h, _ptr(k), _ptr(v), int(length), k.shape[1]))
+
     def close(self) -> None:
         if self._h:
             lib().yue2_hip_cache_free(self._h)
@@ -339,6 +351,13 @@ class Decoder:
         ms = np.zeros(max(steps, 1), dtype=np.float32) if timing else None
         n = _check(lib().yue2_hip_decoder_run(self._h, _ptr(fl), steps, _ptr(tokens), _ptr(ms)))
         return tokens[:n], (ms[:n] if timing else None)
+
+    def logits(self) -> np.ndarray:
+        """The logits the next choose() reads: [rows, vocab], conditional row
+        first (the last step's forward outputs after a run)."""
+        out = np.empty((self.rows, self.model.config.vocab_size), dtype=np.float32)
+        _check(lib().yue2_hip_decoder_logits(self._h, _ptr(out)))
+        return out
 
     KERNELS = {"gate_up": 0, "down": 1, "qkv": 2, "o": 3, "lm_head": 4, "step": 5}
 

@@ -297,6 +297,17 @@ extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logit
     return ran;
 }
 
+extern "C" int32_t yue2_hip_decoder_logits(Yue2Decoder* d, float* out) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!d || !out) return fail(YUE2_ERR_ARG, "null decoder or output");
+    if (!d->started) return fail(YUE2_ERR_ARG, "decoder has not run");
+    hipStream_t s = d->m->stream;
+    hipError_t e = hipMemcpyAsync(out, d->w.logits, sizeof(float) * (size_t)d->rows * d->m->c.vocab_size,
+                                  hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "logits readback");
+}
+
 // The loop's last choose() without a following forward (src/sampling.rs:281).
 static int choose_only(Yue2Decoder* d, const float* first_logits, int32_t* token) {
     if (!d->started)

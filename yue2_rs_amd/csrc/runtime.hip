@@ -553,6 +553,42 @@ extern "C" void yue2_hip_cache_free(Yue2Cache* c) {
 
 extern "C" int32_t yue2_hip_cache_length(const Yue2Cache* c) { return c ? c->length : 0; }
 
+// The device context of a cache from its host K/V mirror, as the reference's
+// Metal bridge does when a cache first reaches the GPU (contextEntry,
+// src/metal.m:633-666): mirror rows hold kv_heads * head_dim BF16-exact f32
+// values, whose high 16 bits are the BF16 the device stores.
+extern "C" int32_t yue2_hip_cache_load(Yue2Cache* c, const float* key, const float* value, int32_t length,
+                                       int32_t stride) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!c || !key || !value) return fail(YUE2_ERR_ARG, "null cache or mirror");
+    const Yue2Config& cf = c->m->c;
+    if (length < 0 || length > c->capacity || length > cf.max_position_embeddings || stride < length)
+        return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    const int Hkv = cf.num_key_value_heads, D = cf.head_dim, width = Hkv * D;
+    hipError_t e = hipStreamSynchronize(c->m->stream);  // no step may be writing the cache
+    if (e != hipSuccess) return hip_fail(e, "cache load sync");
+    std::vector<uint16_t> slab((size_t)width * std::max(length, 1));
+    for (int l = 0; l < cf.num_hidden_layers && length > 0; ++l) {
+        for (int which = 0; which < 2; ++which) {
+            const float* src = (which == 0 ? key : value) + (size_t)l * stride * width;
+            // [kv_heads][length][head_dim]: one head's rows are contiguous on the device
+            for (int p = 0; p < length; ++p)
+                for (int h = 0; h < Hkv; ++h) {
+                    const uint32_t* row = reinterpret_cast<const uint32_t*>(src + (size_t)p * width + (size_t)h * D);
+                    uint16_t* dst = slab.data() + ((size_t)h * length + p) * D;
+                    for (int d = 0; d < D; ++d) dst[d] = (uint16_t)(row[d] >> 16);
+                }
+            uint16_t* base = c->kv + ((size_t)l * 2 + which) * Hkv * (size_t)c->capacity * D;
+            e = hipMemcpy2D(base, (size_t)c->capacity * D * sizeof(uint16_t), slab.data(),
+                            (size_t)length * D * sizeof(uint16_t), (size_t)length * D * sizeof(uint16_t), Hkv,
+                            hipMemcpyHostToDevice);
+            if (e != hipSuccess) return hip_fail(e, "cache load");
+        }
+    }
+    c->length = length;
+    return YUE2_OK;
+}
+
 // Model::forward_phase: token-by-token through the decode-order kernels, so a
 // prefill produces bit-for-bit the cache a sequence of decode steps would.
 extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int32_t n,

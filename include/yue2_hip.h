@@ -113,7 +113,8 @@ typedef enum Yue2Error {
     YUE2_ERR_CONFIG = -11,  /* "Invalid transformer configuration" (src/model.rs:71) */
     YUE2_ERR_DEVICE = -12,  /* no usable device, or a HIP call failed */
     YUE2_ERR_ARG = -13,     /* a null pointer or an unsupported shape */
-    YUE2_ERR_TIES = -14     /* top-k survivors exceed the device sort capacity */
+    YUE2_ERR_TIES = -14     /* top-k survivors exceed the survivor arrays (not reached:
+                               they hold the whole vocabulary) */
 } Yue2Error;
 
 /* Phases of project_phase/choose (src/sampling.rs:81-99).  NONE is the full
@@ -195,7 +196,10 @@ Yue2Decoder *yue2_hip_decoder_new(Yue2Model *m, Yue2Cache *cond, Yue2Cache *unco
 void yue2_hip_decoder_free(Yue2Decoder *d);
 /* Run `steps` token steps.  tokens receives the chosen ids; step_ms (may be
  * NULL) the per-step device time from HIP events.  Returns the number of
- * steps run (it stops at the phase's end token) or a negative Yue2Error. */
+ * steps run or a negative Yue2Error.  With a phase that has an end token the
+ * loop stops at the first end id: it is the last id returned, its step runs
+ * no forward (src/sampling.rs:268-271), so the caches grow by one position
+ * less than the steps returned, and later runs return 0. */
 int32_t yue2_hip_decoder_run(Yue2Decoder *d, const float *first_logits, int32_t steps,
                              int32_t *tokens, float *step_ms);
 /* The logits the decoder's next choose() reads (src/sampling.rs:261-267
@@ -253,6 +257,13 @@ int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t 
  * step kernel is the default for shapes that have one.  Returns 1 when
  * enabled, 0 when off or when the model's shape has no step kernel. */
 int32_t yue2_hip_model_set_step_kernel(Yue2Model *m, int32_t on);
+/* Diagnostics: advance the launch sequence of the model's own workspace (the
+ * one yue2_hip_forward uses) by `add`, as if that many step-kernel launches
+ * had run.  The step kernel's tagged words carry a 20-bit epoch of this
+ * sequence; the library clears them before an epoch could repeat, and this
+ * entry lets a test place launches at that point.  The model must have run a
+ * step-kernel forward. */
+int32_t yue2_hip_model_advance_sequence(Yue2Model *m, int32_t add);
 /* Diagnostics: RMSNorm guard fallbacks taken since the model was opened. */
 int32_t yue2_hip_norm_fallbacks(const Yue2Model *m);
 

@@ -192,10 +192,18 @@ def test_error_rules(gpu, top_k):
     assert dev == ref
 
 
-@pytest.mark.parametrize("top_k", [50, 1000])
-def test_survivor_capacity(gpu, top_k):
-    # 84000 tied entries survive top-k; the device sort holds 2048 and says so
-    lg = np.zeros(V3B, np.float32)
-    with pytest.raises(y2.Yue2Error) as e:
-        y2.choose(lg, S(top_k=top_k), draws=draws(0, V3B))
-    assert e.value.code == -14
+@pytest.mark.parametrize("top_k,ties,seed", [(5000, 0, 0), (50, 3000, 1), (1000, 3000, 2), (50, V3B, 3),
+                                              (V3B, 0, 4)])
+def test_many_survivors(gpu, top_k, ties, seed):
+    """More survivors than the LDS survivor arrays hold (2048): top_k 5000,
+    3000 entries tied at the top-k threshold, the whole vocabulary tied, and
+    top_k = vocabulary (src/sampling.rs:162-174 keeps every tie); with and
+    without top-p."""
+    lg = normal(V3B, seed)
+    if ties:
+        rng = np.random.default_rng(seed)
+        at = rng.choice(V3B, ties, replace=False)
+        lg[at] = np.max(lg) + 1.0  # the best entries, all equal
+    for top_p in (0.93, 1.0):
+        dev, ref = both(lg, S(top_k=top_k, top_p=top_p, temperature=1.3), seed=seed)
+        assert dev == ref

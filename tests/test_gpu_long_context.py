@@ -122,3 +122,24 @@ def test_3b_cfg_batch2_max_context(model_3b):
     the attention of each row spans 384 / 376 blocks, 24 per workgroup."""
     _, gm, om = model_3b
     _check_batch2(gm, om, (24575, 24000), 1, seed=5)
+
+
+def test_epoch_repeat_keeps_parity(reduced):
+    """The step kernel's tagged words carry a 20-bit epoch of the launch
+    sequence.  The second forward below is placed exactly 2^20 launches after
+    the first, so without a clear of the words every word the first launch
+    left (x, q/k/v, the block statistics of all 129 blocks) would already
+    carry the second launch's tags; the library clears them first."""
+    _, gm, om = reduced
+    gc, oc = _caches(gm, om, 8192, 8196, seed=2)
+    t = 11
+    for s in range(3):
+        if s == 1:
+            # the forward's state reset adds 2: the next launch's sequence is
+            # the previous launch's + 2^20
+            gm.advance_sequence((1 << 20) - 3)
+        print(f"forward {s} at context {8192 + s}", flush=True)
+        got = gm.forward([t], gc)
+        want = om.forward([t], oc)
+        assert np.array_equal(bits(got), bits(want)), f"logits differ at forward {s}"
+        t = int(np.argmax(want))

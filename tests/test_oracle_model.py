@@ -1,0 +1,233 @@
+"""Pins of the oracle's composed functions (CPU only).
+
+  * Rotary::apply (src/model.rs:151-168) at tables other than position 0:
+    cos = 0, sin = 1 is an exact quarter turn (a, b) -> (-b, a), and a table
+    that differs per row applies each row's own angles.
+  * Model::hidden / forward / prefill (src/model.rs:452-610) against an
+    independent float64 forward written in numpy from the reference's
+    formulas, on a small model at positions where RoPE matters; the
+    tolerance is stated in the test, and a dropped residual, a swapped norm,
+    a RoPE sign error or a wrong GQA head map all exceed it by far.
+  * A closed-form composition: with W_o = W_down = 0 every layer leaves x =
+    rb(E[t]), so the logits are rb(W_lm . RMSNorm(rb(E[t]))) exactly.
+  * project_phase (src/model.rs:478-507): the ABC / semantic logits equal the
+    full-vocabulary head on the phase's range and the stop row, -inf
+    elsewhere.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yue2_rs_amd import synthetic
+from yue2_rs_amd.api import Config
+
+from helpers import rb
+
+EOD, ABC_END, MUSIC_END, CODEC_OFFSET, CODEC_SIZE = 151643, 151848, 151852, 151853, 32768
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+def test_rotary_quarter_turn_and_identity():
+    half, heads = 16, 3
+    cols = heads * 2 * half
+    x = rb(np.random.default_rng(1).standard_normal((2, cols)).astype(np.float32))
+    cos = np.zeros((2, half), np.float32)
+    sin = np.zeros((2, half), np.float32)
+    cos[0], sin[0] = 0.0, 1.0   # row 0: a quarter turn
+    cos[1], sin[1] = 1.0, 0.0   # row 1: the identity
+    y = x.copy()
+    O.lib().y2o_rotary_apply(_p(y), 2, cols, half, _p(cos), _p(sin))
+    a, b = x[0].reshape(heads, 2, half)[:, 0], x[0].reshape(heads, 2, half)[:, 1]
+    ya, yb = y[0].reshape(heads, 2, half)[:, 0], y[0].reshape(heads, 2, half)[:, 1]
+    assert np.array_equal(ya, -b) and np.array_equal(yb, a)
+    assert np.array_equal(y[1], x[1])
+
+
+def test_rotary_applies_each_rows_angles():
+    """Per-element rotation by (c, s) with the reference's rounding points,
+    c and s exact BF16 values whose products with BF16 inputs are exact
+    (c, s in {+-1/2, +-1}): the result is the exactly rounded rotation."""
+    half, cols = 8, 32
+    rng = np.random.default_rng(2)
+    x = rb(rng.standard_normal((3, cols)).astype(np.float32))
+    vals = np.array([0.5, -0.5, 1.0, -1.0], np.float32)
+    cos = vals[rng.integers(0, 4, (3, half))]
+    sin = vals[rng.integers(0, 4, (3, half))]
+    y = x.copy()
+    O.lib().y2o_rotary_apply(_p(y), 3, cols, half, _p(cos), _p(sin))
+    for r in range(3):
+        for h in range(cols // (2 * half)):
+            a = x[r, h * 2 * half:h * 2 * half + half].astype(np.float64)
+            b = x[r, h * 2 * half + half:(h + 1) * 2 * half].astype(np.float64)
+            c, s = cos[r].astype(np.float64), sin[r].astype(np.float64)
+            want_a = rb((a * c - b * s).astype(np.float32))
+            want_b = rb((b * c + a * s).astype(np.float32))
+            assert np.array_equal(y[r, h * 2 * half:h * 2 * half + half], want_a)
+            assert np.array_equal(y[r, h * 2 * half + half:(h + 1) * 2 * half], want_b)
+
+
+# ---------------------------------------------------------------------------
+# An independent float64 forward (numpy), from the reference's formulas
+
+
+def _bf(a):
+    """BF16 bit patterns (uint16) as float64."""
+    return (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def _r(x):
+    """round_bf16 of float64 values (via f32)."""
+    return rb(np.asarray(x, np.float64).astype(np.float32)).astype(np.float64)
+
+
+def _rmsnorm(x, g, eps):
+    s = _r(1.0 / np.sqrt(np.sum(x * x) / x.size + eps))
+    return _r(_r(x * s) * g)
+
+
+class NumpyModel:
+    """Model::hidden + forward (src/model.rs:452-591) in float64 with the
+    reference's BF16 rounding points; one token at a time."""
+
+    def __init__(self, ck):
+        c = ck.config
+        self.c = c
+        self.E, self.W_lm, self.fn = _bf(ck.embed_tokens), _bf(ck.lm_head), _r(ck.final_norm)
+        self.layers = [{k: (_bf(getattr(w, k)) if getattr(w, k).dtype == np.uint16 else _r(getattr(w, k)))
+                        for k in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
+                                  "input_layernorm", "q_norm", "k_norm", "post_attention_layernorm")}
+                       for w in ck.layers]
+        self.K = [[] for _ in ck.layers]
+        self.V = [[] for _ in ck.layers]
+
+    def rope(self, p):
+        d, th = self.c.head_dim, np.float32(self.c.rope_theta)
+        i = np.arange(d // 2)
+        f = (np.float32(1.0) / np.power(th, (2 * i).astype(np.float32) / np.float32(d))).astype(np.float32)
+        ang = (np.float32(p) * f).astype(np.float32).astype(np.float64)
+        return _r(np.cos(ang)), _r(np.sin(ang))
+
+    def step(self, t):
+        c = self.c
+        H, Hq, Hkv, d = c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        p = len(self.K[0])
+        x = _r(self.E[t])
+        cs, sn = self.rope(p)
+        for l, L in enumerate(self.layers):
+            h = _rmsnorm(x, L["input_layernorm"], c.rms_norm_eps)
+            q = _r(L["q_proj"] @ h).reshape(Hq, d)
+            k = _r(L["k_proj"] @ h).reshape(Hkv, d)
+            v = _r(L["v_proj"] @ h).reshape(Hkv, d)
+            q = np.stack([_rmsnorm(r, L["q_norm"], c.rms_norm_eps) for r in q])
+            k = np.stack([_rmsnorm(r, L["k_norm"], c.rms_norm_eps) for r in k])
+
+            def rot(m):
+                a, b = m[:, :d // 2], m[:, d // 2:]
+                return np.concatenate([_r(_r(a * cs) - _r(b * sn)), _r(_r(b * cs) + _r(a * sn))], axis=1)
+
+            q, k = rot(q), rot(k)
+            self.K[l].append(k)
+            self.V[l].append(v)
+            Ks, Vs = np.stack(self.K[l]), np.stack(self.V[l])  # [L, Hkv, d]
+            att = np.empty((Hq, d))
+            for hq in range(Hq):
+                g = hq // (Hq // Hkv)
+                s = (Ks[:, g, :] @ q[hq]) * np.float64(np.float32(1.0) / np.sqrt(np.float32(d)))
+                e = np.exp(s - s.max())
+                att[hq] = _r((e / e.sum()) @ Vs[:, g, :])
+            x = _r(x + _r(L["o_proj"] @ att.reshape(-1)))
+            h2 = _rmsnorm(x, L["post_attention_layernorm"], c.rms_norm_eps)
+            gt = _r(L["gate_proj"] @ h2)
+            up = _r(L["up_proj"] @ h2)
+            gt = _r(gt / (1.0 + np.exp(-gt)))
+            x = _r(x + _r(L["down_proj"] @ _r(gt * up)))
+        return _r(self.W_lm @ _rmsnorm(x, self.fn, c.rms_norm_eps))
+
+
+SMALL = Config(hidden_size=64, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, head_dim=32,
+               intermediate_size=128, vocab_size=512, max_position_embeddings=256, rms_norm_eps=1e-6,
+               rope_theta=100.0)
+
+
+@pytest.fixture(scope="module")
+def small():
+    ck = synthetic.checkpoint(SMALL, seed=3, std=0.08)
+    # non-trivial gammas (BF16-exact), so each norm's gamma placement shows
+    rng = np.random.default_rng(4)
+    for w in ck.layers:
+        for name in ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm"):
+            a = getattr(w, name)
+            a[:] = rb((0.5 + rng.random(a.size)).astype(np.float32))
+    ck.final_norm[:] = rb((0.5 + rng.random(ck.final_norm.size)).astype(np.float32))
+    return ck
+
+
+# Logits agree to this fraction of their largest magnitude: the two sides
+# differ in summation order and precision, which moves a BF16 rounding by one
+# step now and then (observed: below 1e-4); a RoPE sign error, a dropped
+# residual or swapped norm gammas move the logits by more than their scale.
+TOL = 0.01
+
+
+def test_oracle_forward_matches_float64_numpy(small):
+    om = O.Model(small)
+    nm = NumpyModel(small)
+    ids = synthetic.prompt(40, SMALL.vocab_size, seed=5)
+    cache = om.cache(64)
+    for n, t in enumerate(ids):
+        got = om.forward([int(t)], cache).astype(np.float64)
+        want = nm.step(int(t))
+        scale = np.max(np.abs(want))
+        err = np.max(np.abs(got - want))
+        assert err <= TOL * scale, f"position {n}: max error {err:.4g} vs scale {scale:.4g}"
+    # a 40-token prefill (one chunk) gives the same last logits
+    _, last = om.prefill(ids, 64)
+    assert np.array_equal(last.view(np.uint32), got.astype(np.float32).view(np.uint32))
+
+
+def test_zero_output_projections_leave_the_residual_stream(small):
+    """W_o = W_down = 0: x stays rb(E[t]) through every layer (x + rb(0)),
+    so the logits are the final norm and LM head of the embedding row."""
+    ck = synthetic.checkpoint(SMALL, seed=6, std=0.08)
+    for w in ck.layers:
+        w.o_proj[:] = 0
+        w.down_proj[:] = 0
+    om = O.Model(ck)
+    cache = om.cache(16)
+    H, V = SMALL.hidden_size, SMALL.vocab_size
+    for t in (0, 7, 311):
+        got = om.forward([t], cache)
+        e = ck.embed_tokens[t].astype(np.uint32) << 16
+        x = e.view(np.float32).reshape(1, H).copy()
+        y = np.empty_like(x)
+        O.lib().y2o_norm_apply(_p(x), 1, H, _p(ck.final_norm), C.c_float(SMALL.rms_norm_eps), _p(y))
+        want = np.empty(V, np.float32)
+        O.lib().y2o_linear(_p(ck.lm_head), V, H, _p(y), 1, _p(want))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+PHASE_TINY = Config(hidden_size=64, num_hidden_layers=1, num_attention_heads=2, num_key_value_heads=1,
+                    head_dim=32, intermediate_size=64, vocab_size=184704, max_position_embeddings=64,
+                    rms_norm_eps=1e-6, rope_theta=1e6)
+
+
+@pytest.mark.parametrize("phase,lo,hi,stop", [(O.PHASE_ABC, 0, EOD, ABC_END),
+                                               (O.PHASE_SEMANTIC, CODEC_OFFSET, CODEC_OFFSET + CODEC_SIZE,
+                                                MUSIC_END)])
+def test_project_phase_ranges(phase, lo, hi, stop):
+    ck = synthetic.checkpoint(PHASE_TINY, seed=7)
+    om = O.Model(ck)
+    ids = synthetic.prompt(5, PHASE_TINY.vocab_size, seed=8)
+    c_full, c_phase = om.cache(8), om.cache(8)
+    full = om.forward(ids, c_full)
+    ph = om.forward_phase(ids, c_phase, phase)
+    keep = np.zeros(PHASE_TINY.vocab_size, bool)
+    keep[lo:hi] = True
+    keep[stop] = True
+    assert np.array_equal(ph[keep].view(np.uint32), full[keep].view(np.uint32))
+    assert np.all(ph[~keep] == -np.inf)

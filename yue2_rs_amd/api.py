@@ -115,6 +115,7 @@ def lib() -> C.CDLL:
         "yue2_hip_synthetic_bf16": (None, [vp, sz, u64, u64, f32, i32]),
         "yue2_hip_selftest_math": (i32, [i32, vp, vp, sz]),
         "yue2_hip_norm_fallbacks": (i32, [vp]),
+        "yue2_hip_model_advance_sequence": (i32, [vp, i32]),
         "yue2_hip_decoder_time_kernel": (i32, [vp, i32, i32, vp, vp]),
         "yue2_hip_trace_step": (i32, [vp, vp, vp, i32, vp, i32, vp, vp]),
         "yue2_hip_model_set_step_kernel": (i32, [vp, i32]),
@@ -273,6 +274,11 @@ class Model:
         """Use the persistent token-step kernel for decode steps; returns
         whether it is in use (False when the shape has none)."""
         return bool(_check(lib().yue2_hip_model_set_step_kernel(self._h, 1 if on else 0)))
+
+    def advance_sequence(self, add: int) -> None:
+        """Diagnostics: advance the launch sequence of the model's forward
+        workspace by `add` (the step kernel's tagged-word epoch)."""
+        _check(lib().yue2_hip_model_advance_sequence(self._h, int(add)))
 
     def norm_fallbacks(self) -> int:
         return int(lib().yue2_hip_norm_fallbacks(self._h))

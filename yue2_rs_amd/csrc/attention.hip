@@ -13,6 +13,9 @@ constexpr int kAttnThreads = 512;
 template <int D, int MAXG>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const AttnArgs a) {
     extern __shared__ __align__(16) float e_s[];  // [G][bpw * 64]
+    // no key/value append for a token the sampler chose as the phase's end
+    // (the reference stops before its forward, src/sampling.rs:268-271)
+    if (ld_dev_i(&a.st->done)) return;
     attn_group<kAttnThreads, D, MAXG>(a, blockIdx.x, blockIdx.y, blockIdx.z, e_s);
 }
 

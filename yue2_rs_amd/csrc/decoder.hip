@@ -34,6 +34,7 @@ struct Yue2Decoder {
     MtState* mt = nullptr;
     uint32_t* streams = nullptr;
     void* cand = nullptr;  // chunked choose(): candidate lists and chunk totals
+    void* big = nullptr;   // choose(): survivors beyond the LDS capacity
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
     hipGraph_t graph = nullptr;
@@ -86,6 +87,7 @@ static void decoder_release(Yue2Decoder* d) {
     if (d->mt) (void)hipFree(d->mt);
     if (d->streams) (void)hipFree(d->streams);
     if (d->cand) (void)hipFree(d->cand);
+    if (d->big) (void)hipFree(d->big);
     d->w.release();
 }
 
@@ -136,6 +138,7 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     const int chunks = (V + kChooseChunk - 1) / kChooseChunk;
     if (rc == YUE2_OK && e == hipSuccess && list > 0)
         e = hipMalloc(&d->cand, sizeof(uint64_t) * (size_t)chunks * list + sizeof(int2) * chunks);
+    if (rc == YUE2_OK && e == hipSuccess && d->need_rng) e = hipMalloc(&d->big, survivor_bytes(V));
     if (rc == YUE2_OK && e == hipSuccess) e = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);
     if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->fork, hipEventDisableTiming);
     if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->join, hipEventDisableTiming);
@@ -165,6 +168,7 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
         a.chunks = chunks;
         a.list = list;
     }
+    if (d->big) set_survivor_buffers(a, d->big, V);
     a.cfg_scale = scale;
     a.legacy = legacy;
     if (sampling) {
@@ -258,9 +262,10 @@ extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logit
     if (!d || steps < 0) return fail(YUE2_ERR_ARG, "null decoder or negative steps");
     if (d->ended || steps == 0) return 0;
     if (int rc = check_room(d, steps)) return rc;
+    hipStream_t s = d->m->stream;
+    d->w.reserve_launches(s, steps);
     if (!d->started)
         if (int rc = start(d, first_logits)) return rc;
-    hipStream_t s = d->m->stream;
     if (step_ms && (int)d->events.size() < 2 * steps) {
         while ((int)d->events.size() < 2 * steps) {
             hipEvent_t ev;
@@ -292,7 +297,9 @@ extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logit
         for (int i = 0; i < ran; ++i)
             (void)hipEventElapsedTime(&step_ms[i], d->events[2 * i], d->events[2 * i + 1]);
     if (int rc = read_tokens(d, d->steps_done, ran, tokens)) return rc;
-    for (int b = 0; b < d->rows; ++b) d->caches[b]->length += ran;
+    // the end token's step ran no forward (src/sampling.rs:268-271): its
+    // position holds no key/value
+    for (int b = 0; b < d->rows; ++b) d->caches[b]->length += d->ended ? ran - 1 : ran;
     d->steps_done += ran;
     return ran;
 }
@@ -336,6 +343,7 @@ static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double
     for (int b = 0; b < d->rows; ++b)
         kvb += L * 2.0 * kv * 2.0 * (d->caches[b]->length + 1) + 2.0 * H;
     hipStream_t s = m->stream;
+    d->w.reserve_launches(s, (int64_t)iters + 1);
     hipEvent_t b0, b1;
     if (hipEventCreate(&b0) != hipSuccess) return fail(YUE2_ERR_DEVICE, "hipEventCreate");
     if (hipEventCreate(&b1) != hipSuccess) {
@@ -446,6 +454,7 @@ extern "C" int32_t yue2_hip_choose(const float* logits, int32_t vocab, const Yue
     const size_t o_hist = take(sizeof(int32_t) * std::max(history_len, 1));
     const size_t o_cand = take(list > 0 ? sizeof(uint64_t) * (size_t)chunks * list : 0);
     const size_t o_meta = take(list > 0 ? sizeof(int2) * chunks : 0);
+    const size_t o_big = take(rng ? survivor_bytes(vocab) : 0);
     char* p = nullptr;
     hipError_t e = hipMalloc(&p, at);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(choose)");
@@ -487,6 +496,7 @@ extern "C" int32_t yue2_hip_choose(const float* logits, int32_t vocab, const Yue
             a.chunks = chunks;
             a.list = list;
         }
+        if (rng) set_survivor_buffers(a, p + o_big, vocab);
         launch_choose(s, a);
         e = hipGetLastError();
     }

@@ -11,8 +11,14 @@
 // phases: a dependency costs one store-to-load visibility.
 //
 // Tags: (epoch << 12) | (layer << 4) | kind, epoch = launch sequence + 1
-// (20 bits).  Each word is rewritten every launch; the state reset bumps the
-// sequence, so words left by an aborted launch can never match.  A buffer is
+// (20 bits).  The words of x, q/k/v, the attention output and the SwiGLU
+// output are rewritten every launch; a block statistic or partial is
+// rewritten only by launches whose context reaches its block, so it can keep
+// an old launch's tag indefinitely.  The host therefore clears all words and
+// restarts the sequence before 2^20 launches have run since the last clear
+// (Workspace::reserve_launches): between two clears every launch has its own
+// epoch.  The state reset bumps the sequence, so words left by an aborted
+// launch can never match.  A buffer is
 // rewritten only after all its readers have consumed it: every rewrite
 // depends, through the step's own data dependencies, on outputs that each
 // reader produced after its read (x after down needs every workgroup's

@@ -168,7 +168,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 
 __global__ void advance_kernel(StepState* st, int rows) {
     if (threadIdx.x == 0) {
-        for (int b = 0; b < rows; ++b) st->pos[b] += 1;
+        // an end token's step appended nothing
+        if (!st->done)
+            for (int b = 0; b < rows; ++b) st->pos[b] += 1;
         st->step += 1;
     }
 }
@@ -298,6 +300,14 @@ __global__ void reset_state_kernel(StepState* st, int32_t* c0, int n0, int32_t* 
     }
     for (int i = threadIdx.x; i < n0; i += blockDim.x) c0[i] = 0;
     for (int i = threadIdx.x; i < n1; i += blockDim.x) c1[i] = 0;
+}
+
+__global__ void sequence_kernel(StepState* st, int set, int value) {
+    if (threadIdx.x == 0) st->seq = set ? value : st->seq + value;
+}
+
+void launch_sequence(hipStream_t s, StepState* st, int set, int value) {
+    sequence_kernel<<<1, 64, 0, s>>>(st, set, value);
 }
 
 void launch_fill(hipStream_t s, float* p, size_t n, float v) {

@@ -23,6 +23,13 @@ constexpr int kContext = 24576;
 struct StepState;
 void launch_reset_state(hipStream_t s, StepState* st, int32_t* c0 = nullptr, int n0 = 0,
                         int32_t* c1 = nullptr, int n1 = 0);
+// st->seq = value (set != 0) or st->seq += value.
+void launch_sequence(hipStream_t s, StepState* st, int set, int value);
+
+// The step kernel's tagged words carry a 20-bit epoch (launch sequence + 1).
+// Launches between two clears of the words must stay below this count, so
+// that no word left by an earlier launch can carry a later launch's tag.
+constexpr int64_t kEpochLaunches = (int64_t)1 << 20;
 
 struct LayerDev {
     uint16_t *wqkv, *wo, *wg, *wu, *wd;
@@ -42,11 +49,22 @@ struct Workspace {
     int32_t* token_log = nullptr;
     void* step_args = nullptr;  // device copy of the step kernel's arguments
     void* flow_block = nullptr; // the step kernel's tagged-word buffers
+    size_t flow_words = 0;      // 64-bit words in flow_block
     void* step_host = nullptr;  // host copy of the same (StepArgs)
     bool step_args_ready = false;
+    // Upper bound of the launch-sequence increments since the tagged words
+    // were last cleared (each reset adds 2, each step-kernel launch 1).
+    int64_t seq_bound = 0;
     int ensure(int rows, int max_blocks, const Yue2Config& c);
     // Clear the step state and every sync counter (stream-ordered).
-    void reset(hipStream_t s) { launch_reset_state(s, st, counters, counter_n, bars, 2); }
+    void reset(hipStream_t s) {
+        launch_reset_state(s, st, counters, counter_n, bars, 2);
+        seq_bound += 2;
+    }
+    // Before a reset and n step-kernel launches on stream s: when they could
+    // reach kEpochLaunches since the last clear, clear the tagged words and
+    // restart the sequence at 0 (stream-ordered, no allocation).
+    void reserve_launches(hipStream_t s, int64_t n);
     void release();
     Workspace() = default;
     Workspace(const Workspace&) = delete;

@@ -125,11 +125,24 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     return YUE2_OK;
 }
 
+void Workspace::reserve_launches(hipStream_t s, int64_t n) {
+    if (!flow_block) return;  // no step kernel on this workspace: no tagged words
+    if (seq_bound + n + 2 + 8 < kEpochLaunches) {
+        seq_bound += n;
+        return;
+    }
+    launch_fill(s, static_cast<float*>(flow_block), 2 * flow_words, 0.0f);  // tag 0 matches no poll
+    launch_sequence(s, st, 1, 0);
+    seq_bound = n;
+}
+
 void Workspace::release() {
     if (block) (void)hipFree(block);
     if (flow_block) (void)hipFree(flow_block);
     block = nullptr;
     flow_block = nullptr;
+    flow_words = 0;
+    seq_bound = 0;
     step_args = nullptr;
     step_args_ready = false;
     rows = max_blocks = 0;
@@ -251,7 +264,11 @@ int prepare_step(Yue2Model* m, Workspace& w) {
             return hip_fail(e, "hipMalloc(step dataflow words)");
         }
         e = hipMemset(w.flow_block, 0, words * sizeof(uint64_t));
+        // the sequence restarts with the cleared words
+        if (e == hipSuccess) e = hipMemset(&w.st->seq, 0, sizeof(int32_t));
         if (e != hipSuccess) return hip_fail(e, "hipMemset(step dataflow words)");
+        w.flow_words = words;
+        w.seq_bound = 0;
     }
     uint64_t* p = static_cast<uint64_t*>(w.flow_block);
     a.tx = p;
@@ -518,6 +535,17 @@ extern "C" int32_t yue2_hip_model_set_step_kernel(Yue2Model* m, int32_t on) {
     return m->step_kernel ? 1 : 0;
 }
 
+extern "C" int32_t yue2_hip_model_advance_sequence(Yue2Model* m, int32_t add) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || add < 0) return fail(YUE2_ERR_ARG, "null model or negative advance");
+    Workspace& w = m->ws;
+    if (!w.flow_block) return fail(YUE2_ERR_ARG, "the model has run no step-kernel forward");
+    launch_sequence(m->stream, w.st, 0, add);
+    w.seq_bound += add;
+    hipError_t e = hipStreamSynchronize(m->stream);
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "sequence advance");
+}
+
 extern "C" int32_t yue2_hip_norm_fallbacks(const Yue2Model* m) {
     if (!m) return 0;
     return m->norm_fallbacks;
@@ -609,6 +637,7 @@ extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* i
     kv.base[0] = c->kv;
     kv.capacity[0] = c->capacity;
     hipStream_t s = m->stream;
+    m->ws.reserve_launches(s, n);
     m->ws.reset(s);
     for (int t = 0; t < n; ++t) {
         launch_set_state(s, m->ws.st, 1, c->length + t, 0, ids[t], 0);
@@ -662,6 +691,7 @@ extern "C" int32_t yue2_hip_trace_step(Yue2Model* m, Yue2Cache* c, Yue2Cache* c2
         kv.capacity[b] = cs[b]->capacity;
     }
     hipStream_t s = m->stream;
+    w.reserve_launches(s, 1);
     w.reset(s);
     launch_set_state(s, w.st, rows, c->length, rows > 1 ? c2->length : 0, id, rows > 1 ? id : 0);
     int rc = enqueue_step_fused(m, w, kv, rows, false, YUE2_PHASE_NONE, s, dev, nb);

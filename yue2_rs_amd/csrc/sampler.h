@@ -36,7 +36,21 @@ struct SampleArgs {
     uint64_t* cand;
     int2* meta;
     int chunks, list;
+    // survivors beyond the LDS capacity (any count up to the vocabulary):
+    // order keys [big_cap] (big_cap = vocabulary rounded up to a power of
+    // two, the sort's padding), their exponentials and probabilities [vocab]
+    uint64_t* big;
+    float *big_e, *big_p;
+    int big_cap;
 };
+
+// Entries of SampleArgs::big for a vocabulary: the next power of two >= vocab.
+int survivor_capacity(int vocab);
+// Bytes of the three survivor overflow arrays for a vocabulary.
+size_t survivor_bytes(int vocab);
+// Point a's overflow arrays into `base` (survivor_bytes(vocab) bytes, 8-byte
+// aligned).
+void set_survivor_buffers(SampleArgs& a, void* base, int vocab);
 
 // Length of each chunk's candidate list for these settings, or 0 when the
 // single-workgroup kernel has to run (top-k too large for the chunked path).

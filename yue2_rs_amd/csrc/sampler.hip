@@ -165,14 +165,16 @@ __device__ __forceinline__ float seq_sum(const float* v, int n) {
     return s;
 }
 
-// Steps 6-8 over the n <= kSurvivorMax survivors, given as order keys in
-// surv (scores in sc): sort by score descending and id ascending (:174),
+// Steps 6-8 over the n survivors, given as order keys in surv (scores in
+// sc; surv holds the next power of two >= n entries, e_val and p_s n each:
+// LDS arrays of kSurvivorMax, or the overflow arrays in global memory for
+// more survivors): sort by score descending and id ascending (:174),
 // top-p (:175-190) and renormalisation (:191-197) as sequential f32 sums,
 // then the exponential race in id order (:198-214), whose uniforms are
 // stream positions 2 id and 2 id + 1 of this token's block.  Returns the
 // chosen id in every thread.
 __device__ int32_t race_tail(const SampleArgs& a, int step, const float* sc, uint64_t* surv,
-                             float* e_val, int n, int* s_kept, int* s_sel) {
+                             float* e_val, float* p_s, int n, int* s_kept, int* s_sel) {
     const int tid = threadIdx.x, nt = blockDim.x;
     int n2 = 2;
     while (n2 < n) n2 <<= 1;
@@ -184,7 +186,6 @@ __device__ int32_t race_tail(const SampleArgs& a, int step, const float* sc, uin
     __syncthreads();
     // The sums and the cumulative pass are sequential (in sorted order, as in
     // the reference); the divisions are independent and run on all threads.
-    __shared__ float p_s[kSurvivorMax];
     __shared__ float s_sum;
     const bool nucleus = a.top_p < 1.0f;
     if (nucleus) {
@@ -284,6 +285,7 @@ __device__ int32_t race_tail(const SampleArgs& a, int step, const float* sc, uin
 __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
     __shared__ uint64_t surv[kSurvivorMax];
     __shared__ float e_val[kSurvivorMax];
+    __shared__ float p_buf[kSurvivorMax];
     __shared__ uint32_t hist[256];
     __shared__ int32_t window_ids[kWindowMax];
     __shared__ int32_t s_count, s_bad, s_sel, s_kept;
@@ -371,23 +373,35 @@ __global__ __launch_bounds__(1024) void choose_kernel(const SampleArgs a) {
             __syncthreads();
         }
         const float threshold = from_ukey(s_prefix);
-        // 5. Survivors: finite scores >= threshold (ties kept, :173).
-        if (tid == 0) s_count = 0;
-        __syncthreads();
-        for (int i = tid; i < V; i += 1024) {
-            const float v = sc[i];
-            if (is_finite(v) && v >= threshold) {
-                const int at = atomicAdd(&s_count, 1);
-                if (at < kSurvivorMax) surv[at] = order_key(v, i);
+        // 5. Survivors: finite scores >= threshold (ties kept, :173), into
+        //    LDS, or (when more than it holds survive) into the overflow arrays
+        uint64_t* dst = surv;
+        int n = 0;
+        bool overflow = false;
+        for (int pass = 0; pass < 2; ++pass) {
+            const int cap = pass == 0 ? kSurvivorMax : a.big_cap;
+            __syncthreads();  // every thread has read the previous pass's count
+            if (tid == 0) s_count = 0;
+            __syncthreads();
+            for (int i = tid; i < V; i += 1024) {
+                const float v = sc[i];
+                if (is_finite(v) && v >= threshold) {
+                    const int at = atomicAdd(&s_count, 1);
+                    if (at < cap) dst[at] = order_key(v, i);
+                }
             }
+            __syncthreads();
+            n = s_count;
+            if (n <= cap) break;
+            if (pass == 1 || !a.big) {
+                if (tid == 0) atomicCAS(&st->error, 0, 5);
+                return;
+            }
+            dst = a.big;
+            overflow = true;
         }
-        __syncthreads();
-        const int n = s_count;
-        if (n > kSurvivorMax) {
-            if (tid == 0) atomicCAS(&st->error, 0, 5);
-            return;
-        }
-        selected = race_tail(a, step, sc, surv, e_val, n, &s_kept, &s_sel);
+        selected = overflow ? race_tail(a, step, sc, a.big, a.big_e, a.big_p, n, &s_kept, &s_sel)
+                            : race_tail(a, step, sc, surv, e_val, p_buf, n, &s_kept, &s_sel);
     }
     if (tid == 0) publish(a, step, selected);
 }
@@ -474,6 +488,7 @@ __global__ __launch_bounds__(1024) void finish_kernel(const SampleArgs a) {
     __shared__ uint64_t rescan_last[kChooseChunksMax];
     __shared__ uint64_t surv[kSurvivorMax];
     __shared__ float e_val[kSurvivorMax];
+    __shared__ float p_buf[kSurvivorMax];
     __shared__ uint32_t hist[256];
     __shared__ int32_t wsum[16];
     __shared__ uint64_t red[16];
@@ -601,17 +616,8 @@ __global__ __launch_bounds__(1024) void finish_kernel(const SampleArgs a) {
         __syncthreads();
     }
     const float threshold = from_ukey(s_prefix);
-    // survivors (:173): listed entries >= threshold ...
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        if (tid + 1024 * q >= T) continue;
-        if (key_value(mine[q]) >= threshold) {
-            const int at = atomicAdd(&s_n, 1);
-            if (at < kSurvivorMax) surv[at] = mine[q];
-        }
-    }
-    // ... and, from chunks whose list was cut at an entry equal to the
-    // threshold, the entries after that one in order that equal it too
+    // chunks whose list was cut at an entry equal to the threshold: the
+    // entries after that one in order that equal it survive too
     if (tid < nch && fin > L) {
         const uint64_t last = a.cand[(size_t)tid * L + L - 1];
         if (key_value(last) >= threshold) {
@@ -622,26 +628,49 @@ __global__ __launch_bounds__(1024) void finish_kernel(const SampleArgs a) {
     }
     __syncthreads();
     const int nres = s_nres;
-    for (int r = 0; r < nres; ++r) {
-        const int i = rescan[r] * kChooseChunk + tid;
-        if (i < V) {
-            const float v = a.scores[i];
-            if (is_finite(v) && v >= threshold) {
-                const uint64_t k = order_key(v, i);
-                if (k > rescan_last[r]) {
-                    const int at = atomicAdd(&s_n, 1);
-                    if (at < kSurvivorMax) surv[at] = k;
+    // survivors (:173), into LDS, or (when more than it holds survive) into
+    // the overflow arrays: listed entries >= threshold and the rescans' ties
+    uint64_t* dst = surv;
+    int n = 0;
+    bool overflow = false;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int cap = pass == 0 ? kSurvivorMax : a.big_cap;
+        __syncthreads();  // every thread has read the previous pass's count
+        if (tid == 0) s_n = 0;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (tid + 1024 * q >= T) continue;
+            if (key_value(mine[q]) >= threshold) {
+                const int at = atomicAdd(&s_n, 1);
+                if (at < cap) dst[at] = mine[q];
+            }
+        }
+        for (int r = 0; r < nres; ++r) {
+            const int i = rescan[r] * kChooseChunk + tid;
+            if (i < V) {
+                const float v = a.scores[i];
+                if (is_finite(v) && v >= threshold) {
+                    const uint64_t k = order_key(v, i);
+                    if (k > rescan_last[r]) {
+                        const int at = atomicAdd(&s_n, 1);
+                        if (at < cap) dst[at] = k;
+                    }
                 }
             }
         }
+        __syncthreads();
+        n = s_n;
+        if (n <= cap) break;
+        if (pass == 1 || !a.big) {
+            if (tid == 0) atomicCAS(&st->error, 0, 5);
+            return;
+        }
+        dst = a.big;
+        overflow = true;
     }
-    __syncthreads();
-    const int n = s_n;
-    if (n > kSurvivorMax) {
-        if (tid == 0) atomicCAS(&st->error, 0, 5);
-        return;
-    }
-    const int32_t selected = race_tail(a, step, a.scores, surv, e_val, n, &s_kept, &s_sel);
+    const int32_t selected = overflow ? race_tail(a, step, a.scores, a.big, a.big_e, a.big_p, n, &s_kept, &s_sel)
+                                      : race_tail(a, step, a.scores, surv, e_val, p_buf, n, &s_kept, &s_sel);
     if (tid == 0) publish(a, step, selected);
 }
 
@@ -706,6 +735,23 @@ __global__ __launch_bounds__(256) void mt_generate_kernel(MtState* mt, uint32_t*
     __syncthreads();
     for (int i = tid; i < 624; i += 256) mt->state[i] = s[i];
     if (tid == 0) mt->next = next;
+}
+
+int survivor_capacity(int vocab) {
+    int c = 2;
+    while (c < vocab) c <<= 1;
+    return c;
+}
+
+size_t survivor_bytes(int vocab) {
+    return sizeof(uint64_t) * (size_t)survivor_capacity(vocab) + 2 * sizeof(float) * (size_t)vocab;
+}
+
+void set_survivor_buffers(SampleArgs& a, void* base, int vocab) {
+    a.big_cap = survivor_capacity(vocab);
+    a.big = static_cast<uint64_t*>(base);
+    a.big_e = reinterpret_cast<float*>(a.big + a.big_cap);
+    a.big_p = a.big_e + vocab;
 }
 
 int choose_list_len(int vocab, int mode, float temperature, int top_k) {

@@ -216,7 +216,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     const ArgsPtr args = (ArgsPtr)args_dev;
     const int tid = threadIdx.x, wg = blockIdx.x, nwg = gridDim.x;
     StepState* st = fresh(args)->st;
-    if (ld_dev_i(&st->error)) return;
+    // after an error, or once the sampler chose the phase's end token (the
+    // reference stops before that token's forward, src/sampling.rs:268-271)
+    if (ld_dev_i(&st->error) || ld_dev_i(&st->done)) return;
     const int seq = *gbl(&st->seq);
     const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
     uint4 ring[RMAX];

@@ -253,6 +253,9 @@ int prepare_step(Yue2Model* m, Workspace& w) {
     a.logits = w.logits;
     a.st = w.st;
     if (step_lds_bytes(a, m->cus) > kStepLdsMax) return 1;
+    // one workgroup per CU, all resident together: the polls between them
+    // would otherwise wait for a workgroup that cannot start
+    if (step_resident_per_cu(a, m->cus) < 1) return 1;
     // tagged-word buffers, zero (= no tag) until first written
     const size_t n_x = rows * (size_t)H, n_qkv = rows * qkvw, n_att = rows * qw, n_act = rows * (size_t)I;
     const size_t n_blk = rows * (size_t)Hq * w.blk_stride, n_part = n_blk * D;
@@ -289,7 +292,7 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
                        hipStream_t s, unsigned long long* trace, int trace_slots) {
     if (!trace && !m->step_kernel) return 1;
     if ((head && phase != YUE2_PHASE_NONE) || rows != w.rows || !step_supported(m->c, rows, m->cus)) return 1;
-    if (!w.step_args_ready) return fail(YUE2_ERR_DEVICE, "step kernel arguments not prepared");
+    if (!w.step_args_ready) return 1;  // prepare_step found no resident step kernel: per-phase path
     StepCall call{};
     call.kv = kv;
     call.head = head ? 1 : 0;
@@ -340,6 +343,10 @@ int step_error(const StepState& st) {
     if (st.error == 3) return fail(YUE2_ERR_EMPTY, "Empty sampling distribution");
     if (st.error == 4) return fail(YUE2_ERR_LOGITS, "Model produced invalid logits");
     if (st.error == 5) return fail(YUE2_ERR_TIES, "top-k survivors exceed the device sort capacity");
+    if (st.error == 8)
+        return fail(YUE2_ERR_DEVICE,
+                    "device error 8: a step-kernel workgroup waited too long for another's output "
+                    "(workgroups not all resident, or the device shared with other work)");
     if (st.error != 0) return fail(YUE2_ERR_DEVICE, "device error " + std::to_string(st.error));
     return YUE2_OK;
 }

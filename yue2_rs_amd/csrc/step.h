@@ -47,6 +47,10 @@ bool step_supported(const Yue2Config& c, int rows, int nwg);
 // workgroups; launches need at most kStepLdsMax.
 constexpr size_t kStepLdsMax = 128 * 1024;
 size_t step_lds_bytes(const StepArgs& a, int nwg);
+// Workgroups of the step kernel for these arguments that fit on one CU at
+// once (its registers and dynamic LDS); the launch needs at least 1, since
+// its workgroups wait for each other's outputs.
+int step_resident_per_cu(const StepArgs& a, int nwg);
 hipError_t launch_step(hipStream_t s, const StepArgs* dev_args, const StepArgs& host_args,
                        const StepCall& call, int nwg);
 

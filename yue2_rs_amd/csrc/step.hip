@@ -390,6 +390,27 @@ size_t step_lds_bytes(const StepArgs& a, int nwg) {
     return std::max((size_t)a.rows * kmax * sizeof(float), attn_flow_lds(G, a.head_dim, bpw));
 }
 
+template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
+static int resident_t(size_t lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false>), kStepThreads,
+            lds) != hipSuccess)
+        return 0;
+    return n;
+}
+
+int step_resident_per_cu(const StepArgs& a, int nwg) {
+    const size_t lds = step_lds_bytes(a, nwg);
+    if (lds > kStepLdsMax) return 0;
+    const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
+    if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16)
+        return a.rows == 1 ? resident_t<1, 128, 3, 6, 6, 16, false>(lds) : resident_t<2, 128, 3, 6, 6, 16, false>(lds);
+    if (a.head_dim == 64 && G == 4 && ith == 2)
+        return a.rows == 1 ? resident_t<1, 64, 4, 2, 2, 6, true>(lds) : resident_t<2, 64, 4, 2, 2, 6, true>(lds);
+    return 0;
+}
+
 hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {
     const size_t lds = step_lds_bytes(a, nwg);
     if (lds > kStepLdsMax) return hipErrorInvalidValue;

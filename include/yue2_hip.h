@@ -217,6 +217,19 @@ int32_t yue2_hip_choose(const float *logits, int32_t vocab, const Yue2Sampling *
                         const int32_t *history, int32_t history_len, int32_t step,
                         int32_t phase, int32_t legacy, const uint32_t *draws, int32_t *id);
 
+/* yue2_hip_choose without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, checks,
+ * result and errors as yue2_hip_choose; its device buffers live in one
+ * file-scope scratch array per GPU (9 MiB, held until the process ends), so
+ * vocab is limited to 262144 entries (YUE2_ERR_ARG beyond).  It runs on the
+ * null stream.  Calls on one GPU share that array: the library lock
+ * serialises them within a process, and callers must not overlap calls on
+ * one GPU by other means. */
+int32_t yue2_hip_choose_noalloc(const float *logits, int32_t vocab, const Yue2Sampling *sampling,
+                                const int32_t *history, int32_t history_len, int32_t step,
+                                int32_t phase, int32_t legacy, const uint32_t *draws, int32_t *id);
+
 /* sampling::generate (src/sampling.rs:222-294) on the device. */
 int32_t yue2_hip_generate(Yue2Model *m, const int32_t *prefix, int32_t prefix_len,
                           const Yue2Sampling *sampling, uint64_t seed, int32_t phase,

@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
         "yue2_hip_decoder_logits": (i32, [vp, vp]),
         "yue2_hip_generate": (i32, [vp, vp, i32, vp, u64, i32, vp, i32, f32, i32, vp, vp, vp]),
         "yue2_hip_choose": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, vp, vp]),
+        "yue2_hip_choose_noalloc": (i32, [vp, i32, vp, vp, i32, i32, i32, i32, vp, vp]),
         "yue2_hip_last_error": (C.c_char_p, []),
         "yue2_hip_synchronize": (i32, []),
         "yue2_hip_synthetic_bf16": (None, [vp, sz, u64, u64, f32, i32]),
@@ -395,10 +396,12 @@ class Generated:
 
 
 def choose(logits: np.ndarray, sampling: Sampling, history: Sequence[int] = (), step: int = 0,
-           phase: int = PHASE_NONE, legacy: bool = False, draws: Optional[np.ndarray] = None) -> int:
+           phase: int = PHASE_NONE, legacy: bool = False, draws: Optional[np.ndarray] = None,
+           noalloc: bool = False) -> int:
     """sampling::choose (src/sampling.rs:103-215) on the device for one row of
     logits.  draws: the 2 * vocab MT19937 outputs the call consumes (needed
-    unless temperature is 0)."""
+    unless temperature is 0).  noalloc: through yue2_hip_choose_noalloc (no
+    device allocation; vocabularies up to 262144)."""
     lg = np.ascontiguousarray(logits, dtype=np.float32)
     h = np.ascontiguousarray(history, dtype=np.int32)
     d = None if draws is None else np.ascontiguousarray(draws, dtype=np.uint32)
@@ -406,8 +409,9 @@ def choose(logits: np.ndarray, sampling: Sampling, history: Sequence[int] = (), 
         raise ValueError("draws must hold 2 * vocab outputs")
     out = C.c_int32(-1)
     s = sampling.c()
-    _check(lib().yue2_hip_choose(_ptr(lg), len(lg), C.byref(s), _ptr(h) if len(h) else None, len(h), step,
-                                 phase, int(legacy), _ptr(d), C.byref(out)))
+    fn = lib().yue2_hip_choose_noalloc if noalloc else lib().yue2_hip_choose
+    _check(fn(_ptr(lg), len(lg), C.byref(s), _ptr(h) if len(h) else None, len(h), step, phase, int(legacy),
+              _ptr(d), C.byref(out)))
     return out.value
 
 

@@ -11,6 +11,7 @@
 // the chosen ids are copied back.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -427,56 +428,67 @@ extern "C" int32_t yue2_hip_decoder_time_kernel(Yue2Decoder* d, int32_t kernel, 
     return rc;
 }
 
-// sampling::choose (src/sampling.rs:103-215) for one row of logits.
-extern "C" int32_t yue2_hip_choose(const float* logits, int32_t vocab, const Yue2Sampling* sampling,
-                                   const int32_t* history, int32_t history_len, int32_t step,
-                                   int32_t phase, int32_t legacy, const uint32_t* draws,
-                                   int32_t* id) {
-    std::lock_guard<std::recursive_mutex> guard(library_lock());
-    if (!logits || !id || vocab < 1 || history_len < 0 || step < 0 || (history_len > 0 && !history))
-        return fail(YUE2_ERR_ARG, "bad choose arguments");
-    if (int rc = validate_sampling(sampling)) return rc;
-    if (int rc = check_phase_vocab(phase, vocab)) return rc;
+// Device buffers of one choose() call, carved from one region: the step
+// state, the logits, the tempered scores, the draws, the penalty window, the
+// chunk candidate lists and totals, and the survivor overflow arrays.
+struct ChooseLayout {
+    size_t st, logits, scores, draws, hist, cand, meta, big, total;
+    int list, chunks, hist_n;
+};
+
+static ChooseLayout choose_layout(int vocab, const Yue2Sampling* sampling, int history_len) {
+    ChooseLayout L{};
     const bool rng = sampling->temperature != 0.0f;
-    if (rng && !draws) return fail(YUE2_ERR_ARG, "choose needs 2 * vocab draws");
-    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 HIP device");
-    const size_t V = vocab;
-    const int list = choose_list_len(vocab, 1, sampling->temperature, sampling->top_k);
-    const int chunks = (vocab + kChooseChunk - 1) / kChooseChunk;
+    L.list = choose_list_len(vocab, 1, sampling->temperature, sampling->top_k);
+    L.chunks = (vocab + kChooseChunk - 1) / kChooseChunk;
+    // only the last penalty_window ids of the history are read (:130-131)
+    L.hist_n = std::min(history_len, sampling->penalty_window);
     size_t at = 0;
     auto take = [&](size_t bytes) {
         const size_t o = at;
         at = (at + bytes + 255) / 256 * 256;
         return o;
     };
-    const size_t o_st = take(sizeof(StepState)), o_logits = take(sizeof(float) * V);
-    const size_t o_scores = take(sizeof(float) * V), o_draws = take(rng ? sizeof(uint32_t) * 2 * V : 0);
-    const size_t o_hist = take(sizeof(int32_t) * std::max(history_len, 1));
-    const size_t o_cand = take(list > 0 ? sizeof(uint64_t) * (size_t)chunks * list : 0);
-    const size_t o_meta = take(list > 0 ? sizeof(int2) * chunks : 0);
-    const size_t o_big = take(rng ? survivor_bytes(vocab) : 0);
-    char* p = nullptr;
-    hipError_t e = hipMalloc(&p, at);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(choose)");
-    hipStream_t s = nullptr;
+    const size_t V = vocab;
+    L.st = take(sizeof(StepState));
+    L.logits = take(sizeof(float) * V);
+    L.scores = take(sizeof(float) * V);
+    L.draws = take(rng ? sizeof(uint32_t) * 2 * V : 0);
+    L.hist = take(sizeof(int32_t) * std::max(L.hist_n, 1));
+    L.cand = take(L.list > 0 ? sizeof(uint64_t) * (size_t)L.chunks * L.list : 0);
+    L.meta = take(L.list > 0 ? sizeof(int2) * L.chunks : 0);
+    L.big = take(rng ? survivor_bytes(vocab) : 0);
+    L.total = at;
+    return L;
+}
+
+// One choose() in the region p (laid out by L) on stream s: inputs copied in,
+// the kernels, the chosen id copied out.  Every field the kernels read before
+// writing is written here first (the step state in full), so p may hold
+// anything on entry.
+static int choose_run(char* p, const ChooseLayout& L, hipStream_t s, const float* logits, int32_t vocab,
+                      const Yue2Sampling* sampling, const int32_t* history, int32_t history_len,
+                      int32_t step, int32_t phase, int32_t legacy, const uint32_t* draws, int32_t* id) {
+    const bool rng = sampling->temperature != 0.0f;
+    const size_t V = vocab;
     StepState st{};
     st.step = step;
-    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipMemcpyAsync(p + o_st, &st, sizeof(st), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(p + o_logits, logits, sizeof(float) * V, hipMemcpyHostToDevice, s);
+    hipError_t e = hipMemcpyAsync(p + L.st, &st, sizeof(st), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(p + L.logits, logits, sizeof(float) * V, hipMemcpyHostToDevice, s);
     if (e == hipSuccess && rng)
-        e = hipMemcpyAsync(p + o_draws, draws, sizeof(uint32_t) * 2 * V, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess && history_len > 0)
-        e = hipMemcpyAsync(p + o_hist, history, sizeof(int32_t) * history_len, hipMemcpyHostToDevice, s);
+        e = hipMemcpyAsync(p + L.draws, draws, sizeof(uint32_t) * 2 * V, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess && L.hist_n > 0)
+        e = hipMemcpyAsync(p + L.hist, history + (history_len - L.hist_n), sizeof(int32_t) * L.hist_n,
+                           hipMemcpyHostToDevice, s);
     if (e == hipSuccess) {
         SampleArgs a{};
-        a.logits = reinterpret_cast<const float*>(p + o_logits);
-        a.scores = reinterpret_cast<float*>(p + o_scores);
-        a.stream[0] = a.stream[1] = rng ? reinterpret_cast<const uint32_t*>(p + o_draws) : nullptr;
-        a.history = reinterpret_cast<const int32_t*>(p + o_hist);
-        a.hist_len = history_len;
+        a.logits = reinterpret_cast<const float*>(p + L.logits);
+        a.scores = reinterpret_cast<float*>(p + L.scores);
+        a.stream[0] = a.stream[1] = rng ? reinterpret_cast<const uint32_t*>(p + L.draws) : nullptr;
+        a.history = reinterpret_cast<const int32_t*>(p + L.hist);
+        a.hist_len = L.hist_n;
         a.token_log = nullptr;
-        a.st = reinterpret_cast<StepState*>(p + o_st);
+        a.st = reinterpret_cast<StepState*>(p + L.st);
         a.rows = 1;
         a.vocab = vocab;
         a.phase = phase;
@@ -490,24 +502,100 @@ extern "C" int32_t yue2_hip_choose(const float* logits, int32_t vocab, const Yue
         a.window = sampling->penalty_window;
         a.min_tokens = sampling->min_tokens;
         a.legacy = legacy;
-        if (list > 0) {
-            a.cand = reinterpret_cast<uint64_t*>(p + o_cand);
-            a.meta = reinterpret_cast<int2*>(p + o_meta);
-            a.chunks = chunks;
-            a.list = list;
+        if (L.list > 0) {
+            a.cand = reinterpret_cast<uint64_t*>(p + L.cand);
+            a.meta = reinterpret_cast<int2*>(p + L.meta);
+            a.chunks = L.chunks;
+            a.list = L.list;
         }
-        if (rng) set_survivor_buffers(a, p + o_big, vocab);
+        if (rng) set_survivor_buffers(a, p + L.big, vocab);
         launch_choose(s, a);
         e = hipGetLastError();
     }
-    if (e == hipSuccess) e = hipMemcpyAsync(&st, p + o_st, sizeof(st), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(&st, p + L.st, sizeof(st), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (s) (void)hipStreamDestroy(s);
-    (void)hipFree(p);
     if (e != hipSuccess) return hip_fail(e, "choose");
     if (int rc = step_error(st)) return rc;
     *id = st.ids[0];
     return YUE2_OK;
+}
+
+static int choose_check(const float* logits, int32_t vocab, const Yue2Sampling* sampling, const int32_t* history,
+                        int32_t history_len, int32_t step, int32_t phase, const uint32_t* draws, int32_t* id) {
+    if (!logits || !id || vocab < 1 || history_len < 0 || step < 0 || (history_len > 0 && !history))
+        return fail(YUE2_ERR_ARG, "bad choose arguments");
+    if (int rc = validate_sampling(sampling)) return rc;
+    if (int rc = check_phase_vocab(phase, vocab)) return rc;
+    if (sampling->temperature != 0.0f && !draws) return fail(YUE2_ERR_ARG, "choose needs 2 * vocab draws");
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 HIP device");
+    return YUE2_OK;
+}
+
+// sampling::choose (src/sampling.rs:103-215) for one row of logits.
+extern "C" int32_t yue2_hip_choose(const float* logits, int32_t vocab, const Yue2Sampling* sampling,
+                                   const int32_t* history, int32_t history_len, int32_t step,
+                                   int32_t phase, int32_t legacy, const uint32_t* draws,
+                                   int32_t* id) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (int rc = choose_check(logits, vocab, sampling, history, history_len, step, phase, draws, id)) return rc;
+    const ChooseLayout L = choose_layout(vocab, sampling, history_len);
+    char* p = nullptr;
+    hipError_t e = hipMalloc(&p, L.total);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(choose)");
+    hipStream_t s = nullptr;
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    int rc = e == hipSuccess ? choose_run(p, L, s, logits, vocab, sampling, history, history_len, step, phase,
+                                          legacy, draws, id)
+                             : hip_fail(e, "hipStreamCreate(choose)");
+    if (s) (void)hipStreamDestroy(s);
+    (void)hipFree(p);
+    return rc;
+}
+
+// ---- choose() without allocation -------------------------------------------
+//
+// The scratch of yue2_hip_choose_noalloc: one region per device, laid out by
+// choose_layout for each call.  Its size covers a vocabulary of
+// kNoAllocVocabMax entries with any sampling settings.  In host code the
+// array's name stands for nothing usable: the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+constexpr int kNoAllocVocabMax = 262144;
+constexpr size_t kNoAllocScratchBytes = 9u << 20;  // 8.13 MiB at 262144 entries
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kNoAllocDevices = 64;
+static char* g_scratch_dev[kNoAllocDevices];
+
+// The scratch address on the current device (resolved on its first use).
+static int noalloc_scratch(char** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kNoAllocDevices) return fail(YUE2_ERR_DEVICE, "device index beyond the scratch table");
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return hip_fail(e, "hipGetSymbolAddress(choose scratch)");
+        g_scratch_dev[dev] = static_cast<char*>(ptr);
+    }
+    *out = g_scratch_dev[dev];
+    return YUE2_OK;
+}
+
+extern "C" int32_t yue2_hip_choose_noalloc(const float* logits, int32_t vocab, const Yue2Sampling* sampling,
+                                           const int32_t* history, int32_t history_len, int32_t step,
+                                           int32_t phase, int32_t legacy, const uint32_t* draws, int32_t* id) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (int rc = choose_check(logits, vocab, sampling, history, history_len, step, phase, draws, id)) return rc;
+    if (vocab > kNoAllocVocabMax)
+        return fail(YUE2_ERR_ARG, "vocabulary above the allocation-free choose() limit of 262144 entries");
+    const ChooseLayout L = choose_layout(vocab, sampling, history_len);
+    if (L.total > kNoAllocScratchBytes)
+        return fail(YUE2_ERR_ARG, "choose() request larger than the allocation-free scratch");
+    char* p = nullptr;
+    if (int rc = noalloc_scratch(&p)) return rc;
+    // the null stream: creating one of our own would allocate
+    return choose_run(p, L, nullptr, logits, vocab, sampling, history, history_len, step, phase, legacy, draws,
+                      id);
 }
 
 extern "C" int32_t yue2_hip_generate(Yue2Model* m, const int32_t* prefix, int32_t prefix_len,

@@ -194,17 +194,21 @@ Yue2Decoder *yue2_hip_decoder_new(Yue2Model *m, Yue2Cache *cond, Yue2Cache *unco
                                   const Yue2Sampling *sampling, uint64_t seed, int32_t phase,
                                   float scale, int32_t legacy);
 void yue2_hip_decoder_free(Yue2Decoder *d);
-/* Run `steps` token steps.  tokens receives the chosen ids; step_ms (may be
- * NULL) the per-step device time from HIP events.  Returns the number of
+/* Run `steps` token steps (choose a token, forward it).  tokens receives the
+ * chosen ids; step_ms (may be NULL) the per-step device time from HIP
+ * events.  Each launch forwards a token chosen before it and chooses the
+ * next one, so the token after a run's last is already chosen when the run
+ * returns (the next run starts with its forward).  Returns the number of
  * steps run or a negative Yue2Error.  With a phase that has an end token the
  * loop stops at the first end id: it is the last id returned, its step runs
  * no forward (src/sampling.rs:268-271), so the caches grow by one position
  * less than the steps returned, and later runs return 0. */
 int32_t yue2_hip_decoder_run(Yue2Decoder *d, const float *first_logits, int32_t steps,
                              int32_t *tokens, float *step_ms);
-/* The logits the decoder's next choose() reads (src/sampling.rs:261-267
- * before the mix): rows x vocab f32, the conditional row first; after a run
- * they are the last step's forward outputs.  The decoder must have run. */
+/* The logits of the decoder's last forward, which the choice of the token
+ * after it read (src/sampling.rs:261-267, before the CFG mix); before any
+ * forward, the first logits.  rows x vocab f32, the conditional row first.
+ * The decoder must have run. */
 int32_t yue2_hip_decoder_logits(Yue2Decoder *d, float *out);
 
 /* sampling::choose (src/sampling.rs:103-215) on the device for one row of

@@ -127,3 +127,47 @@ def test_3b_cfg_greedy_step_kernel_matches_oracle(gpu, oracle_threads):
         ol1, ol2 = om.forward([t], o1), om.forward([t], o2)
     assert list(toks) == want
     gm.close()
+
+
+@pytest.fixture(scope="module")
+def tied(gpu, oracle_threads):
+    """The reduced model with exact ties at the top of every step's logits:
+    every embedding carries 4.0 in dimension 0, which stays the largest
+    entry of the final hidden state, and LM-head rows [0, 3000) weigh that
+    dimension alone (1.0), so those 3000 logits are all rb(y[0])."""
+    ck = synthetic.checkpoint(synthetic.REDUCED, seed=2)
+    ck.embed_tokens[:, 0] = 0x4080  # BF16 4.0
+    ck.lm_head[:3000] = 0
+    ck.lm_head[:3000, 0] = 0x3F80   # BF16 1.0
+    gm = y2.Model.open(ck)
+    assert gm.set_step_kernel(True)
+    yield ck, gm, O.Model(ck)
+    gm.close()
+
+
+@pytest.mark.parametrize("ties", [100, 3000])
+@pytest.mark.parametrize("top_k,top_p,scale", [(50, 0.93, 1.0), (64, 1.0, 1.5), (50, 0.93, 1.5), (65, 0.93, 1.0)])
+def test_sampler_with_ties_at_the_top(tied, ties, top_k, top_p, scale):
+    """choose() where the top-k threshold is tied across and within the step
+    kernel's per-workgroup candidate lists: 100 ties (one list cut at the
+    threshold, its rows rescanned) and 3000 (more survivors than the LDS
+    arrays hold).  top_k 65 exceeds the fused lists and runs the separate
+    sampler kernels."""
+    ck, gm, om = tied
+    if ties != 3000:
+        # rows [ties, 3000) back to random rows of their own
+        ck = synthetic.checkpoint(synthetic.REDUCED, seed=2)
+        ck.embed_tokens[:, 0] = 0x4080
+        ck.lm_head[:ties] = 0
+        ck.lm_head[:ties, 0] = 0x3F80
+        gm = y2.Model.open(ck)
+        om = O.Model(ck)
+    V = ck.config.vocab_size
+    s = y2.Sampling(temperature=0.9, top_p=top_p, top_k=top_k, repetition_penalty=1.2, penalty_window=50,
+                    min_tokens=0, max_tokens=8)
+    pos = synthetic.prompt(40, V, seed=5)
+    neg = synthetic.prompt(30, V, seed=6) if scale != 1.0 else None
+    got = y2.generate(gm, pos, s, seed=99, negative=neg, scale=scale)
+    want, trunc = O.generate(om, pos, s, 99, negative=neg, scale=scale)
+    assert got.tokens == want and got.truncated == trunc
+    assert all(t < ties for t in want), "the tied rows carry all the probability"

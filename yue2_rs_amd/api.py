@@ -360,8 +360,9 @@ class Decoder:
         return tokens[:n], (ms[:n] if timing else None)
 
     def logits(self) -> np.ndarray:
-        """The logits the next choose() reads: [rows, vocab], conditional row
-        first (the last step's forward outputs after a run)."""
+        """The logits of the last forward (which the next token's choice
+        read; the first logits before any forward): [rows, vocab],
+        conditional row first."""
         out = np.empty((self.rows, self.model.config.vocab_size), dtype=np.float32)
         _check(lib().yue2_hip_decoder_logits(self._h, _ptr(out)))
         return out

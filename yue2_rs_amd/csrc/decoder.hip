@@ -1,14 +1,23 @@
 // decoder.hip -- the captured token loop of sampling::generate
 // (src/sampling.rs:222-294) on the device.
 //
-// One hipGraph holds a whole loop iteration: choose() over the previous
-// logits (with the CFG mix of a batch-2 decoder) -> embed the chosen id ->
-// every layer for every row -> LM head -> advance the device positions.  When
-// the sampler needs random numbers, a side branch of the same graph
-// generates the next token's block of 2 * vocab MT19937 outputs while the
-// layers run.  Positions, ids, the step counter and the penalty history live
-// in device memory, so the graph replays without parameter updates and only
-// the chosen ids are copied back.
+// The loop's first choose() (over the prefill logits) runs when the decoder
+// starts; after that one hipGraph launch forwards the chosen token and
+// chooses the next one: embed -> every layer for every row -> LM head ->
+// CFG mix + choose() -> advance the device positions.  So the token a run
+// returns last has already been chosen when the run ends, and its forward is
+// the next run's first launch.
+//  * Fused: where the persistent step kernel serves the shape and the
+//    sampler settings fit its candidate lists, the graph is that one kernel:
+//    its last workgroup generates the token's 2 * vocab MT19937 outputs and
+//    finishes choose() while the other workgroups run the layers and score
+//    their rows of the LM head (step.hip).
+//  * Otherwise the forward (step kernel or per-phase kernels) is followed by
+//    the sampler kernels of sampler.hip and an advance kernel, and a side
+//    branch of the same graph generates the draws while the layers run.
+// Positions, ids, the step counter and the penalty history live in device
+// memory, so the graph replays without parameter updates and only the
+// chosen ids are copied back.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,6 +45,8 @@ struct Yue2Decoder {
     uint32_t* streams = nullptr;
     void* cand = nullptr;  // chunked choose(): candidate lists and chunk totals
     void* big = nullptr;   // choose(): survivors beyond the LDS capacity
+    void* fcand = nullptr; // fused sampler: the workers' candidate lists
+    bool fused = false;    // choose() inside the step kernel
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
     hipGraph_t graph = nullptr;
@@ -89,6 +100,7 @@ static void decoder_release(Yue2Decoder* d) {
     if (d->streams) (void)hipFree(d->streams);
     if (d->cand) (void)hipFree(d->cand);
     if (d->big) (void)hipFree(d->big);
+    if (d->fcand) (void)hipFree(d->fcand);
     d->w.release();
 }
 
@@ -121,7 +133,6 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     if (d->rows == 2) cap = std::max(cap, uncond->capacity);
     const int V = m->c.vocab_size;
     int rc = d->w.ensure(d->rows, (cap + kBlockKeys - 1) / kBlockKeys, m->c);
-    if (rc == YUE2_OK && m->step_kernel && prepare_step(m, d->w) < 0) rc = YUE2_ERR_DEVICE;
     d->need_rng = sampling && sampling->temperature != 0.0f;
     hipError_t e = hipSuccess;
     if (rc == YUE2_OK && d->need_rng) {
@@ -140,6 +151,11 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     if (rc == YUE2_OK && e == hipSuccess && list > 0)
         e = hipMalloc(&d->cand, sizeof(uint64_t) * (size_t)chunks * list + sizeof(int2) * chunks);
     if (rc == YUE2_OK && e == hipSuccess && d->need_rng) e = hipMalloc(&d->big, survivor_bytes(V));
+    const int flist = (mode == 0 || temp == 0.0f) ? 1 : (sampling ? sampling->top_k : 1);
+    d->fused = m->step_kernel &&
+               fused_sampler_supported(m->c, d->rows, m->cus, mode, temp, sampling ? sampling->top_k : 1);
+    if (rc == YUE2_OK && e == hipSuccess && d->fused)
+        e = hipMalloc(&d->fcand, sizeof(uint64_t) * (size_t)(m->cus - 1) * flist);
     if (rc == YUE2_OK && e == hipSuccess) e = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);
     if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->fork, hipEventDisableTiming);
     if (rc == YUE2_OK && e == hipSuccess) e = hipEventCreateWithFlags(&d->join, hipEventDisableTiming);
@@ -180,6 +196,26 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
         a.window = sampling->penalty_window;
         a.min_tokens = sampling->min_tokens;
     }
+    // the graph's choose() picks the token after the one its launch forwards
+    a.step_offset = 1;
+    rc = YUE2_OK;
+    if (d->fused) {
+        FusedSampler fs{};
+        fs.a = a;
+        fs.a.stream[0] = fs.a.stream[1] = d->streams;  // one token's draws per launch
+        fs.mt = d->mt;
+        fs.draws = d->streams;
+        fs.cand = static_cast<uint64_t*>(d->fcand);
+        fs.list = flist;
+        rc = prepare_step(m, d->w, &fs);
+        d->fused = rc == YUE2_OK;  // 1: no resident step kernel with a sampler workgroup
+    }
+    if (rc >= 0 && !d->fused && m->step_kernel) rc = prepare_step(m, d->w);
+    if (rc < 0) {
+        decoder_release(d);
+        delete d;
+        return nullptr;
+    }
     return d;
 }
 
@@ -191,7 +227,7 @@ extern "C" void yue2_hip_decoder_free(Yue2Decoder* d) {
     delete d;
 }
 
-// Capture one loop iteration (choose -> forward -> advance) as a graph.
+// Capture one loop iteration (forward -> choose -> advance) as a graph.
 static int capture(Yue2Decoder* d) {
     Yue2Model* m = d->m;
     hipStream_t s = m->stream;
@@ -199,17 +235,22 @@ static int capture(Yue2Decoder* d) {
     hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
     int rc = YUE2_OK;
-    if (d->need_rng) {
-        (void)hipEventRecord(d->fork, s);
-        (void)hipStreamWaitEvent(d->side, d->fork, 0);
-        launch_mt_generate(d->side, d->mt, d->streams, d->streams + draws, draws, d->w.st, 1);
-        (void)hipEventRecord(d->join, d->side);
+    if (d->fused) {
+        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, 1);
+        if (rc == 1) rc = fail(YUE2_ERR_DEVICE, "fused step kernel unavailable");
+    } else {
+        if (d->need_rng) {
+            (void)hipEventRecord(d->fork, s);
+            (void)hipStreamWaitEvent(d->side, d->fork, 0);
+            launch_mt_generate(d->side, d->mt, d->streams, d->streams + draws, draws, d->w.st, 1);
+            (void)hipEventRecord(d->join, d->side);
+        }
+        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+        if (rc == 1) rc = enqueue_step(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+        if (d->need_rng) (void)hipStreamWaitEvent(s, d->join, 0);
+        launch_choose(s, d->sa);
+        launch_advance(s, d->w.st, d->rows);
     }
-    launch_choose(s, d->sa);
-    rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);
-    if (rc == 1) rc = enqueue_step(m, d->w, kv_view(d), d->rows, true, d->phase, s);
-    if (d->need_rng) (void)hipStreamWaitEvent(s, d->join, 0);
-    launch_advance(s, d->w.st, d->rows);
     hipGraph_t g = nullptr;
     e = hipStreamEndCapture(s, &g);
     if (rc != YUE2_OK) {
@@ -236,6 +277,10 @@ static int start(Yue2Decoder* d, const float* first_logits) {
                      d->rows > 1 ? d->caches[1]->length : 0, 0, 0);
     if (d->need_rng)
         launch_mt_generate(s, d->mt, d->streams, d->streams + 2 * V, 2 * V, d->w.st, 0);
+    // the loop's first choose() (step 0), over the prefill logits
+    SampleArgs first = d->sa;
+    first.step_offset = 0;
+    launch_choose(s, first);
     if (int rc = capture(d)) return rc;
     d->started = true;
     return YUE2_OK;
@@ -274,33 +319,35 @@ extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logit
             d->events.push_back(ev);
         }
     }
+    // Token steps_done + i is chosen before launch i forwards it.  Phases
+    // with an end token stop at the first end id, which gets no forward
+    // (src/sampling.rs:268-271).
     const int end = phase_end_id(d->phase);
-    int ran = 0;
+    int launches = 0, ran = 0;
     for (int i = 0; i < steps; ++i) {
-        if (step_ms) (void)hipEventRecord(d->events[2 * i], s);
-        hipError_t e = hipGraphLaunch(d->exec, s);
-        if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
-        if (step_ms) (void)hipEventRecord(d->events[2 * i + 1], s);
-        ++ran;
         if (end >= 0) {
-            // Phases with an end token: stop at the first end id.
             int32_t id = -1;
             if (int rc = read_step_error(d->w, s)) return rc;
             if (int rc = read_tokens(d, d->steps_done + i, 1, &id)) return rc;
             if (id == end) {
                 d->ended = true;
+                ran = i + 1;
                 break;
             }
         }
+        if (step_ms) (void)hipEventRecord(d->events[2 * i], s);
+        hipError_t e = hipGraphLaunch(d->exec, s);
+        if (e != hipSuccess) return hip_fail(e, "hipGraphLaunch");
+        if (step_ms) (void)hipEventRecord(d->events[2 * i + 1], s);
+        ++launches;
     }
+    if (!d->ended) ran = launches;
     if (int rc = read_step_error(d->w, s)) return rc;
     if (step_ms)
-        for (int i = 0; i < ran; ++i)
+        for (int i = 0; i < launches; ++i)
             (void)hipEventElapsedTime(&step_ms[i], d->events[2 * i], d->events[2 * i + 1]);
     if (int rc = read_tokens(d, d->steps_done, ran, tokens)) return rc;
-    // the end token's step ran no forward (src/sampling.rs:268-271): its
-    // position holds no key/value
-    for (int b = 0; b < d->rows; ++b) d->caches[b]->length += d->ended ? ran - 1 : ran;
+    for (int b = 0; b < d->rows; ++b) d->caches[b]->length += launches;
     d->steps_done += ran;
     return ran;
 }
@@ -316,13 +363,12 @@ extern "C" int32_t yue2_hip_decoder_logits(Yue2Decoder* d, float* out) {
     return e == hipSuccess ? YUE2_OK : hip_fail(e, "logits readback");
 }
 
-// The loop's last choose() without a following forward (src/sampling.rs:281).
-static int choose_only(Yue2Decoder* d, const float* first_logits, int32_t* token) {
+// The token chosen after the last run (the loop's next token), without a
+// forward (src/sampling.rs:281: the last step chooses but does not forward).
+static int next_token(Yue2Decoder* d, const float* first_logits, int32_t* token) {
     if (!d->started)
         if (int rc = start(d, first_logits)) return rc;
-    hipStream_t s = d->m->stream;
-    launch_choose(s, d->sa);
-    if (int rc = read_step_error(d->w, s)) return rc;
+    if (int rc = read_step_error(d->w, d->m->stream)) return rc;
     return read_tokens(d, d->steps_done, 1, token);
 }
 
@@ -334,7 +380,8 @@ static int choose_only(Yue2Decoder* d, const float* first_logits, int32_t* token
 static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double* bytes) {
     Yue2Model* m = d->m;
     const Yue2Config& c = m->c;
-    if (!m->step_kernel || !step_supported(c, d->rows, m->cus))
+    const int sample = d->fused ? 2 : 0;  // the fused sampler's work, nothing published
+    if (!m->step_kernel || !step_supported(c, d->rows, m->cus - (sample ? 1 : 0)))
         return fail(YUE2_ERR_ARG, "the decoder does not run the step kernel");
     const double H = c.hidden_size, D = c.head_dim, I = c.intermediate_size, V = c.vocab_size;
     const double q = c.num_attention_heads * D, kv = c.num_key_value_heads * D, L = c.num_hidden_layers;
@@ -351,9 +398,10 @@ static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double
         (void)hipEventDestroy(b0);
         return fail(YUE2_ERR_DEVICE, "hipEventCreate");
     }
-    int rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);  // untimed
+    int rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, sample);  // untimed
     if (rc == YUE2_OK) (void)hipEventRecord(b0, s);
-    for (int i = 0; i < iters && rc == YUE2_OK; ++i) rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+    for (int i = 0; i < iters && rc == YUE2_OK; ++i)
+        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, sample);
     if (rc == YUE2_OK) {
         (void)hipEventRecord(b1, s);
         hipError_t e = hipEventSynchronize(b1);
@@ -641,7 +689,7 @@ extern "C" int32_t yue2_hip_generate(Yue2Model* m, const int32_t* prefix, int32_
                 *truncated = 0;
             } else {
                 int32_t last = -1;
-                rc = choose_only(d, first.data(), &last);
+                rc = next_token(d, first.data(), &last);
                 if (rc == YUE2_OK) {
                     if (last == end) {
                         *count = ran;

@@ -39,7 +39,7 @@
 namespace y2 {
 
 enum FlowKind { FK_QKV = 1, FK_ATT = 2, FK_XO = 3, FK_ACT = 4, FK_XD = 5, FK_BMAX = 6, FK_BSUM = 7,
-                FK_PART = 8 };
+                FK_PART = 8, FK_SMP = 9 };
 constexpr int kDevErrFlow = 8;
 // Words a thread gathers in the attention merge (512 threads): a workgroup
 // merges ceil(G*D/W) outputs over nb <= W * bpw blocks, at most

@@ -168,9 +168,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 
 __global__ void advance_kernel(StepState* st, int rows) {
     if (threadIdx.x == 0) {
-        // an end token's step appended nothing
-        if (!st->done)
-            for (int b = 0; b < rows; ++b) st->pos[b] += 1;
+        // the launch's forward appended one position to every row (a launch
+        // is never made for a token the sampler chose as the end)
+        for (int b = 0; b < rows; ++b) st->pos[b] += 1;
         st->step += 1;
     }
 }

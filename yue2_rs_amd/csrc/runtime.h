@@ -52,6 +52,7 @@ struct Workspace {
     size_t flow_words = 0;      // 64-bit words in flow_block
     void* step_host = nullptr;  // host copy of the same (StepArgs)
     bool step_args_ready = false;
+    int step_sample = 0;        // the step arguments carry a fused sampler
     // Upper bound of the launch-sequence increments since the tagged words
     // were last cleared (each reset adds 2, each step-kernel launch 1).
     int64_t seq_bound = 0;
@@ -105,13 +106,18 @@ bool device_ready();
 int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
                  hipStream_t s);
 // The same step as one persistent kernel when the shape has one (full
-// vocabulary head only); returns 1 when it cannot be used.
+// vocabulary head only); returns 1 when it cannot be used.  sample: the
+// fused sampler's mode (StepCall::sample); the workspace must have been
+// prepared with a sampler for a nonzero mode.
 int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
-                       hipStream_t s, unsigned long long* trace = nullptr, int trace_slots = 0);
+                       hipStream_t s, unsigned long long* trace = nullptr, int trace_slots = 0,
+                       int sample = 0);
 // Upload the workspace's step kernel arguments (synchronous; call after
-// Workspace::ensure and before capturing a graph).  1 when the shape has no
-// step kernel.
-int prepare_step(Yue2Model* m, Workspace& w);
+// Workspace::ensure and before capturing a graph), with the fused sampler
+// when smp is set.  1 when the shape (or the launch with a sampler) has no
+// resident step kernel.
+struct FusedSampler;
+int prepare_step(Yue2Model* m, Workspace& w, const FusedSampler* smp = nullptr);
 void phase_range(int phase, int* start, int* end, int* stop);
 int phase_end_id(int phase);
 int check_phase_vocab(int phase, int vocab);

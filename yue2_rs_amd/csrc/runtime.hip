@@ -223,11 +223,11 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
     return YUE2_OK;
 }
 
-int prepare_step(Yue2Model* m, Workspace& w) {
+int prepare_step(Yue2Model* m, Workspace& w, const FusedSampler* smp) {
     const Yue2Config& c = m->c;
-    const int rows = w.rows;
-    if (!step_supported(c, rows, m->cus)) return 1;
-    if (w.step_args_ready) return YUE2_OK;
+    const int rows = w.rows, sample = smp ? 1 : 0;
+    if (!step_supported(c, rows, m->cus - sample)) return 1;
+    if (w.step_args_ready && w.step_sample == sample) return YUE2_OK;
     const int D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
     const int H = c.hidden_size, I = c.intermediate_size;
     const size_t qw = (size_t)Hq * D, qkvw = (size_t)(Hq + 2 * Hkv) * D;
@@ -252,14 +252,16 @@ int prepare_step(Yue2Model* m, Workspace& w) {
     a.scale = 1.0f / std::sqrt((float)D);
     a.logits = w.logits;
     a.st = w.st;
-    if (step_lds_bytes(a, m->cus) > kStepLdsMax) return 1;
+    if (smp) a.smp = *smp;
+    if (step_launch_lds(a, m->cus, sample) > kStepLdsMax) return 1;
     // one workgroup per CU, all resident together: the polls between them
     // would otherwise wait for a workgroup that cannot start
-    if (step_resident_per_cu(a, m->cus) < 1) return 1;
+    if (step_resident_per_cu(a, m->cus, sample) < 1) return 1;
     // tagged-word buffers, zero (= no tag) until first written
     const size_t n_x = rows * (size_t)H, n_qkv = rows * qkvw, n_att = rows * qw, n_act = rows * (size_t)I;
     const size_t n_blk = rows * (size_t)Hq * w.blk_stride, n_part = n_blk * D;
-    const size_t words = n_x + n_qkv + n_att + n_act + 2 * n_blk + n_part;
+    const size_t n_smp = kStepThreadsMax;  // one sampler word per worker
+    const size_t words = n_x + n_qkv + n_att + n_act + 2 * n_blk + n_part + n_smp;
     if (!w.flow_block) {
         hipError_t e = hipMalloc(&w.flow_block, words * sizeof(uint64_t));
         if (e != hipSuccess) {
@@ -281,21 +283,26 @@ int prepare_step(Yue2Model* m, Workspace& w) {
     a.tbmax = a.tact + n_act;
     a.tbsum = a.tbmax + n_blk;
     a.tpart = a.tbsum + n_blk;
+    a.tsmp = a.tpart + n_part;
     hipError_t e = hipMemcpy(w.step_args, &a, sizeof(StepArgs), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "step arguments upload");
     *reinterpret_cast<StepArgs*>(w.step_host) = a;
     w.step_args_ready = true;
+    w.step_sample = sample;
     return YUE2_OK;
 }
 
 int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
-                       hipStream_t s, unsigned long long* trace, int trace_slots) {
+                       hipStream_t s, unsigned long long* trace, int trace_slots, int sample) {
     if (!trace && !m->step_kernel) return 1;
-    if ((head && phase != YUE2_PHASE_NONE) || rows != w.rows || !step_supported(m->c, rows, m->cus)) return 1;
-    if (!w.step_args_ready) return 1;  // prepare_step found no resident step kernel: per-phase path
+    if (!w.step_args_ready || (sample != 0) != (w.step_sample != 0)) return 1;  // not prepared for this call
+    if ((head && phase != YUE2_PHASE_NONE) || rows != w.rows ||
+        !step_supported(m->c, rows, m->cus - (sample ? 1 : 0)))
+        return 1;
     StepCall call{};
     call.kv = kv;
     call.head = head ? 1 : 0;
+    call.sample = sample;
     call.trace = trace;
     call.trace_slots = trace ? trace_slots : 0;
     hipError_t e = launch_step(s, static_cast<const StepArgs*>(w.step_args),

@@ -24,7 +24,10 @@ struct SampleArgs {
     float* scores;        // [vocab] scratch
     const uint32_t* stream[2];  // 2 * vocab MT19937 outputs, double-buffered by step parity
     const int32_t* history;     // generated ids (the penalty history)
-    int hist_len;               // history length; -1: the step counter
+    int hist_len;               // history length; -1: the step index of the token chosen
+    // the token chosen is number st->step + step_offset of the loop (1 when
+    // the choice follows the step's forward in the same launch sequence)
+    int step_offset;
     int32_t* token_log;         // when set, the chosen id is stored at [step]
     StepState* st;
     int rows, vocab, phase, end_id, mode;  // mode 0: argmax of the mixed logits; 1: choose()

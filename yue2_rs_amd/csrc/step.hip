@@ -31,6 +31,7 @@
 
 #include "dev_attn.h"
 #include "dev_flow.h"
+#include "dev_sample.h"
 #include "dev_gemv.h"
 #include "dev_ring.h"
 #include "kernels.h"
@@ -150,6 +151,266 @@ __device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, fl
     __syncthreads();
 }
 
+// ---- the fused sampler -----------------------------------------------------
+
+__device__ __forceinline__ void st_agent_u64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(gblw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_f32(float* p, float v) {
+    __hip_atomic_store(gblw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent_f32(const float* p) {
+    return __hip_atomic_load(gblw(const_cast<float*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block reductions over the 512 threads (red: 8 words of LDS scratch per
+// value); every thread gets the result.
+__device__ __forceinline__ int block_sum_i(int v, int* red) {
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int t = 0;
+    for (int w = 0; w < kStepThreads / 64; ++w) t += red[w];
+    return t;
+}
+__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
+    for (int m = 32; m >= 1; m >>= 1) v = kmin(v, shfl_xor64(v, m));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t t = ~0ull;
+    for (int w = 0; w < kStepThreads / 64; ++w) t = kmin(t, red[w]);
+    return t;
+}
+
+// A worker's share of the fused sampler: its rows [r0, r1) of the step's
+// logits (just stored by this workgroup) scored as choose() scores every
+// entry -- CFG mix, phase mask, repetition penalty, validity, temperature
+// (src/sampling.rs:117-161, 261-266) -- and its best `list` order keys
+// (score descending, id ascending) published for the sampler workgroup,
+// followed by one tagged word {finite entries | invalid flag << 31}.
+// lds: at least 13 KiB.
+__device__ __forceinline__ void score_rows(const StepArgs* args, int r0, int r1, int w, uint32_t epoch, float* lds) {
+    const FusedSampler& fs = args->smp;
+    const SampleArgs& a = fs.a;
+    StepState* st = args->st;
+    const int tid = threadIdx.x, span = r1 - r0;
+    float* vals = lds;                                                 // [kFusedRowsMax]
+    uint64_t* keys = reinterpret_cast<uint64_t*>(lds + kFusedRowsMax);  // [kFusedRowsMax]
+    int32_t* ids = reinterpret_cast<int32_t*>(keys + kFusedRowsMax);    // [kWindowMax]
+    int* red = ids + kWindowMax;                                       // [16]
+    const int step = *gbl(&st->step) + 1;  // the token this launch chooses
+    // this workgroup's logit stores (lane 0 of each wave) precede the reads
+    __syncthreads();
+    const int wn = load_window(a, step, ids);
+    for (int j = tid; j < kFusedRowsMax; j += kStepThreads)
+        vals[j] = j < span ? mixed_score(a, r0 + j, step) : -__builtin_huge_valf();
+    __syncthreads();
+    if (a.mode == 1) apply_penalty(a, ids, wn, vals, r0, span);
+    const bool greedy = a.mode == 0 || a.temperature == 0.0f;
+    int fin = 0, bad = 0;
+    uint64_t best = ~0ull;
+    for (int j = tid; j < kFusedRowsMax; j += kStepThreads) {
+        const int i = r0 + j;
+        float v = vals[j];
+        uint64_t key = ~0ull;
+        if (j < span) {
+            if (v != v || v == __builtin_huge_valf()) bad = 1;
+            if (!greedy) {
+                if (a.temperature != 1.0f) v = cast(v / a.temperature, a.legacy);
+                st_agent_f32(a.scores + i, v);  // for the sampler's rescans of ties
+            }
+            if (is_finite(v)) {
+                ++fin;
+                key = order_key(v, i);
+            }
+        }
+        best = kmin(best, key);
+        keys[j] = key;
+    }
+    fin = block_sum_i(fin, red);
+    bad = block_sum_i(bad, red + 8);
+    if (greedy) {
+        best = block_min_u64(best, reinterpret_cast<uint64_t*>(red));  // (red's ints are read: barrier inside)
+        if (tid == 0) st_agent_u64(fs.cand + w, best);
+    } else {
+        int n2 = 2;
+        while (n2 < span) n2 <<= 1;
+        __syncthreads();
+        bitonic_sort(keys, n2);
+        const int n = min(fs.list, fin);
+        for (int j = tid; j < n; j += kStepThreads) st_agent_u64(fs.cand + (size_t)w * fs.list + j, keys[j]);
+    }
+    stores_done();  // every candidate and score is stored before the word that announces them
+    __syncthreads();
+    if (tid == 0) st_tag_bits(args->tsmp + w, (uint32_t)fin | (bad ? 0x80000000u : 0u), flow_tag(epoch, 0, FK_SMP));
+}
+
+// The sampler workgroup of the fused sampler, for the token after the one
+// this launch forwards (number st->step + 1 of the loop): the step's 2 *
+// vocab MT19937 draws (src/sampling.rs:198-214 consumes exactly that many),
+// then the rest of choose() over the workers' candidate lists.  Every entry
+// of the global top-k is within its worker's top-k list.  LB bounds the
+// top-k threshold T from below: at least k entries are >= LB, and (LB being
+// no smaller than any full list's k-th entry) every entry above LB is
+// listed.  So T is the k-th listed entry >= LB when k of them exceed LB,
+// and LB otherwise (the k-th entry overall when there is no bound).
+// Survivors are the listed entries >= T plus, from lists cut at an entry
+// equal to T, the worker's further entries equal to T (rescanned); then
+// race_tail.  Live: the id becomes every row's next input and the state
+// advances (ids, token log, end flag, step, positions, MT state).  lds:
+// kSamplerLds bytes.
+__device__ __forceinline__ void sampler_wg(const StepArgs* args, int nwork, uint32_t epoch, bool live, float* lds) {
+    const FusedSampler& fs = args->smp;
+    const SampleArgs& a = fs.a;
+    StepState* st = args->st;
+    const int tid = threadIdx.x, V = a.vocab, K = fs.list;
+    const int step = *gbl(&st->step) + 1;
+    const bool greedy = a.mode == 0 || a.temperature == 0.0f;
+    uint32_t* mts = reinterpret_cast<uint32_t*>(lds);                     // [640]
+    int32_t* finw = reinterpret_cast<int32_t*>(lds + 640);                // [512]
+    int32_t* rescan = finw + 512;                                         // [512]
+    uint64_t* rlast = reinterpret_cast<uint64_t*>(rescan + 512);          // [512]
+    uint64_t* C = rlast + 512;                                            // [kSurvivorMax]
+    float* e_val = reinterpret_cast<float*>(C + kSurvivorMax);            // [kSurvivorMax]
+    float* p_buf = e_val + kSurvivorMax;                                  // [kSurvivorMax]
+    int* misc = reinterpret_cast<int*>(p_buf + kSurvivorMax);             // [32]
+    uint64_t* red = reinterpret_cast<uint64_t*>(misc + 32);               // [8]
+    if (!greedy) mt_fill(fs.mt, fs.draws, 2 * (size_t)V, mts, live);
+    if (!gather_put<kStepThreads, 1>([=](int i) { return args->tsmp + i; }, nwork, flow_tag(epoch, 0, FK_SMP),
+                                     [=](int i, uint32_t bits) { finw[i] = (int32_t)bits; }, st))
+        return;
+    int fin_me = 0, bad_me = 0;
+    if (tid < nwork) {
+        fin_me = finw[tid] & 0x7fffffff;
+        bad_me = ((uint32_t)finw[tid] >> 31) & 1;
+    }
+    const int count = block_sum_i(fin_me, misc);
+    const int bad = block_sum_i(bad_me, misc + 8);
+    if ((a.mode == 1 && bad) || count == 0) {
+        if (tid == 0) set_error(&st->error, count == 0 && !(a.mode == 1 && bad) ? 3 : 4);
+        return;
+    }
+    int32_t id;
+    if (greedy) {
+        const uint64_t k = tid < nwork && fin_me > 0 ? ld_tag(fs.cand + tid) : ~0ull;
+        id = (int32_t)(block_min_u64(k, red) & 0xffffffffu);
+    } else {
+        // LB, the larger of two bounds each with k entries at or above it:
+        // the largest k-th entry of a full list, and the k-th largest of the
+        // lists' first entries (one per worker)
+        const uint64_t* mine = fs.cand + (size_t)tid * K;  // thread t < nwork reads worker t's list
+        const uint64_t head_me = tid < nwork && fin_me > 0 ? ld_tag(mine) : ~0ull;
+        const uint64_t last_me = tid < nwork && fin_me >= K ? ld_tag(mine + K - 1) : ~0ull;
+        const uint64_t lb1 = block_min_u64(last_me, red);
+        C[tid] = head_me;
+        __syncthreads();
+        bitonic_sort(C, kStepThreads);  // the heads in order (absent ones last)
+        const uint64_t lb2 = C[K - 1];
+        const uint64_t lb_key = kmin(lb1, lb2);
+        const bool lb_none = lb_key == ~0ull;
+        const float LB = lb_none ? -__builtin_huge_valf() : key_value(lb_key);
+        __syncthreads();  // C is rewritten below
+        // listed entries >= LB, into C (LDS; the overflow arrays beyond it):
+        // thread t walks worker t's list (values non-increasing) until an
+        // entry falls below LB, four loads in flight at a time
+        uint64_t* dst = C;
+        int cap = kSurvivorMax, nc = 0;
+        const int listed = tid < nwork ? min(K, fin_me) : 0;
+        for (int pass = 0; pass < 2; ++pass) {
+            __syncthreads();
+            if (tid == 0) misc[16] = 0;
+            __syncthreads();
+            bool more = listed > 0;
+            for (int j0 = 0; more && j0 < listed; j0 += 4) {
+                uint64_t k4[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) k4[u] = j0 + u < listed ? ld_tag(mine + j0 + u) : ~0ull;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (j0 + u < listed && key_value(k4[u]) >= LB) {
+                        const int at = atomicAdd(&misc[16], 1);
+                        if (at < cap) dst[at] = k4[u];
+                    } else {
+                        more = false;
+                    }
+                }
+            }
+            __syncthreads();
+            nc = misc[16];
+            if (nc <= cap) break;
+            dst = a.big;
+            cap = a.big_cap;
+        }
+        int n2 = 2;
+        while (n2 < nc) n2 <<= 1;
+        for (int i = nc + tid; i < n2; i += kStepThreads) dst[i] = ~0ull;
+        __syncthreads();
+        bitonic_sort(dst, n2);
+        // T, and the survivors among the listed entries: a prefix of dst
+        float T;
+        if (lb_none) {
+            T = key_value(dst[min(K, nc) - 1]);
+        } else {
+            int above = 0;
+            for (int i = tid; i < nc; i += kStepThreads) above += key_value(dst[i]) > LB;
+            above = block_sum_i(above, misc);
+            T = above >= K ? key_value(dst[K - 1]) : LB;
+        }
+        int ns = 0;
+        for (int i = tid; i < nc; i += kStepThreads) ns += key_value(dst[i]) >= T;
+        ns = block_sum_i(ns, misc + 8);
+        // lists cut at an entry equal to T: the worker's later entries equal to T
+        if (tid == 0) misc[17] = 0;
+        __syncthreads();
+        if (tid < nwork && fin_me > K) {
+            const uint64_t last = ld_tag(fs.cand + (size_t)tid * K + K - 1);
+            if (key_value(last) >= T) {
+                const int r = atomicAdd(&misc[17], 1);
+                rescan[r] = tid;
+                rlast[r] = last;
+            }
+        }
+        __syncthreads();
+        const int nres = misc[17];
+        int n = ns;
+        for (int pass = 0; pass < 2 && nres > 0; ++pass) {
+            __syncthreads();
+            if (tid == 0) misc[18] = ns;
+            __syncthreads();
+            for (int r = 0; r < nres; ++r) {
+                const int lo = part_lo(V, rescan[r], nwork), hi = part_lo(V, rescan[r] + 1, nwork);
+                for (int i = lo + tid; i < hi; i += kStepThreads) {
+                    const float v = ld_agent_f32(a.scores + i);
+                    if (is_finite(v) && v >= T) {
+                        const uint64_t k = order_key(v, i);
+                        if (k > rlast[r]) {
+                            const int at = atomicAdd(&misc[18], 1);
+                            if (at < cap) dst[at] = k;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            n = misc[18];
+            if (n <= cap) break;
+            // more survivors than LDS holds: the prefix moves to the overflow arrays
+            for (int i = tid; i < ns; i += kStepThreads) a.big[i] = dst[i];
+            dst = a.big;
+            cap = a.big_cap;
+        }
+        __syncthreads();
+        id = dst == C ? race_tail(a, step, C, e_val, p_buf, n, &misc[20], &misc[21])
+                      : race_tail(a, step, a.big, a.big_e, a.big_p, n, &misc[20], &misc[21]);
+    }
+    if (live && tid == 0) {
+        publish(a, step, id);
+        for (int b = 0; b < a.rows; ++b) st->pos[b] += 1;
+        st->step = step;
+    }
+}
+
 // ---- the kernel ------------------------------------------------------------
 
 typedef const __attribute__((address_space(4))) StepArgs* ArgsPtr;
@@ -214,13 +475,23 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     constexpr int RMAX = std::max(std::max(Ring<ITH, false>::SIZE, Ring<ITH, true>::SIZE),
                                   std::max(Ring<ITQ, false>::SIZE, Ring<ITI, false>::SIZE));
     const ArgsPtr args = (ArgsPtr)args_dev;
-    const int tid = threadIdx.x, wg = blockIdx.x, nwg = gridDim.x;
+    const int tid = threadIdx.x, wg = blockIdx.x;
+    // with the fused sampler the last workgroup is the sampler and the
+    // others (the workers) share the layers
+    const int nwg = call.sample ? (int)gridDim.x - 1 : (int)gridDim.x;
     StepState* st = fresh(args)->st;
     // after an error, or once the sampler chose the phase's end token (the
     // reference stops before that token's forward, src/sampling.rs:268-271)
     if (ld_dev_i(&st->error) || ld_dev_i(&st->done)) return;
     const int seq = *gbl(&st->seq);
     const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
+    if (call.sample && wg == nwg) {
+        sampler_wg(args_dev, nwg, epoch, call.sample == 1, lds);
+        // the next launch's epoch: every worker read seq before it announced
+        // its candidates, which the sampler waited for
+        if (tid == 0) *gblw(&st->seq) = seq + 1;
+        return;
+    }
     uint4 ring[RMAX];
     float gam[ITH];
     double e_sum[B], w_sum[B];  // this thread's shares of the next RMSNorm's sums
@@ -289,9 +560,13 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int groups = a->kv_heads * B, wpg = nwg / groups;
             const int group = wg / wpg, kvh = a->kv_heads;
-            const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
-            if (!attn_flow<kStepThreads, D, G>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
-                return;
+            if (group < groups) {
+                const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
+                if (!attn_flow<kStepThreads, D, G>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
+                    return;
+            } else {
+                for (int i = 0; i < 6; ++i) tr.mark();  // a workgroup past the groups: no attention
+            }
             tr.mark();
         }
         // ---- O projection + residual ----
@@ -342,9 +617,15 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             tr.mark();
         }
     }
-    // The next launch's epoch.  Workgroup 0 cannot get here before every
-    // workgroup has read seq: its final input needs every workgroup's output.
-    if (wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
+    // the fused sampler's share of this workgroup: its rows of the LM head
+    if (call.sample && call.head) {
+        const int V = fresh(args)->vocab;
+        score_rows(args_dev, part_lo(V, wg, nwg), part_lo(V, wg + 1, nwg), wg, epoch, lds);
+    }
+    // The next launch's epoch (the sampler workgroup's when there is one).
+    // Workgroup 0 cannot get here before every workgroup has read seq: its
+    // final input needs every workgroup's output.
+    if (!call.sample && wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
 }
 
 template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
@@ -371,8 +652,8 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
         exact && grouped &&
         ((c.head_dim == 128 && G == 3 && ith == 6 && itq == 6 && c.intermediate_size == 512 * 16) ||
          (c.head_dim == 64 && G == 4 && ith == 2 && itq == 2 && iti == 6));
-    if (!shape || rows < 1 || rows > 2 || nwg % (c.num_key_value_heads * rows) != 0) return false;
-    const int wpg = nwg / (c.num_key_value_heads * rows);
+    if (!shape || rows < 1 || rows > 2 || nwg < c.num_key_value_heads * rows) return false;
+    const int wpg = nwg / (c.num_key_value_heads * rows);  // workgroups past the groups take no attention
     const int max_blocks = (c.max_position_embeddings + kBlockKeys - 1) / kBlockKeys;
     const int bpw = (max_blocks + wpg - 1) / wpg;
     // the attention's p (G x bpw blocks of f32) is staged in its K region
@@ -400,8 +681,13 @@ static int resident_t(size_t lds) {
     return n;
 }
 
-int step_resident_per_cu(const StepArgs& a, int nwg) {
-    const size_t lds = step_lds_bytes(a, nwg);
+size_t step_launch_lds(const StepArgs& a, int nwg, int sample) {
+    const size_t lds = step_lds_bytes(a, sample ? nwg - 1 : nwg);
+    return sample ? std::max(lds, kSamplerLds) : lds;
+}
+
+int step_resident_per_cu(const StepArgs& a, int nwg, int sample) {
+    const size_t lds = step_launch_lds(a, nwg, sample);
     if (lds > kStepLdsMax) return 0;
     const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
     if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16)
@@ -411,8 +697,16 @@ int step_resident_per_cu(const StepArgs& a, int nwg) {
     return 0;
 }
 
+bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, float temperature, int top_k) {
+    const int workers = nwg - 1;
+    if (workers < 1 || !step_supported(c, rows, workers)) return false;
+    if ((c.vocab_size + workers - 1) / workers > kFusedRowsMax) return false;
+    const bool greedy = mode == 0 || temperature == 0.0f;
+    return greedy || (top_k >= 1 && top_k <= kFusedListMax);
+}
+
 hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {
-    const size_t lds = step_lds_bytes(a, nwg);
+    const size_t lds = step_launch_lds(a, nwg, call.sample);
     if (lds > kStepLdsMax) return hipErrorInvalidValue;
     const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
     if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16) {

@@ -81,8 +81,9 @@ def measure(y2, model, caches, first, sampling, scale, warmup, steps, c):
 
 def measured_traffic(context):
     """HBM bytes per launch of the CFG step kernel from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated against a plain copy),
-    when they were measured at this context; otherwise None."""
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated against a plain copy)
+    of the bench's own timing loop, when they were measured at this context;
+    otherwise None."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "step_kernel_3b_cfg_traffic.md")
     try:
         text = open(path).read()
@@ -94,10 +95,44 @@ def measured_traffic(context):
     return int(vals["traffic_bytes_per_launch"])
 
 
+def host_cpu():
+    """(model name, logical CPUs) of this host."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1
+
+
+def native_oracle():
+    """Build the oracle for this host's CPU (-O3 -march=native) into a
+    temporary directory and point the oracle binding at it; the prebuilt
+    portable library (-O2 x86-64-v3) stays in use if that fails."""
+    import subprocess
+    import tempfile
+    from oracle import oracle as O
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "oracle.c")
+    out = os.path.join(tempfile.mkdtemp(prefix="y2o_"), "liboracle_native.so")
+    cmd = ["gcc", "-O3", "-march=native", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-fopenmp", "-shared",
+           src, "-o", out, "-lm"]
+    try:
+        subprocess.run(cmd, check=True, capture_output=True, timeout=120)
+    except (OSError, subprocess.SubprocessError):
+        return "-O2 -march=x86-64-v3 (prebuilt)"
+    O._lib = None
+    O.LIB = __import__("pathlib").Path(out)
+    return "-O3 -march=native"
+
+
 def cpu_baseline(ckpt, c, prompt_len, scale, sampling, threads, budget_s, max_steps):
     """The oracle's CFG step on the host cores: both rows' forward over a
     synthetic BF16 KV cache of prompt_len positions, CFG mix and choose()."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    flags = native_oracle()
     from oracle import oracle as O
 
     O.set_threads(threads)
@@ -118,11 +153,13 @@ def cpu_baseline(ckpt, c, prompt_len, scale, sampling, threads, budget_s, max_st
         logits = [om.forward([tok], caches[i]) for i in range(2)]
         steps += 1
     wall = time.perf_counter() - t0
+    model, nproc = host_cpu()
     return {"value": steps / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "ms_per_step": 1000.0 * wall / steps,
+            "ms_per_step": 1000.0 * wall / steps, "cpu_model": model, "nproc": nproc, "build": flags,
             "sample": f"{steps} CFG batch-2 steps of the C oracle (restated reference CPU token step, "
-                      f"portable DOT order in place of Accelerate) at context {prompt_len}, synthetic "
-                      f"BF16 KV, {threads} threads"}
+                      f"portable DOT order in place of Accelerate; gcc {flags}) at context {prompt_len}, "
+                      f"synthetic BF16 KV, {threads} threads (the box's CPU share for one GPU) of {nproc} "
+                      f"logical CPUs ({model})"}
 
 
 def main() -> int:
@@ -171,6 +208,25 @@ def main() -> int:
     y2.synchronize()
     log(f"prefill done in {time.perf_counter() - t:.1f}s")
 
+    # Dominant kernel at a context that does not depend on --steps/--warmup:
+    # the CFG decoder takes one step (both caches reach P + 1 positions) and
+    # its step kernel is launched again at that position, timed with HIP
+    # events on the decoder's stream (or, on the per-phase path, its gate/up
+    # + SwiGLU GEMV, the largest weight read of a layer).
+    d0 = y2.Decoder(model, c_pos, c_neg, sampling=sampling, seed=0, scale=args.scale)
+    d0.run(1, first_logits=np.concatenate([l_pos, l_neg]))
+    context = c_pos.length
+    if step_kernel:
+        dom_ms, dom_b = d0.time_kernel("step", args.kernel_iters)
+        dom_name = "step_kernel<2, 128, 3, 6, 6, 16> (whole CFG batch-2 token: 28 layers + LM head + sampler)"
+        traffic = measured_traffic(context)
+    else:
+        dom_ms, dom_b = d0.time_kernel("gate_up", args.kernel_iters)
+        dom_name = "gemv_kernel<2, EPI_SWIGLU, 6, true> (RMSNorm + gate/up + SwiGLU of one layer)"
+        traffic = None
+    l_pos, l_neg = [row.copy() for row in d0.logits()]
+    d0.close()
+
     log(f"batch 1: {W} warmup + {K} timed steps")
     d1, bs1 = measure(y2, model, [c_bs1], l_bs1, sampling, 1.0, W, K, c)
     d1.close()
@@ -180,24 +236,10 @@ def main() -> int:
     log(f"CFG batch 2: {cfg['tokens_per_s']:.1f} steps/s, p50 {cfg['p50_ms']:.3f} ms")
 
     # the per-phase GEMV kernels of the phase-kernel path, for reference
-    others, phase_b = {}, {}
+    others = {}
     for name in ("gate_up", "down", "qkv", "o", "lm_head"):
         ms, by = d2.time_kernel(name, args.kernel_iters if name != "lm_head" else 16)
         others[name] = {"launch_ms": round(ms, 5), "GB_s": round(by / (ms * 1e-3) / 1e9, 1)}
-        phase_b[name] = (ms, by)
-    # Dominant kernel, timed with HIP events on the decoder's stream at the
-    # end of the timed run's context: the persistent step kernel (one launch
-    # per token: all weights, both rows' KV caches), or on the per-phase path
-    # the gate/up + SwiGLU GEMV (the largest weight read per layer).
-    context = c_pos.length
-    if step_kernel:
-        dom_ms, dom_b = d2.time_kernel("step", args.kernel_iters)
-        dom_name = "step_kernel<2, 128, 3, 6, 6, 16> (whole CFG batch-2 token: 28 layers + LM head)"
-        traffic = measured_traffic(context)
-    else:
-        dom_ms, dom_b = phase_b["gate_up"]
-        dom_name = "gemv_kernel<2, EPI_SWIGLU, 6, true> (RMSNorm + gate/up + SwiGLU of one layer)"
-        traffic = None
     d2.close()
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
@@ -207,7 +249,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
-        threads = min(16, os.cpu_count() or 1)
+        threads = min(16, os.cpu_count() or 1)  # one GPU's share of the box's CPUs
         cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 64)
         log(f"CPU baseline: {cpu['value']:.3f} steps/s with {threads} threads")
 

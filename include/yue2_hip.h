@@ -159,6 +159,22 @@ int32_t yue2_hip_sampling_validate(const Yue2Sampling *s);
 Yue2Model *yue2_hip_model_open(const Yue2Config *c, const uint16_t *embed_tokens,
                                const uint16_t *lm_head, const float *final_norm,
                                const Yue2LayerWeights *layers);
+/* Model::open (src/model.rs:418-451) from a checkpoint directory: config.json
+ * (Config::read, src/model.rs:29-73) and model.safetensors, or the shards
+ * named by model.safetensors.index.json (Weights::open,
+ * src/checkpoint.rs:310-386), memory-mapped and checked as the reference
+ * checks them, with its messages (yue2_hip_last_error).  Reads the tensors of
+ * the autoregressive decode path: model.embed_tokens, lm_head (or the tied
+ * embedding), model.norm and per layer input_layernorm, self_attn.{q,k,v,o}
+ * _proj, self_attn.{q,k}_norm, post_attention_layernorm, mlp.{gate,up,down}
+ * _proj.  F32 and F16 matrices are rounded to BF16 as the reference's
+ * converted weights are.  NULL on failure. */
+Yue2Model *yue2_hip_model_open_dir(const char *dir);
+/* The checks of yue2_hip_model_open_dir without a device: config.json, every
+ * shard's header, and the decode path's tensors and shapes.  *out (may be
+ * NULL) receives the configuration.  0 or a negative Yue2Error
+ * (YUE2_ERR_CONFIG where the reference returns InvalidData). */
+int32_t yue2_hip_checkpoint_config(const char *dir, Yue2Config *out);
 /* Model's Drop (src/model.rs:411-416). */
 void yue2_hip_model_free(Yue2Model *m);
 

@@ -97,6 +97,8 @@ def lib() -> C.CDLL:
         "yue2_hip_config_validate": (i32, [vp]),
         "yue2_hip_sampling_validate": (i32, [vp]),
         "yue2_hip_model_open": (vp, [vp, vp, vp, vp, vp]),
+        "yue2_hip_model_open_dir": (vp, [C.c_char_p]),
+        "yue2_hip_checkpoint_config": (i32, [C.c_char_p, vp]),
         "yue2_hip_model_free": (None, [vp]),
         "yue2_hip_cache_new": (vp, [vp, i32]),
         "yue2_hip_cache_free": (None, [vp]),
@@ -171,6 +173,14 @@ class Config:
         cfg = self.c()
         _check(lib().yue2_hip_config_validate(C.byref(cfg)))
 
+    @classmethod
+    def read_dir(cls, path) -> "Config":
+        """Config::read plus the checkpoint's header and tensor checks, without
+        a device; raises Yue2Error with the reference's message."""
+        cfg = _Config()
+        _check(lib().yue2_hip_checkpoint_config(str(path).encode(), C.byref(cfg)))
+        return cls(**{f: getattr(cfg, f) for f, _ in _Config._fields_})
+
 
 @dataclass
 class Sampling:
@@ -240,6 +250,18 @@ class Model:
         if not h:
             raise Yue2Error(-12, L.yue2_hip_last_error().decode())
         return cls(h, checkpoint.config, checkpoint)
+
+    @classmethod
+    def open_dir(cls, path) -> "Model":
+        """Model::open from a checkpoint directory (config.json + safetensors)."""
+        L = lib()
+        h = L.yue2_hip_model_open_dir(str(path).encode())
+        if not h:
+            raise Yue2Error(-11, L.yue2_hip_last_error().decode())
+        cfg = _Config()
+        _check(L.yue2_hip_checkpoint_config(str(path).encode(), C.byref(cfg)))
+        config = Config(**{f: getattr(cfg, f) for f, _ in _Config._fields_})
+        return cls(h, config, None)
 
     def close(self) -> None:
         if self._h:

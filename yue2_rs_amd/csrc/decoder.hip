@@ -152,8 +152,10 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
         e = hipMalloc(&d->cand, sizeof(uint64_t) * (size_t)chunks * list + sizeof(int2) * chunks);
     if (rc == YUE2_OK && e == hipSuccess && d->need_rng) e = hipMalloc(&d->big, survivor_bytes(V));
     const int flist = (mode == 0 || temp == 0.0f) ? 1 : (sampling ? sampling->top_k : 1);
+    int head_lo, head_n, head_stop;
+    head_rows(phase, V, &head_lo, &head_n, &head_stop);
     d->fused = m->step_kernel &&
-               fused_sampler_supported(m->c, d->rows, m->cus, mode, temp, sampling ? sampling->top_k : 1);
+               fused_sampler_supported(m->c, d->rows, m->cus, mode, temp, sampling ? sampling->top_k : 1, head_n);
     if (rc == YUE2_OK && e == hipSuccess && d->fused)
         e = hipMalloc(&d->fcand, sizeof(uint64_t) * (size_t)(m->cus - 1) * flist);
     if (rc == YUE2_OK && e == hipSuccess) e = hipStreamCreateWithFlags(&d->side, hipStreamNonBlocking);

@@ -119,6 +119,8 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
 struct FusedSampler;
 int prepare_step(Yue2Model* m, Workspace& w, const FusedSampler* smp = nullptr);
 void phase_range(int phase, int* start, int* end, int* stop);
+// The LM-head rows of a phase: [lo, lo + n) and the stop row (-1: none).
+void head_rows(int phase, int vocab, int* lo, int* n, int* stop);
 int phase_end_id(int phase);
 int check_phase_vocab(int phase, int vocab);
 int read_step_error(Workspace& w, hipStream_t s);

@@ -296,12 +296,11 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
                        hipStream_t s, unsigned long long* trace, int trace_slots, int sample) {
     if (!trace && !m->step_kernel) return 1;
     if (!w.step_args_ready || (sample != 0) != (w.step_sample != 0)) return 1;  // not prepared for this call
-    if ((head && phase != YUE2_PHASE_NONE) || rows != w.rows ||
-        !step_supported(m->c, rows, m->cus - (sample ? 1 : 0)))
-        return 1;
+    if (rows != w.rows || !step_supported(m->c, rows, m->cus - (sample ? 1 : 0))) return 1;
     StepCall call{};
     call.kv = kv;
     call.head = head ? 1 : 0;
+    head_rows(phase, m->c.vocab_size, &call.head_lo, &call.head_n, &call.head_stop);
     call.sample = sample;
     call.trace = trace;
     call.trace_slots = trace ? trace_slots : 0;
@@ -320,6 +319,18 @@ void phase_range(int phase, int* start, int* end, int* stop) {
         *end = kCodecOffset + kCodecSize;
         *stop = kMusicEnd;
     }
+}
+
+void head_rows(int phase, int vocab, int* lo, int* n, int* stop) {
+    if (phase == YUE2_PHASE_NONE) {
+        *lo = 0;
+        *n = vocab;
+        *stop = -1;
+        return;
+    }
+    int end;
+    phase_range(phase, lo, &end, stop);
+    *n = end - *lo;
 }
 
 int phase_end_id(int phase) {

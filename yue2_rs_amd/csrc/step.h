@@ -54,7 +54,12 @@ struct StepArgs {
 // Per-launch arguments.
 struct StepCall {
     KvView kv;
-    int head;                   // 1: final norm + full-vocabulary LM head into logits
+    // 1: final norm + LM head into logits: rows [head_lo, head_lo + head_n)
+    // and, when head_stop >= 0, that row too; every other logit is -inf
+    // (project_phase, src/model.rs:478-507; the full vocabulary is rows
+    // [0, vocab) without a stop row)
+    int head;
+    int head_lo, head_n, head_stop;
     // 0: no sampler; 1: the fused sampler chooses the next token and advances
     // the state (ids, token log, positions, step, MT state); 2: the same work
     // without publishing anything (timing).  With a sampler the last
@@ -76,7 +81,8 @@ bool step_supported(const Yue2Config& c, int rows, int nwg);
 // True when the fused sampler can serve this decoder on a launch of nwg
 // workgroups (nwg - 1 workers): the shape has a step kernel for the
 // workers, and the settings fit its candidate lists.
-bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, float temperature, int top_k);
+bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, float temperature, int top_k,
+                             int head_n);
 // Dynamic LDS bytes of the step kernel for these arguments on nwg
 // workgroups; launches need at most kStepLdsMax.
 constexpr size_t kStepLdsMax = 128 * 1024;

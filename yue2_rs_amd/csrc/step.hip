@@ -184,18 +184,29 @@ __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t* red) {
     return t;
 }
 
-// A worker's share of the fused sampler: its rows [r0, r1) of the step's
-// logits (just stored by this workgroup) scored as choose() scores every
-// entry -- CFG mix, phase mask, repetition penalty, validity, temperature
-// (src/sampling.rs:117-161, 261-266) -- and its best `list` order keys
-// (score descending, id ascending) published for the sampler workgroup,
-// followed by one tagged word {finite entries | invalid flag << 31}.
-// lds: at least 13 KiB.
-__device__ __forceinline__ void score_rows(const StepArgs* args, int r0, int r1, int w, uint32_t epoch, float* lds) {
+// The LM-head rows worker w computes (and scores): rows [lo, lo + n) split
+// over the workers, plus the stop row (if any) for worker 0.  Every other
+// logit is -inf, so these are the only entries choose() can pick.
+struct HeadRows {
+    int lo, n, stop;
+    __device__ __forceinline__ int r0(int w, int nw) const { return lo + part_lo(n, w, nw); }
+    __device__ __forceinline__ int r1(int w, int nw) const { return lo + part_lo(n, w + 1, nw); }
+    __device__ __forceinline__ int extra(int w) const { return w == 0 ? stop : -1; }
+};
+
+// A worker's share of the fused sampler: its rows [r0, r1) (and `extra`
+// when >= 0) of the step's logits, just stored by this workgroup, scored as
+// choose() scores every entry -- CFG mix, phase mask, repetition penalty,
+// validity, temperature (src/sampling.rs:117-161, 261-266) -- and its best
+// `list` order keys (score descending, id ascending) published for the
+// sampler workgroup, followed by one tagged word {finite entries | invalid
+// flag << 31}.  lds: at least 13 KiB.
+__device__ __forceinline__ void score_rows(const StepArgs* args, int r0, int r1, int extra, int w, uint32_t epoch,
+                                           float* lds) {
     const FusedSampler& fs = args->smp;
     const SampleArgs& a = fs.a;
     StepState* st = args->st;
-    const int tid = threadIdx.x, span = r1 - r0;
+    const int tid = threadIdx.x, span = r1 - r0 + (extra >= 0 ? 1 : 0);
     float* vals = lds;                                                 // [kFusedRowsMax]
     uint64_t* keys = reinterpret_cast<uint64_t*>(lds + kFusedRowsMax);  // [kFusedRowsMax]
     int32_t* ids = reinterpret_cast<int32_t*>(keys + kFusedRowsMax);    // [kWindowMax]
@@ -204,15 +215,19 @@ __device__ __forceinline__ void score_rows(const StepArgs* args, int r0, int r1,
     // this workgroup's logit stores (lane 0 of each wave) precede the reads
     __syncthreads();
     const int wn = load_window(a, step, ids);
+    const int nr = r1 - r0;  // entry j < nr is row r0 + j; entry nr is the extra row
     for (int j = tid; j < kFusedRowsMax; j += kStepThreads)
-        vals[j] = j < span ? mixed_score(a, r0 + j, step) : -__builtin_huge_valf();
+        vals[j] = j < span ? mixed_score(a, j < nr ? r0 + j : extra, step) : -__builtin_huge_valf();
     __syncthreads();
-    if (a.mode == 1) apply_penalty(a, ids, wn, vals, r0, span);
+    if (a.mode == 1) {
+        apply_penalty(a, ids, wn, vals, r0, nr);
+        if (extra >= 0) apply_penalty(a, ids, wn, vals + nr, extra, 1);
+    }
     const bool greedy = a.mode == 0 || a.temperature == 0.0f;
     int fin = 0, bad = 0;
     uint64_t best = ~0ull;
     for (int j = tid; j < kFusedRowsMax; j += kStepThreads) {
-        const int i = r0 + j;
+        const int i = j < nr ? r0 + j : extra;
         float v = vals[j];
         uint64_t key = ~0ull;
         if (j < span) {
@@ -261,7 +276,8 @@ __device__ __forceinline__ void score_rows(const StepArgs* args, int r0, int r1,
 // race_tail.  Live: the id becomes every row's next input and the state
 // advances (ids, token log, end flag, step, positions, MT state).  lds:
 // kSamplerLds bytes.
-__device__ __forceinline__ void sampler_wg(const StepArgs* args, int nwork, uint32_t epoch, bool live, float* lds) {
+__device__ __forceinline__ void sampler_wg(const StepArgs* args, const HeadRows hr, int nwork, uint32_t epoch,
+                                           bool live, float* lds) {
     const FusedSampler& fs = args->smp;
     const SampleArgs& a = fs.a;
     StepState* st = args->st;
@@ -380,8 +396,10 @@ __device__ __forceinline__ void sampler_wg(const StepArgs* args, int nwork, uint
             if (tid == 0) misc[18] = ns;
             __syncthreads();
             for (int r = 0; r < nres; ++r) {
-                const int lo = part_lo(V, rescan[r], nwork), hi = part_lo(V, rescan[r] + 1, nwork);
-                for (int i = lo + tid; i < hi; i += kStepThreads) {
+                const int lo = hr.r0(rescan[r], nwork), hi = hr.r1(rescan[r], nwork);
+                const int extra = hr.extra(rescan[r]);
+                for (int q = lo + tid; q < hi + (extra >= 0 ? 1 : 0); q += kStepThreads) {
+                    const int i = q < hi ? q : extra;
                     const float v = ld_agent_f32(a.scores + i);
                     if (is_finite(v) && v >= T) {
                         const uint64_t k = order_key(v, i);
@@ -485,8 +503,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     if (ld_dev_i(&st->error) || ld_dev_i(&st->done)) return;
     const int seq = *gbl(&st->seq);
     const uint32_t epoch = ((uint32_t)seq + 1u) & 0xFFFFFu;
+    const HeadRows hr{call.head_lo, call.head_n, call.head_stop};
     if (call.sample && wg == nwg) {
-        sampler_wg(args_dev, nwg, epoch, call.sample == 1, lds);
+        sampler_wg(args_dev, hr, nwg, epoch, call.sample == 1, lds);
         // the next launch's epoch: every worker read seq before it announced
         // its candidates, which the sampler waited for
         if (tid == 0) *gblw(&st->seq) = seq + 1;
@@ -532,8 +551,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         {
             ArgsPtr a = fresh(args);
             const int lc = min(l, layers_n - 1);  // layer pointers are never read past the table
-            const int H = a->hidden, n = last ? a->vocab : (a->heads + 2 * a->kv_heads) * D;
-            const uint16_t* w = last ? a->lm_head : layer_at(a, lc)->wqkv;
+            const int H = a->hidden, n = last ? hr.n : (a->heads + 2 * a->kv_heads) * D;
+            const uint16_t* w = last ? a->lm_head + (size_t)hr.lo * H : layer_at(a, lc)->wqkv;
             const int r0 = part_lo(n, wg, nwg), r1 = part_lo(n, wg + 1, nwg);
             if (l > 0) {
                 // the gammas and first weights go out before the wait
@@ -550,8 +569,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(w, nullptr, lds, H, last ? a->logits : nullptr, last ? nullptr : a->tqkv,
-                                         flow_tag(epoch, l, FK_QKV), n, r0, r1, n, ring);
+            gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(w, nullptr, lds, H, last ? a->logits + hr.lo : nullptr,
+                                                          last ? nullptr : a->tqkv, flow_tag(epoch, l, FK_QKV),
+                                                          last ? a->vocab : n, r0, r1, n, ring);
             tr.mark();
         }
         if (last) break;
@@ -617,11 +637,25 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             tr.mark();
         }
     }
-    // the fused sampler's share of this workgroup: its rows of the LM head
-    if (call.sample && call.head) {
-        const int V = fresh(args)->vocab;
-        score_rows(args_dev, part_lo(V, wg, nwg), part_lo(V, wg + 1, nwg), wg, epoch, lds);
+    if (call.head && hr.stop >= 0) {
+        // a phase's LM head (project_phase, src/model.rs:478-507): worker 0
+        // computes the stop row from the normalised x still staged in LDS,
+        // and every worker writes -inf to its share of the other entries
+        ArgsPtr a = fresh(args);
+        const int H = a->hidden, V = a->vocab;
+        const uint16_t* ws = a->lm_head + (size_t)hr.stop * H;
+        const int rn = wg == 0 ? 1 : 0;
+        prefetch_ring<ITH, false>(ws, nullptr, H, 0, rn, 1, ring);
+        gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(ws, nullptr, lds, H, a->logits + hr.stop, nullptr, 0, V, 0, rn,
+                                                      1, ring);
+        const int f0 = part_lo(V, wg, nwg), f1 = part_lo(V, wg + 1, nwg);
+        for (int b = 0; b < B; ++b)
+            for (int i = f0 + tid; i < f1; i += kStepThreads)
+                if ((i < hr.lo || i >= hr.lo + hr.n) && i != hr.stop)
+                    gblw(a->logits)[(size_t)b * V + i] = -__builtin_huge_valf();
     }
+    // the fused sampler's share of this workgroup: its rows of the LM head
+    if (call.sample && call.head) score_rows(args_dev, hr.r0(wg, nwg), hr.r1(wg, nwg), hr.extra(wg), wg, epoch, lds);
     // The next launch's epoch (the sampler workgroup's when there is one).
     // Workgroup 0 cannot get here before every workgroup has read seq: its
     // final input needs every workgroup's output.
@@ -651,6 +685,7 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const bool shape =
         exact && grouped &&
         ((c.head_dim == 128 && G == 3 && ith == 6 && itq == 6 && c.intermediate_size == 512 * 16) ||
+         (c.head_dim == 128 && G == 2 && ith == 4 && itq == 4 && c.intermediate_size == 512 * 12) ||
          (c.head_dim == 64 && G == 4 && ith == 2 && itq == 2 && iti == 6));
     if (!shape || rows < 1 || rows > 2 || nwg < c.num_key_value_heads * rows) return false;
     const int wpg = nwg / (c.num_key_value_heads * rows);  // workgroups past the groups take no attention
@@ -692,15 +727,18 @@ int step_resident_per_cu(const StepArgs& a, int nwg, int sample) {
     const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
     if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16)
         return a.rows == 1 ? resident_t<1, 128, 3, 6, 6, 16, false>(lds) : resident_t<2, 128, 3, 6, 6, 16, false>(lds);
+    if (a.head_dim == 128 && G == 2 && ith == 4 && a.intermediate == 512 * 12)
+        return a.rows == 1 ? resident_t<1, 128, 2, 4, 4, 12, false>(lds) : resident_t<2, 128, 2, 4, 4, 12, false>(lds);
     if (a.head_dim == 64 && G == 4 && ith == 2)
         return a.rows == 1 ? resident_t<1, 64, 4, 2, 2, 6, true>(lds) : resident_t<2, 64, 4, 2, 2, 6, true>(lds);
     return 0;
 }
 
-bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, float temperature, int top_k) {
+bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, float temperature, int top_k,
+                             int head_n) {
     const int workers = nwg - 1;
     if (workers < 1 || !step_supported(c, rows, workers)) return false;
-    if ((c.vocab_size + workers - 1) / workers > kFusedRowsMax) return false;
+    if ((head_n + workers - 1) / workers + 1 > kFusedRowsMax) return false;  // a worker's rows and the stop row
     const bool greedy = mode == 0 || temperature == 0.0f;
     return greedy || (top_k >= 1 && top_k <= kFusedListMax);
 }
@@ -712,6 +750,10 @@ hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, co
     if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16) {
         if (a.rows == 1) return launch_step_t<1, 128, 3, 6, 6, 16, false>(s, dev, call, nwg, lds);
         return launch_step_t<2, 128, 3, 6, 6, 16, false>(s, dev, call, nwg, lds);
+    }
+    if (a.head_dim == 128 && G == 2 && ith == 4 && a.intermediate == 512 * 12) {
+        if (a.rows == 1) return launch_step_t<1, 128, 2, 4, 4, 12, false>(s, dev, call, nwg, lds);
+        return launch_step_t<2, 128, 2, 4, 4, 12, false>(s, dev, call, nwg, lds);
     }
     if (a.head_dim == 64 && G == 4 && ith == 2) {
         if (a.rows == 1) return launch_step_t<1, 64, 4, 2, 2, 6, true>(s, dev, call, nwg, lds);

@@ -201,6 +201,18 @@ int32_t yue2_hip_forward(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t
 int32_t yue2_hip_prefill(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t n,
                          int32_t phase, float *logits);
 
+/* Model::prefill_phase (src/model.rs:508-522) on the matrix cores, into an
+ * empty cache: the prompt goes through the layers in chunks of rows, every
+ * linear a BF16 MFMA GEMM with FP32 accumulation and the attention a causal
+ * flash attention over the BF16 cache.  Every BF16 rounding point of the
+ * decode step is kept, but not its reduction order -- as the reference's own
+ * GPU prefill (MPS GEMMs, src/tensor.rs:991-993, src/metal.m:216-237,
+ * 330-361) differs from its decode GEMV -- so the cache and logits agree
+ * with yue2_hip_prefill within a tolerance, not bit for bit.  head_dim 64 or
+ * 128.  Returns 0 or a negative Yue2Error. */
+int32_t yue2_hip_prefill_mfma(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t n,
+                              int32_t phase, float *logits);
+
 /* A decode loop bound to one cache (batch 1) or to a conditional and an
  * unconditional cache (CFG batch 2).  Each step is one hipGraph launch:
  * embed -> layers -> LM head -> CFG mix -> choose -> next id.  The caches
@@ -283,6 +295,11 @@ void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t te
  * decided together by a 256-thread block (each row's outputs hold its
  * scale).  Returns 0 or a negative Yue2Error. */
 int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
+/* Diagnostics: out = x W^T (M x N f32, the raw FP32 accumulation) through
+ * the prefill's BF16 MFMA GEMM; x [M, K] and w [N, K] BF16 host arrays, K a
+ * multiple of 32.  Returns 0 or a negative Yue2Error. */
+int32_t yue2_hip_selftest_gemm(const uint16_t *x, const uint16_t *w, float *out, int32_t M, int32_t N,
+                               int32_t K);
 /* Execution choice: run decode steps (yue2_hip_forward and decoders created
  * afterwards) through the persistent token-step kernel -- one launch per
  * token, workgroups exchanging tagged words instead of meeting at barriers

@@ -106,6 +106,8 @@ def lib() -> C.CDLL:
         "yue2_hip_cache_load": (i32, [vp, vp, vp, i32, i32]),
         "yue2_hip_forward": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_prefill": (i32, [vp, vp, vp, i32, i32, vp]),
+        "yue2_hip_prefill_mfma": (i32, [vp, vp, vp, i32, i32, vp]),
+        "yue2_hip_selftest_gemm": (i32, [vp, vp, vp, i32, i32, i32]),
         "yue2_hip_decoder_new": (vp, [vp, vp, vp, vp, u64, i32, f32, i32]),
         "yue2_hip_decoder_free": (None, [vp]),
         "yue2_hip_decoder_run": (i32, [vp, vp, i32, vp, vp]),
@@ -291,6 +293,16 @@ class Model:
         arr = np.ascontiguousarray(ids, dtype=np.int32)
         out = np.empty(self.config.vocab_size, dtype=np.float32)
         _check(lib().yue2_hip_prefill(self._h, cache._h, _ptr(arr), len(arr), phase, _ptr(out)))
+        return cache, out
+
+    def prefill_mfma(self, ids: Sequence[int], capacity: int, phase: int = PHASE_NONE):
+        """Model::prefill_phase on the matrix cores (MFMA GEMMs + flash
+        attention): (Cache, logits of the last prompt row).  Agrees with
+        prefill_phase within a tolerance, not bit for bit."""
+        cache = Cache(self, capacity)
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.empty(self.config.vocab_size, dtype=np.float32)
+        _check(lib().yue2_hip_prefill_mfma(self._h, cache._h, _ptr(arr), len(arr), phase, _ptr(out)))
         return cache, out
 
     def set_step_kernel(self, on: bool) -> bool:

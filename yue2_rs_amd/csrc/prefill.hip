@@ -1,0 +1,519 @@
+// prefill.hip -- Model::prefill_phase (src/model.rs:508-522) on the matrix
+// cores: the prompt runs through every layer as chunks of rows, each linear
+// a BF16 MFMA GEMM with FP32 accumulation, the attention a causal
+// flash-attention over the BF16 cache.
+//
+// The reference runs its prefill the same way on its GPU path: multi-row
+// linears go to a GEMM (MPS, src/tensor.rs:991-993, src/metal.m:216-237) and
+// the causal attention to batched matrix products (src/metal.m:330-361),
+// whose summation order differs from the decode GEMV.  So this prefill
+// keeps every BF16 rounding point of the decode step (rb after each linear,
+// the norms, RoPE, SwiGLU, residuals; the RMSNorm scale from the sequential
+// sum of squares) but not the decode path's reduction order: its results
+// agree with the decode-order prefill within a stated tolerance, not bit
+// for bit.  yue2_hip_prefill keeps the bit-exact decode-order prefill.
+//
+// Per chunk of R rows at positions [p0, p0 + R) and per layer: RMSNorm rows
+// -> QKV GEMM (rb) -> QK-norm + RoPE + K/V append -> flash attention (rb)
+// -> O GEMM + residual -> RMSNorm rows -> gate/up GEMM + SwiGLU -> down GEMM
+// + residual.  The final norm and LM head run for the last prompt row only.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <mutex>
+#include <vector>
+
+#include "../../include/yue2_hip.h"
+#include "dev_gemv.h"
+#include "dev_mem.h"
+#include "dev_mfma.h"
+#include "kernels.h"
+#include "runtime.h"
+#include "y2_math.h"
+
+using namespace y2;
+
+namespace y2 {
+
+// ---- GEMM: C = X W^T, X [M, K] BF16, W [N, K] BF16, FP32 accumulation ------
+
+enum GemmEpi {
+    GEPI_RAW = 0,         // c (f32) = the accumulation
+    GEPI_ROUND = 1,       // c (f32) = rb(acc)
+    GEPI_RESID = 2,       // c (f32) = rb(c + rb(acc))  (residual stream, in place)
+    GEPI_SWIGLU_BF16 = 3  // cb (BF16) = rb(rb(silu(rb(gate))) * rb(up)); w = gate rows, w2 = up rows
+};
+
+struct GemmArgs {
+    const uint16_t* x;
+    int ldx;
+    const uint16_t* w;
+    const uint16_t* w2;
+    int ldw;
+    float* c;
+    uint16_t* cb;
+    int ldc;
+    int M, N, K;
+};
+
+constexpr int kGemmTM = 128, kGemmTK = 32, kGemmPad = 8;
+constexpr int kGemmThreads = 256;
+
+// One workgroup computes a 128-row tile of C: 128 columns (64 for the
+// gate/up pair, whose W tile holds 64 gate rows and the same 64 up rows).
+// Wave w takes rows 64 (w / 2) .. + 64 and two 32x32 accumulator tiles per
+// row half: columns 64 (w % 2) + 32 j (the pair: gate and up of columns
+// 32 (w % 2) .. + 32).  The X and W tiles of each 32-wide step of K go
+// through LDS; the next step's global loads are in flight during the MFMAs.
+template <int EPI>
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
+    constexpr bool PAIR = EPI == GEPI_SWIGLU_BF16;
+    constexpr int TN = PAIR ? 64 : 128;  // output columns per tile
+    constexpr int LDS_W = kGemmTK + kGemmPad;
+    __shared__ __align__(16) uint16_t xs[kGemmTM][LDS_W];
+    __shared__ __align__(16) uint16_t ws[128][LDS_W];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kGemmTM, n0 = blockIdx.x * TN;
+    // each thread moves two 16-byte pieces of each tile: row q / 4, k 8 (q % 4)
+    uint4 rx[2], rw[2];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int q = tid + kGemmThreads * s, row = q >> 2, kq = (q & 3) * 8;
+            const int mr = m0 + row;
+            rx[s] = mr < g.M ? ldg4(g.x + (size_t)mr * g.ldx + k0 + kq) : make_uint4(0, 0, 0, 0);
+            const uint16_t* wrow;
+            int nr;
+            if (PAIR) {
+                nr = n0 + (row & 63);
+                wrow = (row < 64 ? g.w : g.w2) + (size_t)nr * g.ldw;
+            } else {
+                nr = n0 + row;
+                wrow = g.w + (size_t)nr * g.ldw;
+            }
+            rw[s] = nr < g.N ? ldg4(wrow + k0 + kq) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    load(0);
+    for (int k0 = 0; k0 < g.K; k0 += kGemmTK) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int q = tid + kGemmThreads * s, row = q >> 2, kq = (q & 3) * 8;
+            *reinterpret_cast<uint4*>(&xs[row][kq]) = rx[s];
+            *reinterpret_cast<uint4*>(&ws[row][kq]) = rw[s];
+        }
+        __syncthreads();
+        if (k0 + kGemmTK < g.K) load(k0 + kGemmTK);
+#pragma unroll
+        for (int kk = 0; kk < kGemmTK; kk += 16) {
+            const int kc = kk + 8 * (lane >> 5);
+            uint4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const uint4*>(&xs[wm * 64 + i * 32 + (lane & 31)][kc]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int wr = PAIR ? j * 64 + wn * 32 : wn * 64 + j * 32;
+                b[j] = *reinterpret_cast<const uint4*>(&ws[wr + (lane & 31)][kc]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+    // epilogue: lane l writes column acc32_col(l) of rows acc32_row(l, r)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, r);
+            if (row >= g.M) continue;
+            if constexpr (PAIR) {
+                const int col = n0 + wn * 32 + acc32_col(lane);
+                if (col < g.N) {
+                    const float o = rb(silu_rb(rb(acc[i][0][r])) * rb(acc[i][1][r]));
+                    g.cb[(size_t)row * g.ldc + col] = bf16_bits(o);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn * 64 + j * 32 + acc32_col(lane);
+                    if (col >= g.N) continue;
+                    float* c = g.c + (size_t)row * g.ldc + col;
+                    const float v = acc[i][j][r];
+                    if constexpr (EPI == GEPI_RAW) *c = v;
+                    else if constexpr (EPI == GEPI_ROUND) *c = rb(v);
+                    else *c = rb(*c + rb(v));
+                }
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& g) {
+    if (g.K % kGemmTK || g.ldx % 8 || g.ldw % 8 || g.M < 1 || g.N < 1) return hipErrorInvalidValue;
+    const int tn = epi == GEPI_SWIGLU_BF16 ? 64 : 128;
+    const dim3 grid((g.N + tn - 1) / tn, (g.M + kGemmTM - 1) / kGemmTM);
+    switch (epi) {
+        case GEPI_RAW: gemm_kernel<GEPI_RAW><<<grid, kGemmThreads, 0, s>>>(g); break;
+        case GEPI_ROUND: gemm_kernel<GEPI_ROUND><<<grid, kGemmThreads, 0, s>>>(g); break;
+        case GEPI_RESID: gemm_kernel<GEPI_RESID><<<grid, kGemmThreads, 0, s>>>(g); break;
+        case GEPI_SWIGLU_BF16: gemm_kernel<GEPI_SWIGLU_BF16><<<grid, kGemmThreads, 0, s>>>(g); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---- rows ----------------------------------------------------------------
+
+constexpr int kRowThreads = 256;
+
+// x[r] = rb(E[ids[r]]) (src/model.rs:452-464).
+__global__ __launch_bounds__(kRowThreads) void embed_rows_kernel(const uint16_t* embed, const int32_t* ids, float* x,
+                                                                 int H) {
+    const int r = blockIdx.x;
+    const uint16_t* e = embed + (size_t)ids[r] * H;
+    for (int i = threadIdx.x; i < H; i += kRowThreads) x[(size_t)r * H + i] = bf16(e[i]);
+}
+
+// out[r] = RMSNorm(x[r]) as BF16 (Norm::apply, src/tensor.rs:1140-1157): the
+// scale decided as the decode step decides it (the sequential f32 sum of
+// squares, dev_gemv.h), one workgroup per row.
+__global__ __launch_bounds__(kRowThreads) void norm_rows_kernel(const float* x, const float* gamma, uint16_t* out,
+                                                                int H, float eps) {
+    extern __shared__ __align__(16) float xs[];
+    const int r = blockIdx.x;
+    for (int i = threadIdx.x; i < H; i += kRowThreads) xs[i] = x[(size_t)r * H + i];
+    __syncthreads();
+    float s[1];
+    norm_scales_block<kRowThreads, 1>(xs, H, eps, nullptr, s);
+    for (int i = threadIdx.x; i < H; i += kRowThreads) out[(size_t)r * H + i] = bf16_bits(rb(rb(xs[i] * s[0]) * gamma[i]));
+}
+
+// Per (row r, head): the per-head RMSNorm of q and k (Norm::heads,
+// src/tensor.rs:1158-1172) and rotate-half RoPE at position p0 + r
+// (src/model.rs:151-168): q heads into q (BF16 [rows][heads][D]), k heads
+// into the cache, and the v heads copied into the cache.  One wave per head.
+struct RopeArgs {
+    const float* qkv;  // [rows][(heads + 2 kv) D], rb'd GEMM outputs
+    uint16_t* q;
+    uint16_t* kv_base;
+    int cap, layer, heads, kv_heads, D, p0;
+    const float *q_norm, *k_norm, *cos_t, *sin_t;
+    float eps;
+};
+
+__global__ __launch_bounds__(64) void rope_append_kernel(const RopeArgs a) {
+    const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, D = a.D, half = D / 2;
+    const int qkvw = (a.heads + 2 * a.kv_heads) * D;
+    const float* v = a.qkv + (size_t)r * qkvw + (size_t)h * D;
+    const int pos = a.p0 + r;
+    if (h >= a.heads + a.kv_heads) {  // a value head: to the cache as is
+        const int g = h - a.heads - a.kv_heads;
+        uint16_t* dst = a.kv_base + ((((size_t)a.layer * 2 + 1) * a.kv_heads + g) * a.cap + pos) * D;
+        for (int d = lane; d < D; d += 64) dst[d] = bf16_bits(v[d]);
+        return;
+    }
+    const bool is_q = h < a.heads;
+    const float* gam = is_q ? a.q_norm : a.k_norm;
+    const float s = norm_scale_wave(v, D, a.eps);
+    const float* ct = a.cos_t + (size_t)pos * half;
+    const float* st = a.sin_t + (size_t)pos * half;
+    uint16_t* dst = is_q ? a.q + ((size_t)r * a.heads + h) * D
+                         : a.kv_base + ((((size_t)a.layer * 2) * a.kv_heads + (h - a.heads)) * a.cap + pos) * D;
+    for (int d = lane; d < half; d += 64) {
+        const float x0 = rb(rb(v[d] * s) * gam[d]);
+        const float x1 = rb(rb(v[d + half] * s) * gam[d + half]);
+        const float c = ct[d], sn = st[d];
+        dst[d] = bf16_bits(rb(rb(x0 * c) - rb(x1 * sn)));
+        dst[d + half] = bf16_bits(rb(rb(x1 * c) + rb(x0 * sn)));
+    }
+}
+
+// ---- causal flash attention over the BF16 cache --------------------------
+
+struct FlashArgs {
+    const uint16_t* q;  // [rows][heads][D] BF16
+    const uint16_t* kv_base;
+    int cap, layer, heads, kv_heads, p0, rows;
+    float scale;
+    uint16_t* out;  // [rows][heads D] BF16 (rb of the attention output)
+};
+
+// One workgroup per (query head h, 64 query rows); wave w takes 16 of them.
+// Keys in tiles of 64: S = Q K^T on 16x16x32 MFMAs (K staged in LDS), the
+// online softmax (row maxima and sums across the 16 lanes of a row group),
+// P through LDS into the A layout and V transposed in LDS for O += P V.
+template <int D>
+__global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
+    constexpr int KT = 64, PADK = 8;
+    __shared__ __align__(16) uint16_t ks[KT][D + PADK];      // K tile, row = key
+    __shared__ __align__(16) uint16_t vt[D][KT + PADK];      // V tile transposed, row = dim
+    __shared__ __align__(16) uint16_t ps[2][4][16][KT + PADK];  // each wave's P (hi, lo), row = query
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x, q0 = blockIdx.y * 64, G = f.heads / f.kv_heads, g = h / G;
+    const int qrow = q0 + wave * 16 + (lane & 15);  // the query row this lane loads for A
+    const uint16_t* Kc = f.kv_base + (((size_t)f.layer * 2) * f.kv_heads + g) * (size_t)f.cap * D;
+    const uint16_t* Vc = f.kv_base + (((size_t)f.layer * 2 + 1) * f.kv_heads + g) * (size_t)f.cap * D;
+    uint4 qa[D / 32];
+#pragma unroll
+    for (int dk = 0; dk < D / 32; ++dk)
+        qa[dk] = qrow < f.rows ? ldg4(f.q + ((size_t)qrow * f.heads + h) * D + dk * 32 + 8 * (lane >> 4))
+                               : make_uint4(0, 0, 0, 0);
+    // this lane's accumulator rows: 4 (lane / 16) + r of the wave's 16
+    int qpos[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qpos[r] = f.p0 + q0 + wave * 16 + 4 * (lane >> 4) + r;
+    float m[4], l[4];
+    f32x4 o[D / 16];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m[r] = -__builtin_huge_valf();
+        l[r] = 0.0f;
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[dt][r] = 0.0f;
+    const int last_key = min(f.p0 + q0 + 63, f.p0 + f.rows - 1);  // keys [0, last_key]
+    const int tiles = last_key / KT + 1;
+    for (int t = 0; t < tiles; ++t) {
+        const int kb = t * KT;
+        // stage K (rows) and V (transposed); keys past last_key are zero
+        for (int u = tid; u < KT * D / 8; u += 256) {
+            const int key = u / (D / 8), d8 = (u % (D / 8)) * 8, kg = kb + key;
+            const bool in = kg <= last_key;
+            const uint4 kv = in ? ldg4(Kc + (size_t)kg * D + d8) : make_uint4(0, 0, 0, 0);
+            const uint4 vv = in ? ldg4(Vc + (size_t)kg * D + d8) : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(&ks[key][d8]) = kv;
+            const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vt[d8 + e][key] = ve[e];
+        }
+        __syncthreads();
+        // S for the wave's 16 rows x 64 keys: four 16x16 tiles
+        f32x4 s[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int dk = 0; dk < D / 32; ++dk) {
+                const uint4 b = *reinterpret_cast<const uint4*>(&ks[kt * 16 + (lane & 15)][dk * 32 + 8 * (lane >> 4)]);
+                acc = mfma16(qa[dk], b, acc);
+            }
+            s[kt] = acc;
+        }
+        // scale, causal mask, online softmax per row
+        float alpha[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float mx = -__builtin_huge_valf();
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const int key = kb + kt * 16 + (lane & 15);
+                const float v = key <= qpos[r] ? s[kt][r] * f.scale : -__builtin_huge_valf();
+                s[kt][r] = v;
+                mx = fmaxf(mx, v);
+            }
+#pragma unroll
+            for (int msk = 8; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+            const float mn = fmaxf(m[r], mx);
+            alpha[r] = mn == -__builtin_huge_valf() ? 1.0f : __expf(m[r] - mn);
+            float sum = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                const float p = mn == -__builtin_huge_valf() ? 0.0f : __expf(s[kt][r] - mn);
+                s[kt][r] = p;
+                sum += p;
+            }
+#pragma unroll
+            for (int msk = 8; msk >= 1; msk >>= 1) sum += __shfl_xor(sum, msk, 64);
+            l[r] = l[r] * alpha[r] + sum;
+            m[r] = mn;
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[dt][r] *= alpha[r];
+        // P into the wave's LDS rows as two BF16 parts, hi = bf16(p) and
+        // lo = bf16(p - hi): V is BF16 (the cache), so P V takes two MFMAs
+        // and keeps about 16 bits of P instead of 8, as the reference's f32
+        // softmax and P V do (src/model.rs:313-397).
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float hi = rb(s[kt][r]);
+                ps[0][wave][4 * (lane >> 4) + r][kt * 16 + (lane & 15)] = bf16_bits(hi);
+                ps[1][wave][4 * (lane >> 4) + r][kt * 16 + (lane & 15)] = bf16_bits(s[kt][r] - hi);
+            }
+        __syncthreads();
+        // O += P V: A = P rows, B = V^T rows (keys contiguous)
+#pragma unroll
+        for (int kk = 0; kk < KT; kk += 32) {
+            const uint4 ah = *reinterpret_cast<const uint4*>(&ps[0][wave][lane & 15][kk + 8 * (lane >> 4)]);
+            const uint4 al = *reinterpret_cast<const uint4*>(&ps[1][wave][lane & 15][kk + 8 * (lane >> 4)]);
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) {
+                const uint4 b = *reinterpret_cast<const uint4*>(&vt[dt * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
+                o[dt] = mfma16(al, b, o[dt]);
+                o[dt] = mfma16(ah, b, o[dt]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = q0 + wave * 16 + 4 * (lane >> 4) + r;
+        if (row >= f.rows) continue;
+        const float inv = 1.0f / l[r];
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+            f.out[(size_t)row * f.heads * D + (size_t)h * D + dt * 16 + (lane & 15)] = bf16_bits(rb(o[dt][r] * inv));
+    }
+}
+
+}  // namespace y2
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr int kPrefillChunk = 1024;  // rows per pass through the layers
+
+struct PrefillBuffers {
+    void* block = nullptr;
+    float *x = nullptr, *qkv = nullptr, *logits_row = nullptr;
+    uint16_t *h = nullptr, *q = nullptr, *att = nullptr, *act = nullptr;
+    int32_t* ids = nullptr;
+    ~PrefillBuffers() {
+        if (block) (void)hipFree(block);
+    }
+};
+
+int run_prefill(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int n, int phase, float* logits) {
+    const Yue2Config& cf = m->c;
+    const int H = cf.hidden_size, D = cf.head_dim, Hq = cf.num_attention_heads, Hkv = cf.num_key_value_heads;
+    const int I = cf.intermediate_size, qw = Hq * D, qkvw = (Hq + 2 * Hkv) * D;
+    const int R = std::min(n, kPrefillChunk);
+    PrefillBuffers b;
+    size_t at = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = at;
+        at = (at + bytes + 255) / 256 * 256;
+        return o;
+    };
+    const size_t o_x = take(sizeof(float) * R * H), o_qkv = take(sizeof(float) * R * qkvw);
+    const size_t o_h = take(2 * (size_t)R * std::max(H, I)), o_q = take(2 * (size_t)R * qw);
+    const size_t o_att = take(2 * (size_t)R * qw), o_act = take(2 * (size_t)R * I);
+    const size_t o_ids = take(sizeof(int32_t) * n);
+    hipError_t e = hipMalloc(&b.block, at);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(prefill buffers)");
+    char* p = static_cast<char*>(b.block);
+    b.x = reinterpret_cast<float*>(p + o_x);
+    b.qkv = reinterpret_cast<float*>(p + o_qkv);
+    b.h = reinterpret_cast<uint16_t*>(p + o_h);
+    b.q = reinterpret_cast<uint16_t*>(p + o_q);
+    b.att = reinterpret_cast<uint16_t*>(p + o_att);
+    b.act = reinterpret_cast<uint16_t*>(p + o_act);
+    b.ids = reinterpret_cast<int32_t*>(p + o_ids);
+    hipStream_t s = m->stream;
+    e = hipMemcpyAsync(b.ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return hip_fail(e, "prefill ids upload");
+    const float eps = cf.rms_norm_eps;
+    const size_t norm_lds = sizeof(float) * H;
+    for (int p0 = 0; p0 < n; p0 += R) {
+        const int rows = std::min(R, n - p0);
+        embed_rows_kernel<<<rows, kRowThreads, 0, s>>>(m->embed, b.ids + p0, b.x, H);
+        for (int l = 0; l < cf.num_hidden_layers; ++l) {
+            const LayerDev& L = m->layers[l];
+            norm_rows_kernel<<<rows, kRowThreads, norm_lds, s>>>(b.x, L.in_norm, b.h, H, eps);
+            GemmArgs g{b.h, H, L.wqkv, nullptr, H, b.qkv, nullptr, qkvw, rows, qkvw, H};
+            if ((e = launch_gemm(s, GEPI_ROUND, g)) != hipSuccess) return hip_fail(e, "prefill qkv gemm");
+            RopeArgs ra{b.qkv, b.q, c->kv, c->capacity, l, Hq, Hkv, D, c->length + p0, L.q_norm, L.k_norm,
+                        m->rope_cos, m->rope_sin, eps};
+            rope_append_kernel<<<dim3(rows, Hq + 2 * Hkv), 64, 0, s>>>(ra);
+            FlashArgs fa{b.q, c->kv, c->capacity, l, Hq, Hkv, c->length + p0, rows, 1.0f / std::sqrt((float)D),
+                         b.att};
+            const dim3 fg(Hq, (rows + 63) / 64);
+            if (D == 128) flash_prefill_kernel<128><<<fg, 256, 0, s>>>(fa);
+            else if (D == 64) flash_prefill_kernel<64><<<fg, 256, 0, s>>>(fa);
+            else return fail(YUE2_ERR_ARG, "MFMA prefill supports head_dim 64 and 128");
+            GemmArgs go{b.att, qw, L.wo, nullptr, qw, b.x, nullptr, H, rows, H, qw};
+            if ((e = launch_gemm(s, GEPI_RESID, go)) != hipSuccess) return hip_fail(e, "prefill o gemm");
+            norm_rows_kernel<<<rows, kRowThreads, norm_lds, s>>>(b.x, L.post_norm, b.h, H, eps);
+            GemmArgs gu{b.h, H, L.wg, L.wu, H, nullptr, b.act, I, rows, I, H};
+            if ((e = launch_gemm(s, GEPI_SWIGLU_BF16, gu)) != hipSuccess) return hip_fail(e, "prefill gate/up gemm");
+            GemmArgs gd{b.act, I, L.wd, nullptr, I, b.x, nullptr, H, rows, H, I};
+            if ((e = launch_gemm(s, GEPI_RESID, gd)) != hipSuccess) return hip_fail(e, "prefill down gemm");
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return hip_fail(e, "prefill kernels");
+        if (p0 + rows == n && logits) {
+            // the final norm and LM head of the last prompt row (project_phase)
+            if (int rc = enqueue_head(m, m->ws, b.x + (size_t)(rows - 1) * H, phase, s)) return rc;
+        }
+    }
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "prefill");
+    c->length += n;
+    if (logits) {
+        e = hipMemcpy(logits, m->ws.logits, sizeof(float) * cf.vocab_size, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return hip_fail(e, "prefill logits readback");
+    }
+    return YUE2_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t yue2_hip_prefill_mfma(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int32_t n, int32_t phase,
+                                         float* logits) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || !c || !ids || c->m != m) return fail(YUE2_ERR_ARG, "null model, cache or ids");
+    if (int rc = check_phase_vocab(phase, m->c.vocab_size)) return rc;
+    if (n <= 0 || c->length != 0) return fail(YUE2_ERR_ARG, "Invalid prefill/cache capacity");
+    if (n > c->capacity || n > m->c.max_position_embeddings)
+        return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
+    for (int i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= m->c.vocab_size) return fail(YUE2_ERR_TOKEN, "Token outside model vocabulary");
+    const Yue2Config& cf = m->c;
+    if ((cf.head_dim != 64 && cf.head_dim != 128) || cf.hidden_size % kGemmTK || cf.intermediate_size % kGemmTK ||
+        (cf.num_attention_heads * cf.head_dim) % kGemmTK)
+        return fail(YUE2_ERR_ARG, "shape without an MFMA prefill");
+    if (int rc = m->ws.ensure(1, (c->capacity + kBlockKeys - 1) / kBlockKeys, m->c)) return rc;
+    return run_prefill(m, c, ids, n, phase, logits);
+}
+
+extern "C" int32_t yue2_hip_selftest_gemm(const uint16_t* x, const uint16_t* w, float* out, int32_t M, int32_t N,
+                                          int32_t K) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!x || !w || !out || M < 1 || N < 1 || K < 1 || K % kGemmTK) return fail(YUE2_ERR_ARG, "bad gemm selftest");
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no gfx950 device");
+    void *dx = nullptr, *dw = nullptr, *dc = nullptr;
+    hipError_t e = hipMalloc(&dx, 2 * (size_t)M * K);
+    if (e == hipSuccess) e = hipMalloc(&dw, 2 * (size_t)N * K);
+    if (e == hipSuccess) e = hipMalloc(&dc, 4 * (size_t)M * N);
+    if (e == hipSuccess) e = hipMemcpy(dx, x, 2 * (size_t)M * K, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(dw, w, 2 * (size_t)N * K, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        GemmArgs g{static_cast<const uint16_t*>(dx), K, static_cast<const uint16_t*>(dw), nullptr, K,
+                   static_cast<float*>(dc), nullptr, N, M, N, K};
+        e = launch_gemm(nullptr, GEPI_RAW, g);
+    }
+    if (e == hipSuccess) e = hipMemcpy(out, dc, 4 * (size_t)M * N, hipMemcpyDeviceToHost);
+    (void)hipFree(dx);
+    (void)hipFree(dw);
+    (void)hipFree(dc);
+    return e == hipSuccess ? YUE2_OK : hip_fail(e, "gemm selftest");
+}

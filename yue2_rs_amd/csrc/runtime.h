@@ -105,6 +105,9 @@ int hip_fail(hipError_t e, const char* what);
 bool device_ready();
 int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
                  hipStream_t s);
+// The final norm and the phase's LM head of `rows` rows x (stride hidden)
+// into w.logits (Model::forward_phase's projection, src/model.rs:469-507).
+int enqueue_head(Yue2Model* m, Workspace& w, const float* x, int phase, hipStream_t s, int rows = 1);
 // The same step as one persistent kernel when the shape has one (full
 // vocabulary head only); returns 1 when it cannot be used.  sample: the
 // fused sampler's mode (StepCall::sample); the workspace must have been

@@ -203,9 +203,17 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
         if ((e = launch_gemv(s, EPI_RESID, da)) != hipSuccess) return hip_fail(e, "gemv(down)");
     }
     if (!head) return YUE2_OK;
+    return enqueue_head(m, w, w.x, phase, s, rows);
+}
+
+int enqueue_head(Yue2Model* m, Workspace& w, const float* x, int phase, hipStream_t s, int rows) {
+    const Yue2Config& c = m->c;
+    const int H = c.hidden_size, V = c.vocab_size;
+    const float eps = c.rms_norm_eps;
+    hipError_t e;
     // final_norm (src/model.rs:590) runs in the LM-head GEMV prologue.
     if (phase == YUE2_PHASE_NONE) {
-        GemvArgs la{m->lm_head, nullptr, w.x, w.logits, H, V, V, H, rows, m->final_norm, eps, w.st};
+        GemvArgs la{m->lm_head, nullptr, x, w.logits, H, V, V, H, rows, m->final_norm, eps, w.st};
         if ((e = launch_gemv(s, EPI_STORE, la)) != hipSuccess) return hip_fail(e, "gemv(lm_head)");
         return YUE2_OK;
     }
@@ -214,10 +222,10 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
     int start, end, stop;
     phase_range(phase, &start, &end, &stop);
     launch_fill(s, w.logits, (size_t)rows * V, -INFINITY);
-    GemvArgs ra{m->lm_head + (size_t)start * H, nullptr, w.x, w.logits + start, H, V, end - start, H, rows,
+    GemvArgs ra{m->lm_head + (size_t)start * H, nullptr, x, w.logits + start, H, V, end - start, H, rows,
                 m->final_norm, eps, w.st};
     if ((e = launch_gemv(s, EPI_STORE, ra)) != hipSuccess) return hip_fail(e, "gemv(lm_head range)");
-    GemvArgs sa{m->lm_head + (size_t)stop * H, nullptr, w.x, w.logits + stop, H, V, 1, H, rows,
+    GemvArgs sa{m->lm_head + (size_t)stop * H, nullptr, x, w.logits + stop, H, V, 1, H, rows,
                 m->final_norm, eps, nullptr};
     if ((e = launch_gemv(s, EPI_STORE, sa)) != hipSuccess) return hip_fail(e, "gemv(lm_head stop)");
     return YUE2_OK;

@@ -13,6 +13,16 @@ only the token id comes back.  Weights, KV caches and prompts are resident in
 HBM before the timed region.  The batch-1 line (no CFG) is measured the same
 way on its own cache.
 
+The prompts are prefilled on the matrix cores (yue2_hip_prefill_mfma:
+BF16 MFMA GEMMs + causal flash attention; --prefill exact uses the
+bit-exact decode-order kernels instead); the prefill's own rate is reported
+beside the decode line.
+
+--workload long: the long-context run on the same model -- 24000-token
+prompts for both CFG rows, then CFG batch-2 decode to the full 24576-token
+context, reporting ms/token as the context grows and the step kernel's
+roofline at the last position (24576 attended keys).
+
 Prints one JSON line.  Progress goes to stderr.
 """
 from __future__ import annotations
@@ -77,6 +87,39 @@ def measure(y2, model, caches, first, sampling, scale, warmup, steps, c):
         "hbm_roofline_frac": step_bytes(c, rows, mean_ctx) / (wall / steps) / HBM_PEAK,
         "bytes_per_step": step_bytes(c, rows, mean_ctx),
     }
+
+
+MFMA_BF16_PEAK = 2.5e15  # MI355X dense BF16 matrix FLOP/s
+
+
+def prefill_flops(c, n: int) -> float:
+    """Algorithmic FLOPs of prefilling n tokens: every layer linear once per
+    token, the causal attention (QK^T and PV over 1..n keys per query head),
+    the LM head of the last row."""
+    H, D, I, V = c.hidden_size, c.head_dim, c.intermediate_size, c.vocab_size
+    q, kv = c.num_attention_heads * D, c.num_key_value_heads * D
+    linear = 2.0 * n * c.num_hidden_layers * (H * (q + 2 * kv) + q * H + 3 * H * I)
+    attention = c.num_hidden_layers * c.num_attention_heads * 4.0 * D * n * (n + 1) / 2.0
+    return linear + attention + 2.0 * V * H
+
+
+def prefill(y2, model, c, ids, cap, mode):
+    """(cache, last-row logits, seconds) of one prompt."""
+    y2.synchronize()
+    t = time.perf_counter()
+    if mode == "mfma":
+        cache, logits = model.prefill_mfma(ids, cap)
+    else:
+        cache, logits = model.prefill_phase(ids, cap)
+    y2.synchronize()
+    return cache, logits, time.perf_counter() - t
+
+
+def prefill_report(c, n, seconds, mode):
+    fl = prefill_flops(c, n)
+    return {"mode": mode, "tokens": n, "s": round(seconds, 4), "tokens_per_s": round(n / seconds, 1),
+            "TFLOP_s": round(fl / seconds / 1e12, 2), "mfma_frac": round(fl / seconds / MFMA_BF16_PEAK, 4),
+            "flops": fl}
 
 
 def measured_traffic(context):
@@ -174,6 +217,10 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=112)
     ap.add_argument("--step-kernel", type=int, default=1, choices=[0, 1],
                     help="1 (default): one persistent kernel per token; 0: one kernel per phase")
+    ap.add_argument("--prefill", default="mfma", choices=["mfma", "exact"],
+                    help="mfma (default): matrix-core prefill; exact: decode-order (bit-exact) prefill")
+    ap.add_argument("--workload", default="decode", choices=["decode", "long"],
+                    help="decode (default): 2048-token prompts; long: 24000-token prompts decoded to 24576")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)",
@@ -188,25 +235,26 @@ def main() -> int:
         print("no gfx950 device available", file=sys.stderr)
         return 1
     c = synthetic.CLASS_3B
-    W, K, P = args.warmup, args.steps, args.prompt
     log("generating synthetic 3B-class weights")
     t = time.perf_counter()
     ckpt = synthetic.checkpoint(c, seed=0, threads=16)
     log(f"weights ready in {time.perf_counter() - t:.1f}s; uploading")
     model = y2.Model.open(ckpt)
     step_kernel = model.set_step_kernel(bool(args.step_kernel))
+    if args.workload == "long":
+        return long_context(args, y2, synthetic, c, ckpt, model, step_kernel)
+    W, K, P = args.warmup, args.steps, args.prompt
     cond_ids = synthetic.prompt(P, c.vocab_size, seed=0)
     neg_ids = synthetic.prompt(P, c.vocab_size, seed=1)
     cap = P + W + K + 1
     sampling = y2.Sampling(temperature=0.9, top_p=0.93, top_k=50, repetition_penalty=1.2, penalty_window=50,
                            min_tokens=0, max_tokens=W + K + 1)
-    log(f"prefilling 3 x {P} tokens (decode-order kernels)")
-    t = time.perf_counter()
-    c_bs1, l_bs1 = model.prefill_phase(cond_ids, cap)
-    c_pos, l_pos = model.prefill_phase(cond_ids, cap)
-    c_neg, l_neg = model.prefill_phase(neg_ids, cap)
-    y2.synchronize()
-    log(f"prefill done in {time.perf_counter() - t:.1f}s")
+    log(f"prefilling 3 x {P} tokens ({args.prefill})")
+    c_bs1, l_bs1, _ = prefill(y2, model, c, cond_ids, cap, args.prefill)
+    c_pos, l_pos, t_pos = prefill(y2, model, c, cond_ids, cap, args.prefill)
+    c_neg, l_neg, t_neg = prefill(y2, model, c, neg_ids, cap, args.prefill)
+    pre = prefill_report(c, P, min(t_pos, t_neg), args.prefill)
+    log(f"prefill: {pre['tokens_per_s']:.0f} tokens/s, {pre['TFLOP_s']:.1f} TFLOP/s")
 
     # Dominant kernel at a context that does not depend on --steps/--warmup:
     # the CFG decoder takes one step (both caches reach P + 1 positions) and
@@ -283,9 +331,95 @@ def main() -> int:
                 "hbm_roofline_frac": round(bs1["hbm_roofline_frac"], 4),
                 "bytes_per_step": int(bs1["bytes_per_step"])},
         "roofline": roofline,
+        "prefill": pre,
         "phase_kernels": others,
         "cpu_baseline": cpu,
         "norm_fallbacks": model.norm_fallbacks(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def long_context(args, y2, synthetic, c, ckpt, model, step_kernel):
+    """24000-token prompts for both CFG rows (matrix-core prefill), then CFG
+    batch-2 decode to the full 24576-token context in segments of 64 steps,
+    each segment's per-step HIP-event times giving ms/token at its context.
+    The step kernel is timed alone at the last free position (24575: 24576
+    attended keys) before the final step fills it."""
+    P, full = 24000, c.max_position_embeddings
+    steps = full - P
+    cond_ids = synthetic.prompt(P, c.vocab_size, seed=0)
+    neg_ids = synthetic.prompt(P, c.vocab_size, seed=1)
+    sampling = y2.Sampling(temperature=0.9, top_p=0.93, top_k=50, repetition_penalty=1.2, penalty_window=50,
+                           min_tokens=0, max_tokens=steps + 1)
+    log(f"prefilling 2 x {P} tokens ({args.prefill})")
+    c_pos, l_pos, t_pos = prefill(y2, model, c, cond_ids, full, args.prefill)
+    log(f"conditional row prefilled in {t_pos:.2f}s")
+    c_neg, l_neg, t_neg = prefill(y2, model, c, neg_ids, full, args.prefill)
+    pre = prefill_report(c, P, min(t_pos, t_neg), args.prefill)
+    log(f"prefill: {pre['tokens_per_s']:.0f} tokens/s, {pre['TFLOP_s']:.1f} TFLOP/s")
+    dec = y2.Decoder(model, c_pos, c_neg, sampling=sampling, seed=0, scale=args.scale)
+    curve, times = [], []
+    first = np.concatenate([l_pos, l_neg])
+    y2.synchronize()
+    t0 = time.perf_counter()
+    done = 0
+    while done < steps - 1:
+        n = min(64, steps - 1 - done)
+        ctx = c_pos.length
+        toks, ms = dec.run(n, first_logits=first if done == 0 else None, timing=True)
+        assert len(toks) == n, "decode stopped early"
+        times.extend(ms)
+        curve.append({"context": int(ctx), "steps": n, "p50_ms": round(float(np.percentile(ms, 50)), 4),
+                      "mean_ms": round(float(np.mean(ms)), 4)})
+        log(f"context {ctx}..{ctx + n}: p50 {curve[-1]['p50_ms']:.3f} ms/token")
+        done += n
+    y2.synchronize()
+    wall = time.perf_counter() - t0
+    context = c_pos.length
+    if step_kernel:
+        dom_ms, dom_b = dec.time_kernel("step", 32)
+        dom_name = "step_kernel<2, 128, 3, 6, 6, 16> (whole CFG batch-2 token: 28 layers + LM head + sampler)"
+    else:
+        dom_ms, dom_b = dec.time_kernel("gate_up", args.kernel_iters)
+        dom_name = "gemv_kernel<2, EPI_SWIGLU, 6, true> (RMSNorm + gate/up + SwiGLU of one layer)"
+    toks, ms = dec.run(1, timing=True)
+    times.extend(ms)
+    assert c_pos.length == full and c_neg.length == full
+    dec.close()
+    achieved = dom_b / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(achieved / 8000.0, 4), "traffic": None, "kernel": dom_name,
+                "launch_ms": round(dom_ms, 5), "bytes_per_launch": int(dom_b), "context": context}
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle on host cores)")
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 16)
+        log(f"CPU baseline: {cpu['value']:.3f} steps/s with {threads} threads")
+    timed = steps - 1
+    out = {
+        "metric": METRIC,
+        "value": round(timed / wall, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": timed,
+        "warmup": 0,
+        "ms_per_step": round(1000.0 * wall / timed, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"3B-class long-context CFG batch-2 decode, {P}-token prompts decoded to "
+                               f"{full} positions, T 0.9 / top-k 50 / top-p 0.93 / penalty 1.2",
+                   "prompt": P, "context_end": full, "global_batch": 2, "parallelism": "none (1 GPU)",
+                   "execution": "persistent step kernel" if step_kernel else "one kernel per phase"},
+        "p50_ms": round(float(np.percentile(times, 50)), 4),
+        "ms_per_token_vs_context": curve,
+        "roofline": roofline,
+        "prefill": pre,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     return 0

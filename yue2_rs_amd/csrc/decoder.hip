@@ -390,8 +390,13 @@ static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double
     const double weights = L * (2.0 * (H * (q + 2.0 * kv) + q * H + 3.0 * H * I) + 4.0 * (2.0 * H + 2.0 * D)) +
                            2.0 * V * H + 4.0 * H;
     double kvb = 0.0;
-    for (int b = 0; b < d->rows; ++b)
-        kvb += L * 2.0 * kv * 2.0 * (d->caches[b]->length + 1) + 2.0 * H;
+    for (int b = 0; b < d->rows; ++b) {
+        // the timed launches write the new token's K/V at position `length`
+        const Yue2Cache* ch = d->caches[b];
+        if (ch->length >= ch->capacity || ch->length >= c.max_position_embeddings)
+            return fail(YUE2_ERR_CONTEXT, "no free cache position to time the step kernel at");
+        kvb += L * 2.0 * kv * 2.0 * (ch->length + 1) + 2.0 * H;
+    }
     hipStream_t s = m->stream;
     d->w.reserve_launches(s, (int64_t)iters + 1);
     hipEvent_t b0, b1;

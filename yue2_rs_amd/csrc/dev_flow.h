@@ -360,9 +360,9 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         const int c = lane % SCPL, kk = lane / SCPL;
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
-                // a later chunk (long contexts): stage it, then patch the new key
+                // a later chunk (long contexts), requested during the previous
+                // chunk's scores: stage it, then patch the new key
                 __syncthreads();
-                load_chunk(Kc, cb, kr);
                 store_chunk(Ks, kr);
                 __syncthreads();
                 const int kp = pos - j0 - cb * kBlockKeys;
@@ -371,6 +371,8 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                         reinterpret_cast<uint16_t*>(Ks)[(size_t)kp * D + d] = bf16_bits(k_s[d]);
                 __syncthreads();
             }
+            // the next chunk's loads stay in flight while this one is scored
+            if (cb + kAttnChunk < nbl) load_chunk(Kc, cb + kAttnChunk, kr);
             const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
             for (int kg = wave; kg * SKPW < keys; kg += NW) {
                 const int kl = kg * SKPW + kk;  // key within the chunk (rows past `keys` are never stored)
@@ -415,6 +417,9 @@ m = xor_max<32>(m);
     // ---- phase 2: M, exp(s - M) and block sums -----------------------------
     const uint32_t t_bsum = flow_tag(a.epoch, a.layer, FK_BSUM);
     {
+        // (long contexts) the second V chunk is requested before the waits
+        // for the group's block statistics
+        if (kAttnChunk < nbl) load_chunk(Vc, kAttnChunk, vr);
         if (!gather<NT, (G * MAXNB + NT - 1) / NT>(a.bmax + hbase, Gq * nb, nb, a.blk_stride, t_bmax, red_s, st))
             return false;
         mark();
@@ -472,8 +477,8 @@ m = xor_max<32>(m);
         const int t = lane / LPS, c = lane % LPS;
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
+                // requested one chunk ahead, as the keys
                 __syncthreads();
-                load_chunk(Vc, cb, vr);
                 store_chunk(Vs, vr);
                 __syncthreads();
                 const int kp = pos - j0 - cb * kBlockKeys;
@@ -481,6 +486,7 @@ m = xor_max<32>(m);
                     for (int d = tid; d < D; d += NT)
                         reinterpret_cast<uint16_t*>(Vs)[(size_t)kp * D + d] = bf16_bits(v_s[d]);
                 __syncthreads();
+                if (cb + kAttnChunk < nbl) load_chunk(Vc, cb + kAttnChunk, vr);
             }
             const int cblocks = min(kAttnChunk, nbl - cb);
             for (int it = wave; it < cblocks * 2; it += NW) {

@@ -297,7 +297,7 @@ void yue2_hip_synthetic_bf16(uint16_t *out, size_t n, uint64_t seed, uint64_t te
 int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t n);
 /* Diagnostics: out = x W^T (M x N f32, the raw FP32 accumulation) through
  * the prefill's BF16 MFMA GEMM; x [M, K] and w [N, K] BF16 host arrays, K a
- * multiple of 32.  Returns 0 or a negative Yue2Error. */
+ * multiple of 64.  Returns 0 or a negative Yue2Error. */
 int32_t yue2_hip_selftest_gemm(const uint16_t *x, const uint16_t *w, float *out, int32_t M, int32_t N,
                                int32_t K);
 /* Execution choice: run decode steps (yue2_hip_forward and decoders created
@@ -356,12 +356,18 @@ int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, Yue2Cache *c2, int32_t i
  * yue2_hip_bench_copy: hipMemcpyAsync of `bytes` (a multiple of 256) from
  * one device buffer to another, once untimed and then `iters` times;
  * *avg_ms = mean time per copy (each reads and writes `bytes`).
- * All three return 0 or a negative Yue2Error. */
+ * yue2_hip_bench_gemm: the prefill's BF16 MFMA GEMM C = X W^T (X [M x K],
+ * W [N x K], K a multiple of 64, f32 rounded output; pair != 0: the
+ * gate/up pair, W and a second [N x K] matrix with the SwiGLU epilogue),
+ * once untimed and then `iters` times; *flops = 2 M K x (weight rows).
+ * All return 0 or a negative Yue2Error. */
 int32_t yue2_hip_bench_gemv(int32_t n, int32_t k, int32_t rows, int32_t copies, int32_t iters, float *avg_ms,
                             double *bytes);
 int32_t yue2_hip_bench_attention(int32_t context, int32_t rows, int32_t layers, int32_t iters, float *avg_ms,
                                  double *bytes);
 int32_t yue2_hip_bench_copy(int64_t bytes, int32_t iters, float *avg_ms);
+int32_t yue2_hip_bench_gemm(int32_t M, int32_t N, int32_t K, int32_t pair, int32_t iters, float *avg_ms,
+                            double *flops);
 
 #ifdef __cplusplus
 }

@@ -21,8 +21,10 @@ decode-order prefill on the same seeded checkpoint and prompt:
     difference growing as the square root of the depth);
   * the argmax of every compared row is the same id;
   * phase-restricted heads: the same -inf pattern.
-Prompts of 1 token (the attention over one key), 65 and 1100 tokens cross the 64-row flash tiles and the 1024-row
-chunks of the prefill."""
+Prompts of 1 token (the attention over one key), 65 and 1100 tokens cross
+the 64-key and 128-query flash tiles; 4100 tokens (against the decode-order
+GPU prefill, itself bit-exact with the oracle) cross the 4096-row chunks of
+the prefill."""
 import dataclasses
 
 import numpy as np
@@ -57,7 +59,7 @@ def _gemm(x16, w16):
     return out
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1, 32), (128, 128, 32), (200, 300, 96), (257, 129, 512)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 64), (128, 128, 64), (200, 300, 192), (257, 129, 512)])
 def test_gemm_small_integers_exact(gpu, M, N, K):
     rng = np.random.default_rng(M * 7 + N)
     x = _bf16(rng.integers(-4, 5, (M, K)).astype(np.float32))
@@ -78,9 +80,9 @@ def test_gemm_random_within_bound(gpu, M, N, K):
 
 
 def test_gemm_rejects_ragged_k(gpu):
-    x = np.zeros((4, 48), np.uint16)
+    x = np.zeros((4, 96), np.uint16)
     out = np.empty((4, 4), np.float32)
-    assert y2.lib().yue2_hip_selftest_gemm(x.ctypes.data, x.ctypes.data, out.ctypes.data, 4, 4, 48) < 0
+    assert y2.lib().yue2_hip_selftest_gemm(x.ctypes.data, x.ctypes.data, out.ctypes.data, 4, 4, 96) < 0
 
 
 def _close(got, want, tol, what):
@@ -116,6 +118,24 @@ def test_prefill_within_tolerance(two_layer, n):
     t = int(np.argmax(ol))
     _close(gm.forward([t], gc), om.forward([t], oc), TWO_LAYER_TOL, "next-step logits")
     gc.close()
+
+
+def test_prefill_crosses_chunks(gpu):
+    ck = synthetic.checkpoint(synthetic.REDUCED, seed=3)
+    gm = y2.Model.open(ck)
+    try:
+        n = 4100
+        ids = synthetic.prompt(n, synthetic.REDUCED.vocab_size, seed=5)
+        c1, l1 = gm.prefill_phase(ids, n + 2)
+        c2, l2 = gm.prefill_mfma(ids, n + 2)
+        assert c2.length == n
+        _close(l2, l1, TWO_LAYER_TOL, "prefill logits")
+        t = int(np.argmax(l1))
+        _close(gm.forward([t], c2), gm.forward([t], c1), TWO_LAYER_TOL, "next-step logits")
+        c1.close()
+        c2.close()
+    finally:
+        gm.close()
 
 
 def test_prefill_needs_empty_cache(two_layer):

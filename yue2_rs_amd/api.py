@@ -127,6 +127,7 @@ def lib() -> C.CDLL:
         "yue2_hip_bench_gemv": (i32, [i32, i32, i32, i32, i32, vp, vp]),
         "yue2_hip_bench_attention": (i32, [i32, i32, i32, i32, vp, vp]),
         "yue2_hip_bench_copy": (i32, [C.c_int64, i32, vp]),
+        "yue2_hip_bench_gemm": (i32, [i32, i32, i32, i32, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -57,31 +57,34 @@ struct GemmArgs {
     int M, N, K;
 };
 
-constexpr int kGemmTM = 128, kGemmTK = 32, kGemmPad = 8;
+constexpr int kGemmTM = 128, kGemmTK = 64, kGemmPad = 8;
 constexpr int kGemmThreads = 256;
 
 // One workgroup computes a 128-row tile of C: 128 columns (64 for the
 // gate/up pair, whose W tile holds 64 gate rows and the same 64 up rows).
 // Wave w takes rows 64 (w / 2) .. + 64 and two 32x32 accumulator tiles per
 // row half: columns 64 (w % 2) + 32 j (the pair: gate and up of columns
-// 32 (w % 2) .. + 32).  The X and W tiles of each 32-wide step of K go
-// through LDS; the next step's global loads are in flight during the MFMAs.
+// 32 (w % 2) .. + 32).  The X and W tiles of each 64-wide step of K go
+// through two LDS buffers in turn: step k + 1 is stored from registers
+// while step k is multiplied, and step k + 2's global loads are then in
+// flight; one barrier per step.
 template <int EPI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
     constexpr bool PAIR = EPI == GEPI_SWIGLU_BF16;
     constexpr int TN = PAIR ? 64 : 128;  // output columns per tile
     constexpr int LDS_W = kGemmTK + kGemmPad;
-    __shared__ __align__(16) uint16_t xs[kGemmTM][LDS_W];
-    __shared__ __align__(16) uint16_t ws[128][LDS_W];
+    constexpr int PER = kGemmTM * kGemmTK / 8 / kGemmThreads;  // uint4 per thread per tile and operand
+    __shared__ __align__(16) uint16_t xs[2][kGemmTM][LDS_W];
+    __shared__ __align__(16) uint16_t ws[2][128][LDS_W];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kGemmTM, n0 = blockIdx.x * TN;
-    // each thread moves two 16-byte pieces of each tile: row q / 4, k 8 (q % 4)
-    uint4 rx[2], rw[2];
+    // each thread moves PER 16-byte pieces of each tile: row q / 8, k 8 (q % 8)
+    uint4 rx[PER], rw[PER];
     auto load = [&](int k0) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int q = tid + kGemmThreads * s, row = q >> 2, kq = (q & 3) * 8;
+        for (int s = 0; s < PER; ++s) {
+            const int q = tid + kGemmThreads * s, row = q >> 3, kq = (q & 7) * 8;
             const int mr = m0 + row;
             rx[s] = mr < g.M ? ldg4(g.x + (size_t)mr * g.ldx + k0 + kq) : make_uint4(0, 0, 0, 0);
             const uint16_t* wrow;
@@ -96,6 +99,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
             rw[s] = nr < g.N ? ldg4(wrow + k0 + kq) : make_uint4(0, 0, 0, 0);
         }
     };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int s = 0; s < PER; ++s) {
+            const int q = tid + kGemmThreads * s, row = q >> 3, kq = (q & 7) * 8;
+            *reinterpret_cast<uint4*>(&xs[buf][row][kq]) = rx[s];
+            *reinterpret_cast<uint4*>(&ws[buf][row][kq]) = rw[s];
+        }
+    };
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -103,31 +114,35 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    const int steps = g.K / kGemmTK;
     load(0);
-    for (int k0 = 0; k0 < g.K; k0 += kGemmTK) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int q = tid + kGemmThreads * s, row = q >> 2, kq = (q & 3) * 8;
-            *reinterpret_cast<uint4*>(&xs[row][kq]) = rx[s];
-            *reinterpret_cast<uint4*>(&ws[row][kq]) = rw[s];
-        }
-        __syncthreads();
-        if (k0 + kGemmTK < g.K) load(k0 + kGemmTK);
+    store(0);
+    if (steps > 1) load(kGemmTK);
+    __syncthreads();
+    for (int st = 0; st < steps; ++st) {
+        const int cur = st & 1;
 #pragma unroll
         for (int kk = 0; kk < kGemmTK; kk += 16) {
             const int kc = kk + 8 * (lane >> 5);
             uint4 a[2], b[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const uint4*>(&xs[wm * 64 + i * 32 + (lane & 31)][kc]);
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const uint4*>(&xs[cur][wm * 64 + i * 32 + (lane & 31)][kc]);
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int wr = PAIR ? j * 64 + wn * 32 : wn * 64 + j * 32;
-                b[j] = *reinterpret_cast<const uint4*>(&ws[wr + (lane & 31)][kc]);
+                b[j] = *reinterpret_cast<const uint4*>(&ws[cur][wr + (lane & 31)][kc]);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        }
+        if (st + 1 < steps) {
+            // the other buffer was last read in step st - 1, before the
+            // barrier that ended it
+            store(cur ^ 1);
+            if (st + 2 < steps) load((st + 2) * kGemmTK);
         }
         __syncthreads();
     }
@@ -250,18 +265,26 @@ struct FlashArgs {
     uint16_t* out;  // [rows][heads D] BF16 (rb of the attention output)
 };
 
-// One workgroup per (query head h, 64 query rows); wave w takes 16 of them.
-// Keys in tiles of 64: S = Q K^T on 16x16x32 MFMAs (K staged in LDS), the
-// online softmax (row maxima and sums across the 16 lanes of a row group),
-// P through LDS into the A layout and V transposed in LDS for O += P V.
+// One workgroup per (query head h, kFlashRows = 128 query rows); wave w
+// takes 16 of them.  Keys in tiles of 64: S = Q K^T on 16x16x32 MFMAs (K
+// staged in LDS), the online softmax (row maxima and sums across the 16
+// lanes of a row group, DPP), P through LDS into the A layout and V
+// transposed in LDS for O += P V.  The next tile's K and V are requested
+// into registers while the current one is computed.  V^T is written as
+// dwords (two keys per thread), 32 consecutive keys of one dim row per
+// 32 lanes, so the transposing stores do not conflict on LDS banks.
+constexpr int kFlashRows = 128, kFlashThreads = 512, kFlashKT = 64;
+
 template <int D>
-__global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
-    constexpr int KT = 64, PADK = 8;
-    __shared__ __align__(16) uint16_t ks[KT][D + PADK];      // K tile, row = key
-    __shared__ __align__(16) uint16_t vt[D][KT + PADK];      // V tile transposed, row = dim
-    __shared__ __align__(16) uint16_t ps[2][4][16][KT + PADK];  // each wave's P (hi, lo), row = query
+__global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const FlashArgs f) {
+    constexpr int KT = kFlashKT, PADK = 8, NW = kFlashThreads / 64;
+    constexpr int KN = KT * D / 8, VN = (KT / 2) * (D / 8);  // K uint4 and V key-pair units per tile
+    constexpr int KU = (KN + kFlashThreads - 1) / kFlashThreads, VU = (VN + kFlashThreads - 1) / kFlashThreads;
+    __shared__ __align__(16) uint16_t ks[KT][D + PADK];           // K tile, row = key
+    __shared__ __align__(16) uint16_t vt[D][KT + PADK];           // V tile transposed, row = dim
+    __shared__ __align__(16) uint16_t ps[2][NW][16][KT + PADK];   // each wave's P (hi, lo), row = query
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.x, q0 = blockIdx.y * 64, G = f.heads / f.kv_heads, g = h / G;
+    const int h = blockIdx.x, q0 = blockIdx.y * kFlashRows, G = f.heads / f.kv_heads, g = h / G;
     const int qrow = q0 + wave * 16 + (lane & 15);  // the query row this lane loads for A
     const uint16_t* Kc = f.kv_base + (((size_t)f.layer * 2) * f.kv_heads + g) * (size_t)f.cap * D;
     const uint16_t* Vc = f.kv_base + (((size_t)f.layer * 2 + 1) * f.kv_heads + g) * (size_t)f.cap * D;
@@ -285,22 +308,51 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
     for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[dt][r] = 0.0f;
-    const int last_key = min(f.p0 + q0 + 63, f.p0 + f.rows - 1);  // keys [0, last_key]
+    const int last_key = min(f.p0 + q0 + kFlashRows - 1, f.p0 + f.rows - 1);  // keys [0, last_key]
     const int tiles = last_key / KT + 1;
+    // tile loads: K as uint4 of rows (key u / (D/8), dims 8 (u % (D/8)));
+    // V as key pairs (keys 2 (v % 32) and + 1, dims 8 (v / 32)); keys past
+    // last_key are zero
+    uint4 kr[KU], vr[VU][2];
+    auto load_tile = [&](int t) {
+        const int kb = t * KT;
+#pragma unroll
+        for (int i = 0; i < KU; ++i) {
+            const int u = tid + i * kFlashThreads, kg = kb + u / (D / 8);
+            kr[i] = u < KN && kg <= last_key ? ldg4(Kc + (size_t)kg * D + (u % (D / 8)) * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i) {
+            const int v = tid + i * kFlashThreads, kg = kb + 2 * (v % (KT / 2)), d8 = (v / (KT / 2)) * 8;
+            const bool in = v < VN;
+            vr[i][0] = in && kg <= last_key ? ldg4(Vc + (size_t)kg * D + d8) : make_uint4(0, 0, 0, 0);
+            vr[i][1] = in && kg + 1 <= last_key ? ldg4(Vc + (size_t)(kg + 1) * D + d8) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    load_tile(0);
     for (int t = 0; t < tiles; ++t) {
         const int kb = t * KT;
-        // stage K (rows) and V (transposed); keys past last_key are zero
-        for (int u = tid; u < KT * D / 8; u += 256) {
-            const int key = u / (D / 8), d8 = (u % (D / 8)) * 8, kg = kb + key;
-            const bool in = kg <= last_key;
-            const uint4 kv = in ? ldg4(Kc + (size_t)kg * D + d8) : make_uint4(0, 0, 0, 0);
-            const uint4 vv = in ? ldg4(Vc + (size_t)kg * D + d8) : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint4*>(&ks[key][d8]) = kv;
-            const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
+        // stage this tile (its loads were issued a tile ago), request the next
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vt[d8 + e][key] = ve[e];
+        for (int i = 0; i < KU; ++i) {
+            const int u = tid + i * kFlashThreads;
+            if (u < KN) *reinterpret_cast<uint4*>(&ks[u / (D / 8)][(u % (D / 8)) * 8]) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i) {
+            const int v = tid + i * kFlashThreads, kp = 2 * (v % (KT / 2)), d8 = (v / (KT / 2)) * 8;
+            if (v >= VN) continue;
+            const uint32_t* a0 = reinterpret_cast<const uint32_t*>(&vr[i][0]);
+            const uint32_t* a1 = reinterpret_cast<const uint32_t*>(&vr[i][1]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // dims d8 + 2e (low halves) and d8 + 2e + 1 (high halves) of keys kp, kp + 1
+                *reinterpret_cast<uint32_t*>(&vt[d8 + 2 * e][kp]) = (a0[e] & 0xffffu) | (a1[e] << 16);
+                *reinterpret_cast<uint32_t*>(&vt[d8 + 2 * e + 1][kp]) = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
+            }
         }
         __syncthreads();
+        if (t + 1 < tiles) load_tile(t + 1);
         // S for the wave's 16 rows x 64 keys: four 16x16 tiles
         f32x4 s[4];
 #pragma unroll
@@ -313,7 +365,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
             }
             s[kt] = acc;
         }
-        // scale, causal mask, online softmax per row
+        // scale, causal mask, online softmax per row (the row's 16 lanes)
         float alpha[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -325,8 +377,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
                 s[kt][r] = v;
                 mx = fmaxf(mx, v);
             }
-#pragma unroll
-            for (int msk = 8; msk >= 1; msk >>= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+            mx = xor_max<8>(mx);
             const float mn = fmaxf(m[r], mx);
             alpha[r] = mn == -__builtin_huge_valf() ? 1.0f : __expf(m[r] - mn);
             float sum = 0.0f;
@@ -336,8 +387,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
                 s[kt][r] = p;
                 sum += p;
             }
-#pragma unroll
-            for (int msk = 8; msk >= 1; msk >>= 1) sum += __shfl_xor(sum, msk, 64);
+            sum = xor_sum<8>(sum);
             l[r] = l[r] * alpha[r] + sum;
             m[r] = mn;
         }
@@ -348,7 +398,8 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
         // P into the wave's LDS rows as two BF16 parts, hi = bf16(p) and
         // lo = bf16(p - hi): V is BF16 (the cache), so P V takes two MFMAs
         // and keeps about 16 bits of P instead of 8, as the reference's f32
-        // softmax and P V do (src/model.rs:313-397).
+        // softmax and P V do (src/model.rs:313-397).  The rows are the
+        // wave's own: a wave-level LDS fence orders them before the reads.
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -357,7 +408,9 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
                 ps[0][wave][4 * (lane >> 4) + r][kt * 16 + (lane & 15)] = bf16_bits(hi);
                 ps[1][wave][4 * (lane >> 4) + r][kt * 16 + (lane & 15)] = bf16_bits(s[kt][r] - hi);
             }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // O += P V: A = P rows, B = V^T rows (keys contiguous)
 #pragma unroll
         for (int kk = 0; kk < KT; kk += 32) {
@@ -370,7 +423,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
                 o[dt] = mfma16(ah, b, o[dt]);
             }
         }
-        __syncthreads();
+        __syncthreads();  // every wave is done with this tile's K and V
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -391,7 +444,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashArgs f) {
 
 namespace {
 
-constexpr int kPrefillChunk = 1024;  // rows per pass through the layers
+constexpr int kPrefillChunk = 4096;  // rows per pass through the layers
 
 struct PrefillBuffers {
     void* block = nullptr;
@@ -447,9 +500,9 @@ int run_prefill(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int n, int phase
             rope_append_kernel<<<dim3(rows, Hq + 2 * Hkv), 64, 0, s>>>(ra);
             FlashArgs fa{b.q, c->kv, c->capacity, l, Hq, Hkv, c->length + p0, rows, 1.0f / std::sqrt((float)D),
                          b.att};
-            const dim3 fg(Hq, (rows + 63) / 64);
-            if (D == 128) flash_prefill_kernel<128><<<fg, 256, 0, s>>>(fa);
-            else if (D == 64) flash_prefill_kernel<64><<<fg, 256, 0, s>>>(fa);
+            const dim3 fg(Hq, (rows + kFlashRows - 1) / kFlashRows);
+            if (D == 128) flash_prefill_kernel<128><<<fg, kFlashThreads, 0, s>>>(fa);
+            else if (D == 64) flash_prefill_kernel<64><<<fg, kFlashThreads, 0, s>>>(fa);
             else return fail(YUE2_ERR_ARG, "MFMA prefill supports head_dim 64 and 128");
             GemmArgs go{b.att, qw, L.wo, nullptr, qw, b.x, nullptr, H, rows, H, qw};
             if ((e = launch_gemm(s, GEPI_RESID, go)) != hipSuccess) return hip_fail(e, "prefill o gemm");
@@ -516,4 +569,59 @@ extern "C" int32_t yue2_hip_selftest_gemm(const uint16_t* x, const uint16_t* w, 
     (void)hipFree(dw);
     (void)hipFree(dc);
     return e == hipSuccess ? YUE2_OK : hip_fail(e, "gemm selftest");
+}
+
+namespace {
+// BF16 operands of N(0, 1)-like magnitude from a counter hash (the matrix
+// cores' power, and so their clock, depends on the bits they toggle).
+__global__ void bench_fill_kernel(uint16_t* p, size_t n, uint64_t seed) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        uint64_t z = seed * 0x9e3779b97f4a7c15ull + i;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        p[i] = bf16_bits(rb(((float)(z >> 40) * 0x1.0p-24f - 0.5f) * 3.46f));
+    }
+}
+}  // namespace
+
+extern "C" int32_t yue2_hip_bench_gemm(int32_t M, int32_t N, int32_t K, int32_t pair, int32_t iters,
+                                       float* avg_ms, double* flops) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!avg_ms || !flops || M < 1 || N < 1 || K < 1 || K % kGemmTK || iters < 1)
+        return fail(YUE2_ERR_ARG, "bad GEMM benchmark request");
+    if (!device_ready()) return fail(YUE2_ERR_DEVICE, "no usable gfx950 device");
+    const int wrows = pair ? 2 * N : N;
+    void *dx = nullptr, *dw = nullptr, *dc = nullptr;
+    hipError_t e = hipMalloc(&dx, 2 * (size_t)M * K);
+    if (e == hipSuccess) e = hipMalloc(&dw, 2 * (size_t)wrows * K);
+    if (e == hipSuccess) e = hipMalloc(&dc, 4 * (size_t)M * N);
+    if (e == hipSuccess) {
+        bench_fill_kernel<<<1024, 256>>>(static_cast<uint16_t*>(dx), (size_t)M * K, 1);
+        bench_fill_kernel<<<1024, 256>>>(static_cast<uint16_t*>(dw), (size_t)wrows * K, 2);
+        e = hipGetLastError();
+    }
+    hipEvent_t a = nullptr, b = nullptr;
+    if (e == hipSuccess) e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    const uint16_t* w = static_cast<const uint16_t*>(dw);
+    GemmArgs g{static_cast<const uint16_t*>(dx), K, w, pair ? w + (size_t)N * K : nullptr, K, static_cast<float*>(dc),
+               static_cast<uint16_t*>(dc), N, M, N, K};
+    const int epi = pair ? GEPI_SWIGLU_BF16 : GEPI_ROUND;
+    if (e == hipSuccess) e = launch_gemm(nullptr, epi, g);
+    if (e == hipSuccess) e = hipEventRecord(a, nullptr);
+    for (int i = 0; i < iters && e == hipSuccess; ++i) e = launch_gemm(nullptr, epi, g);
+    if (e == hipSuccess) e = hipEventRecord(b, nullptr);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    float ms = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    (void)hipFree(dx);
+    (void)hipFree(dw);
+    (void)hipFree(dc);
+    if (e != hipSuccess) return hip_fail(e, "GEMM benchmark");
+    *avg_ms = ms / (float)iters;
+    *flops = 2.0 * M * (double)wrows * K;
+    return YUE2_OK;
 }

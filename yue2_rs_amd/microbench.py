@@ -10,12 +10,16 @@ layer-call = b 4096 L (the K and V rows).
 Copy: a plain 256 MiB device-to-device hipMemcpy, the practical HBM rate
 (bytes = read + written) and the calibration workload of the FETCH_SIZE /
 WRITE_SIZE counters.
+GEMM (the prefill's BF16 MFMA GEMM at the 3B-class linears for a 2048-row
+prompt chunk) and prefill (the whole matrix-core prefill of 2048- and
+24000-token prompts through the 3B-class model, random-init weights),
+against the 2.5 PFLOP/s dense BF16 matrix peak.
 
 Every timed launch reads another copy of its operands (more than 512 MB in
 total), so the 256 MB Infinity Cache cannot serve repeats.  One JSON line per
 case on stdout.
 
-    python -m yue2_rs_amd.microbench [gemv|attention|copy|all]
+    python -m yue2_rs_amd.microbench [gemv|attention|copy|gemm|prefill|all]
 """
 from __future__ import annotations
 
@@ -26,6 +30,8 @@ import sys
 from .api import _check, available, lib
 
 HBM_PEAK = 8.0e12
+MFMA_BF16_PEAK = 2.5e15
+GEMM_SHAPES = [("qkv", 5120, 3072, 0), ("o", 3072, 3072, 0), ("gate_up", 8192, 3072, 1), ("down", 3072, 8192, 0)]
 GEMV_SHAPES = [("qkv", 5120, 3072), ("o", 3072, 3072), ("gate_up", 16384, 3072), ("down", 3072, 8192),
                ("lm_head", 84000, 3072)]
 CONTEXTS = [1024, 4096, 16384, 24576]
@@ -56,6 +62,42 @@ def copy(nbytes: int = 256 * 2**20, iters: int = 20) -> dict:
             "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
 
 
+def gemm(m: int, n: int, k: int, pair: int, iters: int = 50) -> dict:
+    ms, fl = C.c_float(0), C.c_double(0)
+    _check(lib().yue2_hip_bench_gemm(m, n, k, pair, iters, C.byref(ms), C.byref(fl)))
+    tf = fl.value / (ms.value * 1e-3) / 1e12
+    return {"m": m, "n": n, "k": k, "pair": pair, "launch_us": round(ms.value * 1e3, 2), "flops": fl.value,
+            "TFLOP_s": round(tf, 1), "frac": round(tf * 1e12 / MFMA_BF16_PEAK, 4)}
+
+
+def prefill(tokens) -> list:
+    """The matrix-core prefill of each prompt length through the 3B-class
+    model (seed-0 weights and prompt), the second of two runs timed."""
+    import time
+    from . import synthetic
+    from .api import Model, synchronize
+    c = synthetic.CLASS_3B
+    model = Model.open(synthetic.checkpoint(c, seed=0, threads=16))
+    out = []
+    for n in tokens:
+        ids = synthetic.prompt(n, c.vocab_size, seed=0)
+        for _ in range(2):
+            synchronize()
+            t = time.perf_counter()
+            cache, _ = model.prefill_mfma(ids, n)
+            synchronize()
+            dt = time.perf_counter() - t
+            cache.close()
+        H, D, I, V = c.hidden_size, c.head_dim, c.intermediate_size, c.vocab_size
+        q, kv = c.num_attention_heads * D, c.num_key_value_heads * D
+        fl = (2.0 * n * c.num_hidden_layers * (H * (q + 2 * kv) + q * H + 3 * H * I) +
+              c.num_hidden_layers * c.num_attention_heads * 4.0 * D * n * (n + 1) / 2.0 + 2.0 * V * H)
+        out.append({"tokens": n, "s": round(dt, 4), "tokens_per_s": round(n / dt, 1), "flops": fl,
+                    "TFLOP_s": round(fl / dt / 1e12, 1), "frac": round(fl / dt / MFMA_BF16_PEAK, 4)})
+    model.close()
+    return out
+
+
 def main(argv=None) -> int:
     what = (argv or sys.argv[1:] or ["all"])[0]
     if not available():
@@ -71,6 +113,12 @@ def main(argv=None) -> int:
                 print(json.dumps({"bench": "attention", **attention(L, rows)}), flush=True)
     if what in ("copy", "all"):
         print(json.dumps({"bench": "copy", **copy()}), flush=True)
+    if what in ("gemm", "all"):
+        for name, n, k, pair in GEMM_SHAPES:
+            print(json.dumps({"bench": "gemm", "shape": name, **gemm(2048, n, k, pair)}), flush=True)
+    if what in ("prefill", "all"):
+        for r in prefill([2048, 24000]):
+            print(json.dumps({"bench": "prefill", **r}), flush=True)
     return 0
 
 

@@ -213,6 +213,43 @@ int32_t yue2_hip_prefill(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t
 int32_t yue2_hip_prefill_mfma(Yue2Model *m, Yue2Cache *c, const int32_t *ids, int32_t n,
                               int32_t phase, float *logits);
 
+/* The NAR (acoustic) pathway's host weights (Model::open, src/model.rs:
+ * 418-451; Layer::load nar_*, :264-269): per layer the AR layer's tensor set
+ * (nar_input_layernorm, nar_self_attn.{q,k,v,o}_proj and {q,k}_norm,
+ * nar_pre_mlp_layernorm, nar_mlp.*); the linears with biases, BF16 matrices
+ * [out, in] and f32 biases (rounded to BF16 where used, Linear::finish):
+ * vae2llm [hidden x latent], llm2vae [latent x hidden], time_embedder.mlp.0
+ * [hidden x 256], time_embedder.mlp.2 [hidden x hidden]; latent_pos_embed.pe
+ * [max_latent_frames x hidden] BF16; Config's latent_dim (a multiple of 64
+ * here), max_latent_frames and timestep_shift (src/model.rs:45-47). */
+typedef struct Yue2NarWeights {
+    int32_t latent_dim, max_latent_frames;
+    float timestep_shift;
+    const uint16_t *vae2llm, *llm2vae, *time_in, *time_out, *latent_pos;
+    const float *vae2llm_bias, *llm2vae_bias, *time_in_bias, *time_out_bias;
+    const Yue2LayerWeights *layers; /* num_hidden_layers entries */
+} Yue2NarWeights;
+
+/* Uploads the NAR pathway next to the model's AR weights (replacing any
+ * earlier one).  Returns 0 or a negative Yue2Error. */
+int32_t yue2_hip_nar_load(Yue2Model *m, const Yue2NarWeights *w);
+
+/* Model::velocity (src/model.rs:611-698) on the matrix cores (the stack the
+ * reference hands to yue2_metal_stack, src/metal.m:429-538): `frames` latent
+ * rows state [frames x latent] (BF16-exact values, as the flow-matching loop
+ * keeps them) padded with a zero row on each side, vae2llm, the timestep
+ * embedding of raw_t and the latent position rows, the NAR layers with
+ * non-causal attention over the cache's first min(nar_cond_end, length)
+ * positions (all when nar_cond_end is 0) and the rows' own keys (RoPE from
+ * the cache length; the cache is not modified), the final norm and llm2vae:
+ * out [frames x latent] f32.  The linears are BF16 MFMA GEMMs, so the result
+ * agrees with the CPU restatement within a tolerance (as the reference's GPU
+ * stack does with its CPU path), not bit for bit.  Needs cache length +
+ * frames + 2 <= max_position_embeddings.  Returns 0 or a negative
+ * Yue2Error. */
+int32_t yue2_hip_velocity(Yue2Model *m, const Yue2Cache *c, const float *state, int32_t frames, double raw_t,
+                          int32_t nar_cond_end, float *out);
+
 /* A decode loop bound to one cache (batch 1) or to a conditional and an
  * unconditional cache (CFG batch 2).  Each step is one hipGraph launch:
  * embed -> layers -> LM head -> CFG mix -> choose -> next id.  The caches

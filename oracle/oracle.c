@@ -487,6 +487,124 @@ int y2o_prefill(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,
 /* MT19937 (src/sampling.rs:10-63)                                          */
 /* ------------------------------------------------------------------------ */
 
+/* ------------------------------------------------------------------------ */
+/* NAR velocity (src/model.rs:611-698)                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Linear::apply + finish with a bias (src/tensor.rs:1101-1117):
+ * y = rb(DOT(W[i], x[r]) + rb(b[i])). */
+static void linear_bias(const uint16_t *w, const float *b, int out, int in, const float *x, int rows,
+                        float *y) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int i = 0; i < out; ++i) {
+        const uint16_t *wi = w + (size_t)i * in;
+        float bi = rb(b[i]);
+        for (int r = 0; r < rows; ++r) y[(size_t)r * out + i] = rb(y2o_dot_bf16(wi, x + (size_t)r * in, in) + bi);
+    }
+}
+
+int y2o_velocity(const y2o_model *m, const y2o_nar *nar, const y2o_cache *cache, const float *state,
+                 int frames, double raw_t, int nar_cond_end, float *out) {
+    const y2o_config *c = &m->c;
+    if (frames <= 0 || cache->layers != c->layers) return Y2O_ERR_CONTEXT;
+    const int n = frames + 2, H = c->hidden, L = nar->latent, d = c->head_dim;
+    const int qw = c->heads * d, kw = c->kv_heads * d, I = c->intermediate;
+    const int visible = nar_cond_end > 0 ? (nar_cond_end < cache->length ? nar_cond_end : cache->length)
+                                         : cache->length;
+    const int keys = visible + n;
+    float *pad = (float *)calloc((size_t)n * L, sizeof(float));
+    float *x = (float *)malloc(sizeof(float) * (size_t)n * H);
+    float *h = (float *)malloc(sizeof(float) * (size_t)n * H);
+    float *q = (float *)malloc(sizeof(float) * (size_t)n * qw);
+    float *k = (float *)malloc(sizeof(float) * (size_t)n * kw);
+    float *v = (float *)malloc(sizeof(float) * (size_t)n * kw);
+    float *att = (float *)malloc(sizeof(float) * (size_t)n * qw);
+    float *g = (float *)malloc(sizeof(float) * (size_t)n * I);
+    float *u = (float *)malloc(sizeof(float) * (size_t)n * I);
+    float *kk = (float *)malloc(sizeof(float) * (size_t)keys * kw);
+    float *vv = (float *)malloc(sizeof(float) * (size_t)keys * kw);
+    float *cs = (float *)malloc(sizeof(float) * (size_t)n * (d / 2));
+    float *sn = (float *)malloc(sizeof(float) * (size_t)n * (d / 2));
+    float *t0 = (float *)malloc(sizeof(float) * (size_t)H);
+    float *t1 = (float *)malloc(sizeof(float) * (size_t)H);
+    int rc = Y2O_OK;
+    if (!pad || !x || !h || !q || !k || !v || !att || !g || !u || !kk || !vv || !cs || !sn || !t0 || !t1) {
+        rc = Y2O_ERR_ALLOC;
+        goto done;
+    }
+    /* padded latents: zero first and last rows (:620-622), vae2llm (:623) */
+    memcpy(pad + L, state, sizeof(float) * (size_t)frames * L);
+    linear_bias(nar->vae2llm, nar->vae2llm_b, H, L, pad, n, x);
+    /* timestep (:624-628) */
+    {
+        const float raw = rb((float)raw_t);
+        const float sig = rb(1.0f / (1.0f + y2o_expf(-raw)));
+        const float top = rb(nar->shift * sig);
+        const float bottom = rb(1.0f + rb((nar->shift - 1.0f) * sig));
+        const float t = rb(top / bottom);
+        float sinus[256];
+        for (int i = 0; i < 128; ++i) {
+            const float f = y2o_expf(-logf(10000.0f) * (float)i / 128.0f);
+            sinus[i] = rb(cosf(t * f));
+            sinus[128 + i] = rb(sinf(t * f));
+        }
+        /* time_in, rb(silu), time_out (:635-639) */
+        linear_bias(nar->time_in, nar->time_in_b, H, 256, sinus, 1, t0);
+        for (int i = 0; i < H; ++i) t0[i] = rb(t0[i] / (1.0f + y2o_expf(-t0[i])));
+        linear_bias(nar->time_out, nar->time_out_b, H, H, t0, 1, t1);
+    }
+    /* time and latent position rows (:640-649) */
+    for (int r = 0; r < n; ++r) {
+        const int pr = r < nar->max_frames - 1 ? r : nar->max_frames - 1;
+        for (int i = 0; i < H; ++i) {
+            const float pe = rb(y2o_bf16_to_f32(nar->latent_pos[(size_t)pr * H + i]));
+            float *xv = x + (size_t)r * H + i;
+            *xv = rb(rb(*xv + t1[i]) + pe);
+        }
+    }
+    /* NAR layers (:680-695), RoPE from the cache length (src/model.rs:741) */
+    y2o_rotary_table(cache->length, n, d, c->theta, cs, sn);
+    for (int l = 0; l < c->layers; ++l) {
+        const y2o_layer *P = &nar->layers[l];
+        y2o_norm_apply(x, n, H, P->input_norm, c->eps, h);
+        y2o_linear(P->q, qw, H, h, n, q);
+        y2o_linear(P->k, kw, H, h, n, k);
+        y2o_linear(P->v, kw, H, h, n, v);
+        y2o_norm_heads(q, n * c->heads, d, P->q_norm, c->eps);
+        y2o_norm_heads(k, n * c->kv_heads, d, P->k_norm, c->eps);
+        y2o_rotary_apply(q, n, qw, d / 2, cs, sn);
+        y2o_rotary_apply(k, n, kw, d / 2, cs, sn);
+        const float *kc = cache->key + (size_t)l * cache->capacity * kw;
+        const float *vc = cache->value + (size_t)l * cache->capacity * kw;
+        memcpy(kk, kc, sizeof(float) * (size_t)visible * kw);
+        memcpy(vv, vc, sizeof(float) * (size_t)visible * kw);
+        memcpy(kk + (size_t)visible * kw, k, sizeof(float) * (size_t)n * kw);
+        memcpy(vv + (size_t)visible * kw, v, sizeof(float) * (size_t)n * kw);
+        /* attention(q, key, value, c, None, None): every row sees every key */
+        for (int r = 0; r < n; ++r)
+            y2o_attention_row(q + (size_t)r * qw, kk, vv, keys, c->heads, c->kv_heads, d, att + (size_t)r * qw);
+        y2o_linear(P->o, H, qw, att, n, h);
+        for (size_t i = 0; i < (size_t)n * H; ++i) x[i] = rb(x[i] + h[i]);
+        y2o_norm_apply(x, n, H, P->post_norm, c->eps, h);
+        y2o_linear(P->gate, I, H, h, n, g);
+        y2o_linear(P->up, I, H, h, n, u);
+        for (size_t i = 0; i < (size_t)n * I; ++i) {
+            float gv = g[i];
+            gv = rb(gv / (1.0f + y2o_expf(-gv)));
+            g[i] = rb(gv * u[i]);
+        }
+        y2o_linear(P->down, H, I, g, n, h);
+        for (size_t i = 0; i < (size_t)n * H; ++i) x[i] = rb(x[i] + h[i]);
+    }
+    /* llm2vae(final_norm(x)[1 .. n-1]) (:696-697) */
+    y2o_norm_apply(x + H, frames, H, m->final_norm, c->eps, h);
+    linear_bias(nar->llm2vae, nar->llm2vae_b, L, H, h, frames, out);
+done:
+    free(pad); free(x); free(h); free(q); free(k); free(v); free(att); free(g); free(u);
+    free(kk); free(vv); free(cs); free(sn); free(t0); free(t1);
+    return rc;
+}
+
 void y2o_mt_seed(y2o_mt *g, uint64_t seed) {
     g->state[0] = (uint32_t)seed;
     for (int i = 1; i < 624; ++i)

@@ -69,6 +69,14 @@
  *                    greedy ids, 32 sampled CFG ids) written by
  *                    tests/golden/make_golden.py; chunked prefill equals the
  *                    token-by-token step (the GPU tests run both).
+ *   y2o_velocity    linear biases, the timestep embedding and the position
+ *                    rows from closed forms on a model whose NAR linears and
+ *                    layers are zero (tests/test_oracle_nar.py); with
+ *                    non-causal attention, a row's output does not depend on
+ *                    the order of the other rows' keys only through their
+ *                    set -- permuting the frames permutes the outputs when
+ *                    no position-dependent term enters (RoPE start, latent
+ *                    position rows equal); parity unpinned beyond these.
  *   Accelerate's exact summation order, macOS libm cos/sin/powf and the real
  *   checkpoint's logits cannot be run here: parity with those is unpinned
  *   beyond the checks above.
@@ -183,6 +191,27 @@ int y2o_forward_phase(const y2o_model *m, y2o_cache *cache, const int32_t *ids, 
 int y2o_project_phase(const y2o_model *m, const float *x, int phase, float *logits);
 /* Model::prefill (src/model.rs:592-610): 256-token chunks, logits of the last row. */
 int y2o_prefill(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *logits);
+
+/* The NAR (acoustic) pathway (Model::open, src/model.rs:418-451; Layer::load
+ * nar_*, :264-269): NAR layers with the AR layer's tensors, the linears with
+ * biases (vae2llm [H, latent], llm2vae [latent, H], time_embedder.mlp.0
+ * [H, 256], time_embedder.mlp.2 [H, H]; biases f32, BF16-rounded where used
+ * as Linear::finish does) and latent_pos_embed.pe [max_frames, H] BF16. */
+typedef struct {
+    int32_t latent, max_frames;
+    float shift;
+    const uint16_t *vae2llm, *llm2vae, *time_in, *time_out, *latent_pos;
+    const float *vae2llm_b, *llm2vae_b, *time_in_b, *time_out_b;
+    const y2o_layer *layers;
+} y2o_nar;
+
+/* Model::velocity (src/model.rs:611-698) for `frames` latent rows (state
+ * [frames, latent]) against the AR cache: out [frames, latent].  The keys
+ * are the cache's first min(nar_cond_end, length) positions (all when
+ * nar_cond_end is 0) followed by the rows' own; RoPE positions start at the
+ * cache length; the cache is not modified. */
+int y2o_velocity(const y2o_model *m, const y2o_nar *nar, const y2o_cache *cache, const float *state,
+                 int frames, double raw_t, int nar_cond_end, float *out);
 
 void y2o_mt_seed(y2o_mt *g, uint64_t seed);
 uint32_t y2o_mt_next(y2o_mt *g);

@@ -35,6 +35,13 @@ class Layer(C.Structure):
         "q", "k", "v", "o", "gate", "up", "down", "input_norm", "q_norm", "k_norm", "post_norm")]
 
 
+class NarS(C.Structure):
+    _fields_ = [("latent", C.c_int32), ("max_frames", C.c_int32), ("shift", C.c_float)] + [
+        (n, C.c_void_p) for n in ("vae2llm", "llm2vae", "time_in", "time_out", "latent_pos",
+                                  "vae2llm_b", "llm2vae_b", "time_in_b", "time_out_b")] + [
+        ("layers", C.POINTER(Layer))]
+
+
 class ModelS(C.Structure):
     _fields_ = [("c", Config), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
                 ("final_norm", C.c_void_p), ("layers", C.POINTER(Layer))]
@@ -88,6 +95,7 @@ def lib() -> C.CDLL:
             "y2o_forward": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_forward_phase": (i32, [vp, C.POINTER(CacheS), vp, i32, i32, vp]),
             "y2o_prefill": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
+            "y2o_velocity": (i32, [vp, vp, C.POINTER(CacheS), vp, i32, f64, i32, vp]),
             "y2o_mt_seed": (None, [vp, C.c_uint64]),
             "y2o_mt_next": (C.c_uint32, [vp]),
             "y2o_mt_discard": (None, [vp, C.c_uint64]),
@@ -161,6 +169,35 @@ class Model:
             if rc:
                 raise RuntimeError(f"oracle error {rc}")
         return cache, out
+
+
+class Nar:
+    """Oracle NAR pathway over the same host arrays (a NarWeights) as the GPU's."""
+
+    def __init__(self, model: Model, w):
+        self.model, self.w = model, w
+        n = len(w.layers)
+        self._layers = (Layer * n)()
+        for i, lw in enumerate(w.layers):
+            L = self._layers[i]
+            L.q, L.k, L.v, L.o = _p(lw.q_proj), _p(lw.k_proj), _p(lw.v_proj), _p(lw.o_proj)
+            L.gate, L.up, L.down = _p(lw.gate_proj), _p(lw.up_proj), _p(lw.down_proj)
+            L.input_norm, L.q_norm = _p(lw.input_layernorm), _p(lw.q_norm)
+            L.k_norm, L.post_norm = _p(lw.k_norm), _p(lw.post_attention_layernorm)
+        self._n = NarS(w.latent_dim, w.max_latent_frames, w.timestep_shift,
+                       _p(w.vae2llm), _p(w.llm2vae), _p(w.time_in), _p(w.time_out), _p(w.latent_pos),
+                       _p(w.vae2llm_bias), _p(w.llm2vae_bias), _p(w.time_in_bias), _p(w.time_out_bias),
+                       self._layers)
+
+    def velocity(self, state: np.ndarray, cache: "Cache", raw_t: float, nar_cond_end: int = 0) -> np.ndarray:
+        """Model::velocity (src/model.rs:611-698): state [frames, latent]."""
+        st = np.ascontiguousarray(state, dtype=np.float32)
+        out = np.empty_like(st)
+        rc = lib().y2o_velocity(self.model.ref, C.byref(self._n), cache.ptr, _p(st), st.shape[0], raw_t,
+                                nar_cond_end, _p(out))
+        if rc:
+            raise RuntimeError(f"oracle error {rc}")
+        return out
 
 
 class Cache:

@@ -55,6 +55,13 @@ class _LayerWeights(C.Structure):
         "input_layernorm", "q_norm", "k_norm", "post_attention_layernorm")]
 
 
+class _NarWeights(C.Structure):
+    _fields_ = [("latent_dim", C.c_int32), ("max_latent_frames", C.c_int32), ("timestep_shift", C.c_float)] + [
+        (n, C.c_void_p) for n in ("vae2llm", "llm2vae", "time_in", "time_out", "latent_pos", "vae2llm_bias",
+                                  "llm2vae_bias", "time_in_bias", "time_out_bias")] + [
+        ("layers", C.POINTER(_LayerWeights))]
+
+
 class _Sampling(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_int32),
                 ("repetition_penalty", C.c_float), ("penalty_window", C.c_int32),
@@ -107,6 +114,8 @@ def lib() -> C.CDLL:
         "yue2_hip_forward": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_prefill": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_prefill_mfma": (i32, [vp, vp, vp, i32, i32, vp]),
+        "yue2_hip_nar_load": (i32, [vp, vp]),
+        "yue2_hip_velocity": (i32, [vp, vp, vp, i32, C.c_double, i32, vp]),
         "yue2_hip_selftest_gemm": (i32, [vp, vp, vp, i32, i32, i32]),
         "yue2_hip_decoder_new": (vp, [vp, vp, vp, vp, u64, i32, f32, i32]),
         "yue2_hip_decoder_free": (None, [vp]),
@@ -222,6 +231,28 @@ class LayerWeights:
 
 
 @dataclass
+class NarWeights:
+    """Host weights of the NAR (acoustic) pathway (Model::open,
+    src/model.rs:418-451): per layer the AR layer's tensor set, the linears
+    vae2llm [H, latent], llm2vae [latent, H], time_embedder.mlp.0 [H, 256]
+    and .2 [H, H] as uint16 BF16 arrays with float32 biases, and
+    latent_pos_embed.pe [max_latent_frames, H] as uint16 BF16."""
+    latent_dim: int
+    max_latent_frames: int
+    timestep_shift: float
+    vae2llm: np.ndarray
+    vae2llm_bias: np.ndarray
+    llm2vae: np.ndarray
+    llm2vae_bias: np.ndarray
+    time_in: np.ndarray
+    time_in_bias: np.ndarray
+    time_out: np.ndarray
+    time_out_bias: np.ndarray
+    latent_pos: np.ndarray
+    layers: list = field(default_factory=list)
+
+
+@dataclass
 class Checkpoint:
     """Host weights of one AR model: BF16 matrices as uint16 arrays [out, in],
     norm gammas as float32 arrays."""
@@ -305,6 +336,26 @@ class Model:
         out = np.empty(self.config.vocab_size, dtype=np.float32)
         _check(lib().yue2_hip_prefill_mfma(self._h, cache._h, _ptr(arr), len(arr), phase, _ptr(out)))
         return cache, out
+
+    def load_nar(self, w: "NarWeights") -> None:
+        """Upload the NAR pathway (its host arrays stay referenced by the model)."""
+        layers = (_LayerWeights * len(w.layers))()
+        for i, lw in enumerate(w.layers):
+            for f, _ in _LayerWeights._fields_:
+                setattr(layers[i], f, _ptr(getattr(lw, f)))
+        s = _NarWeights(w.latent_dim, w.max_latent_frames, w.timestep_shift, _ptr(w.vae2llm), _ptr(w.llm2vae),
+                        _ptr(w.time_in), _ptr(w.time_out), _ptr(w.latent_pos), _ptr(w.vae2llm_bias),
+                        _ptr(w.llm2vae_bias), _ptr(w.time_in_bias), _ptr(w.time_out_bias), layers)
+        _check(lib().yue2_hip_nar_load(self._h, C.byref(s)))
+        self._nar = w
+
+    def velocity(self, state: np.ndarray, cache: "Cache", raw_t: float, nar_cond_end: int = 0) -> np.ndarray:
+        """Model::velocity (src/model.rs:611-698): state [frames, latent] ->
+        [frames, latent], on the matrix cores."""
+        st = np.ascontiguousarray(state, dtype=np.float32)
+        out = np.empty_like(st)
+        _check(lib().yue2_hip_velocity(self._h, cache._h, _ptr(st), st.shape[0], raw_t, nar_cond_end, _ptr(out)))
+        return out
 
     def set_step_kernel(self, on: bool) -> bool:
         """Use the persistent token-step kernel for decode steps; returns

@@ -29,6 +29,7 @@
 #include "dev_mem.h"
 #include "dev_mfma.h"
 #include "kernels.h"
+#include "prefill.h"
 #include "runtime.h"
 #include "y2_math.h"
 
@@ -38,26 +39,7 @@ namespace y2 {
 
 // ---- GEMM: C = X W^T, X [M, K] BF16, W [N, K] BF16, FP32 accumulation ------
 
-enum GemmEpi {
-    GEPI_RAW = 0,         // c (f32) = the accumulation
-    GEPI_ROUND = 1,       // c (f32) = rb(acc)
-    GEPI_RESID = 2,       // c (f32) = rb(c + rb(acc))  (residual stream, in place)
-    GEPI_SWIGLU_BF16 = 3  // cb (BF16) = rb(rb(silu(rb(gate))) * rb(up)); w = gate rows, w2 = up rows
-};
-
-struct GemmArgs {
-    const uint16_t* x;
-    int ldx;
-    const uint16_t* w;
-    const uint16_t* w2;
-    int ldw;
-    float* c;
-    uint16_t* cb;
-    int ldc;
-    int M, N, K;
-};
-
-constexpr int kGemmTM = 128, kGemmTK = 64, kGemmPad = 8;
+constexpr int kGemmTM = 128, kGemmPad = 8;
 constexpr int kGemmThreads = 256;
 
 // One workgroup computes a 128-row tile of C: 128 columns (64 for the
@@ -164,11 +146,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
                 for (int j = 0; j < 2; ++j) {
                     const int col = n0 + wn * 64 + j * 32 + acc32_col(lane);
                     if (col >= g.N) continue;
-                    float* c = g.c + (size_t)row * g.ldc + col;
+                    const size_t at = (size_t)row * g.ldc + col;
                     const float v = acc[i][j][r];
-                    if constexpr (EPI == GEPI_RAW) *c = v;
-                    else if constexpr (EPI == GEPI_ROUND) *c = rb(v);
-                    else *c = rb(*c + rb(v));
+                    if constexpr (EPI == GEPI_RAW) g.c[at] = v;
+                    else if constexpr (EPI == GEPI_ROUND) g.c[at] = rb(v);
+                    else if constexpr (EPI == GEPI_RESID) g.c[at] = rb(g.c[at] + rb(v));
+                    else if constexpr (EPI == GEPI_BIAS) g.c[at] = rb(v + g.bias[col]);
+                    else g.cb[at] = bf16_bits(silu_rb(rb(v + g.bias[col])));
                 }
             }
         }
@@ -177,6 +161,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
 
 hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& g) {
     if (g.K % kGemmTK || g.ldx % 8 || g.ldw % 8 || g.M < 1 || g.N < 1) return hipErrorInvalidValue;
+    if ((epi == GEPI_BIAS || epi == GEPI_BIAS_SILU_BF16) && !g.bias) return hipErrorInvalidValue;
     const int tn = epi == GEPI_SWIGLU_BF16 ? 64 : 128;
     const dim3 grid((g.N + tn - 1) / tn, (g.M + kGemmTM - 1) / kGemmTM);
     switch (epi) {
@@ -184,6 +169,8 @@ hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& g) {
         case GEPI_ROUND: gemm_kernel<GEPI_ROUND><<<grid, kGemmThreads, 0, s>>>(g); break;
         case GEPI_RESID: gemm_kernel<GEPI_RESID><<<grid, kGemmThreads, 0, s>>>(g); break;
         case GEPI_SWIGLU_BF16: gemm_kernel<GEPI_SWIGLU_BF16><<<grid, kGemmThreads, 0, s>>>(g); break;
+        case GEPI_BIAS: gemm_kernel<GEPI_BIAS><<<grid, kGemmThreads, 0, s>>>(g); break;
+        case GEPI_BIAS_SILU_BF16: gemm_kernel<GEPI_BIAS_SILU_BF16><<<grid, kGemmThreads, 0, s>>>(g); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -217,25 +204,18 @@ __global__ __launch_bounds__(kRowThreads) void norm_rows_kernel(const float* x, 
 
 // Per (row r, head): the per-head RMSNorm of q and k (Norm::heads,
 // src/tensor.rs:1158-1172) and rotate-half RoPE at position p0 + r
-// (src/model.rs:151-168): q heads into q (BF16 [rows][heads][D]), k heads
-// into the cache, and the v heads copied into the cache.  One wave per head.
-struct RopeArgs {
-    const float* qkv;  // [rows][(heads + 2 kv) D], rb'd GEMM outputs
-    uint16_t* q;
-    uint16_t* kv_base;
-    int cap, layer, heads, kv_heads, D, p0;
-    const float *q_norm, *k_norm, *cos_t, *sin_t;
-    float eps;
-};
-
+// (src/model.rs:151-168): q heads into q, k heads to their slot, and the v
+// heads copied to theirs.  One wave per head.
 __global__ __launch_bounds__(64) void rope_append_kernel(const RopeArgs a) {
     const int r = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, D = a.D, half = D / 2;
     const int qkvw = (a.heads + 2 * a.kv_heads) * D;
     const float* v = a.qkv + (size_t)r * qkvw + (size_t)h * D;
     const int pos = a.p0 + r;
-    if (h >= a.heads + a.kv_heads) {  // a value head: to the cache as is
+    uint16_t* kvb = a.kv_out ? a.kv_out : a.kv_base;
+    const int slot = a.kv_out ? a.slot0 + r : pos, cap = a.kv_out ? a.cap_out : a.cap;
+    if (h >= a.heads + a.kv_heads) {  // a value head: to its slot as is
         const int g = h - a.heads - a.kv_heads;
-        uint16_t* dst = a.kv_base + ((((size_t)a.layer * 2 + 1) * a.kv_heads + g) * a.cap + pos) * D;
+        uint16_t* dst = kvb + ((((size_t)a.layer * 2 + 1) * a.kv_heads + g) * cap + slot) * D;
         for (int d = lane; d < D; d += 64) dst[d] = bf16_bits(v[d]);
         return;
     }
@@ -245,7 +225,7 @@ __global__ __launch_bounds__(64) void rope_append_kernel(const RopeArgs a) {
     const float* ct = a.cos_t + (size_t)pos * half;
     const float* st = a.sin_t + (size_t)pos * half;
     uint16_t* dst = is_q ? a.q + ((size_t)r * a.heads + h) * D
-                         : a.kv_base + ((((size_t)a.layer * 2) * a.kv_heads + (h - a.heads)) * a.cap + pos) * D;
+                         : kvb + ((((size_t)a.layer * 2) * a.kv_heads + (h - a.heads)) * cap + slot) * D;
     for (int d = lane; d < half; d += 64) {
         const float x0 = rb(rb(v[d] * s) * gam[d]);
         const float x1 = rb(rb(v[d + half] * s) * gam[d + half]);
@@ -256,14 +236,6 @@ __global__ __launch_bounds__(64) void rope_append_kernel(const RopeArgs a) {
 }
 
 // ---- causal flash attention over the BF16 cache --------------------------
-
-struct FlashArgs {
-    const uint16_t* q;  // [rows][heads][D] BF16
-    const uint16_t* kv_base;
-    int cap, layer, heads, kv_heads, p0, rows;
-    float scale;
-    uint16_t* out;  // [rows][heads D] BF16 (rb of the attention output)
-};
 
 // One workgroup per (query head h, kFlashRows = 128 query rows); wave w
 // takes 16 of them.  Keys in tiles of 64: S = Q K^T on 16x16x32 MFMAs (K
@@ -288,15 +260,21 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const Flas
     const int qrow = q0 + wave * 16 + (lane & 15);  // the query row this lane loads for A
     const uint16_t* Kc = f.kv_base + (((size_t)f.layer * 2) * f.kv_heads + g) * (size_t)f.cap * D;
     const uint16_t* Vc = f.kv_base + (((size_t)f.layer * 2 + 1) * f.kv_heads + g) * (size_t)f.cap * D;
+    // the second key source (non-causal): keys from split on
+    const uint16_t* K2 = f.kv2 ? f.kv2 + (((size_t)f.layer * 2) * f.kv_heads + g) * (size_t)f.cap2 * D : Kc;
+    const uint16_t* V2 = f.kv2 ? f.kv2 + (((size_t)f.layer * 2 + 1) * f.kv_heads + g) * (size_t)f.cap2 * D : Vc;
+    const int split = f.kv2 ? f.split : 0x7fffffff;
     uint4 qa[D / 32];
 #pragma unroll
     for (int dk = 0; dk < D / 32; ++dk)
         qa[dk] = qrow < f.rows ? ldg4(f.q + ((size_t)qrow * f.heads + h) * D + dk * 32 + 8 * (lane >> 4))
                                : make_uint4(0, 0, 0, 0);
     // this lane's accumulator rows: 4 (lane / 16) + r of the wave's 16
+    // the last key each row sees (non-causal: every key)
+    const int all_keys = f.noncausal ? f.split + f.rows - 1 : 0;
     int qpos[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) qpos[r] = f.p0 + q0 + wave * 16 + 4 * (lane >> 4) + r;
+    for (int r = 0; r < 4; ++r) qpos[r] = f.noncausal ? all_keys : f.p0 + q0 + wave * 16 + 4 * (lane >> 4) + r;
     float m[4], l[4];
     f32x4 o[D / 16];
 #pragma unroll
@@ -308,7 +286,7 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const Flas
     for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) o[dt][r] = 0.0f;
-    const int last_key = min(f.p0 + q0 + kFlashRows - 1, f.p0 + f.rows - 1);  // keys [0, last_key]
+    const int last_key = f.noncausal ? all_keys : min(f.p0 + q0 + kFlashRows - 1, f.p0 + f.rows - 1);  // keys [0, last_key]
     const int tiles = last_key / KT + 1;
     // tile loads: K as uint4 of rows (key u / (D/8), dims 8 (u % (D/8)));
     // V as key pairs (keys 2 (v % 32) and + 1, dims 8 (v / 32)); keys past
@@ -319,14 +297,17 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const Flas
 #pragma unroll
         for (int i = 0; i < KU; ++i) {
             const int u = tid + i * kFlashThreads, kg = kb + u / (D / 8);
-            kr[i] = u < KN && kg <= last_key ? ldg4(Kc + (size_t)kg * D + (u % (D / 8)) * 8) : make_uint4(0, 0, 0, 0);
+            const uint16_t* kp = kg < split ? Kc + (size_t)kg * D : K2 + (size_t)(kg - split) * D;
+            kr[i] = u < KN && kg <= last_key ? ldg4(kp + (u % (D / 8)) * 8) : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < VU; ++i) {
             const int v = tid + i * kFlashThreads, kg = kb + 2 * (v % (KT / 2)), d8 = (v / (KT / 2)) * 8;
             const bool in = v < VN;
-            vr[i][0] = in && kg <= last_key ? ldg4(Vc + (size_t)kg * D + d8) : make_uint4(0, 0, 0, 0);
-            vr[i][1] = in && kg + 1 <= last_key ? ldg4(Vc + (size_t)(kg + 1) * D + d8) : make_uint4(0, 0, 0, 0);
+            const uint16_t* v0 = kg < split ? Vc + (size_t)kg * D : V2 + (size_t)(kg - split) * D;
+            const uint16_t* v1 = kg + 1 < split ? Vc + (size_t)(kg + 1) * D : V2 + (size_t)(kg + 1 - split) * D;
+            vr[i][0] = in && kg <= last_key ? ldg4(v0 + d8) : make_uint4(0, 0, 0, 0);
+            vr[i][1] = in && kg + 1 <= last_key ? ldg4(v1 + d8) : make_uint4(0, 0, 0, 0);
         }
     };
     load_tile(0);
@@ -436,6 +417,28 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const Flas
     }
 }
 
+hipError_t launch_norm_rows(hipStream_t s, const float* x, const float* gamma, uint16_t* out, int rows, int H,
+                            float eps) {
+    if (rows < 1) return hipSuccess;
+    norm_rows_kernel<<<rows, kRowThreads, sizeof(float) * H, s>>>(x, gamma, out, H, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_append(hipStream_t s, const RopeArgs& a, int rows) {
+    if (rows < 1) return hipSuccess;
+    rope_append_kernel<<<dim3(rows, a.heads + 2 * a.kv_heads), 64, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_flash(hipStream_t s, const FlashArgs& f, int head_dim) {
+    if (f.rows < 1) return hipSuccess;
+    const dim3 grid(f.heads, (f.rows + kFlashRows - 1) / kFlashRows);
+    if (head_dim == 128) flash_prefill_kernel<128><<<grid, kFlashThreads, 0, s>>>(f);
+    else if (head_dim == 64) flash_prefill_kernel<64><<<grid, kFlashThreads, 0, s>>>(f);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 }  // namespace y2
 
 // ---------------------------------------------------------------------------
@@ -486,27 +489,25 @@ int run_prefill(Yue2Model* m, Yue2Cache* c, const int32_t* ids, int n, int phase
     e = hipMemcpyAsync(b.ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return hip_fail(e, "prefill ids upload");
     const float eps = cf.rms_norm_eps;
-    const size_t norm_lds = sizeof(float) * H;
     for (int p0 = 0; p0 < n; p0 += R) {
         const int rows = std::min(R, n - p0);
         embed_rows_kernel<<<rows, kRowThreads, 0, s>>>(m->embed, b.ids + p0, b.x, H);
         for (int l = 0; l < cf.num_hidden_layers; ++l) {
             const LayerDev& L = m->layers[l];
-            norm_rows_kernel<<<rows, kRowThreads, norm_lds, s>>>(b.x, L.in_norm, b.h, H, eps);
+            if ((e = launch_norm_rows(s, b.x, L.in_norm, b.h, rows, H, eps)) != hipSuccess)
+                return hip_fail(e, "prefill norm");
             GemmArgs g{b.h, H, L.wqkv, nullptr, H, b.qkv, nullptr, qkvw, rows, qkvw, H};
             if ((e = launch_gemm(s, GEPI_ROUND, g)) != hipSuccess) return hip_fail(e, "prefill qkv gemm");
             RopeArgs ra{b.qkv, b.q, c->kv, c->capacity, l, Hq, Hkv, D, c->length + p0, L.q_norm, L.k_norm,
                         m->rope_cos, m->rope_sin, eps};
-            rope_append_kernel<<<dim3(rows, Hq + 2 * Hkv), 64, 0, s>>>(ra);
+            if ((e = launch_rope_append(s, ra, rows)) != hipSuccess) return hip_fail(e, "prefill rope");
             FlashArgs fa{b.q, c->kv, c->capacity, l, Hq, Hkv, c->length + p0, rows, 1.0f / std::sqrt((float)D),
                          b.att};
-            const dim3 fg(Hq, (rows + kFlashRows - 1) / kFlashRows);
-            if (D == 128) flash_prefill_kernel<128><<<fg, kFlashThreads, 0, s>>>(fa);
-            else if (D == 64) flash_prefill_kernel<64><<<fg, kFlashThreads, 0, s>>>(fa);
-            else return fail(YUE2_ERR_ARG, "MFMA prefill supports head_dim 64 and 128");
+            if ((e = launch_flash(s, fa, D)) != hipSuccess) return hip_fail(e, "prefill attention");
             GemmArgs go{b.att, qw, L.wo, nullptr, qw, b.x, nullptr, H, rows, H, qw};
             if ((e = launch_gemm(s, GEPI_RESID, go)) != hipSuccess) return hip_fail(e, "prefill o gemm");
-            norm_rows_kernel<<<rows, kRowThreads, norm_lds, s>>>(b.x, L.post_norm, b.h, H, eps);
+            if ((e = launch_norm_rows(s, b.x, L.post_norm, b.h, rows, H, eps)) != hipSuccess)
+                return hip_fail(e, "prefill norm");
             GemmArgs gu{b.h, H, L.wg, L.wu, H, nullptr, b.act, I, rows, I, H};
             if ((e = launch_gemm(s, GEPI_SWIGLU_BF16, gu)) != hipSuccess) return hip_fail(e, "prefill gate/up gemm");
             GemmArgs gd{b.act, I, L.wd, nullptr, I, b.x, nullptr, H, rows, H, I};

@@ -75,6 +75,21 @@ struct Workspace {
 
 }  // namespace y2
 
+namespace y2 {
+// The NAR (acoustic) pathway's device weights (yue2_hip_nar_load): one
+// allocation; the layers as LayerDev (fused q/k/v rows), the linears' biases
+// BF16-rounded f32.
+struct NarDev {
+    void* block = nullptr;
+    int latent = 0, max_frames = 0;
+    float shift = 1.0f;
+    std::vector<LayerDev> layers;
+    uint16_t *vae2llm = nullptr, *llm2vae = nullptr, *time_in = nullptr, *time_out = nullptr,
+             *latent_pos = nullptr;
+    float *vae2llm_b = nullptr, *llm2vae_b = nullptr, *time_in_b = nullptr, *time_out_b = nullptr;
+};
+}  // namespace y2
+
 struct Yue2Model {
     Yue2Config c{};
     hipStream_t stream = nullptr;
@@ -88,6 +103,7 @@ struct Yue2Model {
     bool step_kernel = false;            // decode steps through the persistent kernel (default where supported)
     y2::Workspace ws;  // batch-1 workspace of the parity API
     int norm_fallbacks = 0;
+    y2::NarDev nar;    // loaded by yue2_hip_nar_load
 };
 
 struct Yue2Cache {

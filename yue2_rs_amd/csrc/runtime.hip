@@ -557,6 +557,7 @@ extern "C" void yue2_hip_model_free(Yue2Model* m) {
     m->ws.release();
     if (m->layers_dev) (void)hipFree(m->layers_dev);
     if (m->block) (void)hipFree(m->block);
+    if (m->nar.block) (void)hipFree(m->nar.block);
     (void)hipStreamDestroy(m->stream);
     delete m;
 }

@@ -14,18 +14,24 @@ GEMM (the prefill's BF16 MFMA GEMM at the 3B-class linears for a 2048-row
 prompt chunk) and prefill (the whole matrix-core prefill of 2048- and
 24000-token prompts through the 3B-class model, random-init weights),
 against the 2.5 PFLOP/s dense BF16 matrix peak.
+NAR (the velocity stack of the acoustic stage on the 3B-class model with a
+random-init NAR pathway): one call for 11786 latent frames after a 1000-token
+prefix, the largest chunk a 24576-position context holds (synthesize,
+src/model.rs:717-722), keys = prefix + codec chunk + the frames.
 
 Every timed launch reads another copy of its operands (more than 512 MB in
 total), so the 256 MB Infinity Cache cannot serve repeats.  One JSON line per
 case on stdout.
 
-    python -m yue2_rs_amd.microbench [gemv|attention|copy|gemm|prefill|all]
+    python -m yue2_rs_amd.microbench [gemv|attention|copy|gemm|prefill|nar|all]
 """
 from __future__ import annotations
 
 import ctypes as C
 import json
 import sys
+
+import numpy as np
 
 from .api import _check, available, lib
 
@@ -98,6 +104,38 @@ def prefill(tokens) -> list:
     return out
 
 
+def nar(prefix: int = 1000, frames: int = 11786) -> dict:
+    """One velocity call (the second of two timed) for `frames` latent rows
+    against an AR cache of prefix + frames + 1 positions (the chunk's ids:
+    prefix, codec tokens, the end token)."""
+    import time
+    from . import synthetic
+    from .api import Model, synchronize
+    c = synthetic.CLASS_3B
+    model = Model.open(synthetic.checkpoint(c, seed=0, threads=16))
+    model.load_nar(synthetic.nar_weights(c, seed=0, threads=16))
+    length = prefix + frames + 1
+    cache, _ = model.prefill_mfma(synthetic.prompt(length, c.vocab_size, seed=0), length)
+    st = np.random.default_rng(0).standard_normal((frames, 64)).astype(np.float32)
+    st = (st.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    for _ in range(2):
+        synchronize()
+        t = time.perf_counter()
+        model.velocity(st, cache, 0.5)
+        synchronize()
+        dt = time.perf_counter() - t
+    cache.close()
+    model.close()
+    H, D, I = c.hidden_size, c.head_dim, c.intermediate_size
+    q, kv = c.num_attention_heads * D, c.num_key_value_heads * D
+    n, keys = frames + 2, length + frames + 2
+    fl = (2.0 * n * c.num_hidden_layers * (H * (q + 2 * kv) + q * H + 3 * H * I) +
+          c.num_hidden_layers * c.num_attention_heads * 4.0 * D * n * keys +
+          2.0 * n * 64 * H * 2 + 2.0 * (256 * H + H * H))
+    return {"frames": frames, "keys": keys, "s": round(dt, 4), "flops": fl, "TFLOP_s": round(fl / dt / 1e12, 1),
+            "frac": round(fl / dt / MFMA_BF16_PEAK, 4)}
+
+
 def main(argv=None) -> int:
     what = (argv or sys.argv[1:] or ["all"])[0]
     if not available():
@@ -116,6 +154,8 @@ def main(argv=None) -> int:
     if what in ("gemm", "all"):
         for name, n, k, pair in GEMM_SHAPES:
             print(json.dumps({"bench": "gemm", "shape": name, **gemm(2048, n, k, pair)}), flush=True)
+    if what in ("nar", "all"):
+        print(json.dumps({"bench": "nar_velocity", **nar()}), flush=True)
     if what in ("prefill", "all"):
         for r in prefill([2048, 24000]):
             print(json.dumps({"bench": "prefill", **r}), flush=True)

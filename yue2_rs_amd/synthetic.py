@@ -10,10 +10,11 @@ from __future__ import annotations
 
 import numpy as np
 
-from .api import Checkpoint, Config, LayerWeights, lib
+from .api import Checkpoint, Config, LayerWeights, NarWeights, lib
 
 # Tensor ids of the generator (one independent stream per tensor).
 EMBED, LM_HEAD, LAYER_BASE, PER_LAYER = 0, 1, 16, 8
+NAR_BASE = 1 << 16  # the NAR pathway's tensors
 PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
 REDUCED = Config(hidden_size=1024, num_hidden_layers=2, num_attention_heads=16, num_key_value_heads=4,
@@ -51,6 +52,33 @@ def checkpoint(c: Config, seed: int = 0, std: float = 0.02, threads: int = 0) ->
                                    q_norm=np.ones(D, np.float32), k_norm=np.ones(D, np.float32),
                                    post_attention_layernorm=np.ones(H, np.float32)))
     return Checkpoint(c, embed, head, np.ones(H, np.float32), layers)
+
+
+def nar_weights(c: Config, seed: int = 0, std: float = 0.02, latent_dim: int = 64,
+                max_latent_frames: int = 24576, timestep_shift: float = 1.0, threads: int = 0) -> NarWeights:
+    """Random-init NAR pathway for config c: BF16 weights ~N(0, std), biases
+    BF16-exact ~N(0, std) as float32, latent position rows ~N(0, std), norms 1."""
+    H, D = c.hidden_size, c.head_dim
+    t = iter(range(NAR_BASE, NAR_BASE + 64))
+
+    def mat(shape):
+        return bf16_normal(shape, seed, next(t), std, threads)
+
+    def bias(n):
+        b = bf16_normal((n,), seed, next(t), std, threads)
+        return (b.astype(np.uint32) << 16).view(np.float32)
+
+    layers = []
+    sh = shapes(c)
+    for l in range(c.num_hidden_layers):
+        mats = {n: bf16_normal(sh[n], seed, NAR_BASE + 256 + l * PER_LAYER + j, std, threads)
+                for j, n in enumerate(PROJECTIONS)}
+        layers.append(LayerWeights(**mats, input_layernorm=np.ones(H, np.float32),
+                                   q_norm=np.ones(D, np.float32), k_norm=np.ones(D, np.float32),
+                                   post_attention_layernorm=np.ones(H, np.float32)))
+    return NarWeights(latent_dim, max_latent_frames, timestep_shift,
+                      mat((H, latent_dim)), bias(H), mat((latent_dim, H)), bias(latent_dim),
+                      mat((H, 256)), bias(H), mat((H, H)), bias(H), mat((max_latent_frames, H)), layers)
 
 
 class MT19937:

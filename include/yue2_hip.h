@@ -250,6 +250,16 @@ int32_t yue2_hip_nar_load(Yue2Model *m, const Yue2NarWeights *w);
 int32_t yue2_hip_velocity(Yue2Model *m, const Yue2Cache *c, const float *state, int32_t frames, double raw_t,
                           int32_t nar_cond_end, float *out);
 
+/* Model::synthesize (src/model.rs:699-775), the acoustic stage: the song's
+ * noise (Generator::normal_tensor of MT19937(seed), src/sampling.rs:64-79,
+ * on the host), then per chunk of (min(24576, max positions) - prefix_len -
+ * 3) / 2 frames the AR prefill of prefix + codec ids (+ 151853) + MUSIC_END
+ * on the matrix cores and `steps` midpoint flow-matching steps, two
+ * yue2_hip_velocity calls each; out [codec_len x 64].  Returns 0 or a
+ * negative Yue2Error with the reference's messages. */
+int32_t yue2_hip_synthesize(Yue2Model *m, const int32_t *prefix, int32_t prefix_len, const int32_t *codec,
+                            int32_t codec_len, uint64_t seed, int32_t steps, float *out);
+
 /* A decode loop bound to one cache (batch 1) or to a conditional and an
  * unconditional cache (CFG batch 2).  Each step is one hipGraph launch:
  * embed -> layers -> LM head -> CFG mix -> choose -> next id.  The caches

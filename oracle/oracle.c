@@ -605,6 +605,88 @@ done:
     return rc;
 }
 
+/* uniform_f32 (src/sampling.rs:56-58) */
+static float mt_uniform_f32(y2o_mt *g) { return (float)(y2o_mt_next(g) & 0x00ffffffu) / 16777216.0f; }
+
+void y2o_normal(uint64_t seed, int n, float *out) {
+    y2o_mt g;
+    y2o_mt_seed(&g, seed);
+    for (int i = 0; i < n; ++i) out[i] = mt_uniform_f32(&g);
+    for (int b = 0; b + 16 <= n; b += 16) {
+        float *blk = out + b;
+        for (int i = 0; i < 8; ++i) {
+            const float radius = sqrtf(-2.0f * logf(1.0f - blk[i]));
+            const float theta = (float)(2.0 * 3.14159265358979323846 * (double)blk[i + 8]);
+            blk[i] = radius * cosf(theta);
+            blk[i + 8] = radius * sinf(theta);
+        }
+    }
+}
+
+/* logit (src/model.rs:777-779) */
+static double logit(double t) {
+    double v = log(t / (1.0 - t));
+    return v < -20.0 ? -20.0 : v > 20.0 ? 20.0 : v;
+}
+
+
+int y2o_synthesize(const y2o_model *m, const y2o_nar *nar, const int32_t *prefix, int prefix_len,
+                   const int32_t *codec, int codec_len, uint64_t seed, int steps, float *out) {
+    const int L = nar->latent;
+    if (L != 64 || codec_len <= 0 || steps <= 0) return Y2O_ERR_CODEC;
+    for (int i = 0; i < codec_len; ++i)
+        if (codec[i] < 0 || codec[i] >= CODEC_SIZE) return Y2O_ERR_CODEC;
+    const int capacity = CONTEXT < m->c.max_pos ? CONTEXT : m->c.max_pos;
+    if (capacity < prefix_len + 3 || (capacity - prefix_len - 3) / 2 <= 0) return Y2O_ERR_CONTEXT;
+    const int size = (capacity - prefix_len - 3) / 2;
+    float *noise = (float *)malloc(sizeof(float) * (size_t)codec_len * L);
+    float *first = (float *)malloc(sizeof(float) * (size_t)size * L);
+    float *mid = (float *)malloc(sizeof(float) * (size_t)size * L);
+    int32_t *ids = (int32_t *)malloc(sizeof(int32_t) * (size_t)(prefix_len + size + 1));
+    float *logits = (float *)malloc(sizeof(float) * (size_t)m->c.vocab);
+    int rc = Y2O_OK;
+    if (!noise || !first || !mid || !ids || !logits) {
+        rc = Y2O_ERR_ALLOC;
+        goto done;
+    }
+    y2o_normal(seed, codec_len * L, noise);
+    const float dt = 1.0f / (float)steps;
+    for (int start = 0; start < codec_len; start += size) {
+        const int end = start + size < codec_len ? start + size : codec_len, frames = end - start;
+        int n = 0;
+        for (int i = 0; i < prefix_len; ++i) ids[n++] = prefix[i];
+        for (int i = start; i < end; ++i) ids[n++] = codec[i] + CODEC_OFFSET;
+        ids[n++] = MUSIC_END;
+        y2o_cache *cache = y2o_cache_new(&m->c, n);
+        if (!cache) {
+            rc = Y2O_ERR_ALLOC;
+            goto done;
+        }
+        rc = y2o_prefill(m, cache, ids, n, logits);
+        float *state = out + (size_t)start * L;
+        for (size_t i = 0; i < (size_t)frames * L; ++i) state[i] = rb(noise[(size_t)start * L + i]);
+        for (int step = 0; step < steps && rc == Y2O_OK; ++step) {
+            const double t = 1.0 - (double)step / (double)steps;
+            rc = y2o_velocity(m, nar, cache, state, frames, logit(t), 0, first);
+            if (rc) break;
+            for (size_t i = 0; i < (size_t)frames * L; ++i) mid[i] = rb(state[i] - rb(first[i] * (dt / 2.0f)));
+            rc = y2o_velocity(m, nar, cache, mid, frames, logit(t - 0.5 / (double)steps), 0, first);
+            if (rc) break;
+            for (size_t i = 0; i < (size_t)frames * L; ++i) state[i] = rb(state[i] - rb(first[i] * dt));
+        }
+        y2o_cache_free(cache);
+        if (rc) goto done;
+        for (size_t i = 0; i < (size_t)frames * L; ++i)
+            if (!isfinite(state[i])) {
+                rc = Y2O_ERR_LOGITS;
+                goto done;
+            }
+    }
+done:
+    free(noise); free(first); free(mid); free(ids); free(logits);
+    return rc;
+}
+
 void y2o_mt_seed(y2o_mt *g, uint64_t seed) {
     g->state[0] = (uint32_t)seed;
     for (int i = 1; i < 624; ++i)

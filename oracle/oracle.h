@@ -77,6 +77,11 @@
  *                    set -- permuting the frames permutes the outputs when
  *                    no position-dependent term enters (RoPE start, latent
  *                    position rows equal); parity unpinned beyond these.
+ *   y2o_normal      pairs (i, i + 8) of a block share the radius: x^2 + y^2
+ *                    = -2 ln(1 - u) of the MT19937 draw; moments of N(0, 1).
+ *   y2o_synthesize  steps and chunking from the loop's invariants: with zero
+ *                    velocity (zero llm2vae and bias) the output is the
+ *                    rounded noise; chunks of (capacity - prefix - 3) / 2.
  *   Accelerate's exact summation order, macOS libm cos/sin/powf and the real
  *   checkpoint's logits cannot be run here: parity with those is unpinned
  *   beyond the checks above.
@@ -212,6 +217,17 @@ typedef struct {
  * cache length; the cache is not modified. */
 int y2o_velocity(const y2o_model *m, const y2o_nar *nar, const y2o_cache *cache, const float *state,
                  int frames, double raw_t, int nar_cond_end, float *out);
+
+/* Generator::normal_tensor (src/sampling.rs:64-79): n (a multiple of 16)
+ * uniform_f32 draws, then Box-Muller within each block of 16 (libm
+ * logf/sqrtf/cosf/sinf in f32, the angle 2 pi u in f64). */
+void y2o_normal(uint64_t seed, int n, float *out);
+
+/* Model::synthesize (src/model.rs:699-775): codec_len latent frames
+ * ([codec_len, latent], latent 64) from the prefix and the codec ids by the
+ * midpoint flow-matching loop over `steps` steps per context chunk. */
+int y2o_synthesize(const y2o_model *m, const y2o_nar *nar, const int32_t *prefix, int prefix_len,
+                   const int32_t *codec, int codec_len, uint64_t seed, int steps, float *out);
 
 void y2o_mt_seed(y2o_mt *g, uint64_t seed);
 uint32_t y2o_mt_next(y2o_mt *g);

@@ -96,6 +96,8 @@ def lib() -> C.CDLL:
             "y2o_forward_phase": (i32, [vp, C.POINTER(CacheS), vp, i32, i32, vp]),
             "y2o_prefill": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_velocity": (i32, [vp, vp, C.POINTER(CacheS), vp, i32, f64, i32, vp]),
+            "y2o_normal": (None, [C.c_uint64, i32, vp]),
+            "y2o_synthesize": (i32, [vp, vp, vp, i32, vp, i32, C.c_uint64, i32, vp]),
             "y2o_mt_seed": (None, [vp, C.c_uint64]),
             "y2o_mt_next": (C.c_uint32, [vp]),
             "y2o_mt_discard": (None, [vp, C.c_uint64]),
@@ -198,6 +200,25 @@ class Nar:
         if rc:
             raise RuntimeError(f"oracle error {rc}")
         return out
+
+
+    def synthesize(self, prefix, codec, seed: int, steps: int) -> np.ndarray:
+        """Model::synthesize (src/model.rs:699-775): [len(codec), latent]."""
+        p = np.ascontiguousarray(prefix, dtype=np.int32)
+        cd = np.ascontiguousarray(codec, dtype=np.int32)
+        out = np.empty((len(cd), self.w.latent_dim), np.float32)
+        rc = lib().y2o_synthesize(self.model.ref, C.byref(self._n), _p(p), len(p), _p(cd), len(cd), seed, steps,
+                                  _p(out))
+        if rc:
+            raise RuntimeError(f"oracle error {rc}")
+        return out
+
+
+def normal(seed: int, n: int) -> np.ndarray:
+    """Generator::normal_tensor's values (src/sampling.rs:64-79)."""
+    out = np.empty(n, np.float32)
+    lib().y2o_normal(seed, n, _p(out))
+    return out
 
 
 class Cache:

@@ -100,3 +100,50 @@ def test_errors(gpu):
         gc.close()
     finally:
         gm.close()
+
+
+MUSIC = dataclasses.replace(synthetic.REDUCED, hidden_size=128, num_hidden_layers=2, num_attention_heads=2,
+                            num_key_value_heads=1, intermediate_size=256, vocab_size=184704,
+                            max_position_embeddings=128)
+
+
+@pytest.fixture(scope="module")
+def music(gpu, oracle_threads):
+    ck = synthetic.checkpoint(MUSIC, seed=3)
+    nw = synthetic.nar_weights(MUSIC, seed=3, max_latent_frames=64, timestep_shift=3.0)
+    gm = y2.Model.open(ck)
+    gm.load_nar(nw)
+    yield ck, nw, gm, O.Nar(O.Model(ck), nw)
+    gm.close()
+
+
+def test_synthesize_matches_oracle(music):
+    """Model::synthesize: two chunks of (128 - 20 - 3) / 2 = 52 and 38
+    frames, two midpoint steps each (four velocities); the device's noise is
+    the oracle's bit for bit (same MT19937 and libm), the latents agree within
+    the velocity tolerance."""
+    ck, nw, gm, nar = music
+    prefix, codec = synthetic.prompt(20, 151643, seed=7), synthetic.prompt(90, 32768, seed=6)
+    got = gm.synthesize(prefix, codec, 42, 2)
+    want = nar.synthesize(prefix, codec, 42, 2)
+    _close(got, want, "synthesize")
+
+
+def test_synthesize_without_velocity_returns_the_noise(music):
+    ck, nw, gm, nar = music
+    z = dataclasses.replace(nw, llm2vae=np.zeros_like(nw.llm2vae), llm2vae_bias=np.zeros_like(nw.llm2vae_bias))
+    gz = y2.Model.open(ck)
+    try:
+        gz.load_nar(z)
+        got = gz.synthesize(synthetic.prompt(20, 151643, seed=7), synthetic.prompt(90, 32768, seed=6), 42, 2)
+        want = rb(O.normal(42, 90 * 64)).reshape(90, 64)
+        assert np.array_equal(bits(got), bits(want))
+    finally:
+        gz.close()
+
+
+def test_synthesize_rejects(music):
+    ck, nw, gm, nar = music
+    for prefix, codec, steps in (([1] * 20, [], 2), ([1] * 20, [32768], 2), ([1] * 20, [5], 0), ([1] * 124, [5], 2)):
+        with pytest.raises(y2.Yue2Error):
+            gm.synthesize(prefix, codec, 1, steps)

@@ -226,3 +226,46 @@ def test_condition_end_limits_the_keys(oracle_threads):
     va, vb = nar.velocity(state, a, 0.1, 30), nar.velocity(state, b, 0.1, 30)
     assert np.array_equal(va.view(np.uint32), vb.view(np.uint32))
     assert not np.array_equal(nar.velocity(state, a, 0.1).view(np.uint32), nar.velocity(state, b, 0.1).view(np.uint32))
+
+
+def test_normal_tensor_pairs():
+    """Generator::normal_tensor (src/sampling.rs:64-79): in each block of 16
+    the pair (i, i + 8) shares the radius, x^2 + y^2 = -2 ln(1 - u_i) for the
+    i-th uniform_f32 draw of MT19937(seed), and the values are N(0, 1)."""
+    n = 16 * 4000
+    v = O.normal(11, n).astype(np.float64)
+    g = synthetic.MT19937(11)
+    u = np.array([(g.next_u32() & 0xFFFFFF) / 16777216.0 for _ in range(n)])
+    blk = v.reshape(-1, 16)
+    ub = u.reshape(-1, 16)
+    r2 = blk[:, :8] ** 2 + blk[:, 8:] ** 2
+    want = -2.0 * np.log(1.0 - ub[:, :8])
+    assert np.allclose(r2, want, rtol=2e-5, atol=1e-6)
+    assert abs(v.mean()) < 0.02 and abs(v.std() - 1.0) < 0.02
+
+
+MUSIC = Config(hidden_size=128, num_hidden_layers=2, num_attention_heads=2, num_key_value_heads=1, head_dim=64,
+               intermediate_size=256, vocab_size=184704, max_position_embeddings=128, rms_norm_eps=1e-6,
+               rope_theta=10000.0)
+
+
+def test_synthesize_without_velocity_returns_the_noise(oracle_threads):
+    """With llm2vae and its bias zero the velocity is +0, every midpoint step
+    keeps the state, and the result is the rounded noise in chunk order."""
+    ck = synthetic.checkpoint(MUSIC, seed=3)
+    nw = synthetic.nar_weights(MUSIC, seed=3, max_latent_frames=64)
+    nw.llm2vae = np.zeros_like(nw.llm2vae)
+    nw.llm2vae_bias = np.zeros_like(nw.llm2vae_bias)
+    nar = O.Nar(O.Model(ck), nw)
+    codec = synthetic.prompt(90, 32768, seed=6)
+    got = nar.synthesize(synthetic.prompt(20, 151643, seed=7), codec, 42, 2)
+    want = rb(O.normal(42, 90 * 64)).reshape(90, 64)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_synthesize_rejects(oracle_threads):
+    ck = synthetic.checkpoint(MUSIC, seed=3)
+    nar = O.Nar(O.Model(ck), synthetic.nar_weights(MUSIC, seed=3, max_latent_frames=64))
+    for prefix, codec, steps in (([1] * 20, [], 2), ([1] * 20, [32768], 2), ([1] * 20, [5], 0), ([1] * 124, [5], 2)):
+        with pytest.raises(RuntimeError):
+            nar.synthesize(prefix, codec, 1, steps)

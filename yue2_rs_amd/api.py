@@ -116,6 +116,7 @@ def lib() -> C.CDLL:
         "yue2_hip_prefill_mfma": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_nar_load": (i32, [vp, vp]),
         "yue2_hip_velocity": (i32, [vp, vp, vp, i32, C.c_double, i32, vp]),
+        "yue2_hip_synthesize": (i32, [vp, vp, i32, vp, i32, C.c_uint64, i32, vp]),
         "yue2_hip_selftest_gemm": (i32, [vp, vp, vp, i32, i32, i32]),
         "yue2_hip_decoder_new": (vp, [vp, vp, vp, vp, u64, i32, f32, i32]),
         "yue2_hip_decoder_free": (None, [vp]),
@@ -355,6 +356,14 @@ class Model:
         st = np.ascontiguousarray(state, dtype=np.float32)
         out = np.empty_like(st)
         _check(lib().yue2_hip_velocity(self._h, cache._h, _ptr(st), st.shape[0], raw_t, nar_cond_end, _ptr(out)))
+        return out
+
+    def synthesize(self, prefix: Sequence[int], codec: Sequence[int], seed: int, steps: int) -> np.ndarray:
+        """Model::synthesize (src/model.rs:699-775): [len(codec), 64] latents."""
+        p = np.ascontiguousarray(prefix, dtype=np.int32)
+        cd = np.ascontiguousarray(codec, dtype=np.int32)
+        out = np.empty((len(cd), 64), np.float32)
+        _check(lib().yue2_hip_synthesize(self._h, _ptr(p), len(p), _ptr(cd), len(cd), seed, steps, _ptr(out)))
         return out
 
     def set_step_kernel(self, on: bool) -> bool:

@@ -64,7 +64,7 @@ extern "C" int32_t yue2_hip_nar_load(Yue2Model* m, const Yue2NarWeights* w) {
     const int qw = c.num_attention_heads * D, kw = c.num_key_value_heads * D, qkvw = qw + 2 * kw;
     if (Lat <= 0 || Lat % kGemmTK || w->max_latent_frames < 1 || !(w->timestep_shift > 0.0f) ||
         !std::isfinite(w->timestep_shift))
-        return fail(YUE2_ERR_CONFIG, "Invalid model config");
+        return fail(YUE2_ERR_CONFIG, "Invalid transformer configuration");
     if (H % kGemmTK || I % kGemmTK || qw % kGemmTK || (D != 64 && D != 128))
         return fail(YUE2_ERR_ARG, "shape without an MFMA NAR stack");
     if (!w->vae2llm || !w->llm2vae || !w->time_in || !w->time_out || !w->latent_pos || !w->vae2llm_bias ||
@@ -284,4 +284,92 @@ extern "C" int32_t yue2_hip_velocity(Yue2Model* m, const Yue2Cache* c, const flo
     (void)hipStreamSynchronize(s);
     (void)hipFree(block);
     return rc;
+}
+
+namespace {
+
+// Generator::normal_tensor (src/sampling.rs:64-79): n uniform_f32 draws of
+// MT19937(seed), then Box-Muller within each block of 16 (libm logf, sqrtf,
+// cosf, sinf in f32; the angle 2 pi u in f64).  Host work in the reference.
+void normal_tensor(uint64_t seed, size_t n, float* out) {
+    uint32_t st[624];
+    st[0] = (uint32_t)seed;
+    for (int i = 1; i < 624; ++i) st[i] = 1812433253u * (st[i - 1] ^ (st[i - 1] >> 30)) + (uint32_t)i;
+    int next = 624;
+    auto draw = [&]() {
+        if (next == 624) {
+            for (int i = 0; i < 624; ++i) {
+                const uint32_t bits = (st[i] & 0x80000000u) | (st[(i + 1) % 624] & 0x7fffffffu);
+                st[i] = st[(i + 397) % 624] ^ (bits >> 1) ^ ((bits & 1u) ? 0x9908b0dfu : 0u);
+            }
+            next = 0;
+        }
+        uint32_t y = st[next++];
+        y ^= y >> 11;
+        y ^= (y << 7) & 0x9d2c5680u;
+        y ^= (y << 15) & 0xefc60000u;
+        y ^= y >> 18;
+        return y;
+    };
+    for (size_t i = 0; i < n; ++i) out[i] = (float)(draw() & 0x00ffffffu) / 16777216.0f;
+    for (size_t b = 0; b + 16 <= n; b += 16) {
+        float* blk = out + b;
+        for (int i = 0; i < 8; ++i) {
+            const float radius = sqrtf(-2.0f * logf(1.0f - blk[i]));
+            const float theta = (float)(2.0 * M_PI * (double)blk[i + 8]);
+            blk[i] = radius * cosf(theta);
+            blk[i + 8] = radius * sinf(theta);
+        }
+    }
+}
+
+// logit (src/model.rs:777-779)
+double logit(double t) { return std::clamp(std::log(t / (1.0 - t)), -20.0, 20.0); }
+
+}  // namespace
+
+extern "C" int32_t yue2_hip_synthesize(Yue2Model* m, const int32_t* prefix, int32_t prefix_len, const int32_t* codec,
+                                       int32_t codec_len, uint64_t seed, int32_t steps, float* out) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m || (prefix_len > 0 && !prefix) || !codec || !out || prefix_len < 0)
+        return fail(YUE2_ERR_ARG, "null model, ids or output");
+    if (!m->nar.block) return fail(YUE2_ERR_ARG, "NAR weights not loaded");
+    const int Lat = m->nar.latent;
+    bool codec_ok = codec_len > 0 && steps > 0 && Lat == 64;
+    for (int i = 0; codec_ok && i < codec_len; ++i) codec_ok = codec[i] >= 0 && codec[i] < kCodecSize;
+    if (!codec_ok) return fail(YUE2_ERR_ARG, "Expected nonempty codec tokens and a 64-dimensional latent model");
+    const int capacity = std::min(kContext, m->c.max_position_embeddings);
+    if (capacity - prefix_len - 3 < 2) return fail(YUE2_ERR_CONTEXT, "Prefix leaves no acoustic context");
+    const int size = (capacity - prefix_len - 3) / 2;
+    // the whole song's noise once, sliced at the chunks (:724-726)
+    std::vector<float> noise((size_t)codec_len * Lat), first((size_t)size * Lat), mid(first.size());
+    normal_tensor(seed, noise.size(), noise.data());
+    const float dt = 1.0f / (float)steps;
+    std::vector<int32_t> ids;
+    for (int start = 0; start < codec_len; start += size) {
+        const int end = std::min(start + size, codec_len), frames = end - start;
+        ids.assign(prefix, prefix + prefix_len);
+        for (int i = start; i < end; ++i) ids.push_back(codec[i] + kCodecOffset);
+        ids.push_back(kMusicEnd);
+        Yue2Cache* cache = yue2_hip_cache_new(m, (int)ids.size());
+        if (!cache) return YUE2_ERR_ALLOC;
+        int rc = yue2_hip_prefill_mfma(m, cache, ids.data(), (int)ids.size(), YUE2_PHASE_NONE, nullptr);
+        float* state = out + (size_t)start * Lat;
+        for (size_t i = 0; i < (size_t)frames * Lat; ++i) state[i] = rb(noise[(size_t)start * Lat + i]);
+        // the midpoint steps (:745-758)
+        for (int step = 0; step < steps && rc == YUE2_OK; ++step) {
+            const double t = 1.0 - (double)step / (double)steps;
+            rc = yue2_hip_velocity(m, cache, state, frames, logit(t), 0, first.data());
+            if (rc) break;
+            for (size_t i = 0; i < (size_t)frames * Lat; ++i) mid[i] = rb(state[i] - rb(first[i] * (dt / 2.0f)));
+            rc = yue2_hip_velocity(m, cache, mid.data(), frames, logit(t - 0.5 / (double)steps), 0, first.data());
+            if (rc) break;
+            for (size_t i = 0; i < (size_t)frames * Lat; ++i) state[i] = rb(state[i] - rb(first[i] * dt));
+        }
+        yue2_hip_cache_free(cache);
+        if (rc) return rc;
+        for (size_t i = 0; i < (size_t)frames * Lat; ++i)
+            if (!std::isfinite(state[i])) return fail(YUE2_ERR_LOGITS, "Flow matching produced nonfinite latents");
+    }
+    return YUE2_OK;
 }

@@ -260,6 +260,32 @@ int32_t yue2_hip_velocity(Yue2Model *m, const Yue2Cache *c, const float *state, 
 int32_t yue2_hip_synthesize(Yue2Model *m, const int32_t *prefix, int32_t prefix_len, const int32_t *codec,
                             int32_t codec_len, uint64_t seed, int32_t steps, float *out);
 
+/* The VAE decoder (src/vae.rs), FP32 on the device.  Vae::open
+ * (src/vae.rs:635-669) with decoder_only: config.json (model_type
+ * yue2_vae, decoder_config) and the safetensors file(s) of `dir`, checked and
+ * weight-normed as the reference does, with its messages.  NULL on failure. */
+typedef struct Yue2Vae Yue2Vae;
+Yue2Vae *yue2_hip_vae_open(const char *dir);
+void yue2_hip_vae_free(Yue2Vae *v);
+/* info[0..5] = sample_rate, latent_dim, audio_channels, downsampling_ratio,
+ * decode_core_frames, decode_halo_frames. */
+int32_t yue2_hip_vae_info(const Yue2Vae *v, int32_t *info);
+/* Vae::natural_output_length (src/vae.rs:670-675): audio rows for `frames`
+ * latent rows, or a negative Yue2Error. */
+int64_t yue2_hip_vae_output_length(const Yue2Vae *v, int32_t frames);
+/* Vae::required_halo (src/vae.rs:676-681). */
+int32_t yue2_hip_vae_required_halo(const Yue2Vae *v, int32_t core);
+/* Vae::decode (src/vae.rs:688-727): z [frames x latent_dim] -> out
+ * [output_length x audio_channels].  The convolutions run in FP32 on the
+ * device in their own summation order, so results agree with the CPU
+ * restatement within FP32 rounding (a tolerance), not bit for bit.
+ * Returns 0 or a negative Yue2Error. */
+int32_t yue2_hip_vae_decode(Yue2Vae *v, const float *z, int32_t frames, float *out);
+/* Vae::decode_tiled (src/vae.rs:729-762): core-frame tiles with `halo`
+ * frames on each side (at least yue2_hip_vae_required_halo(core)). */
+int32_t yue2_hip_vae_decode_tiled(Yue2Vae *v, const float *z, int32_t frames, int32_t core, int32_t halo,
+                                  float *out);
+
 /* A decode loop bound to one cache (batch 1) or to a conditional and an
  * unconditional cache (CFG batch 2).  Each step is one hipGraph launch:
  * embed -> layers -> LM head -> CFG mix -> choose -> next id.  The caches
@@ -347,6 +373,13 @@ int32_t yue2_hip_selftest_math(int32_t which, const void *in, void *out, size_t 
  * multiple of 64.  Returns 0 or a negative Yue2Error. */
 int32_t yue2_hip_selftest_gemm(const uint16_t *x, const uint16_t *w, float *out, int32_t M, int32_t N,
                                int32_t K);
+/* Diagnostics: one convolution through the VAE's device kernel, w in the
+ * checkpoint layout ([out, in, k], or [in, out, k] transposed; no weight
+ * norm), bias [cout] or NULL, x [frames x cin] -> out [length x cout]
+ * (Conv::length, src/vae.rs:147-153).  Returns 0 or a negative Yue2Error. */
+int32_t yue2_hip_selftest_conv(int32_t transpose, int32_t cin, int32_t cout, int32_t kernel, int32_t stride,
+                               int32_t padding, int32_t dilation, const float *x, int32_t frames, const float *w,
+                               const float *bias, float *out);
 /* Execution choice: run decode steps (yue2_hip_forward and decoders created
  * afterwards) through the persistent token-step kernel -- one launch per
  * token, workgroups exchanging tagged words instead of meeting at barriers

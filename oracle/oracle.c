@@ -687,6 +687,124 @@ done:
     return rc;
 }
 
+/* ------------------------------------------------------------------------ */
+/* VAE decoder (src/vae.rs:49-611), FP32                                    */
+/* ------------------------------------------------------------------------ */
+
+int y2o_conv_length(int transpose, int n, int kernel, int stride, int padding, int dilation) {
+    if (transpose) return (n - 1) * stride + dilation * (kernel - 1) + 1 - 2 * padding;
+    return (n + 2 * padding - dilation * (kernel - 1) - 1) / stride + 1;
+}
+
+/* Each output is the f32 sum over the patch columns (input channel major,
+ * tap minor, the im2col order of Conv::apply), then the bias. */
+void y2o_conv(int transpose, int cin, int cout, int kernel, int stride, int padding, int dilation,
+              const float *x, int frames, const float *w, const float *b, float *out) {
+    const int length = y2o_conv_length(transpose, frames, kernel, stride, padding, dilation);
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+    for (int t = 0; t < length; ++t)
+        for (int o = 0; o < cout; ++o) {
+            float acc = 0.0f;
+            for (int i = 0; i < cin; ++i)
+                for (int j = 0; j < kernel; ++j) {
+                    long src;
+                    float wv;
+                    if (transpose) {
+                        const long pos = (long)t + padding - (long)j * dilation;
+                        if (pos < 0 || pos % stride) continue;
+                        src = pos / stride;
+                        wv = w[((size_t)i * cout + o) * kernel + j];
+                    } else {
+                        src = (long)t * stride + (long)j * dilation - padding;
+                        wv = w[((size_t)o * cin + i) * kernel + j];
+                    }
+                    if (src < 0 || src >= frames) continue;
+                    acc += x[(size_t)src * cin + i] * wv;
+                }
+            out[(size_t)t * cout + o] = acc + (b ? b[o] : 0.0f);
+        }
+}
+
+int y2o_vae_length(const y2o_vae_op *ops, int nops, int frames) {
+    int n = frames;
+    for (int k = 0; k < nops; ++k)
+        if (ops[k].kind == Y2O_VAE_CONV || ops[k].kind == Y2O_VAE_CONVT)
+            n = y2o_conv_length(ops[k].kind == Y2O_VAE_CONVT, n, ops[k].kernel, ops[k].stride, ops[k].padding,
+                                ops[k].dilation);
+    return n;
+}
+
+int y2o_vae_run(const y2o_vae_op *ops, int nops, const float *x0, int frames, int channels, float *out,
+                int *out_frames, int *out_channels) {
+    int n = frames, c = channels;
+    float *x = (float *)malloc(sizeof(float) * (size_t)n * c);
+    float *res = NULL;
+    int res_n = 0, res_c = 0, rc = Y2O_OK;
+    if (!x) return Y2O_ERR_ALLOC;
+    memcpy(x, x0, sizeof(float) * (size_t)n * c);
+    for (int k = 0; k < nops && rc == Y2O_OK; ++k) {
+        const y2o_vae_op *op = &ops[k];
+        if (op->kind == Y2O_VAE_CONV || op->kind == Y2O_VAE_CONVT) {
+            const int tr = op->kind == Y2O_VAE_CONVT;
+            if (c != op->cin) { rc = Y2O_ERR_CONTEXT; break; }
+            /* weight norm (Conv::load, src/vae.rs:86-97): rows of v's first dimension */
+            const int rows = tr ? op->cin : op->cout, cols = (tr ? op->cout : op->cin) * op->kernel;
+            float *w = (float *)malloc(sizeof(float) * (size_t)rows * cols);
+            const int len = y2o_conv_length(tr, n, op->kernel, op->stride, op->padding, op->dilation);
+            float *y = (float *)malloc(sizeof(float) * (size_t)(len > 0 ? len : 1) * op->cout);
+            if (!w || !y || len <= 0) { free(w); free(y); rc = len <= 0 ? Y2O_ERR_CONTEXT : Y2O_ERR_ALLOC; break; }
+            for (int r = 0; r < rows; ++r) {
+                float ss = 0.0f;
+                for (int q = 0; q < cols; ++q) ss += op->v[(size_t)r * cols + q] * op->v[(size_t)r * cols + q];
+                const float norm = sqrtf(ss), f = op->g[r] / norm;
+                for (int q = 0; q < cols; ++q) w[(size_t)r * cols + q] = op->v[(size_t)r * cols + q] * f;
+            }
+            y2o_conv(tr, op->cin, op->cout, op->kernel, op->stride, op->padding, op->dilation, x, n, w, op->b, y);
+            free(w);
+            free(x);
+            x = y;
+            n = len;
+            c = op->cout;
+        } else if (op->kind == Y2O_VAE_SNAKE) {
+            /* Activation::Snake (src/vae.rs:292-306): alpha, beta = exp(params) */
+            for (int i = 0; i < c; ++i) {
+                const float a = expf(op->alpha[i]), ib = 1.0f / (expf(op->beta[i]) + 1e-9f);
+                for (int t = 0; t < n; ++t) {
+                    float *v = x + (size_t)t * c + i;
+                    const float s = sinf(*v * a);
+                    *v += ib * (s * s);
+                }
+            }
+        } else if (op->kind == Y2O_VAE_ELU) {
+            for (size_t i = 0; i < (size_t)n * c; ++i)
+                if (x[i] < 0.0f) x[i] = expf(x[i]) - 1.0f;
+        } else if (op->kind == Y2O_VAE_TANH) {
+            for (size_t i = 0; i < (size_t)n * c; ++i) x[i] = tanhf(x[i]);
+        } else if (op->kind == Y2O_VAE_RES_BEGIN) {
+            free(res);
+            res = (float *)malloc(sizeof(float) * (size_t)n * c);
+            if (!res) { rc = Y2O_ERR_ALLOC; break; }
+            memcpy(res, x, sizeof(float) * (size_t)n * c);
+            res_n = n;
+            res_c = c;
+        } else if (op->kind == Y2O_VAE_RES_END) {
+            /* Op::Residual: h.add(&x, false) (src/vae.rs:390-394) */
+            if (!res || res_n != n || res_c != c) { rc = Y2O_ERR_CONTEXT; break; }
+            for (size_t i = 0; i < (size_t)n * c; ++i) x[i] = x[i] + res[i];
+            free(res);
+            res = NULL;
+        }
+    }
+    if (rc == Y2O_OK) {
+        memcpy(out, x, sizeof(float) * (size_t)n * c);
+        *out_frames = n;
+        *out_channels = c;
+    }
+    free(x);
+    free(res);
+    return rc;
+}
+
 void y2o_mt_seed(y2o_mt *g, uint64_t seed) {
     g->state[0] = (uint32_t)seed;
     for (int i = 1; i < 624; ++i)

@@ -82,6 +82,11 @@
  *   y2o_synthesize  steps and chunking from the loop's invariants: with zero
  *                    velocity (zero llm2vae and bias) the output is the
  *                    rounded noise; chunks of (capacity - prefix - 3) / 2.
+ *   y2o_conv        the reference's own convolution known-answer cases and
+ *                    scalar formula (src/vae.rs:812-892, tolerance 2e-6).
+ *   y2o_vae_*       closed forms (SnakeBeta at alpha = beta = 1, ELU, tanh,
+ *                    the weight norm's row norms = |g|), Conv::length, and a
+ *                    tiled decode equal to the whole decode on every core row.
  *   Accelerate's exact summation order, macOS libm cos/sin/powf and the real
  *   checkpoint's logits cannot be run here: parity with those is unpinned
  *   beyond the checks above.
@@ -228,6 +233,33 @@ void y2o_normal(uint64_t seed, int n, float *out);
  * midpoint flow-matching loop over `steps` steps per context chunk. */
 int y2o_synthesize(const y2o_model *m, const y2o_nar *nar, const int32_t *prefix, int prefix_len,
                    const int32_t *codec, int codec_len, uint64_t seed, int steps, float *out);
+
+/* The VAE decoder (src/vae.rs:49-611) as a list of operations in network
+ * order.  Conv / ConvT carry the weight-norm pair (v [out, in, k], or
+ * [in, out, k] transposed; g [rows of v]) and a bias (NULL: none); Snake
+ * carries the alpha and beta parameters (exp taken here); Residual begin /
+ * end bracket a residual unit.  All FP32 (no BF16 rounding). */
+enum {
+    Y2O_VAE_CONV = 0, Y2O_VAE_CONVT = 1, Y2O_VAE_SNAKE = 2, Y2O_VAE_ELU = 3, Y2O_VAE_TANH = 4,
+    Y2O_VAE_RES_BEGIN = 5, Y2O_VAE_RES_END = 6
+};
+typedef struct {
+    int32_t kind, cin, cout, kernel, stride, padding, dilation;
+    const float *v, *g, *b, *alpha, *beta;
+} y2o_vae_op;
+
+/* Conv::apply / transposed (src/vae.rs:165-257) with ready weights w
+ * ([out, in, k], or [in, out, k] transposed) and bias b (may be NULL):
+ * out [length, cout], x [frames, cin]. */
+void y2o_conv(int transpose, int cin, int cout, int kernel, int stride, int padding, int dilation,
+              const float *x, int frames, const float *w, const float *b, float *out);
+/* Conv::length (src/vae.rs:147-153) */
+int y2o_conv_length(int transpose, int n, int kernel, int stride, int padding, int dilation);
+/* Op::apply of the whole list (src/vae.rs:378-397): out [*out_frames, *out_channels]
+ * (the caller sizes out from y2o_vae_length). */
+int y2o_vae_run(const y2o_vae_op *ops, int nops, const float *x, int frames, int channels, float *out,
+                int *out_frames, int *out_channels);
+int y2o_vae_length(const y2o_vae_op *ops, int nops, int frames);
 
 void y2o_mt_seed(y2o_mt *g, uint64_t seed);
 uint32_t y2o_mt_next(y2o_mt *g);

@@ -42,6 +42,14 @@ class NarS(C.Structure):
         ("layers", C.POINTER(Layer))]
 
 
+class VaeOpS(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("kind", "cin", "cout", "kernel", "stride", "padding", "dilation")] + [
+        (n, C.c_void_p) for n in ("v", "g", "b", "alpha", "beta")]
+
+
+VAE_CONV, VAE_CONVT, VAE_SNAKE, VAE_ELU, VAE_TANH, VAE_RES_BEGIN, VAE_RES_END = range(7)
+
+
 class ModelS(C.Structure):
     _fields_ = [("c", Config), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
                 ("final_norm", C.c_void_p), ("layers", C.POINTER(Layer))]
@@ -97,6 +105,10 @@ def lib() -> C.CDLL:
             "y2o_prefill": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_velocity": (i32, [vp, vp, C.POINTER(CacheS), vp, i32, f64, i32, vp]),
             "y2o_normal": (None, [C.c_uint64, i32, vp]),
+            "y2o_conv": (None, [i32, i32, i32, i32, i32, i32, i32, vp, i32, vp, vp, vp]),
+            "y2o_conv_length": (i32, [i32, i32, i32, i32, i32, i32]),
+            "y2o_vae_run": (i32, [vp, i32, vp, i32, i32, vp, vp, vp]),
+            "y2o_vae_length": (i32, [vp, i32, i32]),
             "y2o_synthesize": (i32, [vp, vp, vp, i32, vp, i32, C.c_uint64, i32, vp]),
             "y2o_mt_seed": (None, [vp, C.c_uint64]),
             "y2o_mt_next": (C.c_uint32, [vp]),
@@ -212,6 +224,54 @@ class Nar:
         if rc:
             raise RuntimeError(f"oracle error {rc}")
         return out
+
+
+def conv(transpose, x, w, b, kernel, stride, padding, dilation):
+    """Conv::apply / transposed with ready weights (src/vae.rs:165-257)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    frames, cin = x.shape
+    cout = w.shape[1] if transpose else w.shape[0]
+    n = lib().y2o_conv_length(int(transpose), frames, kernel, stride, padding, dilation)
+    out = np.empty((n, cout), np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, np.float32)
+    lib().y2o_conv(int(transpose), cin, cout, kernel, stride, padding, dilation, _p(x), frames, _p(w), _p(bb),
+                   _p(out))
+    return out
+
+
+class VaeOps:
+    """An operation list of the VAE decoder (y2o_vae_op) over numpy arrays:
+    entries (kind, dict of ints, dict of arrays)."""
+
+    def __init__(self, ops):
+        self._keep = []
+        self._ops = (VaeOpS * len(ops))()
+        for k, (kind, ints, arrs) in enumerate(ops):
+            o = self._ops[k]
+            o.kind = kind
+            for f in ("cin", "cout", "kernel", "stride", "padding", "dilation"):
+                setattr(o, f, int(ints.get(f, 0)))
+            for f in ("v", "g", "b", "alpha", "beta"):
+                a = arrs.get(f)
+                if a is not None:
+                    a = np.ascontiguousarray(a, np.float32)
+                    self._keep.append(a)
+                    setattr(o, f, a.ctypes.data)
+        self.n = len(ops)
+
+    def length(self, frames: int) -> int:
+        return lib().y2o_vae_length(self._ops, self.n, frames)
+
+    def run(self, x) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        n = self.length(x.shape[0])
+        out = np.empty(n * 4096, np.float32)  # channels of any op stay below 4096
+        fr, ch = C.c_int(0), C.c_int(0)
+        rc = lib().y2o_vae_run(self._ops, self.n, _p(x), x.shape[0], x.shape[1], _p(out), C.byref(fr), C.byref(ch))
+        if rc:
+            raise RuntimeError(f"oracle error {rc}")
+        return out[:fr.value * ch.value].reshape(fr.value, ch.value)
 
 
 def normal(seed: int, n: int) -> np.ndarray:

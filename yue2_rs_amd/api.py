@@ -117,6 +117,14 @@ def lib() -> C.CDLL:
         "yue2_hip_nar_load": (i32, [vp, vp]),
         "yue2_hip_velocity": (i32, [vp, vp, vp, i32, C.c_double, i32, vp]),
         "yue2_hip_synthesize": (i32, [vp, vp, i32, vp, i32, C.c_uint64, i32, vp]),
+        "yue2_hip_vae_open": (vp, [C.c_char_p]),
+        "yue2_hip_vae_free": (None, [vp]),
+        "yue2_hip_vae_info": (i32, [vp, vp]),
+        "yue2_hip_vae_output_length": (C.c_int64, [vp, i32]),
+        "yue2_hip_vae_required_halo": (i32, [vp, i32]),
+        "yue2_hip_vae_decode": (i32, [vp, vp, i32, vp]),
+        "yue2_hip_vae_decode_tiled": (i32, [vp, vp, i32, i32, i32, vp]),
+        "yue2_hip_selftest_conv": (i32, [i32, i32, i32, i32, i32, i32, i32, vp, i32, vp, vp, vp]),
         "yue2_hip_selftest_gemm": (i32, [vp, vp, vp, i32, i32, i32]),
         "yue2_hip_decoder_new": (vp, [vp, vp, vp, vp, u64, i32, f32, i32]),
         "yue2_hip_decoder_free": (None, [vp]),
@@ -419,6 +427,49 @@ class Cache:
     def close(self) -> None:
         if self._h:
             lib().yue2_hip_cache_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Vae:
+    """The VAE decoder (src/vae.rs:611-762) on the device."""
+
+    def __init__(self, path):
+        L = lib()
+        self._h = L.yue2_hip_vae_open(str(path).encode())
+        if not self._h:
+            raise Yue2Error(-11, L.yue2_hip_last_error().decode())
+        info = np.zeros(6, np.int32)
+        _check(L.yue2_hip_vae_info(self._h, _ptr(info)))
+        (self.sample_rate, self.latent_dim, self.audio_channels, self.downsampling_ratio, self.core_frames,
+         self.halo_frames) = (int(v) for v in info)
+
+    def output_length(self, frames: int) -> int:
+        return _check(int(lib().yue2_hip_vae_output_length(self._h, frames)))
+
+    def required_halo(self, core: int) -> int:
+        return _check(lib().yue2_hip_vae_required_halo(self._h, core))
+
+    def decode(self, z: np.ndarray) -> np.ndarray:
+        z = np.ascontiguousarray(z, dtype=np.float32)
+        out = np.empty((max(self.output_length(z.shape[0]), 0), self.audio_channels), np.float32)
+        _check(lib().yue2_hip_vae_decode(self._h, _ptr(z), z.shape[0], _ptr(out)))
+        return out
+
+    def decode_tiled(self, z: np.ndarray, core: int, halo: int) -> np.ndarray:
+        z = np.ascontiguousarray(z, dtype=np.float32)
+        out = np.empty((max(self.output_length(z.shape[0]), 0), self.audio_channels), np.float32)
+        _check(lib().yue2_hip_vae_decode_tiled(self._h, _ptr(z), z.shape[0], core, halo, _ptr(out)))
+        return out
+
+    def close(self) -> None:
+        if self._h:
+            lib().yue2_hip_vae_free(self._h)
             self._h = None
 
     def __del__(self):

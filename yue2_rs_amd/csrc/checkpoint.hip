@@ -26,6 +26,7 @@
 
 #include "../../include/yue2_hip.h"
 #include "runtime.h"
+#include "vae.h"
 #include "y2_math.h"
 
 using namespace y2;
@@ -507,6 +508,184 @@ const float* f32_data(const Tensor& t, std::vector<std::vector<float>>* keep) {
 }
 
 }  // namespace
+
+namespace y2 {
+
+// Vae::open (src/vae.rs:635-669) with network(.., decoder = true)
+// (:470-546), Conv::load (:67-146) and Activation::load (:268-281).
+int vae_read(const char* dir_c, VaeHost* out) {
+    if (!dir_c || !out) return fail(YUE2_ERR_ARG, "null VAE directory");
+    const std::string dir(dir_c);
+    std::string text, err;
+    if (!read_file(dir + "/config.json", &text)) return fail(YUE2_ERR_ARG, "cannot read " + dir + "/config.json");
+    Json v;
+    if (!parse_json(text.data(), text.size(), &v, &err)) return invalid(err);
+    if (v.kind != Json::OBJ) return invalid("Expected JSON object");
+    bool ok = true;
+    auto text_or = [&](const Json& o, const char* k, const char* d) {
+        const Json* j = o.get(k);
+        if (j && j->kind != Json::STR) ok = false;
+        return j && j->kind == Json::STR ? j->str : std::string(d);
+    };
+    auto size_or = [&](const Json& o, const char* k, size_t d) -> int {
+        const Json* j = o.get(k);
+        size_t s = d;
+        if (j && !as_size(*j, &s)) ok = false;
+        if (s > 0x7fffffff) ok = false;
+        return (int)s;
+    };
+    auto bool_or = [&](const Json& o, const char* k, bool d) {
+        const Json* j = o.get(k);
+        if (j && j->kind != Json::BOOL) ok = false;
+        return j && j->kind == Json::BOOL ? j->b : d;
+    };
+    auto sizes = [&](const Json& o, const char* k, std::vector<int>* r) {
+        const Json* j = o.get(k);
+        if (!j || j->kind != Json::ARR) return false;
+        for (const Json& e : j->arr) {
+            size_t s;
+            if (!as_size(e, &s) || s > 0x7fffffff) return false;
+            r->push_back((int)s);
+        }
+        return true;
+    };
+    if (text_or(v, "model_type", "yue2_vae") != "yue2_vae") return invalid("Expected YuE2 VAE checkpoint");
+    const Json* dc = v.get("decoder_config");
+    if (!dc || dc->kind != Json::OBJ) return invalid("Missing key decoder_config");
+    out->ratio = size_or(v, "downsampling_ratio", 1920);
+    out->latent_dim = size_or(v, "latent_dim", 64);
+    out->sample_rate = size_or(v, "sample_rate", 48000);
+    out->audio_channels = size_or(v, "audio_channels", 2);
+    out->core_frames = size_or(v, "decode_core_frames", 1024);
+    out->halo_frames = size_or(v, "decode_halo_frames", 16);
+    std::vector<int> strides, mults{1}, cm;
+    if (!sizes(*dc, "strides", &strides) || !sizes(*dc, "c_mults", &cm)) return invalid("Invalid VAE channel list");
+    mults.insert(mults.end(), cm.begin(), cm.end());
+    long prod = 1;
+    for (int st : strides) prod = std::min<long>(prod * st, 1L << 40);
+    if (prod != out->ratio || size_or(*dc, "latent_dim", 32) != out->latent_dim ||
+        size_or(*dc, "out_channels", 2) != out->audio_channels || out->sample_rate == 0)
+        return invalid("VAE configuration mismatch");
+    const int base = size_or(*dc, "channels", 128);
+    if (strides.size() + 1 != mults.size() || std::count(strides.begin(), strides.end(), 0) ||
+        std::count(mults.begin(), mults.end(), 0) || base == 0)
+        return invalid("Invalid Oobleck channel/stride configuration");
+    for (const char* k : {"antialias_activation", "use_filter", "use_nearest_upsample"})
+        if (bool_or(*dc, k, false)) return invalid(std::string("Unsupported VAE option ") + k);
+    const bool snake = bool_or(*dc, "use_snake", false);
+    if (snake && text_or(*dc, "snake_type", "vanilla") != "vanilla") return invalid("Expected vanilla SnakeBeta");
+    const int out_ch = size_or(*dc, "out_channels", 2);
+    const bool final_tanh = bool_or(*dc, "final_tanh", true);
+    if (!ok) return invalid("Invalid configuration value");
+    // Weights::open over the VAE directory
+    Checkpoint ck;
+    std::set<std::string> files;
+    std::string index_json;
+    if (read_file(dir + "/model.safetensors.index.json", &index_json)) {
+        Json iv;
+        if (!parse_json(index_json.data(), index_json.size(), &iv, &err)) return invalid(err);
+        const Json* wm = iv.get("weight_map");
+        if (!wm || wm->kind != Json::OBJ) return invalid("Missing weight_map");
+        for (const auto& kv : wm->obj) {
+            if (kv.second.kind != Json::STR) return invalid("Invalid weight_map entry");
+            files.insert(kv.second.str);
+        }
+    } else {
+        files.insert("model.safetensors");
+    }
+    for (const std::string& f : files)
+        if (int rc = open_shard(dir, f, &ck)) return rc;
+    auto f32 = [](const Tensor& t) {
+        std::vector<float> r(t.count());
+        std::memcpy(r.data(), t.bytes(), r.size() * 4);
+        return r;
+    };
+    auto conv = [&](const std::string& name, int in, int outc, int k, int stride, int pad, int dil, bool tr,
+                    bool bias) -> int {
+        const std::vector<size_t> shape = tr ? std::vector<size_t>{(size_t)in, (size_t)outc, (size_t)k}
+                                             : std::vector<size_t>{(size_t)outc, (size_t)in, (size_t)k};
+        const Tensor *tv, *tg;
+        if (int rc = checked(ck, name + ".weight_v", shape, &tv)) return rc;
+        if (int rc = checked(ck, name + ".weight_g", {shape[0], 1, 1}, &tg)) return rc;
+        if (tv->dtype != DT_F32 || tg->dtype != DT_F32) return invalid("VAE weights must remain FP32");
+        VaeOpHost op;
+        op.kind = tr ? VAE_CONVT : VAE_CONV;
+        op.cin = in;
+        op.cout = outc;
+        op.kernel = k;
+        op.stride = stride;
+        op.padding = pad;
+        op.dilation = dil;
+        op.w = f32(*tv);
+        const std::vector<float> gain = f32(*tg);
+        const size_t cols = shape[1] * (size_t)k;
+        for (size_t r = 0; r < shape[0]; ++r) {
+            float* row = op.w.data() + r * cols;
+            float ss = 0.0f;  // the sequential f32 sum of squares (src/vae.rs:89)
+            for (size_t q = 0; q < cols; ++q) ss += row[q] * row[q];
+            const float norm = std::sqrt(ss);
+            if (!std::isfinite(norm) || norm == 0.0f) return invalid("Invalid VAE weight normalization");
+            const float f = gain[r] / norm;
+            for (size_t q = 0; q < cols; ++q) row[q] *= f;
+        }
+        if (bias) {
+            const Tensor* tb;
+            if (int rc = checked(ck, name + ".bias", {(size_t)outc}, &tb)) return rc;
+            if (tb->dtype != DT_F32) return invalid("VAE bias must be FP32");
+            op.b = f32(*tb);
+        }
+        out->ops.push_back(std::move(op));
+        return YUE2_OK;
+    };
+    auto act = [&](const std::string& name, int c) -> int {
+        VaeOpHost op;
+        if (!snake) {
+            op.kind = VAE_ELU;
+            out->ops.push_back(std::move(op));
+            return YUE2_OK;
+        }
+        const Tensor *ta, *tb;
+        if (int rc = checked(ck, name + ".alpha", {(size_t)c}, &ta)) return rc;
+        if (int rc = checked(ck, name + ".beta", {(size_t)c}, &tb)) return rc;
+        if (ta->dtype != DT_F32 || tb->dtype != DT_F32) return invalid("VAE activation must be FP32");
+        op.kind = VAE_SNAKE;
+        op.cin = op.cout = c;
+        op.a = f32(*ta);
+        op.ib = f32(*tb);
+        for (float& x : op.a) x = expf(x);
+        for (float& x : op.ib) x = 1.0f / (expf(x) + 1e-9f);
+        out->ops.push_back(std::move(op));
+        return YUE2_OK;
+    };
+    out->ops.clear();
+    const std::string d = "decoder";
+    if (int rc = conv(d + ".layers.0", out->latent_dim, base * mults.back(), 7, 1, 3, 1, false, true)) return rc;
+    int index = 1;
+    for (int i = (int)mults.size() - 1; i >= 1; --i) {
+        const int in = base * mults[i], oc = base * mults[i - 1], st = strides[i - 1];
+        const std::string p = d + ".layers." + std::to_string(index) + ".layers";
+        if (int rc = act(p + ".0", in)) return rc;
+        if (int rc = conv(p + ".1", in, oc, 2 * st, st, (st + 1) / 2, 1, true, true)) return rc;
+        const int dils[3] = {1, 3, 9};
+        for (int r = 0; r < 3; ++r) {
+            // residual (src/vae.rs:427-466)
+            const std::string rp = p + "." + std::to_string(r + 2) + ".layers";
+            out->ops.push_back(VaeOpHost{VAE_RES_BEGIN});
+            if (int rc = act(rp + ".0", oc)) return rc;
+            if (int rc = conv(rp + ".1", oc, oc, 7, 1, 3 * dils[r], dils[r], false, true)) return rc;
+            if (int rc = act(rp + ".2", oc)) return rc;
+            if (int rc = conv(rp + ".3", oc, oc, 1, 1, 0, 1, false, true)) return rc;
+            out->ops.push_back(VaeOpHost{VAE_RES_END});
+        }
+        ++index;
+    }
+    if (int rc = act(d + ".layers." + std::to_string(index), base)) return rc;
+    if (int rc = conv(d + ".layers." + std::to_string(index + 1), base, out_ch, 7, 1, 3, 1, false, false)) return rc;
+    if (final_tanh) out->ops.push_back(VaeOpHost{VAE_TANH});
+    return YUE2_OK;
+}
+
+}  // namespace y2
 
 extern "C" int32_t yue2_hip_checkpoint_config(const char* dir, Yue2Config* out) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());

@@ -19,11 +19,18 @@ random-init NAR pathway): one call for 11786 latent frames after a 1000-token
 prefix, the largest chunk a 24576-position context holds (synthesize,
 src/model.rs:717-722), keys = prefix + codec chunk + the frames.
 
+VAE (the FP32 decoder at an Oobleck shape of the reference's default
+downsampling ratio 1920, random-init): one decode of a 512 + 2 x 16-frame
+tile, the reference's decode_tiled core and halo (src/pipeline.rs:279,415),
+and decode_tiled of 4500 frames (three minutes of 48 kHz audio), against the
+157.3 TFLOP/s FP32 peak.  FLOPs = 2 x the multiply-adds of every
+convolution (a transposed one: kernel taps per input row).
+
 Every timed launch reads another copy of its operands (more than 512 MB in
 total), so the 256 MB Infinity Cache cannot serve repeats.  One JSON line per
 case on stdout.
 
-    python -m yue2_rs_amd.microbench [gemv|attention|copy|gemm|prefill|nar|all]
+    python -m yue2_rs_amd.microbench [gemv|attention|copy|gemm|prefill|nar|vae|all]
 """
 from __future__ import annotations
 
@@ -37,6 +44,7 @@ from .api import _check, available, lib
 
 HBM_PEAK = 8.0e12
 MFMA_BF16_PEAK = 2.5e15
+FP32_PEAK = 157.3e12
 GEMM_SHAPES = [("qkv", 5120, 3072, 0), ("o", 3072, 3072, 0), ("gate_up", 8192, 3072, 1), ("down", 3072, 8192, 0)]
 GEMV_SHAPES = [("qkv", 5120, 3072), ("o", 3072, 3072), ("gate_up", 16384, 3072), ("down", 3072, 8192),
                ("lm_head", 84000, 3072)]
@@ -136,6 +144,59 @@ def nar(prefix: int = 1000, frames: int = 11786) -> dict:
             "frac": round(fl / dt / MFMA_BF16_PEAK, 4)}
 
 
+def vae_flops(cfg: dict, frames: int) -> float:
+    """2 x the multiply-adds of the decoder's convolutions for `frames`
+    latent rows (even strides: each block multiplies the length by its
+    stride)."""
+    d = cfg["decoder_config"]
+    ch, mults, strides = d["channels"], [1] + list(d["c_mults"]), d["strides"]
+    n, f = frames, 2.0 * d["latent_dim"] * ch * mults[-1] * 7 * frames
+    for i in range(len(mults) - 1, 0, -1):
+        cin, cout, s = ch * mults[i], ch * mults[i - 1], strides[i - 1]
+        f += 2.0 * cin * cout * 2 * s * n
+        n *= s
+        f += 3 * 2.0 * cout * cout * (7 + 1) * n
+    return f + 2.0 * ch * d["out_channels"] * 7 * n
+
+
+def vae(tile: int = 544, song: int = 4500) -> list:
+    """Wall-clock seconds of Vae::decode for one tile (the second of two
+    calls) and of decode_tiled over `song` frames, latents in host memory,
+    audio back in host memory."""
+    import tempfile
+    import time
+    from . import synthetic
+    from .api import Vae
+    cfg, t = synthetic.vae(0, **synthetic.VAE_1920)
+    with tempfile.TemporaryDirectory() as d:
+        v = Vae(synthetic.write_vae(d, cfg, t))
+    del t
+    out = []
+    try:
+        rng = np.random.default_rng(0)
+        z = rng.standard_normal((tile, cfg["latent_dim"])).astype(np.float32)
+        for _ in range(2):
+            t0 = time.perf_counter()
+            v.decode(z)
+            dt = time.perf_counter() - t0
+        fl = vae_flops(cfg, tile)
+        out.append({"frames": tile, "s": round(dt, 4), "flops": fl, "TFLOP_s": round(fl / dt / 1e12, 1),
+                    "frac": round(fl / dt / FP32_PEAK, 4)})
+        z = rng.standard_normal((song, cfg["latent_dim"])).astype(np.float32)
+        core, halo = cfg["decode_core_frames"], cfg["decode_halo_frames"]
+        t0 = time.perf_counter()
+        audio = v.decode_tiled(z, core, halo)
+        dt = time.perf_counter() - t0
+        fl = sum(vae_flops(cfg, min(song, e + halo) - max(0, s - halo))
+                 for s, e in ((s, min(s + core, song)) for s in range(0, song, core)))
+        out.append({"frames": song, "tiled": [core, halo], "audio_s": audio.shape[0] / cfg["sample_rate"],
+                    "s": round(dt, 4), "x_realtime": round(audio.shape[0] / cfg["sample_rate"] / dt, 1),
+                    "flops": fl, "TFLOP_s": round(fl / dt / 1e12, 1), "frac": round(fl / dt / FP32_PEAK, 4)})
+    finally:
+        v.close()
+    return out
+
+
 def main(argv=None) -> int:
     what = (argv or sys.argv[1:] or ["all"])[0]
     if not available():
@@ -156,6 +217,9 @@ def main(argv=None) -> int:
             print(json.dumps({"bench": "gemm", "shape": name, **gemm(2048, n, k, pair)}), flush=True)
     if what in ("nar", "all"):
         print(json.dumps({"bench": "nar_velocity", **nar()}), flush=True)
+    if what in ("vae", "all"):
+        for r in vae():
+            print(json.dumps({"bench": "vae", **r}), flush=True)
     if what in ("prefill", "all"):
         for r in prefill([2048, 24000]):
             print(json.dumps({"bench": "prefill", **r}), flush=True)

@@ -4,9 +4,15 @@ The real YuE2 checkpoint is downloaded by the reference and is not available
 offline, so the benchmark models are random-init: BF16 weights ~N(0, 0.02)
 from the library's counter-based generator, all norm gammas 1.  Prompts are
 uniform token ids from MT19937 (the reference's generator,
-src/sampling.rs:10-42): id = next_u32() mod vocab.
+src/sampling.rs:10-42): id = next_u32() mod vocab.  VAE decoders are written
+as checkpoint directories in the layout Vae::open reads (src/vae.rs:635-669)
+with numpy-generated FP32 weights.
 """
 from __future__ import annotations
+
+import json
+import struct
+from pathlib import Path
 
 import numpy as np
 
@@ -111,3 +117,79 @@ def prompt(n: int, vocab: int, seed: int = 0) -> np.ndarray:
     """n uniform token ids: MT19937(seed).next_u32() mod vocab."""
     g = MT19937(seed)
     return np.array([g.next_u32() % vocab for _ in range(n)], dtype=np.int32)
+
+
+# An Oobleck decoder at the reference's default downsampling ratio (1920,
+# src/vae.rs:643; 48 kHz audio from 25 latent frames per second) with the
+# common Oobleck widths 128 x (1, 2, 4, 8, 16).  The YuE2 VAE's own config
+# ships with its checkpoint, which is not available offline.
+VAE_1920 = dict(channels=128, c_mults=(1, 2, 4, 8, 16), strides=(2, 4, 4, 6, 10), latent=64, out_channels=2,
+                core=512, halo=16)
+
+
+def vae(seed=0, channels=8, c_mults=(2, 4), strides=(2, 4), latent=16, out_channels=2, snake=True,
+        final_tanh=True, core=8, halo=6):
+    """(config.json dict, {tensor name: FP32 array}) of a random-init decoder
+    under the reference's tensor names (network, src/vae.rs:470-546; residual
+    units, :427-466): weight-norm pairs with g in [0.5, 1.5), biases
+    ~N(0, 0.01), SnakeBeta log-parameters ~N(0, 0.04)."""
+    rng = np.random.default_rng(seed)
+    cfg = {"model_type": "yue2_vae", "latent_dim": latent, "sample_rate": 48000, "audio_channels": out_channels,
+           "downsampling_ratio": int(np.prod(strides)), "decode_core_frames": core, "decode_halo_frames": halo,
+           "decoder_config": {"channels": channels, "c_mults": list(c_mults), "strides": list(strides),
+                              "latent_dim": latent, "out_channels": out_channels, "use_snake": snake,
+                              "final_tanh": final_tanh}}
+    t = {}
+
+    def conv(name, cin, cout, k, transpose=False, bias=True):
+        shape = (cin, cout, k) if transpose else (cout, cin, k)
+        t[f"{name}.weight_v"] = rng.standard_normal(shape).astype(np.float32)
+        t[f"{name}.weight_g"] = rng.uniform(0.5, 1.5, (shape[0], 1, 1)).astype(np.float32)
+        if bias:
+            t[f"{name}.bias"] = (0.1 * rng.standard_normal(cout)).astype(np.float32)
+
+    def act(name, c):
+        if snake:
+            t[f"{name}.alpha"] = (0.2 * rng.standard_normal(c)).astype(np.float32)
+            t[f"{name}.beta"] = (0.2 * rng.standard_normal(c)).astype(np.float32)
+
+    mults = [1] + list(c_mults)
+    conv("decoder.layers.0", latent, channels * mults[-1], 7)
+    index = 1
+    for i in range(len(mults) - 1, 0, -1):
+        cin, cout, s = channels * mults[i], channels * mults[i - 1], strides[i - 1]
+        p = f"decoder.layers.{index}.layers"
+        act(f"{p}.0", cin)
+        conv(f"{p}.1", cin, cout, 2 * s, transpose=True)
+        for r in (2, 3, 4):
+            act(f"{p}.{r}.layers.0", cout)
+            conv(f"{p}.{r}.layers.1", cout, cout, 7)
+            act(f"{p}.{r}.layers.2", cout)
+            conv(f"{p}.{r}.layers.3", cout, cout, 1)
+        index += 1
+    act(f"decoder.layers.{index}", channels)
+    conv(f"decoder.layers.{index + 1}", channels, out_channels, 7, bias=False)
+    return cfg, t
+
+
+def safetensors_bytes(tensors):
+    """A safetensors file: tensors is a list of (name, dtype string, shape,
+    raw bytes), stored in that order."""
+    header, off = {}, 0
+    for name, dt, shape, data in tensors:
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(data)]}
+        off += len(data)
+    header["__metadata__"] = {"format": "pt"}
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    return struct.pack("<Q", len(h)) + h + b"".join(d for _, _, _, d in tensors)
+
+
+def write_vae(directory, cfg, tensors) -> Path:
+    """config.json and model.safetensors (FP32) of a VAE decoder."""
+    path = Path(directory)
+    path.mkdir(parents=True, exist_ok=True)
+    (path / "config.json").write_text(json.dumps(cfg))
+    items = [(n, "F32", a.shape, np.ascontiguousarray(a, np.float32).tobytes()) for n, a in sorted(tensors.items())]
+    (path / "model.safetensors").write_bytes(safetensors_bytes(items))
+    return path

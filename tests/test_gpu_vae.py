@@ -4,6 +4,9 @@ oracle's restatement (tests/test_oracle_vae.py pins it).
 - The reference's own convolution known-answer cases through the device
   convolution kernel, at the reference's tolerance 2e-6, and two transposed
   ones with kernel < stride (output phases that see no tap get the bias).
+- Shapes that reach every branch of the matrix-core (FP32 MFMA) and narrow
+  convolution kernels against a float64 convolution: max |difference|
+  <= 1e-5 (FP32 sums of at most 910 products of magnitude < 0.5).
 - Whole decodes of synthetic checkpoints written in the reference's layout
   (SnakeBeta and ELU variants; one with 256 channels, so several input
   chunks and output tiles per convolution; one without the final tanh):
@@ -24,7 +27,7 @@ from oracle import oracle as O
 import yue2_rs_amd as y2
 
 from test_oracle_vae import KAT, SPARSE, kat_case
-from vae_files import decode_f64, oracle_ops, required_halo, synthetic_vae, write_vae_dir
+from vae_files import CONV_SHAPES, conv_case, decode_f64, oracle_ops, required_halo, synthetic_vae, write_vae_dir
 
 pytestmark = pytest.mark.gpu
 
@@ -39,6 +42,23 @@ def test_convolution_known_answers(gpu, case):
                                          bias.ctypes.data, out.ctypes.data)
     assert rc == 0, y2.lib().yue2_hip_last_error().decode()
     assert np.abs(out - expected).max() < 2e-6
+
+
+def _selftest(transpose, cin, cout, kernel, stride, padding, dilation, x, w, bias, length):
+    out = np.empty((length, cout), np.float32)
+    rc = y2.lib().yue2_hip_selftest_conv(int(transpose), cin, cout, kernel, stride, padding, dilation,
+                                         x.ctypes.data, x.shape[0], np.ascontiguousarray(w).ctypes.data,
+                                         bias.ctypes.data, out.ctypes.data)
+    assert rc == 0, y2.lib().yue2_hip_last_error().decode()
+    return out
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES)
+def test_convolution_shapes(gpu, shape):
+    transpose, cin, cout, kernel, stride, padding, dilation, frames = shape
+    x, w, b, want = conv_case(*shape)
+    got = _selftest(transpose, cin, cout, kernel, stride, padding, dilation, x, w, b, want.shape[0])
+    assert np.abs(got - want).max() <= 1e-5
 
 
 CASES = {

@@ -10,6 +10,8 @@
   convolution of one-hot rows have row norms |g|.
 - Conv::length and a tiled decode equal to the whole decode on every core
   row (each output depends only on its receptive field).
+- The float64 convolution the device self-tests use, against the same
+  known answers, and the oracle's convolution against it on those shapes.
 - The whole decoder against an independent float64 evaluation: within the
   FP32 rounding the network's gain allows (1e-4 of the output scale on a
   small network; the wide one amplifies it, see the device test)."""
@@ -17,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from vae_files import decode_f64, decode_tiled, oracle_ops, required_halo, synthetic_vae
+from vae_files import CONV_SHAPES, conv_case, conv_f64, decode_f64, decode_tiled, oracle_ops, required_halo, synthetic_vae
 
 KAT = [(False, 1, 3, 1, 7), (False, 1, 9, 3, 7), (False, 2, 1, 1, 4), (True, 2, 1, 1, 4), (True, 5, 3, 1, 10),
        (True, 6, 3, 1, 12)]
@@ -120,3 +122,20 @@ def test_decoder_against_float64(kw):
     got = oracle_ops(cfg, t).run(z)
     want = decode_f64(cfg, t, z)
     assert np.abs(got - want).max() <= 1e-4 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("case", KAT + SPARSE)
+def test_float64_convolution_known_answers(case):
+    transpose, stride, padding, dilation, kernel = case
+    x, w, bias, expected = kat_case(*case)
+    got = conv_f64(transpose, x, w, bias, kernel, stride, padding, dilation)
+    assert np.abs(got - expected).max() < 1e-12
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES)
+def test_oracle_convolution_shapes(shape):
+    transpose, cin, cout, kernel, stride, padding, dilation, frames = shape
+    x, w, b, want = conv_case(*shape)
+    got = O.conv(transpose, x, w, b, kernel, stride, padding, dilation)
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() < 1e-5

@@ -158,3 +158,52 @@ def decode_f64(cfg, t, z):
         index += 1
     x = conv(act(x, f"decoder.layers.{index}"), f"decoder.layers.{index + 1}", 7, p=3, bias=False)
     return np.tanh(x) if d.get("final_tanh", True) else x
+
+
+def conv_f64(transpose, x, w, bias, kernel, stride, padding, dilation):
+    """One convolution in float64: x [frames, cin], w [cout, cin, k] (plain)
+    or [cin, cout, k] (transposed), bias [cout] or None."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    n = x.shape[0]
+    if transpose:
+        length = (n - 1) * stride + dilation * (kernel - 1) + 1 - 2 * padding
+        y = np.zeros((length, w.shape[1]))
+        for j in range(kernel):
+            rows = np.arange(n) * stride + j * dilation - padding
+            ok = (rows >= 0) & (rows < length)
+            np.add.at(y, rows[ok], x[ok] @ w[:, :, j])
+    else:
+        length = (n + 2 * padding - dilation * (kernel - 1) - 1) // stride + 1
+        y = np.zeros((length, w.shape[0]))
+        for j in range(kernel):
+            src = np.arange(length) * stride + j * dilation - padding
+            ok = (src >= 0) & (src < n)
+            y[ok] += x[src[ok]] @ w[:, :, j].T
+    if bias is not None:
+        y += np.asarray(bias, np.float64)
+    return y
+
+
+# (transpose, cin, cout, kernel, stride, padding, dilation, frames): shapes
+# that reach every branch of the device convolutions -- the matrix-core
+# kernel with 16-byte and scalar input loads, several output-channel tiles,
+# ten phases, phases without a tap and a strided plain convolution; the
+# narrow kernel with several row tiles and a ragged channel chunk.
+CONV_SHAPES = [
+    (False, 20, 40, 7, 1, 9, 3, 300),
+    (False, 6, 130, 7, 1, 3, 1, 200),
+    (True, 24, 64, 20, 10, 5, 1, 40),
+    (True, 16, 33, 2, 4, 0, 1, 50),
+    (False, 8, 48, 4, 2, 1, 1, 300),
+    (False, 130, 3, 7, 1, 27, 9, 600),
+    (False, 64, 16, 7, 1, 3, 1, 100),
+]
+
+
+def conv_case(transpose, cin, cout, kernel, stride, padding, dilation, frames, seed=0):
+    rng = np.random.default_rng(seed)
+    x = (0.5 * rng.standard_normal((frames, cin))).astype(np.float32)
+    w = (0.1 * rng.standard_normal((cin, cout, kernel) if transpose else (cout, cin, kernel))).astype(np.float32)
+    b = (0.1 * rng.standard_normal(cout)).astype(np.float32)
+    return x, w, b, conv_f64(transpose, x, w, b, kernel, stride, padding, dilation)

@@ -8,16 +8,24 @@
 // a 7-tap convolution to the audio channels and tanh.  Everything is FP32,
 // as the reference's MPSGraph and eager paths are.
 //
-// One kernel computes every convolution: output rows o0 + ostride * m take
-// the sum over taps q and input channels i of x[m * istride + off_q][i] *
-// W_q[i][o] (+ bias, + the residual input).  A plain convolution is one
-// launch (ostride 1, istride = stride, off_q = q * dilation - padding); a
-// transposed one is one launch per output phase p < stride, whose rows
-// p + stride * m see exactly the taps j = (p + padding) mod stride + q *
-// stride at source rows m + (p + padding - j) / stride -- the polyphase form
-// of the reference's per-phase packing (src/vae.rs:107-126).  Each 64 x 64
-// output tile stages 16 input channels of its source rows and the taps'
-// weights in LDS; each thread keeps a 4 x 4 block of outputs.
+// Every convolution is a GEMM over output rows o0 + ostride * m: the sum
+// over taps q and input channels i of x[m * istride + off_q][i] * W_q[i][o]
+// (+ bias, + the residual input).  A plain convolution has one phase
+// (ostride 1, istride = stride, off_q = q * dilation - padding); a
+// transposed one has `stride` phases, launched together, whose rows p +
+// stride * m see exactly the taps j = (p + padding) mod stride + q * stride
+// at source rows m + (p + padding - j) / stride -- the polyphase form of the
+// reference's per-phase packing (src/vae.rs:107-126).  The activation
+// before a convolution (SnakeBeta or ELU) is applied while its input is
+// staged, and a final tanh in the epilogue, so activations never make a
+// round trip through HBM.
+//
+// conv_mfma_kernel: 128 x 128 output tiles, 4 waves of 2 x 2 FP32 MFMA
+// blocks (v_mfma_f32_32x32x2_f32); per 8-channel chunk the source rows and
+// every tap's weights are staged in LDS (52 KB for 7 taps: two workgroups
+// per CU); step t of a chunk feeds lane half h channel 4h + t, so each lane
+// reads its 4 channels with one 16-byte LDS load.  conv_narrow_kernel: outputs with at most 16 channels (the audio
+// projection), one output row per thread on the vector ALUs.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -34,78 +42,297 @@ using namespace y2;
 namespace y2 {
 namespace {
 
-constexpr int kConvTile = 64, kConvChunk = 16, kConvTaps = 8, kConvSpan = 256;
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-struct ConvArgs {
-    const float* x;
-    int rows_in, cin;
-    const float* w;  // tap slabs [k][cin][cout]
-    const float* b;  // [cout] or null
-    const float* res;  // added to the output (same layout) or null
-    float* y;
-    int cout, m_count, istride, ostride, o0, ntaps, off_min;
-    int off[kConvTaps], slab[kConvTaps];
+constexpr int kMaxTaps = 8, kMaxPhases = 16;
+constexpr int kMmaTile = 128;
+constexpr int kChunk = 16, kNarrowRows = 256, kNarrowPad = 17;
+constexpr size_t kMaxLds = 160 * 1024;
+enum { ACT_NONE = 0, ACT_SNAKE = 1, ACT_ELU = 2 };
+
+struct ConvPlan {
+    const float* x;         // [rows_in][cin]
+    const float* w;         // tap slabs in the kernel's layout
+    const float* b;         // [cout] or null
+    const float* res;       // [rows][cout] added to the output, or null
+    float* y;               // [rows][cout]
+    const float* alpha;     // SnakeBeta exp(alpha), 1 / (exp(beta) + 1e-9) per input channel
+    const float* inv_beta;
+    int rows_in, cin, cin_pad, cout, cout_pad, istride, ostride, tanh_out, span, ltaps;
+    int m_count[kMaxPhases], o0[kMaxPhases], ntaps[kMaxPhases], off_min[kMaxPhases];
+    int off[kMaxPhases][kMaxTaps], slab[kMaxPhases][kMaxTaps];
 };
 
-__global__ __launch_bounds__(256) void conv_kernel(const ConvArgs a) {
-    __shared__ float xs[kConvSpan][kConvChunk];
-    __shared__ __align__(16) float ws[kConvTaps][kConvChunk][kConvTile];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-    const int m0 = blockIdx.x * kConvTile, c0 = blockIdx.y * kConvTile;
-    const int src_lo = m0 * a.istride + a.off_min;
-    int off_max = a.off_min;
-    for (int q = 0; q < a.ntaps; ++q) off_max = max(off_max, a.off[q]);
-    const int span = (kConvTile - 1) * a.istride + off_max - a.off_min + 1;
-    float acc[4][4];
+// Conv::apply's product, then the bias; Op::Residual's h + x; the final tanh.
+__device__ __forceinline__ void conv_store(const ConvPlan& p, int m, int o, float acc) {
+    const size_t at = (size_t)(p.o0[blockIdx.z] + p.ostride * m) * p.cout + o;
+    float v = acc + (p.b ? p.b[o] : 0.0f);
+    if (p.res) v = v + p.res[at];
+    if (p.tanh_out) v = tanhf(v);
+    p.y[at] = v;
+}
+
+// Rows [src_lo, src_lo + span) x channels [c0, c0 + 16) of the input,
+// activated as Activation::apply does (src/vae.rs:282-320), into LDS rows
+// of kNarrowPad floats; zero outside the input.  (Batching every thread's
+// loads ahead of their use measured slower here: the extra registers halve
+// the occupancy that hides this kernel's latency.)
+template <int ACT>
+__device__ __forceinline__ void stage_rows(const ConvPlan& p, float* X, int src_lo, int c0) {
+    for (int u = threadIdx.x; u < p.span * 4; u += blockDim.x) {
+        const int r = u >> 2, ch = c0 + 4 * (u & 3), src = src_lo + r;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (src >= 0 && src < p.rows_in) {
+            const float* row = p.x + (size_t)src * p.cin;
+            if ((p.cin & 3) == 0) {
+                if (ch < p.cin) {
+                    const float4 t = *reinterpret_cast<const float4*>(row + ch);
+                    v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+                }
+            } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+                for (int e = 0; e < 4; ++e)
+                    if (ch + e < p.cin) v[e] = row[ch + e];
+            }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
-    for (int i0 = 0; i0 < a.cin; i0 += kConvChunk) {
-        for (int u = tid; u < span * kConvChunk; u += 256) {
-            const int r = u / kConvChunk, c = u % kConvChunk, src = src_lo + r, i = i0 + c;
-            xs[r][c] = src >= 0 && src < a.rows_in && i < a.cin ? a.x[(size_t)src * a.cin + i] : 0.0f;
+            for (int e = 0; e < 4; ++e)
+                if (ch + e < p.cin) {
+                    if constexpr (ACT == ACT_SNAKE) {
+                        const float t = sinf(v[e] * p.alpha[ch + e]);
+                        v[e] = v[e] + p.inv_beta[ch + e] * (t * t);
+                    } else if constexpr (ACT == ACT_ELU) {
+                        v[e] = v[e] < 0.0f ? expf(v[e]) - 1.0f : v[e];
+                    }
+                }
         }
-        for (int u = tid; u < a.ntaps * kConvChunk * kConvTile; u += 256) {
-            const int q = u / (kConvChunk * kConvTile), c = (u / kConvTile) % kConvChunk, o = u % kConvTile;
-            const int i = i0 + c, oc = c0 + o;
-            ws[q][c][o] = i < a.cin && oc < a.cout ? a.w[((size_t)a.slab[q] * a.cin + i) * a.cout + oc] : 0.0f;
-        }
-        __syncthreads();
-        for (int q = 0; q < a.ntaps; ++q) {
-            const int base = a.off[q] - a.off_min;
-#pragma unroll 4
-            for (int c = 0; c < kConvChunk; ++c) {
-                const float4 wv = *reinterpret_cast<const float4*>(&ws[q][c][tx * 4]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float xv = xs[(ty * 4 + r) * a.istride + base][c];
-                    acc[r][0] = __builtin_fmaf(xv, wv.x, acc[r][0]);
-                    acc[r][1] = __builtin_fmaf(xv, wv.y, acc[r][1]);
-                    acc[r][2] = __builtin_fmaf(xv, wv.z, acc[r][2]);
-                    acc[r][3] = __builtin_fmaf(xv, wv.w, acc[r][3]);
+        for (int e = 0; e < 4; ++e) X[r * kNarrowPad + 4 * (u & 3) + e] = v[e];
+    }
+}
+
+// Weight slabs [k][cin_pad / KC][cout_pad][KC]; x [rows][cin], y [rows][cout].
+// Chunk ck + 1's rows and weights are loaded into registers while chunk
+// ck's MFMAs run, then activated and written to LDS between two barriers.
+// KC = 8 for up to 8 taps (52 KB of LDS for 7), KC = 32 for up to 2 (the
+// 1-tap and the transposed convolutions).  NT > 0: exactly NT taps in every
+// phase, so the (tap, group) steps unroll without branches; NT = 0: up to
+// 8 taps, counted per phase.  VEC: cin % 4 == 0, 16-byte source loads.
+template <int ACT, int NT, int KC, bool VEC>
+__global__ __launch_bounds__(256, 2) void conv_mfma_kernel(const ConvPlan p) {
+    constexpr int MAXT = NT > 0 ? NT : kMaxTaps;
+    constexpr int PITCH = KC + 4, G = KC / 4;  // LDS row pitch (floats), float4 groups per row
+    constexpr int XS = KC == 8 ? 3 : NT == 1 ? 4 : 5;  // float4 slots per thread for the source rows
+    constexpr int WE = KC / 8;                 // float4 slots per thread per tap; MFMA groups per tap
+    extern __shared__ __align__(16) float lds[];
+    float* W = lds;                                    // [ltaps][128][PITCH]
+    float* X = lds + p.ltaps * kMmaTile * PITCH;       // [span][PITCH]
+    const int ph = blockIdx.z, m_count = p.m_count[ph];
+    const int m0 = blockIdx.x * kMmaTile, n0 = blockIdx.y * kMmaTile;
+    if (m0 >= m_count) return;
+    const int ntaps = NT > 0 ? NT : p.ntaps[ph];
+    const int src_lo = m0 * p.istride + p.off_min[ph], nchunks = p.cin_pad / KC;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+    const int wm = wave >> 1, wn = wave & 1;
+    int offs[MAXT], slabs[MAXT];
+#pragma unroll
+    for (int q = 0; q < MAXT; ++q) {
+        offs[q] = p.off[ph][q] - p.off_min[ph];
+        slabs[q] = p.slab[ph][q];
+    }
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    // source-row slot s: item u = tid + 256 s (row u / G, channels 4 (u % G) ..); weight slot q WE + e:
+    // item tid + 256 e of tap q (output row n0 + item / G, channels 4 (item % G) ..)
+    f32x4 xr[XS], wr[MAXT * WE], ar = {}, br = {};
+    for (int ck = -1; ck < nchunks; ++ck) {
+        const int nx = ck + 1;
+        if (nx < nchunks) {
+            // unconditional loads from clamped addresses (a conditional load would make the
+            // compiler wait for every load where the branches join); the store zeroes what lies
+            // outside the input
+            const int c0 = nx * KC, ch = c0 + 4 * (tid % G);
+#pragma unroll
+            for (int s = 0; s < XS; ++s) {
+                const int u = tid + 256 * s, src = min(max(src_lo + u / G, 0), p.rows_in - 1);
+                const float* row = p.x + (size_t)src * p.cin;
+                if constexpr (VEC) {
+                    xr[s] = *reinterpret_cast<const f32x4*>(row + min(ch, p.cin - 4));
+                } else {
+                    xr[s] = f32x4{row[min(ch, p.cin - 1)], row[min(ch + 1, p.cin - 1)], row[min(ch + 2, p.cin - 1)],
+                                  row[min(ch + 3, p.cin - 1)]};
+                }
+            }
+            if constexpr (ACT == ACT_SNAKE) {
+                if constexpr (VEC) {
+                    ar = *reinterpret_cast<const f32x4*>(p.alpha + min(ch, p.cin - 4));
+                    br = *reinterpret_cast<const f32x4*>(p.inv_beta + min(ch, p.cin - 4));
+                } else {
+                    const int l = p.cin - 1;
+                    ar = f32x4{p.alpha[min(ch, l)], p.alpha[min(ch + 1, l)], p.alpha[min(ch + 2, l)],
+                               p.alpha[min(ch + 3, l)]};
+                    br = f32x4{p.inv_beta[min(ch, l)], p.inv_beta[min(ch + 1, l)], p.inv_beta[min(ch + 2, l)],
+                               p.inv_beta[min(ch + 3, l)]};
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < MAXT; ++q)
+                if (NT > 0 || q < ntaps)
+#pragma unroll
+                    for (int e = 0; e < WE; ++e) {
+                        const int it = tid + 256 * e;
+                        wr[q * WE + e] = *reinterpret_cast<const f32x4*>(
+                            p.w + (((size_t)slabs[q] * nchunks + nx) * p.cout_pad + n0 + it / G) * KC + 4 * (it % G));
+                    }
+        }
+        if (ck >= 0) {
+            // step (q, g): lane half h supplies channels (KC / 2) h + 4 g .. + 3 of the chunk, to A and B alike
+#pragma unroll
+            for (int k = 0; k < MAXT * WE; ++k) {
+                const int q = k / WE, g = k % WE;
+                if (NT > 0 || q < ntaps) {
+                    f32x4 a[2], b[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        a[i] = *reinterpret_cast<const f32x4*>(
+                            X + ((wm * 64 + i * 32 + l32) * p.istride + offs[q]) * PITCH + (KC / 2) * h + 4 * g);
+                        b[i] = *reinterpret_cast<const f32x4*>(W + (q * kMmaTile + wn * 64 + i * 32 + l32) * PITCH +
+                                                                (KC / 2) * h + 4 * g);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
                 }
             }
         }
         __syncthreads();
-    }
+        if (nx < nchunks) {
+            const int c0 = nx * KC, ch = c0 + 4 * (tid % G);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = m0 + ty * 4 + r;
-        if (m >= a.m_count) continue;
-        const size_t row = (size_t)(a.o0 + a.ostride * m) * a.cout;
+            for (int s = 0; s < XS; ++s) {
+                const int u = tid + 256 * s, src = src_lo + u / G;
+                if (u < p.span * G) {
+                    f32x4 v = xr[s];
+                    if constexpr (ACT == ACT_SNAKE) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int o = c0 + tx * 4 + c;
-            if (o >= a.cout) continue;
-            float v = acc[r][c] + (a.b ? a.b[o] : 0.0f);  // Conv::apply: the product, then the bias
-            if (a.res) v = v + a.res[row + o];           // Op::Residual: h + x
-            a.y[row + o] = v;
+                        for (int e = 0; e < 4; ++e) {
+                            const float t = sinf(v[e] * ar[e]);
+                            v[e] = v[e] + br[e] * (t * t);
+                        }
+                    } else if constexpr (ACT == ACT_ELU) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = v[e] < 0.0f ? expf(v[e]) - 1.0f : v[e];
+                    }
+                    const bool row_ok = src >= 0 && src < p.rows_in;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (!row_ok || ch + e >= p.cin) v[e] = 0.0f;
+                    *reinterpret_cast<f32x4*>(X + (u / G) * PITCH + 4 * (u % G)) = v;
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < MAXT; ++q)
+                if (NT > 0 || q < ntaps)
+#pragma unroll
+                    for (int e = 0; e < WE; ++e) {
+                        const int it = tid + 256 * e;
+                        *reinterpret_cast<f32x4*>(W + (q * kMmaTile + it / G) * PITCH + 4 * (it % G)) =
+                            wr[q * WE + e];
+                    }
+            __syncthreads();
         }
     }
+    // C layout of the 32 x 32 blocks: register r of lane l is row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32.  A block's 16 residual values are
+    // requested together (clamped addresses), then added and stored.
+    const int ostride = p.ostride, o0 = p.o0[ph], cout = p.cout;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int o = n0 + wn * 64 + j * 32 + l32, oc = min(o, cout - 1);
+            const float bias = p.b ? p.b[oc] : 0.0f;
+            float rv[16];
+            if (p.res) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = min(m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3), m_count - 1);
+                    rv[r] = p.res[(size_t)(o0 + ostride * m) * cout + oc];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < m_count && o < cout) {
+                    float v = acc[i][j][r] + bias;  // Conv::apply: the product, then the bias
+                    if (p.res) v = v + rv[r];       // Op::Residual: h + x
+                    if (p.tanh_out) v = tanhf(v);
+                    p.y[(size_t)(o0 + ostride * m) * cout + o] = v;
+                }
+            }
+        }
 }
 
-// Activation::apply (src/vae.rs:282-320), out of place.
+// Weight slabs [k][cin_pad][CO]; one output row per thread.
+template <int CO, int ACT>
+__global__ __launch_bounds__(256) void conv_narrow_kernel(const ConvPlan p) {
+    extern __shared__ __align__(16) float lds[];
+    float* W = lds;                                  // [ltaps][16][CO]
+    float* X = lds + p.ltaps * kChunk * CO;          // [span][kNarrowPad]
+    const int ph = blockIdx.z, m_count = p.m_count[ph], m0 = blockIdx.x * kNarrowRows;
+    if (m0 >= m_count) return;
+    const int ntaps = p.ntaps[ph], src_lo = m0 * p.istride + p.off_min[ph], tid = threadIdx.x;
+    float acc[CO];
+#pragma unroll
+    for (int o = 0; o < CO; ++o) acc[o] = 0.0f;
+    for (int c0 = 0; c0 < p.cin_pad; c0 += kChunk) {
+        stage_rows<ACT>(p, X, src_lo, c0);
+        for (int u = tid; u < ntaps * kChunk * CO; u += 256) {
+            const int q = u / (kChunk * CO), rest = u % (kChunk * CO);
+            W[u] = p.w[((size_t)p.slab[ph][q] * p.cin_pad + c0) * CO + rest];
+        }
+        __syncthreads();
+        for (int q = 0; q < ntaps; ++q) {
+            const float* xr = X + (tid * p.istride + p.off[ph][q] - p.off_min[ph]) * kNarrowPad;
+#pragma unroll 4
+            for (int c = 0; c < kChunk; ++c) {
+                const float xv = xr[c];
+#pragma unroll
+                for (int o = 0; o < CO; ++o) acc[o] = __builtin_fmaf(xv, W[(q * kChunk + c) * CO + o], acc[o]);
+            }
+        }
+        __syncthreads();
+    }
+    const int m = m0 + tid;
+    if (m < m_count)
+#pragma unroll
+        for (int o = 0; o < CO; ++o)
+            if (o < p.cout) conv_store(p, m, o, acc[o]);
+}
+
+// An activation that no convolution follows, out of place.
 __global__ __launch_bounds__(256) void activation_kernel(const float* x, float* y, size_t n, int c, int kind,
                                                          const float* alpha, const float* inv_beta) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
@@ -133,62 +360,149 @@ int conv_length(const VaeOpHost& op, int n) {
     return (n + 2 * op.padding - op.dilation * (op.kernel - 1) - 1) / op.stride + 1;
 }
 
-hipError_t launch_conv(hipStream_t s, ConvArgs a) {
-    if (a.m_count <= 0) return hipSuccess;
-    if (a.ntaps == 0) a.off[0] = 0;  // no tap: the rows get the bias (and the residual) only
-    a.off_min = a.off[0];
-    int off_max = a.off[0];
-    for (int q = 1; q < a.ntaps; ++q) {
-        a.off_min = std::min(a.off_min, a.off[q]);
-        off_max = std::max(off_max, a.off[q]);
-    }
-    if (a.ntaps < 0 || a.ntaps > kConvTaps || (kConvTile - 1) * a.istride + off_max - a.off_min + 1 > kConvSpan)
-        return hipErrorInvalidValue;
-    const dim3 grid((a.m_count + kConvTile - 1) / kConvTile, (a.cout + kConvTile - 1) / kConvTile);
-    conv_kernel<<<grid, 256, 0, s>>>(a);
-    return hipGetLastError();
+// The device form of one convolution: which kernel, its channel chunk and
+// padded widths.
+struct ConvShape {
+    bool mfma = false;
+    int chunk = kChunk, cin_pad = 0, cout_pad = 0;
+};
+
+// Source rows a 128-row output tile reads: at most 160 (32-channel chunks)
+// or 384 (8-channel chunks), from the register slots of the kernel.
+int mfma_span(const VaeOpHost& op) {
+    if (op.kind == VAE_CONVT) return kMmaTile - 1 + (op.kernel - 1) / op.stride + 1;
+    return (kMmaTile - 1) * op.stride + op.dilation * (op.kernel - 1) + 1;
 }
 
-// One convolution (plain or transposed) of x [n, cin] into y [length, cout]
-// with device tap slabs w [k][cin][cout].
-hipError_t run_conv(hipStream_t s, const VaeOpHost& op, const float* w, const float* b, const float* x, int n,
-                    float* y, const float* res) {
-    const int len = conv_length(op, n);
-    if (op.kind == VAE_CONV) {
-        if (op.kernel > kConvTaps) return hipErrorInvalidValue;
-        ConvArgs a{x, n, op.cin, w, b, res, y, op.cout, len, op.stride, 1, 0, op.kernel};
-        for (int q = 0; q < op.kernel; ++q) {
-            a.off[q] = q * op.dilation - op.padding;
-            a.slab[q] = q;
-        }
-        return launch_conv(s, a);
-    }
-    if (op.dilation != 1) return hipErrorInvalidValue;
-    for (int ph = 0; ph < op.stride; ++ph) {
-        ConvArgs a{x, n, op.cin, w, b, res, y, op.cout, (len - ph + op.stride - 1) / op.stride, 1, op.stride, ph, 0};
-        for (int j = (ph + op.padding) % op.stride; j < op.kernel; j += op.stride) {
-            if (a.ntaps == kConvTaps) return hipErrorInvalidValue;
-            a.off[a.ntaps] = (ph + op.padding - j) / op.stride;  // exact: j = ph + padding (mod stride)
-            a.slab[a.ntaps] = j;
-            ++a.ntaps;
-        }
-        if (hipError_t e = launch_conv(s, a); e != hipSuccess) return e;
-    }
-    return hipSuccess;
+ConvShape conv_shape(const VaeOpHost& op) {
+    ConvShape c;
+    c.mfma = op.cout > 16;
+    const int taps = op.kind == VAE_CONVT ? (op.kernel + op.stride - 1) / op.stride : op.kernel;
+    const bool uniform = op.kind == VAE_CONV || op.kernel % op.stride == 0;  // every phase has `taps` taps
+    c.chunk = !c.mfma ? kChunk : taps <= 2 && uniform && op.cin % 4 == 0 && mfma_span(op) <= 160 ? 32 : 8;
+    c.cin_pad = (op.cin + c.chunk - 1) / c.chunk * c.chunk;
+    c.cout_pad = c.mfma ? (op.cout + kMmaTile - 1) / kMmaTile * kMmaTile : op.cout <= 2 ? 2 : op.cout <= 4 ? 4
+                                                                         : op.cout <= 8 ? 8 : 16;
+    return c;
 }
 
-// Tap slabs [k][cin][cout] from the checkpoint layout ([out, in, k] or, for
-// a transposed convolution, [in, out, k]).
-std::vector<float> tap_slabs(const VaeOpHost& op) {
-    std::vector<float> t((size_t)op.kernel * op.cin * op.cout);
+// Tap slabs in the kernel's layout from the checkpoint layout ([out, in, k]
+// or, for a transposed convolution, [in, out, k]); zero padding.
+std::vector<float> conv_slabs(const VaeOpHost& op, const ConvShape& c) {
+    std::vector<float> t((size_t)op.kernel * c.cin_pad * c.cout_pad, 0.0f);
+    const int nchunks = c.cin_pad / c.chunk;
     for (int o = 0; o < op.cout; ++o)
         for (int i = 0; i < op.cin; ++i)
             for (int j = 0; j < op.kernel; ++j) {
                 const size_t src = op.kind == VAE_CONVT ? ((size_t)i * op.cout + o) * op.kernel + j
                                                         : ((size_t)o * op.cin + i) * op.kernel + j;
-                t[((size_t)j * op.cin + i) * op.cout + o] = op.w[src];
+                const size_t dst = c.mfma ? ((((size_t)j * nchunks + i / c.chunk) * c.cout_pad + o) * c.chunk +
+                                             i % c.chunk)
+                                          : (((size_t)j * c.cin_pad + i) * c.cout_pad + o);
+                t[dst] = op.w[src];
             }
     return t;
+}
+
+template <typename K>
+hipError_t launch(K kernel, dim3 grid, size_t lds, hipStream_t s, const ConvPlan& p) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+    kernel<<<grid, 256, lds, s>>>(p);
+    return hipGetLastError();
+}
+
+// One convolution (plain or transposed) of x [n, cin] into y [length, cout]:
+// act is the activation applied to x on the way in (ACT_*, SnakeBeta's
+// folded parameters), res the residual added to the output, tanh_out the
+// final tanh.
+hipError_t run_conv(hipStream_t s, const VaeOpHost& op, const ConvShape& c, const float* w, const float* b,
+                    const float* x, int n, float* y, const float* res, int act, const float* alpha,
+                    const float* inv_beta, bool tanh_out) {
+    const int len = conv_length(op, n);
+    if (len <= 0) return hipErrorInvalidValue;
+    ConvPlan p{};
+    p.x = x, p.w = w, p.b = b, p.res = res, p.y = y, p.alpha = alpha, p.inv_beta = inv_beta;
+    p.rows_in = n, p.cin = op.cin, p.cin_pad = c.cin_pad, p.cout = op.cout, p.cout_pad = c.cout_pad;
+    p.tanh_out = tanh_out ? 1 : 0;
+    int phases = 1;
+    if (op.kind == VAE_CONV) {
+        if (op.kernel > kMaxTaps) return hipErrorInvalidValue;
+        p.istride = op.stride, p.ostride = 1, p.m_count[0] = len, p.ntaps[0] = op.kernel;
+        for (int q = 0; q < op.kernel; ++q) {
+            p.off[0][q] = q * op.dilation - op.padding;
+            p.slab[0][q] = q;
+        }
+    } else {
+        if (op.dilation != 1 || op.stride > kMaxPhases) return hipErrorInvalidValue;
+        phases = op.stride, p.istride = 1, p.ostride = op.stride;
+        for (int ph = 0; ph < phases; ++ph) {
+            p.o0[ph] = ph;
+            p.m_count[ph] = std::max(0, (len - ph + op.stride - 1) / op.stride);
+            for (int j = (ph + op.padding) % op.stride; j < op.kernel; j += op.stride) {
+                if (p.ntaps[ph] == kMaxTaps) return hipErrorInvalidValue;
+                p.off[ph][p.ntaps[ph]] = (ph + op.padding - j) / op.stride;  // exact: j = ph + padding (mod stride)
+                p.slab[ph][p.ntaps[ph]] = j;
+                ++p.ntaps[ph];
+            }
+        }
+    }
+    const int tile = c.mfma ? kMmaTile : kNarrowRows;
+    int mtiles = 0;
+    for (int ph = 0; ph < phases; ++ph) {
+        int lo = 0, hi = 0;
+        if (p.ntaps[ph] > 0) lo = hi = p.off[ph][0];
+        for (int q = 1; q < p.ntaps[ph]; ++q) {
+            lo = std::min(lo, p.off[ph][q]);
+            hi = std::max(hi, p.off[ph][q]);
+        }
+        p.off_min[ph] = lo;
+        p.span = std::max(p.span, (tile - 1) * p.istride + hi - lo + 1);
+        p.ltaps = std::max(p.ltaps, p.ntaps[ph]);
+        mtiles = std::max(mtiles, (p.m_count[ph] + tile - 1) / tile);
+    }
+    if (mtiles == 0) return hipSuccess;
+    const size_t pitch = c.chunk + 4;
+    const size_t lds = c.mfma ? sizeof(float) * ((size_t)p.ltaps * kMmaTile * pitch + (size_t)p.span * pitch)
+                              : sizeof(float) * ((size_t)p.ltaps * kChunk * c.cout_pad + (size_t)p.span * kNarrowPad);
+    if (lds > kMaxLds) return hipErrorInvalidValue;
+    if (c.mfma) {
+        const dim3 grid(mtiles, c.cout_pad / kMmaTile, phases);
+#define Y2_MFMA(T, KC, VEC)                                                                           \
+    {                                                                                                 \
+        if (act == ACT_SNAKE) return launch(conv_mfma_kernel<ACT_SNAKE, T, KC, VEC>, grid, lds, s, p); \
+        if (act == ACT_ELU) return launch(conv_mfma_kernel<ACT_ELU, T, KC, VEC>, grid, lds, s, p);     \
+        return launch(conv_mfma_kernel<ACT_NONE, T, KC, VEC>, grid, lds, s, p);                       \
+    }
+        // the kernels' register slots hold span * KC / 4 source floats4 over 256 threads
+        bool same = true;  // every phase has ltaps taps
+        for (int ph = 0; ph < phases; ++ph) same = same && p.ntaps[ph] == p.ltaps;
+        const bool vec = op.cin % 4 == 0;
+        if (c.chunk == 32 && vec) {
+            if (same && p.ltaps == 1 && p.span * 8 <= 4 * 256) Y2_MFMA(1, 32, true)
+            if (same && p.ltaps == 2 && p.span * 8 <= 5 * 256) Y2_MFMA(2, 32, true)
+        }
+        if (c.chunk == 8 && p.span * 2 <= 3 * 256) {
+            if (same && p.ltaps == 7 && vec) Y2_MFMA(7, 8, true)
+            if (p.ltaps <= kMaxTaps && vec) Y2_MFMA(0, 8, true)
+            if (p.ltaps <= kMaxTaps) Y2_MFMA(0, 8, false)
+        }
+#undef Y2_MFMA
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(mtiles, 1, phases);
+#define Y2_NARROW(CO)                                                                       \
+    if (c.cout_pad == CO) {                                                                 \
+        if (act == ACT_SNAKE) return launch(conv_narrow_kernel<CO, ACT_SNAKE>, grid, lds, s, p); \
+        if (act == ACT_ELU) return launch(conv_narrow_kernel<CO, ACT_ELU>, grid, lds, s, p);     \
+        return launch(conv_narrow_kernel<CO, ACT_NONE>, grid, lds, s, p);                   \
+    }
+    Y2_NARROW(2)
+    Y2_NARROW(4)
+    Y2_NARROW(8)
+    Y2_NARROW(16)
+#undef Y2_NARROW
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -197,7 +511,10 @@ std::vector<float> tap_slabs(const VaeOpHost& op) {
 struct Yue2Vae {
     y2::VaeHost host;
     std::vector<float*> w, b, a, ib;  // per op, device
+    std::vector<y2::ConvShape> shape;  // per op: the convolution's kernel and padded widths
     void* block = nullptr;
+    void* acts = nullptr;  // three activation buffers, kept between calls
+    size_t acts_bytes = 0;
     hipStream_t stream = nullptr;
 };
 
@@ -206,6 +523,7 @@ extern "C" void yue2_hip_vae_free(Yue2Vae* v) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (v->stream) (void)hipStreamSynchronize(v->stream);
     if (v->block) (void)hipFree(v->block);
+    if (v->acts) (void)hipFree(v->acts);
     if (v->stream) (void)hipStreamDestroy(v->stream);
     delete v;
 }
@@ -230,9 +548,11 @@ extern "C" Yue2Vae* yue2_hip_vae_open(const char* dir) {
     };
     const size_t nops = v->host.ops.size();
     std::vector<size_t> ow(nops), ob(nops), oa(nops), oi(nops);
+    v->shape.assign(nops, ConvShape{});
     for (size_t k = 0; k < nops; ++k) {
         const VaeOpHost& op = v->host.ops[k];
-        ow[k] = take(op.w.size());
+        if (op.kind == VAE_CONV || op.kind == VAE_CONVT) v->shape[k] = conv_shape(op);
+        ow[k] = take((size_t)op.kernel * v->shape[k].cin_pad * v->shape[k].cout_pad);
         ob[k] = take(op.b.size());
         oa[k] = take(op.a.size());
         oi[k] = take(op.ib.size());
@@ -256,7 +576,7 @@ extern "C" Yue2Vae* yue2_hip_vae_open(const char* dir) {
             *dst = reinterpret_cast<float*>(base + off);
             e = hipMemcpy(*dst, src.data(), src.size() * sizeof(float), hipMemcpyHostToDevice);
         };
-        if (op.kind == VAE_CONV || op.kind == VAE_CONVT) up(tap_slabs(op), ow[k], &v->w[k]);
+        if (op.kind == VAE_CONV || op.kind == VAE_CONVT) up(conv_slabs(op, v->shape[k]), ow[k], &v->w[k]);
         up(op.b, ob[k], &v->b[k]);
         up(op.a, oa[k], &v->a[k]);
         up(op.ib, oi[k], &v->ib[k]);
@@ -327,7 +647,10 @@ extern "C" int32_t yue2_hip_vae_required_halo(const Yue2Vae* v, int32_t core) {
 namespace {
 
 // Vae::decode's network on the device (src/vae.rs:688-727): z [frames,
-// latent] -> out [length, audio channels].
+// latent] -> out [length, audio channels].  An activation that a
+// convolution follows is applied inside that convolution, a residual unit's
+// sum in its last convolution's epilogue, a final tanh in the last
+// convolution's.
 int vae_decode(Yue2Vae* v, const float* z, int frames, float* out) {
     const VaeHost& h = v->host;
     if (!z || !out || frames <= 0) return fail(YUE2_ERR_ARG, "Expected finite nonempty [frames,64] latents");
@@ -343,14 +666,19 @@ int vae_decode(Yue2Vae* v, const float* z, int frames, float* out) {
             if (n <= 0) return fail(YUE2_ERR_ARG, "VAE latent too short");
             most = std::max(most, (size_t)n * c);
         }
-    float* buf[3] = {nullptr, nullptr, nullptr};
-    void* block = nullptr;
     const size_t stride = (most * sizeof(float) + 255) / 256 * 256;
-    hipError_t e = hipMalloc(&block, 3 * stride);
-    if (e != hipSuccess) return hip_fail(e, "VAE activations");
-    for (int i = 0; i < 3; ++i) buf[i] = reinterpret_cast<float*>(static_cast<char*>(block) + i * stride);
     hipStream_t s = v->stream;
-    int cur = 0, res = -1;
+    hipError_t e = hipSuccess;
+    if (3 * stride > v->acts_bytes) {
+        if (v->acts) (void)hipFree(v->acts);
+        v->acts = nullptr;
+        v->acts_bytes = 0;
+        if ((e = hipMalloc(&v->acts, 3 * stride)) != hipSuccess) return hip_fail(e, "VAE activations");
+        v->acts_bytes = 3 * stride;
+    }
+    float* buf[3];
+    for (int i = 0; i < 3; ++i) buf[i] = reinterpret_cast<float*>(static_cast<char*>(v->acts) + i * stride);
+    int cur = 0, res = -1, pending = -1;  // pending: an activation waiting for the next convolution
     n = frames;
     c = h.latent_dim;
     auto free_buf = [&]() {
@@ -358,16 +686,25 @@ int vae_decode(Yue2Vae* v, const float* z, int frames, float* out) {
             if (i != cur && i != res) return i;
         return -1;
     };
+    auto is_conv = [&](size_t k) { return k < h.ops.size() && (h.ops[k].kind == VAE_CONV || h.ops[k].kind == VAE_CONVT); };
     e = hipMemcpyAsync(buf[0], z, sizeof(float) * (size_t)frames * c, hipMemcpyHostToDevice, s);
     int rc = e == hipSuccess ? YUE2_OK : hip_fail(e, "VAE input");
     const size_t nops = h.ops.size();
     for (size_t k = 0; k < nops && rc == YUE2_OK; ++k) {
         const VaeOpHost& op = h.ops[k];
         const int dst = free_buf();
-        if (op.kind == VAE_CONV || op.kind == VAE_CONVT) {
-            // the unit's residual joins in this convolution's epilogue when it ends the unit
+        if (is_conv(k)) {
             const bool join = k + 1 < nops && h.ops[k + 1].kind == VAE_RES_END && res >= 0;
-            e = run_conv(s, op, v->w[k], v->b[k], buf[cur], n, buf[dst], join ? buf[res] : nullptr);
+            const bool tanh_out = !join && k + 1 < nops && h.ops[k + 1].kind == VAE_TANH;
+            int act = ACT_NONE;
+            const float *alpha = nullptr, *inv_beta = nullptr;
+            if (pending >= 0) {
+                act = h.ops[pending].kind == VAE_SNAKE ? ACT_SNAKE : ACT_ELU;
+                alpha = v->a[pending];
+                inv_beta = v->ib[pending];
+            }
+            e = run_conv(s, op, v->shape[k], v->w[k], v->b[k], buf[cur], n, buf[dst], join ? buf[res] : nullptr, act,
+                         alpha, inv_beta, tanh_out);
             if (e != hipSuccess) {
                 rc = hip_fail(e, "VAE convolution");
                 break;
@@ -375,10 +712,11 @@ int vae_decode(Yue2Vae* v, const float* z, int frames, float* out) {
             n = conv_length(op, n);
             c = op.cout;
             cur = dst;
-            if (join) {
-                res = -1;
-                ++k;  // the RES_END
-            }
+            pending = -1;
+            if (join) res = -1;
+            if (join || tanh_out) ++k;  // the RES_END or TANH it absorbed
+        } else if ((op.kind == VAE_SNAKE || op.kind == VAE_ELU) && is_conv(k + 1)) {
+            pending = (int)k;
         } else if (op.kind == VAE_SNAKE || op.kind == VAE_ELU || op.kind == VAE_TANH) {
             const size_t cnt = (size_t)n * c;
             activation_kernel<<<(unsigned)std::min<size_t>((cnt + 255) / 256, 65536), 256, 0, s>>>(
@@ -399,7 +737,6 @@ int vae_decode(Yue2Vae* v, const float* z, int frames, float* out) {
         if (e != hipSuccess) rc = hip_fail(e, "VAE output");
     }
     (void)hipStreamSynchronize(s);
-    (void)hipFree(block);
     if (rc == YUE2_OK)
         for (size_t i = 0; i < (size_t)n * c; ++i)
             if (!std::isfinite(out[i])) return fail(YUE2_ERR_LOGITS, "VAE produced nonfinite audio");
@@ -461,7 +798,8 @@ extern "C" int32_t yue2_hip_selftest_conv(int32_t transpose, int32_t cin, int32_
     op.w.assign(w, w + (size_t)cin * cout * kernel);
     const int len = conv_length(op, frames);
     if (len <= 0) return fail(YUE2_ERR_ARG, "bad convolution selftest");
-    const std::vector<float> slabs = tap_slabs(op);
+    const ConvShape shape = conv_shape(op);
+    const std::vector<float> slabs = conv_slabs(op, shape);
     float *dx = nullptr, *dw = nullptr, *db = nullptr, *dy = nullptr;
     hipError_t e = hipMalloc(&dx, sizeof(float) * (size_t)frames * cin);
     if (e == hipSuccess) e = hipMalloc(&dw, sizeof(float) * slabs.size());
@@ -470,7 +808,9 @@ extern "C" int32_t yue2_hip_selftest_conv(int32_t transpose, int32_t cin, int32_
     if (e == hipSuccess) e = hipMemcpy(dx, x, sizeof(float) * (size_t)frames * cin, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(dw, slabs.data(), sizeof(float) * slabs.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess && bias) e = hipMemcpy(db, bias, sizeof(float) * cout, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = run_conv(nullptr, op, dw, bias ? db : nullptr, dx, frames, dy, nullptr);
+    if (e == hipSuccess)
+        e = run_conv(nullptr, op, shape, dw, bias ? db : nullptr, dx, frames, dy, nullptr, ACT_NONE, nullptr, nullptr,
+                     false);
     if (e == hipSuccess) e = hipMemcpy(out, dy, sizeof(float) * (size_t)len * cout, hipMemcpyDeviceToHost);
     (void)hipFree(dx);
     (void)hipFree(dw);

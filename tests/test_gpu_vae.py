@@ -102,6 +102,10 @@ def test_tiled_decode_is_the_whole_decode(gpu, tmp_path):
         assert np.array_equal(tiled.view(np.uint32), full.view(np.uint32))
         with pytest.raises(y2.Yue2Error, match="VAE halo must be at least"):
             vae.decode_tiled(z, core, halo - 1)
+        bad = z.copy()
+        bad[40, 3] = np.inf  # the latent is validated before the halo, as validate_latent runs first
+        with pytest.raises(y2.Yue2Error, match="Expected finite nonempty"):
+            vae.decode_tiled(bad, core, halo - 1)
     finally:
         vae.close()
 

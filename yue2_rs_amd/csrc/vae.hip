@@ -757,6 +757,8 @@ extern "C" int32_t yue2_hip_vae_decode_tiled(Yue2Vae* v, const float* z, int32_t
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!v || !z || !out || frames <= 0) return fail(YUE2_ERR_ARG, "Expected finite nonempty [frames,64] latents");
     const VaeHost& h = v->host;
+    for (size_t i = 0; i < (size_t)frames * h.latent_dim; ++i)  // validate_latent before the halo check
+        if (!std::isfinite(z[i])) return fail(YUE2_ERR_ARG, "Expected finite nonempty [frames,64] latents");
     if (core <= 0 || halo < yue2_hip_vae_required_halo(v, std::max(core, 1)))
         return fail(YUE2_ERR_ARG, "VAE halo must be at least " + std::to_string(yue2_hip_vae_required_halo(v, std::max(core, 1))));
     const int64_t length = yue2_hip_vae_output_length(v, frames);

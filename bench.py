@@ -23,6 +23,13 @@ prompts for both CFG rows, then CFG batch-2 decode to the full 24576-token
 context, reporting ms/token as the context grows and the step kernel's
 roofline at the last position (24576 attended keys).
 
+--workload yue2: the same loop on the YuE2 shape (the reference's Config
+defaults, src/model.rs:35-44: hidden 2048, 28 layers, 16 q / 8 KV heads,
+head_dim 128, SwiGLU 6144, vocab 184704, RoPE theta 1e6) in the semantic
+phase of Pipeline::generate_semantic: the LM head reads the 32768 codec rows
+and MUSIC_END (project_phase, src/model.rs:478-507); min_tokens keeps the
+end token out until the timed steps are done.
+
 Prints one JSON line.  Progress goes to stderr.
 """
 from __future__ import annotations
@@ -44,26 +51,28 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def weight_bytes(c) -> int:
+def weight_bytes(c, head_rows=None) -> int:
+    """Every layer's weights and norms, the final norm and the LM head rows
+    one step reads (all of them, or a phase's rows and its stop row)."""
     H, D, I, V = c.hidden_size, c.head_dim, c.intermediate_size, c.vocab_size
     q, kv = c.num_attention_heads * D, c.num_key_value_heads * D
     per_layer = 2 * (H * (q + 2 * kv) + q * H + 3 * H * I) + 4 * (2 * H + 2 * D)
-    return c.num_hidden_layers * per_layer + 2 * V * H + 4 * H
+    return c.num_hidden_layers * per_layer + 2 * (V if head_rows is None else head_rows) * H + 4 * H
 
 
 def kv_bytes_per_position(c) -> int:
     return c.num_hidden_layers * 2 * c.num_key_value_heads * c.head_dim * 2
 
 
-def step_bytes(c, rows: int, context: float) -> float:
+def step_bytes(c, rows: int, context: float, head_rows=None) -> float:
     """Algorithmic HBM bytes of one step: every weight once, each row's KV for
     `context` attended positions plus the new token's K/V, its embedding row."""
-    return weight_bytes(c) + rows * (kv_bytes_per_position(c) * (context + 1) + 2 * c.hidden_size)
+    return weight_bytes(c, head_rows) + rows * (kv_bytes_per_position(c) * (context + 1) + 2 * c.hidden_size)
 
 
-def measure(y2, model, caches, first, sampling, scale, warmup, steps, c):
+def measure(y2, model, caches, first, sampling, scale, warmup, steps, c, phase=0, head_rows=None):
     dec = y2.Decoder(model, caches[0], caches[1] if len(caches) > 1 else None, sampling=sampling, seed=0,
-                     scale=scale)
+                     scale=scale, phase=phase)
     dec.run(warmup, first_logits=first)
     ctx0 = caches[0].length
     y2.synchronize()
@@ -84,8 +93,8 @@ def measure(y2, model, caches, first, sampling, scale, warmup, steps, c):
         "mean_event_ms": float(np.mean(ms)),
         "context_start": int(ctx0),
         "context_end": [int(x) for x in ctx],
-        "hbm_roofline_frac": step_bytes(c, rows, mean_ctx) / (wall / steps) / HBM_PEAK,
-        "bytes_per_step": step_bytes(c, rows, mean_ctx),
+        "hbm_roofline_frac": step_bytes(c, rows, mean_ctx, head_rows) / (wall / steps) / HBM_PEAK,
+        "bytes_per_step": step_bytes(c, rows, mean_ctx, head_rows),
     }
 
 
@@ -219,8 +228,9 @@ def main() -> int:
                     help="1 (default): one persistent kernel per token; 0: one kernel per phase")
     ap.add_argument("--prefill", default="mfma", choices=["mfma", "exact"],
                     help="mfma (default): matrix-core prefill; exact: decode-order (bit-exact) prefill")
-    ap.add_argument("--workload", default="decode", choices=["decode", "long"],
-                    help="decode (default): 2048-token prompts; long: 24000-token prompts decoded to 24576")
+    ap.add_argument("--workload", default="decode", choices=["decode", "long", "yue2"],
+                    help="decode (default): 2048-token prompts; long: 24000-token prompts decoded to 24576; "
+                         "yue2: the YuE2 shape in the semantic phase")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)",
@@ -234,6 +244,8 @@ def main() -> int:
     if not y2.available():
         print("no gfx950 device available", file=sys.stderr)
         return 1
+    if args.workload == "yue2":
+        return yue2_shape(args, y2, synthetic)
     c = synthetic.CLASS_3B
     log("generating synthetic 3B-class weights")
     t = time.perf_counter()
@@ -335,6 +347,95 @@ def main() -> int:
         "phase_kernels": others,
         "cpu_baseline": cpu,
         "norm_fallbacks": model.norm_fallbacks(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def yue2_shape(args, y2, synthetic):
+    """The decode loop on the YuE2 shape in the semantic phase: CFG batch 2
+    and batch 1 after 2048-token prompts (matrix-core prefill), the step
+    kernel timed alone one position past the prompts."""
+    c = synthetic.YUE2
+    log("generating synthetic YuE2-shape weights")
+    ckpt = synthetic.checkpoint(c, seed=0, threads=16)
+    model = y2.Model.open(ckpt)
+    step_kernel = model.set_step_kernel(bool(args.step_kernel))
+    W, K, P = args.warmup, args.steps, args.prompt
+    phase = y2.PHASE_SEMANTIC
+    head_rows = 32768 + 1  # the codec rows and MUSIC_END
+    cond_ids = synthetic.prompt(P, c.vocab_size, seed=0)
+    neg_ids = synthetic.prompt(P, c.vocab_size, seed=1)
+    cap = P + W + K + 1
+    sampling = y2.Sampling(temperature=0.9, top_p=0.93, top_k=50, repetition_penalty=1.2, penalty_window=50,
+                           min_tokens=W + K + 2, max_tokens=W + K + 2)
+    log(f"prefilling 3 x {P} tokens ({args.prefill})")
+    def pre(ids):
+        y2.synchronize()
+        t = time.perf_counter()
+        if args.prefill == "mfma":
+            cache, logits = model.prefill_mfma(ids, cap, phase)
+        else:
+            cache, logits = model.prefill_phase(ids, cap, phase)
+        y2.synchronize()
+        return cache, logits, time.perf_counter() - t
+    c_bs1, l_bs1, _ = pre(cond_ids)
+    c_pos, l_pos, t_pos = pre(cond_ids)
+    c_neg, l_neg, t_neg = pre(neg_ids)
+    prep = prefill_report(c, P, min(t_pos, t_neg), args.prefill)
+    d0 = y2.Decoder(model, c_pos, c_neg, sampling=sampling, seed=0, scale=args.scale, phase=phase)
+    d0.run(1, first_logits=np.concatenate([l_pos, l_neg]))
+    context = c_pos.length
+    if not step_kernel:
+        print("--workload yue2 times the step kernel: run it with --step-kernel 1", file=sys.stderr)
+        return 2
+    dom_ms, dom_b = d0.time_kernel("step", args.kernel_iters)
+    l_pos, l_neg = [row.copy() for row in d0.logits()]
+    d0.close()
+    log(f"batch 1: {W} warmup + {K} timed steps")
+    d1, bs1 = measure(y2, model, [c_bs1], l_bs1, sampling, 1.0, W, K, c, phase, head_rows)
+    d1.close()
+    log(f"CFG batch 2: {W} warmup + {K} timed steps")
+    d2, cfg = measure(y2, model, [c_pos, c_neg], np.concatenate([l_pos, l_neg]), sampling, args.scale, W, K, c,
+                      phase, head_rows)
+    d2.close()
+    log(f"CFG batch 2: {cfg['tokens_per_s']:.1f} steps/s, p50 {cfg['p50_ms']:.3f} ms")
+    achieved = dom_b / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(achieved / 8000.0, 4), "traffic": None,
+                "kernel": "step_kernel (whole CFG batch-2 token of the YuE2 shape: 28 layers + semantic-phase "
+                          "LM head + sampler)",
+                "launch_ms": round(dom_ms, 5), "bytes_per_launch": int(dom_b), "context": context}
+    out = {
+        "metric": METRIC,
+        "value": round(cfg["tokens_per_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(cfg["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "YuE2-shape AR decode loop, semantic phase, CFG batch 2 (guidance 1.5), T 0.9 / "
+                               f"top-k 50 / top-p 0.93 / penalty 1.2, {P}-token prompts, {K} steps",
+                   "layers": c.num_hidden_layers, "hidden": c.hidden_size, "heads": c.num_attention_heads,
+                   "kv_heads": c.num_key_value_heads, "head_dim": c.head_dim,
+                   "intermediate": c.intermediate_size, "vocab": c.vocab_size, "head_rows": head_rows,
+                   "prompt": P, "global_batch": 2, "parallelism": "none (1 GPU)",
+                   "execution": "persistent step kernel"},
+        "p50_ms": round(cfg["p50_ms"], 4),
+        "p90_ms": round(cfg["p90_ms"], 4),
+        "hbm_roofline_frac": round(cfg["hbm_roofline_frac"], 4),
+        "bytes_per_step": int(cfg["bytes_per_step"]),
+        "bs1": {"tokens_per_s": round(bs1["tokens_per_s"], 2), "ms_per_step": round(bs1["ms_per_step"], 4),
+                "p50_ms": round(bs1["p50_ms"], 4), "hbm_roofline_frac": round(bs1["hbm_roofline_frac"], 4),
+                "bytes_per_step": int(bs1["bytes_per_step"])},
+        "roofline": roofline,
+        "prefill": prep,
+        "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -387,8 +387,12 @@ static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double
         return fail(YUE2_ERR_ARG, "the decoder does not run the step kernel");
     const double H = c.hidden_size, D = c.head_dim, I = c.intermediate_size, V = c.vocab_size;
     const double q = c.num_attention_heads * D, kv = c.num_key_value_heads * D, L = c.num_hidden_layers;
+    // the LM head reads the phase's rows and its stop row (project_phase)
+    int lo = 0, n = 0, stop = -1;
+    head_rows(d->phase, (int)V, &lo, &n, &stop);
+    const double head = 2.0 * H * (n + (stop >= 0 && (stop < lo || stop >= lo + n) ? 1.0 : 0.0));
     const double weights = L * (2.0 * (H * (q + 2.0 * kv) + q * H + 3.0 * H * I) + 4.0 * (2.0 * H + 2.0 * D)) +
-                           2.0 * V * H + 4.0 * H;
+                           head + 4.0 * H;
     double kvb = 0.0;
     for (int b = 0; b < d->rows; ++b) {
         // the timed launches write the new token's K/V at position `length`

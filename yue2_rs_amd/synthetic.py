@@ -26,6 +26,10 @@ PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "
 REDUCED = Config(hidden_size=1024, num_hidden_layers=2, num_attention_heads=16, num_key_value_heads=4,
                  head_dim=64, intermediate_size=2816, vocab_size=32768, max_position_embeddings=24576,
                  rms_norm_eps=1e-6, rope_theta=10000.0)
+# The reference's Config defaults (src/model.rs:35-44): the YuE2 shape.
+YUE2 = Config(hidden_size=2048, num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
+              head_dim=128, intermediate_size=6144, vocab_size=184704, max_position_embeddings=24576,
+              rms_norm_eps=1e-6, rope_theta=1e6)
 CLASS_3B = Config(hidden_size=3072, num_hidden_layers=28, num_attention_heads=24, num_key_value_heads=8,
                   head_dim=128, intermediate_size=8192, vocab_size=84000, max_position_embeddings=24576,
                   rms_norm_eps=1e-6, rope_theta=10000.0)

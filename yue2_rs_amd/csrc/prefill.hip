@@ -238,26 +238,34 @@ __global__ __launch_bounds__(64) void rope_append_kernel(const RopeArgs a) {
 // ---- causal flash attention over the BF16 cache --------------------------
 
 // One workgroup per (query head h, kFlashRows = 128 query rows); wave w
-// takes 16 of them.  Keys in tiles of 64: S = Q K^T on 16x16x32 MFMAs (K
-// staged in LDS), the online softmax (row maxima and sums across the 16
-// lanes of a row group, DPP), P through LDS into the A layout and V
-// transposed in LDS for O += P V.  The next tile's K and V are requested
-// into registers while the current one is computed.  V^T is written as
-// dwords (two keys per thread), 32 consecutive keys of one dim row per
-// 32 lanes, so the transposing stores do not conflict on LDS banks.
+// takes 16 of them.  Keys in tiles of 64.  The scores are computed
+// transposed, S^T = K Q^T on 16x16x32 MFMAs (K staged in LDS is the A
+// operand, the wave's 16 query rows the B operand), so lane l holds query
+// l % 16 and keys 16 kt + 4 (l / 16) + r of the tile: a query's online
+// softmax is one lane's 16 values and two exchanges (lane distances 32, 16).
+// P then feeds O^T += V^T P^T from registers: in the MFMA's K dimension,
+// lane group j = l / 16 supplies the keys it holds (32 c + 4 j .. + 3 and
+// 32 c + 16 + 4 j .. + 3 of each 32-key chunk c), and V^T's A fragment reads
+// the same keys with two 8-byte LDS loads.  The next tile's K and V are
+// requested into registers while the current one is computed.  V^T is
+// written as dwords (two keys per thread), 32 consecutive keys of one dim
+// row per 32 lanes, so the transposing stores do not conflict on LDS banks;
+// its rows are 34 dwords apart, so 16 lanes' 8-byte reads of 16 rows do not
+// either.  (Workgroups that cover all query heads of a KV head, each staged
+// K/V tile serving two or three heads, measured slower: their waves need
+// ~234 registers, so fewer of them fit.)
 constexpr int kFlashRows = 128, kFlashThreads = 512, kFlashKT = 64;
 
 template <int D>
-__global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const FlashArgs f) {
-    constexpr int KT = kFlashKT, PADK = 8, NW = kFlashThreads / 64;
+__global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const FlashArgs f) {
+    constexpr int KT = kFlashKT, PADK = 8, PADV = 4;
     constexpr int KN = KT * D / 8, VN = (KT / 2) * (D / 8);  // K uint4 and V key-pair units per tile
     constexpr int KU = (KN + kFlashThreads - 1) / kFlashThreads, VU = (VN + kFlashThreads - 1) / kFlashThreads;
-    __shared__ __align__(16) uint16_t ks[KT][D + PADK];           // K tile, row = key
-    __shared__ __align__(16) uint16_t vt[D][KT + PADK];           // V tile transposed, row = dim
-    __shared__ __align__(16) uint16_t ps[2][NW][16][KT + PADK];   // each wave's P (hi, lo), row = query
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __align__(16) uint16_t ks[KT][D + PADK];  // K tile, row = key
+    __shared__ __align__(16) uint16_t vt[D][KT + PADV];  // V tile transposed, row = dim
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane >> 4, qi = lane & 15;
     const int h = blockIdx.x, q0 = blockIdx.y * kFlashRows, G = f.heads / f.kv_heads, g = h / G;
-    const int qrow = q0 + wave * 16 + (lane & 15);  // the query row this lane loads for A
+    const int qrow = q0 + wave * 16 + qi;  // this lane's query row
     const uint16_t* Kc = f.kv_base + (((size_t)f.layer * 2) * f.kv_heads + g) * (size_t)f.cap * D;
     const uint16_t* Vc = f.kv_base + (((size_t)f.layer * 2 + 1) * f.kv_heads + g) * (size_t)f.cap * D;
     // the second key source (non-causal): keys from split on
@@ -267,21 +275,15 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const Flas
     uint4 qa[D / 32];
 #pragma unroll
     for (int dk = 0; dk < D / 32; ++dk)
-        qa[dk] = qrow < f.rows ? ldg4(f.q + ((size_t)qrow * f.heads + h) * D + dk * 32 + 8 * (lane >> 4))
+        qa[dk] = qrow < f.rows ? ldg4(f.q + ((size_t)qrow * f.heads + h) * D + dk * 32 + 8 * j)
                                : make_uint4(0, 0, 0, 0);
-    // this lane's accumulator rows: 4 (lane / 16) + r of the wave's 16
-    // the last key each row sees (non-causal: every key)
+    // the last key this lane's query sees (non-causal: every key), and the
+    // smallest such position in the wave
     const int all_keys = f.noncausal ? f.split + f.rows - 1 : 0;
-    int qpos[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) qpos[r] = f.noncausal ? all_keys : f.p0 + q0 + wave * 16 + 4 * (lane >> 4) + r;
-    float m[4], l[4];
-    f32x4 o[D / 16];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -__builtin_huge_valf();
-        l[r] = 0.0f;
-    }
+    const int qpos = f.noncausal ? all_keys : f.p0 + qrow;
+    const int wave_first = f.noncausal ? all_keys : f.p0 + q0 + wave * 16;
+    float m = -__builtin_huge_valf(), l = 0.0f;
+    f32x4 o[D / 16];  // O^T: register r of tile dt is dim 16 dt + 4 j + r of this lane's query
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
@@ -334,86 +336,88 @@ __global__ __launch_bounds__(kFlashThreads) void flash_prefill_kernel(const Flas
         }
         __syncthreads();
         if (t + 1 < tiles) load_tile(t + 1);
-        // S for the wave's 16 rows x 64 keys: four 16x16 tiles
+        // S^T for 64 keys x the wave's 16 queries: four 16x16 tiles;
+        // s[kt][r] = score of key kb + 16 kt + 4 j + r for query qrow
         f32x4 s[4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int dk = 0; dk < D / 32; ++dk) {
-                const uint4 b = *reinterpret_cast<const uint4*>(&ks[kt * 16 + (lane & 15)][dk * 32 + 8 * (lane >> 4)]);
-                acc = mfma16(qa[dk], b, acc);
+                const uint4 a = *reinterpret_cast<const uint4*>(&ks[kt * 16 + qi][dk * 32 + 8 * j]);
+                acc = mfma16(a, qa[dk], acc);
             }
             s[kt] = acc;
         }
-        // scale, causal mask, online softmax per row (the row's 16 lanes)
-        float alpha[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float mx = -__builtin_huge_valf();
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const int key = kb + kt * 16 + (lane & 15);
-                const float v = key <= qpos[r] ? s[kt][r] * f.scale : -__builtin_huge_valf();
-                s[kt][r] = v;
-                mx = fmaxf(mx, v);
-            }
-            mx = xor_max<8>(mx);
-            const float mn = fmaxf(m[r], mx);
-            alpha[r] = mn == -__builtin_huge_valf() ? 1.0f : __expf(m[r] - mn);
-            float sum = 0.0f;
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                const float p = mn == -__builtin_huge_valf() ? 0.0f : __expf(s[kt][r] - mn);
-                s[kt][r] = p;
-                sum += p;
-            }
-            sum = xor_sum<8>(sum);
-            l[r] = l[r] * alpha[r] + sum;
-            m[r] = mn;
-        }
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[dt][r] *= alpha[r];
-        // P into the wave's LDS rows as two BF16 parts, hi = bf16(p) and
-        // lo = bf16(p - hi): V is BF16 (the cache), so P V takes two MFMAs
-        // and keeps about 16 bits of P instead of 8, as the reference's f32
-        // softmax and P V do (src/model.rs:313-397).  The rows are the
-        // wave's own: a wave-level LDS fence orders them before the reads.
+        // scale, causal mask (tiles that reach past the wave's first query), online softmax
+        const bool masked = kb + KT - 1 > wave_first;
+        float mx = -__builtin_huge_valf();
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float hi = rb(s[kt][r]);
-                ps[0][wave][4 * (lane >> 4) + r][kt * 16 + (lane & 15)] = bf16_bits(hi);
-                ps[1][wave][4 * (lane >> 4) + r][kt * 16 + (lane & 15)] = bf16_bits(s[kt][r] - hi);
+                float v = s[kt][r] * f.scale;
+                if (masked && kb + kt * 16 + 4 * j + r > qpos) v = -__builtin_huge_valf();
+                s[kt][r] = v;
+                mx = fmaxf(mx, v);
             }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O += P V: A = P rows, B = V^T rows (keys contiguous)
+        mx = xor_max<32, 16>(mx);
+        const float mn = fmaxf(m, mx);
+        const float alpha = mn == -__builtin_huge_valf() ? 1.0f : __expf(m - mn);
+        float sum = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < KT; kk += 32) {
-            const uint4 ah = *reinterpret_cast<const uint4*>(&ps[0][wave][lane & 15][kk + 8 * (lane >> 4)]);
-            const uint4 al = *reinterpret_cast<const uint4*>(&ps[1][wave][lane & 15][kk + 8 * (lane >> 4)]);
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = mn == -__builtin_huge_valf() ? 0.0f : __expf(s[kt][r] - mn);
+                s[kt][r] = p;
+                sum += p;
+            }
+        sum = xor_sum<32, 16>(sum);
+        l = l * alpha + sum;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
+        // O^T += V^T P^T per 32-key chunk.  P enters in two BF16 parts, hi =
+        // bf16(p) and lo = bf16(p - hi): V is BF16 (the cache), so P V takes
+        // two MFMAs and keeps about 16 bits of P instead of 8, as the
+        // reference's f32 softmax and P V do (src/model.rs:313-397).
+        // Element 2w (+1) of chunk c: key 32c + 4j + 2w (+1) for w < 2,
+        // 32c + 16 + 4j + 2w - 4 (+1) after.
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float p0 = s[2 * c + (w >> 1)][2 * (w & 1)], p1 = s[2 * c + (w >> 1)][2 * (w & 1) + 1];
+                const float h0 = rb(p0), h1 = rb(p1);
+                hw[w] = (uint32_t)bf16_bits(h0) | ((uint32_t)bf16_bits(h1) << 16);
+                lw[w] = (uint32_t)bf16_bits(p0 - h0) | ((uint32_t)bf16_bits(p1 - h1) << 16);
+            }
+            const uint4 ph = make_uint4(hw[0], hw[1], hw[2], hw[3]), pl = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 #pragma unroll
             for (int dt = 0; dt < D / 16; ++dt) {
-                const uint4 b = *reinterpret_cast<const uint4*>(&vt[dt * 16 + (lane & 15)][kk + 8 * (lane >> 4)]);
-                o[dt] = mfma16(al, b, o[dt]);
-                o[dt] = mfma16(ah, b, o[dt]);
+                const uint16_t* vrow = &vt[dt * 16 + qi][32 * c + 4 * j];
+                const uint2 v0 = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 v1 = *reinterpret_cast<const uint2*>(vrow + 16);
+                const uint4 a = make_uint4(v0.x, v0.y, v1.x, v1.y);
+                o[dt] = mfma16(a, pl, o[dt]);
+                o[dt] = mfma16(a, ph, o[dt]);
             }
         }
         __syncthreads();  // every wave is done with this tile's K and V
     }
+    if (qrow < f.rows) {
+        const float inv = 1.0f / l;
+        uint16_t* orow = f.out + (size_t)qrow * f.heads * D + (size_t)h * D + 4 * j;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = q0 + wave * 16 + 4 * (lane >> 4) + r;
-        if (row >= f.rows) continue;
-        const float inv = 1.0f / l[r];
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt)
-            f.out[(size_t)row * f.heads * D + (size_t)h * D + dt * 16 + (lane & 15)] = bf16_bits(rb(o[dt][r] * inv));
+        for (int dt = 0; dt < D / 16; ++dt) {
+            const uint32_t w0 = (uint32_t)bf16_bits(rb(o[dt][0] * inv)) | ((uint32_t)bf16_bits(rb(o[dt][1] * inv)) << 16);
+            const uint32_t w1 = (uint32_t)bf16_bits(rb(o[dt][2] * inv)) | ((uint32_t)bf16_bits(rb(o[dt][3] * inv)) << 16);
+            *reinterpret_cast<uint2*>(orow + dt * 16) = make_uint2(w0, w1);
+        }
     }
 }
 

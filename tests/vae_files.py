@@ -188,13 +188,14 @@ def conv_f64(transpose, x, w, bias, kernel, stride, padding, dilation):
 # (transpose, cin, cout, kernel, stride, padding, dilation, frames): shapes
 # that reach every branch of the device convolutions -- the matrix-core
 # kernel with 16-byte and scalar input loads, several output-channel tiles,
-# ten phases, phases without a tap and a strided plain convolution; the
+# ten and twenty phases, phases without a tap and a strided plain convolution; the
 # narrow kernel with several row tiles and a ragged channel chunk.
 CONV_SHAPES = [
     (False, 20, 40, 7, 1, 9, 3, 300),
     (False, 6, 130, 7, 1, 3, 1, 200),
     (True, 24, 64, 20, 10, 5, 1, 40),
     (True, 16, 33, 2, 4, 0, 1, 50),
+    (True, 8, 40, 40, 20, 10, 1, 12),
     (False, 8, 48, 4, 2, 1, 1, 300),
     (False, 130, 3, 7, 1, 27, 9, 600),
     (False, 64, 16, 7, 1, 3, 1, 100),

@@ -255,6 +255,8 @@ __global__ __launch_bounds__(64) void rope_append_kernel(const RopeArgs a) {
 // K/V tile serving two or three heads, measured slower: their waves need
 // ~234 registers, so fewer of them fit.)
 constexpr int kFlashRows = 128, kFlashThreads = 512, kFlashKT = 64;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
 template <int D>
 __global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const FlashArgs f) {
@@ -282,6 +284,7 @@ __global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const F
     const int all_keys = f.noncausal ? f.split + f.rows - 1 : 0;
     const int qpos = f.noncausal ? all_keys : f.p0 + qrow;
     const int wave_first = f.noncausal ? all_keys : f.p0 + q0 + wave * 16;
+    const float scale2 = f.scale * 1.4426950408889634f;  // log2(e)
     float m = -__builtin_huge_valf(), l = 0.0f;
     f32x4 o[D / 16];  // O^T: register r of tile dt is dim 16 dt + 4 j + r of this lane's query
 #pragma unroll
@@ -349,37 +352,39 @@ __global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const F
             }
             s[kt] = acc;
         }
-        // scale, causal mask (tiles that reach past the wave's first query), online softmax
+        // scale (in log2 units: exp2 is the hardware exponential), causal mask
+        // (tiles that reach past the wave's first query), online softmax
         const bool masked = kb + KT - 1 > wave_first;
         float mx = -__builtin_huge_valf();
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float v = s[kt][r] * f.scale;
+                float v = s[kt][r] * scale2;
                 if (masked && kb + kt * 16 + 4 * j + r > qpos) v = -__builtin_huge_valf();
                 s[kt][r] = v;
                 mx = fmaxf(mx, v);
             }
         mx = xor_max<32, 16>(mx);
         const float mn = fmaxf(m, mx);
-        const float alpha = mn == -__builtin_huge_valf() ? 1.0f : __expf(m - mn);
+        const float alpha = mn == -__builtin_huge_valf() ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
         float sum = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = mn == -__builtin_huge_valf() ? 0.0f : __expf(s[kt][r] - mn);
+                const float p = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s[kt][r] - mn);
                 s[kt][r] = p;
                 sum += p;
             }
         sum = xor_sum<32, 16>(sum);
         l = l * alpha + sum;
         m = mn;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f))  // some row's maximum moved
 #pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt)
+            for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
+                for (int r = 0; r < 4; ++r) o[dt][r] *= alpha;
         // O^T += V^T P^T per 32-key chunk.  P enters in two BF16 parts, hi =
         // bf16(p) and lo = bf16(p - hi): V is BF16 (the cache), so P V takes
         // two MFMAs and keeps about 16 bits of P instead of 8, as the
@@ -391,10 +396,11 @@ __global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const F
             uint32_t hw[4], lw[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const float p0 = s[2 * c + (w >> 1)][2 * (w & 1)], p1 = s[2 * c + (w >> 1)][2 * (w & 1) + 1];
-                const float h0 = rb(p0), h1 = rb(p1);
-                hw[w] = (uint32_t)bf16_bits(h0) | ((uint32_t)bf16_bits(h1) << 16);
-                lw[w] = (uint32_t)bf16_bits(p0 - h0) | ((uint32_t)bf16_bits(p1 - h1) << 16);
+                // two values per conversion (v_cvt_pk_bf16_f32, round to nearest even)
+                const f32x2 pv = {s[2 * c + (w >> 1)][2 * (w & 1)], s[2 * c + (w >> 1)][2 * (w & 1) + 1]};
+                hw[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv, bf16x2v));
+                const f32x2 lv = {pv[0] - u2f(hw[w] << 16), pv[1] - u2f(hw[w] & 0xffff0000u)};
+                lw[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lv, bf16x2v));
             }
             const uint4 ph = make_uint4(hw[0], hw[1], hw[2], hw[3]), pl = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 #pragma unroll

@@ -45,7 +45,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxTaps = 8, kMaxPhases = 16;
+constexpr int kMaxTaps = 8, kMaxPhases = 32;  // ConvPlan stays under the 4 KB kernel-argument limit
 constexpr int kMmaTile = 128;
 constexpr int kChunk = 16, kNarrowRows = 256, kNarrowPad = 17;
 constexpr size_t kMaxLds = 160 * 1024;

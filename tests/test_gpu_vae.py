@@ -15,6 +15,13 @@ oracle's restatement (tests/test_oracle_vae.py pins it).
   max |device - f64| <= 4 * max |oracle - f64| + 1e-6 (the wide random
   network amplifies rounding: its activations reach ~200 and both FP32 paths
   sit ~1e-3 from float64; the small ones ~5e-5).
+- The full Oobleck shape of the reference's default ratio (widths 128 x (1,
+  2, 4, 8, 16), strides (2, 4, 4, 6, 10): 1024- and 2048-channel tiles, ten-
+  and six-phase transposed convolutions) on 2 latent frames, with the
+  weight-norm gains scaled by 0.3 so the activations stay O(1) and FP32
+  rounding is not amplified into noise (at gain 1 the oracle itself is 0.1
+  from float64 there): the same contract against float64, and against the
+  oracle.
 - decode_tiled with the required halo equals the whole decode bit for bit
   (every output sees the same arithmetic); a smaller halo is refused; the
   reference's configuration checks and messages."""
@@ -25,6 +32,7 @@ import pytest
 
 from oracle import oracle as O
 import yue2_rs_amd as y2
+from yue2_rs_amd import synthetic
 
 from test_oracle_vae import KAT, SPARSE, kat_case
 from vae_files import CONV_SHAPES, conv_case, decode_f64, oracle_ops, required_halo, synthetic_vae, write_vae_dir
@@ -84,6 +92,24 @@ def test_decode_matches_oracle(gpu, tmp_path, name):
         d, ref = np.abs(got - exact).max(), np.abs(want - exact).max()
         print(f"{name}: device-f64 {d:.3g}, oracle-f64 {ref:.3g}, device-oracle {np.abs(got - want).max():.3g}",
               flush=True)
+        assert d <= 4 * ref + 1e-6
+    finally:
+        vae.close()
+
+
+def test_decode_1920_shape(gpu, tmp_path):
+    cfg, t = synthetic.vae(0, **synthetic.VAE_1920)
+    t = {k: (v * np.float32(0.3) if k.endswith("weight_g") else v) for k, v in t.items()}
+    vae = y2.Vae(write_vae_dir(tmp_path / "big", cfg, t))
+    try:
+        z = np.random.default_rng(1).standard_normal((2, cfg["latent_dim"])).astype(np.float32)
+        got = vae.decode(z)
+        exact = decode_f64(cfg, t, z)
+        want = oracle_ops(cfg, t).run(z)
+        assert got.shape == want.shape == exact.shape == (2 * 1920, 2)
+        d, ref = np.abs(got - exact).max(), np.abs(want - exact).max()
+        print(f"1920 shape: device-f64 {d:.3g}, oracle-f64 {ref:.3g}, device-oracle {np.abs(got - want).max():.3g}, "
+              f"output std {exact.std():.3g}", flush=True)
         assert d <= 4 * ref + 1e-6
     finally:
         vae.close()

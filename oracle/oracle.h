@@ -83,10 +83,14 @@
  *                    velocity (zero llm2vae and bias) the output is the
  *                    rounded noise; chunks of (capacity - prefix - 3) / 2.
  *   y2o_conv        the reference's own convolution known-answer cases and
- *                    scalar formula (src/vae.rs:812-892, tolerance 2e-6).
+ *                    scalar formula (src/vae.rs:812-892, tolerance 2e-6);
+ *                    within 1e-5 of a float64 convolution on shapes with
+ *                    up to 130 channels, 20 phases and dilation 9.
  *   y2o_vae_*       closed forms (SnakeBeta at alpha = beta = 1, ELU, tanh,
- *                    the weight norm's row norms = |g|), Conv::length, and a
- *                    tiled decode equal to the whole decode on every core row.
+ *                    the weight norm's row norms = |g|), Conv::length, a
+ *                    tiled decode equal to the whole decode on every core row,
+ *                    and the whole decoder within 1e-4 of an independent
+ *                    float64 evaluation (tests/vae_files.py decode_f64).
  *   Accelerate's exact summation order, macOS libm cos/sin/powf and the real
  *   checkpoint's logits cannot be run here: parity with those is unpinned
  *   beyond the checks above.

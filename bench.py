@@ -210,7 +210,7 @@ def cpu_baseline(ckpt, c, prompt_len, scale, sampling, threads, budget_s, max_st
             "ms_per_step": 1000.0 * wall / steps, "cpu_model": model, "nproc": nproc, "build": flags,
             "sample": f"{steps} CFG batch-2 steps of the C oracle (restated reference CPU token step, "
                       f"portable DOT order in place of Accelerate; gcc {flags}) at context {prompt_len}, "
-                      f"synthetic BF16 KV, {threads} threads (the box's CPU share for one GPU) of {nproc} "
+                      f"synthetic BF16 KV, {threads} threads (one GPU's share of the host's CPUs) of {nproc} "
                       f"logical CPUs ({model})"}
 
 
@@ -309,7 +309,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
-        threads = min(16, os.cpu_count() or 1)  # one GPU's share of the box's CPUs
+        threads = min(16, os.cpu_count() or 1)  # one GPU's share of the host's CPUs
         cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 64)
         log(f"CPU baseline: {cpu['value']:.3f} steps/s with {threads} threads")
 

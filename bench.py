@@ -233,7 +233,7 @@ def main() -> int:
                          "yue2: the YuE2 shape in the semantic phase")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus must be 1)",
+        print("bench.py measures one GPU: the library has no multi-GPU path (--gpus must be 1)",
               file=sys.stderr)
         return 2
 

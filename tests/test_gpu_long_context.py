@@ -124,6 +124,29 @@ def test_3b_cfg_batch2_max_context(model_3b):
     _check_batch2(gm, om, (24575, 24000), 1, seed=5)
 
 
+@pytest.fixture(scope="module")
+def model_yue2(gpu, oracle_threads):
+    import dataclasses
+    c = dataclasses.replace(synthetic.YUE2, num_hidden_layers=2)
+    ck = synthetic.checkpoint(c, seed=1, threads=16)
+    gm = y2.Model.open(ck)
+    assert gm.set_step_kernel(True)
+    yield ck, gm, O.Model(ck)
+    gm.close()
+
+
+def test_yue2_batch1_context_8192(model_yue2):
+    _, gm, om = model_yue2
+    _check_batch1(gm, om, 8192, 2, seed=6)
+
+
+def test_yue2_cfg_batch2_context_8192(model_yue2):
+    """The YuE2 shape's step kernel (two query heads per KV head) on the
+    chunk-restage path for both rows."""
+    _, gm, om = model_yue2
+    _check_batch2(gm, om, (8192, 8150), 2, seed=7)
+
+
 def test_epoch_repeat_keeps_parity(reduced):
     """The step kernel's tagged words carry a 20-bit epoch of the launch
     sequence.  The second forward below is placed exactly 2^20 launches after

@@ -147,6 +147,11 @@ def test_yue2_cfg_batch2_context_8192(model_yue2):
     _check_batch2(gm, om, (8192, 8150), 2, seed=7)
 
 
+def test_yue2_cfg_batch2_max_context(model_yue2):
+    _, gm, om = model_yue2
+    _check_batch2(gm, om, (24575, 24100), 1, seed=8)
+
+
 def test_epoch_repeat_keeps_parity(reduced):
     """The step kernel's tagged words carry a 20-bit epoch of the launch
     sequence.  The second forward below is placed exactly 2^20 launches after

@@ -117,6 +117,34 @@ def test_3b_cfg_batch2_context_3100(model_3b):
     _check_batch2(gm, om, (3100, 3063), 2, seed=4)
 
 
+def test_3b_cfg_sampled_context_2048(model_3b):
+    """Config 4's loop at its own context: CFG batch 2 (guidance 1.5) with T
+    0.9, top-k 50, top-p 0.93 and penalty 1.2 over 50 tokens, from caches of
+    2048 positions, against sampling::generate's loop (src/sampling.rs:
+    258-291) replayed on the oracle: the mix, choose() with the generated
+    tokens as history and the same MT19937 stream, then each row's forward."""
+    _, gm, om = model_3b
+    V, steps, seed, scale = om.config.vocab_size, 6, 1234, 1.5
+    s = y2.Sampling(temperature=0.9, top_p=0.93, top_k=50, repetition_penalty=1.2, penalty_window=50,
+                    min_tokens=0, max_tokens=steps)
+    (g0, o0), (g1, o1) = (_caches(gm, om, 2048, 2048 + steps, 11 + i) for i in range(2))
+    rng = np.random.default_rng(5)
+    first = [(3.0 * rng.standard_normal(V)).astype(np.float32) for _ in range(2)]
+    dec = y2.Decoder(gm, g0, g1, sampling=s, seed=seed, scale=scale)
+    got, _ = dec.run(steps, first_logits=np.concatenate(first))
+    dec.close()
+    gen = O.Generator(seed)
+    cond, uncond = first
+    want = []
+    for step in range(steps):
+        t = O.choose(O.cfg_mix(cond, uncond, scale), s, want, step, y2.PHASE_NONE, False, gen)
+        want.append(t)
+        print(f"sampled CFG step {step}: oracle {t}, device {int(got[step]) if step < len(got) else None}", flush=True)
+        if step + 1 < steps:
+            cond, uncond = om.forward([t], o0), om.forward([t], o1)
+    assert list(got) == want
+
+
 def test_3b_cfg_batch2_max_context(model_3b):
     """Config 5's end point: the new tokens at positions 24575 and 24000, so
     the attention of each row spans 384 / 376 blocks, 24 per workgroup."""

@@ -24,7 +24,9 @@ decode-order prefill on the same seeded checkpoint and prompt:
 Prompts of 1 token (the attention over one key), 65 and 1100 tokens cross
 the 64-key and 128-query flash tiles; 4100 tokens (against the decode-order
 GPU prefill, itself bit-exact with the oracle) cross the 4096-row chunks of
-the prefill."""
+the prefill; 24000 tokens at the 3B layer shape (two layers) are the long
+prompt of the long-context workload: six chunks, up to 375 key tiles per
+query tile."""
 import dataclasses
 
 import numpy as np
@@ -90,6 +92,7 @@ def _close(got, want, tol, what):
     assert np.array_equal(fin, np.isfinite(got)), f"{what}: -inf pattern differs"
     d = np.abs(got[fin] - want[fin]).max()
     s = want[fin].std()
+    print(f"{what}: max |d| {d:.4g} = {d / s:.4f} std", flush=True)
     assert d <= tol * s, f"{what}: max |d| {d:.4g} > {tol} * std {s:.4g}"
     assert int(np.argmax(got)) == int(np.argmax(want)), f"{what}: argmax differs"
 
@@ -130,6 +133,24 @@ def test_prefill_crosses_chunks(gpu):
         c2, l2 = gm.prefill_mfma(ids, n + 2)
         assert c2.length == n
         _close(l2, l1, TWO_LAYER_TOL, "prefill logits")
+        t = int(np.argmax(l1))
+        _close(gm.forward([t], c2), gm.forward([t], c1), TWO_LAYER_TOL, "next-step logits")
+        c1.close()
+        c2.close()
+    finally:
+        gm.close()
+
+
+def test_prefill_24000_tokens_3b_shape(gpu):
+    cfg = dataclasses.replace(synthetic.CLASS_3B, num_hidden_layers=2, vocab_size=32768)
+    gm = y2.Model.open(synthetic.checkpoint(cfg, seed=4, threads=16))
+    try:
+        n = 24000
+        ids = synthetic.prompt(n, cfg.vocab_size, seed=6)
+        c1, l1 = gm.prefill_phase(ids, n + 2)
+        c2, l2 = gm.prefill_mfma(ids, n + 2)
+        assert c2.length == n
+        _close(l2, l1, TWO_LAYER_TOL, "24000-token prefill logits")
         t = int(np.argmax(l1))
         _close(gm.forward([t], c2), gm.forward([t], c1), TWO_LAYER_TOL, "next-step logits")
         c1.close()

@@ -180,6 +180,28 @@ def test_yue2_cfg_batch2_max_context(model_yue2):
     _check_batch2(gm, om, (24575, 24100), 1, seed=8)
 
 
+@pytest.fixture(scope="module")
+def phase_3b(gpu, oracle_threads):
+    """Two layers of the 3B shape (24 query / 8 KV heads, head_dim 128) on
+    the per-phase kernels: the split-KV attention kernel of the decode
+    attention microbenchmark."""
+    import dataclasses
+    c = dataclasses.replace(synthetic.CLASS_3B, num_hidden_layers=2, vocab_size=32768)
+    ck = synthetic.checkpoint(c, seed=2, threads=16)
+    gm = y2.Model.open(ck)
+    assert not gm.set_step_kernel(False)
+    yield ck, gm, O.Model(ck)
+    gm.close()
+
+
+@pytest.mark.parametrize("length", [1024, 4096, 16384, 24575])
+def test_phase_kernels_cfg_batch2_attention_lengths(phase_3b, length):
+    """The attention microbenchmark's KV lengths at CFG batch 2 through the
+    per-phase split-KV attention: both rows' logits bit for bit."""
+    _, gm, om = phase_3b
+    _check_batch2(gm, om, (length, length - 21), 1, seed=length % 11)
+
+
 def test_epoch_repeat_keeps_parity(reduced):
     """The step kernel's tagged words carry a 20-bit epoch of the launch
     sequence.  The second forward below is placed exactly 2^20 launches after

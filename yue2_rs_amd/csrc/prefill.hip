@@ -38,142 +38,266 @@ using namespace y2;
 namespace y2 {
 
 // ---- GEMM: C = X W^T, X [M, K] BF16, W [N, K] BF16, FP32 accumulation ------
+//
+// A workgroup computes a TM-row tile of C against a tile of TW rows of W: TW
+// output columns, or for the gate/up pair TW/2 columns whose W tile holds
+// TW/2 gate rows and the same TW/2 up rows.  Its waves form a WVM x WVN grid,
+// each an (TM/WVM) x (TW/WVN) block of 32x32x16 MFMA accumulators (the pair:
+// the gate blocks of its columns, then the up blocks).
+//
+// The X and W tiles of each 64-wide step of K go from global memory straight
+// into LDS (global_load_lds_dwordx4: each lane's 16 bytes land at the wave's
+// LDS address + 16 * lane, with no registers and no LDS store instructions)
+// through NST buffers, so NST - 1 steps are in flight while one is
+// multiplied.  Tile rows are 128 bytes of eight 16-byte units, chunk c of
+// row r stored at unit c ^ ((r >> 1) & 7): a 16-byte LDS read serves sixteen
+// lanes per cycle from 64 four-byte banks, and its lanes 0-15 read one chunk
+// of sixteen consecutive rows, which then fall in sixteen different 16-byte
+// bank groups (r & 1 picks the half of the 256 bytes, the XOR the group).  The waits are explicit: after a step's MFMA operands are all
+// read, the wave waits until its own loads of the next step have landed
+// (vmcnt counts the DMA loads; the later steps' stay in flight), one barrier
+// makes every wave's part visible and frees the buffer just read, which
+// then takes step t + NST.  The next 16-wide substep's operands are read
+// between the current substep's MFMAs.
+template <int TM_, int TW_, int WVM_, int WVN_, int NST_>
+struct GemmTile {
+    static constexpr int TM = TM_, TW = TW_, WVM = WVM_, WVN = WVN_, NST = NST_;
+    static constexpr int THREADS = 64 * WVM * WVN;
+    static constexpr int WM = TM / WVM, WN = TW / WVN;   // wave block
+    static constexpr int MI = WM / 32, NJ = WN / 32;     // 32x32 accumulators per wave
+    static constexpr int XU = TM * kGemmTK / 8;          // 16-byte units of the X tile
+    static constexpr int WU = TW * kGemmTK / 8;          // of the W tile
+    static constexpr int SU = XU + WU;                   // per buffer
+    static constexpr int LX = XU / THREADS, LW = WU / THREADS;  // DMA loads per lane per step
+    static constexpr size_t LDS = (size_t)NST * SU * 16;
+    static_assert(XU % THREADS == 0 && WU % THREADS == 0, "whole DMA loads per wave");
+    static_assert(WM % 32 == 0 && WN % 64 == 0, "the pair needs gate and up blocks in every wave");
+    static_assert(NST >= 2 && (NST - 1) * (LX + LW) < 64, "vmcnt range");
+};
+// 256 x 256 with 8 waves of 64 x 128 (two per SIMD); 128 x 256 with 8 waves
+// of 64 x 64 and three buffers for grids the larger tile would leave short of
+// workgroups.  (Measured on the 3B shapes with random operands against
+// 128 x 64 and 64 x 64 wave blocks, four-wave tiles and 32-wide K steps.)
+using GemmBig = GemmTile<256, 256, 4, 2, 2>;
+using GemmNarrow = GemmTile<128, 256, 2, 4, 3>;
 
-constexpr int kGemmTM = 128, kGemmPad = 8;
-constexpr int kGemmThreads = 256;
+__device__ __forceinline__ int gemm_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int gemm_unit(int row, int c) { return row * 8 + (c ^ gemm_swz(row)); }
 
-// One workgroup computes a 128-row tile of C: 128 columns (64 for the
-// gate/up pair, whose W tile holds 64 gate rows and the same 64 up rows).
-// Wave w takes rows 64 (w / 2) .. + 64 and two 32x32 accumulator tiles per
-// row half: columns 64 (w % 2) + 32 j (the pair: gate and up of columns
-// 32 (w % 2) .. + 32).  The X and W tiles of each 64-wide step of K go
-// through two LDS buffers in turn: step k + 1 is stored from registers
-// while step k is multiplied, and step k + 2's global loads are then in
-// flight; one barrier per step.
-template <int EPI>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) const y2_u32x4 lds_u32x4;
+
+__device__ __forceinline__ f32x16 mfma32v(y2_u32x4 a, y2_u32x4 b, f32x16 c) {
+    bf16x8 x, y;
+    __builtin_memcpy(&x, &a, 16);
+    __builtin_memcpy(&y, &b, 16);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, y, c, 0, 0, 0);
+}
+
+template <int EPI, class T>
+__global__ __launch_bounds__(T::THREADS, 1) void gemm_kernel(const GemmArgs g) {
     constexpr bool PAIR = EPI == GEPI_SWIGLU_BF16;
-    constexpr int TN = PAIR ? 64 : 128;  // output columns per tile
-    constexpr int LDS_W = kGemmTK + kGemmPad;
-    constexpr int PER = kGemmTM * kGemmTK / 8 / kGemmThreads;  // uint4 per thread per tile and operand
-    __shared__ __align__(16) uint16_t xs[2][kGemmTM][LDS_W];
-    __shared__ __align__(16) uint16_t ws[2][128][LDS_W];
+    constexpr int TN = PAIR ? T::TW / 2 : T::TW;  // output columns per tile
+    extern __shared__ __align__(16) uint16_t gsm[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * kGemmTM, n0 = blockIdx.x * TN;
-    // each thread moves PER 16-byte pieces of each tile: row q / 8, k 8 (q % 8)
-    uint4 rx[PER], rw[PER];
-    auto load = [&](int k0) {
+    const int wm = wave / T::WVN, wn = wave % T::WVN;
+    const int m0 = blockIdx.y * T::TM, n0 = blockIdx.x * TN;
+    const int steps = g.K / kGemmTK;
+    // this lane's source of each of its DMA units (rows past the matrix read
+    // its last row: they only feed outputs that are not stored)
+    const uint16_t* sx[T::LX];
+    const uint16_t* sw[T::LW];
 #pragma unroll
-        for (int s = 0; s < PER; ++s) {
-            const int q = tid + kGemmThreads * s, row = q >> 3, kq = (q & 7) * 8;
-            const int mr = m0 + row;
-            rx[s] = mr < g.M ? ldg4(g.x + (size_t)mr * g.ldx + k0 + kq) : make_uint4(0, 0, 0, 0);
-            const uint16_t* wrow;
-            int nr;
-            if (PAIR) {
-                nr = n0 + (row & 63);
-                wrow = (row < 64 ? g.w : g.w2) + (size_t)nr * g.ldw;
-            } else {
-                nr = n0 + row;
-                wrow = g.w + (size_t)nr * g.ldw;
-            }
-            rw[s] = nr < g.N ? ldg4(wrow + k0 + kq) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < T::LX; ++j) {
+        const int u = (wave * T::LX + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ gemm_swz(row);
+        sx[j] = g.x + (size_t)min(m0 + row, g.M - 1) * g.ldx + 8 * c;
+    }
+#pragma unroll
+    for (int j = 0; j < T::LW; ++j) {
+        const int u = (wave * T::LW + j) * 64 + lane, row = u >> 3, c = (u & 7) ^ gemm_swz(row);
+        const uint16_t* w = g.w;
+        int r = row;
+        if (PAIR && row >= T::TW / 2) {
+            w = g.w2;
+            r = row - T::TW / 2;
+        }
+        sw[j] = w + (size_t)min(n0 + r, g.N - 1) * g.ldw + 8 * c;
+    }
+    auto issue = [&](int step, int buf) {
+        const int k0 = step * kGemmTK;
+        uint16_t* base = gsm + (size_t)buf * T::SU * 8;
+#pragma unroll
+        for (int j = 0; j < T::LX; ++j)
+            __builtin_amdgcn_global_load_lds((Y2_GLOBAL void*)(sx[j] + k0),
+                                             (lds_void*)(base + (wave * T::LX + j) * 64 * 8), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < T::LW; ++j)
+            __builtin_amdgcn_global_load_lds((Y2_GLOBAL void*)(sw[j] + k0),
+                                             (lds_void*)(base + (T::XU + (wave * T::LW + j) * 64) * 8), 16, 0, 0);
+    };
+    // W tile row of accumulator column block j of this wave
+    auto wrow = [&](int j) {
+        if constexpr (PAIR)
+            return (j < T::NJ / 2 ? 0 : T::TW / 2) + wn * (T::WN / 2) + 32 * (j % (T::NJ / 2));
+        else
+            return wn * T::WN + 32 * j;
+    };
+    // (explicit LDS reads of a native vector type: through generic pointers
+    // the compiler waits for every DMA load in flight before each read)
+    auto operands = [&](const uint16_t* base, int sub, y2_u32x4* a, y2_u32x4* b) {
+        const int c = sub * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < T::MI; ++i) {
+            const int row = wm * T::WM + i * 32 + (lane & 31);
+            a[i] = *(lds_u32x4*)(base + gemm_unit(row, c) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < T::NJ; ++j) {
+            const int row = wrow(j) + (lane & 31);
+            b[j] = *(lds_u32x4*)(base + (T::XU + gemm_unit(row, c)) * 8);
         }
     };
-    auto store = [&](int buf) {
+    auto buffer = [&](int t) { return gsm + (size_t)(t % T::NST) * T::SU * 8; };
+
+    f32x16 acc[T::MI][T::NJ];
 #pragma unroll
-        for (int s = 0; s < PER; ++s) {
-            const int q = tid + kGemmThreads * s, row = q >> 3, kq = (q & 7) * 8;
-            *reinterpret_cast<uint4*>(&xs[buf][row][kq]) = rx[s];
-            *reinterpret_cast<uint4*>(&ws[buf][row][kq]) = rw[s];
-        }
-    };
-    f32x16 acc[2][2];
+    for (int i = 0; i < T::MI; ++i)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < T::NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    const int steps = g.K / kGemmTK;
-    load(0);
-    store(0);
-    if (steps > 1) load(kGemmTK);
-    __syncthreads();
-    for (int st = 0; st < steps; ++st) {
-        const int cur = st & 1;
+    const int pre = min(steps, T::NST);
+    for (int t = 0; t < pre; ++t) issue(t, t);
+    if (pre == T::NST) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((T::NST - 1) * (T::LX + T::LW)) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    y2_u32x4 fa[2][T::MI], fb[2][T::NJ];
+    operands(buffer(0), 0, fa[0], fb[0]);
+    for (int t = 0; t < steps; ++t) {
+        const uint16_t* cur = buffer(t);
 #pragma unroll
-        for (int kk = 0; kk < kGemmTK; kk += 16) {
-            const int kc = kk + 8 * (lane >> 5);
-            uint4 a[2], b[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[i] = *reinterpret_cast<const uint4*>(&xs[cur][wm * 64 + i * 32 + (lane & 31)][kc]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int wr = PAIR ? j * 64 + wn * 32 : wn * 64 + j * 32;
-                b[j] = *reinterpret_cast<const uint4*>(&ws[cur][wr + (lane & 31)][kc]);
+        for (int sub = 0; sub < kGemmTK / 16; ++sub) {
+            const int f = sub & 1;
+            if (sub + 1 < kGemmTK / 16) {
+                operands(cur, sub + 1, fa[f ^ 1], fb[f ^ 1]);
+            } else if (t + 1 < steps) {
+                // every operand of step t is in registers (lgkmcnt) and this
+                // wave's loads of step t + 1 have landed (later steps' stay
+                // in flight); after the barrier every wave's have, and the
+                // buffer of step t takes step t + NST
+                if (t + T::NST - 1 < steps)
+                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((T::NST - 2) * (T::LX + T::LW)) : "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+                asm volatile("s_barrier" ::: "memory");
+                if (t + T::NST < steps) issue(t + T::NST, t % T::NST);
+                operands(buffer(t + 1), 0, fa[f ^ 1], fb[f ^ 1]);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < T::MI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < T::NJ; ++j) acc[i][j] = mfma32v(fa[f][i], fb[f][j], acc[i][j]);
+            // the next substep's operand reads between these MFMAs
+#pragma unroll
+            for (int q = 0; q < T::MI + T::NJ; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, T::MI * T::NJ - (T::MI + T::NJ), 0);
         }
-        if (st + 1 < steps) {
-            // the other buffer was last read in step st - 1, before the
-            // barrier that ended it
-            store(cur ^ 1);
-            if (st + 2 < steps) load((st + 2) * kGemmTK);
-        }
-        __syncthreads();
     }
-    // epilogue: lane l writes column acc32_col(l) of rows acc32_row(l, r)
+    // epilogue: lane l holds column acc32_col(l) of rows acc32_row(l, r)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < T::MI; ++i) {
+        const int rbase = m0 + wm * T::WM + i * 32;
+        if constexpr (PAIR) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm * 64 + i * 32 + acc32_row(lane, r);
-            if (row >= g.M) continue;
-            if constexpr (PAIR) {
-                const int col = n0 + wn * 32 + acc32_col(lane);
-                if (col < g.N) {
-                    const float o = rb(silu_rb(rb(acc[i][0][r])) * rb(acc[i][1][r]));
+            for (int j = 0; j < T::NJ / 2; ++j) {
+                const int col = n0 + wn * (T::WN / 2) + 32 * j + acc32_col(lane);
+                if (col >= g.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + acc32_row(lane, r);
+                    if (row >= g.M) continue;
+                    const float o = rb(silu_rb(rb(acc[i][j][r])) * rb(acc[i][j + T::NJ / 2][r]));
                     g.cb[(size_t)row * g.ldc + col] = bf16_bits(o);
                 }
-            } else {
+            }
+        } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = n0 + wn * 64 + j * 32 + acc32_col(lane);
-                    if (col >= g.N) continue;
+            for (int j = 0; j < T::NJ; ++j) {
+                const int col = n0 + wn * T::WN + 32 * j + acc32_col(lane);
+                if (col >= g.N) continue;
+                // the residual values of the block are all requested before
+                // the first is used
+                float cur[16];
+                if constexpr (EPI == GEPI_RESID) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = min(rbase + acc32_row(lane, r), g.M - 1);
+                        cur[r] = g.c[(size_t)row * g.ldc + col];
+                    }
+                }
+                const float bias = EPI == GEPI_BIAS || EPI == GEPI_BIAS_SILU_BF16 ? g.bias[col] : 0.0f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + acc32_row(lane, r);
+                    if (row >= g.M) continue;
                     const size_t at = (size_t)row * g.ldc + col;
                     const float v = acc[i][j][r];
                     if constexpr (EPI == GEPI_RAW) g.c[at] = v;
                     else if constexpr (EPI == GEPI_ROUND) g.c[at] = rb(v);
-                    else if constexpr (EPI == GEPI_RESID) g.c[at] = rb(g.c[at] + rb(v));
-                    else if constexpr (EPI == GEPI_BIAS) g.c[at] = rb(v + g.bias[col]);
-                    else g.cb[at] = bf16_bits(silu_rb(rb(v + g.bias[col])));
+                    else if constexpr (EPI == GEPI_RESID) g.c[at] = rb(cur[r] + rb(v));
+                    else if constexpr (EPI == GEPI_BIAS) g.c[at] = rb(v + bias);
+                    else g.cb[at] = bf16_bits(silu_rb(rb(v + bias)));
                 }
             }
         }
     }
 }
 
+template <int EPI, class T>
+static hipError_t launch_gemm_t(hipStream_t s, const GemmArgs& g) {
+    // more than the default 64 KiB of dynamic LDS: allowed once per kernel
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<EPI, T>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)T::LDS);
+    if (attr != hipSuccess) return attr;
+    const int tn = EPI == GEPI_SWIGLU_BF16 ? T::TW / 2 : T::TW;
+    const dim3 grid((g.N + tn - 1) / tn, (g.M + T::TM - 1) / T::TM);
+    gemm_kernel<EPI, T><<<grid, T::THREADS, T::LDS, s>>>(g);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_gemm_e(hipStream_t s, const GemmArgs& g) {
+    // the 256 x 256 tile unless its grid would fill fewer than half the CUs
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        return n;
+    }();
+    const int tn = EPI == GEPI_SWIGLU_BF16 ? GemmBig::TW / 2 : GemmBig::TW;
+    const long tiles = (long)((g.N + tn - 1) / tn) * ((g.M + GemmBig::TM - 1) / GemmBig::TM);
+    return 2 * tiles >= cus ? launch_gemm_t<EPI, GemmBig>(s, g) : launch_gemm_t<EPI, GemmNarrow>(s, g);
+}
+
 hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& g) {
     if (g.K % kGemmTK || g.ldx % 8 || g.ldw % 8 || g.M < 1 || g.N < 1) return hipErrorInvalidValue;
+    // the tile loads move 16-byte units
+    if (((uintptr_t)g.x | (uintptr_t)g.w | (uintptr_t)g.w2) & 15) return hipErrorInvalidValue;
     if ((epi == GEPI_BIAS || epi == GEPI_BIAS_SILU_BF16) && !g.bias) return hipErrorInvalidValue;
-    const int tn = epi == GEPI_SWIGLU_BF16 ? 64 : 128;
-    const dim3 grid((g.N + tn - 1) / tn, (g.M + kGemmTM - 1) / kGemmTM);
+    if (epi == GEPI_SWIGLU_BF16 && !g.w2) return hipErrorInvalidValue;
     switch (epi) {
-        case GEPI_RAW: gemm_kernel<GEPI_RAW><<<grid, kGemmThreads, 0, s>>>(g); break;
-        case GEPI_ROUND: gemm_kernel<GEPI_ROUND><<<grid, kGemmThreads, 0, s>>>(g); break;
-        case GEPI_RESID: gemm_kernel<GEPI_RESID><<<grid, kGemmThreads, 0, s>>>(g); break;
-        case GEPI_SWIGLU_BF16: gemm_kernel<GEPI_SWIGLU_BF16><<<grid, kGemmThreads, 0, s>>>(g); break;
-        case GEPI_BIAS: gemm_kernel<GEPI_BIAS><<<grid, kGemmThreads, 0, s>>>(g); break;
-        case GEPI_BIAS_SILU_BF16: gemm_kernel<GEPI_BIAS_SILU_BF16><<<grid, kGemmThreads, 0, s>>>(g); break;
+        case GEPI_RAW: return launch_gemm_e<GEPI_RAW>(s, g);
+        case GEPI_ROUND: return launch_gemm_e<GEPI_ROUND>(s, g);
+        case GEPI_RESID: return launch_gemm_e<GEPI_RESID>(s, g);
+        case GEPI_SWIGLU_BF16: return launch_gemm_e<GEPI_SWIGLU_BF16>(s, g);
+        case GEPI_BIAS: return launch_gemm_e<GEPI_BIAS>(s, g);
+        case GEPI_BIAS_SILU_BF16: return launch_gemm_e<GEPI_BIAS_SILU_BF16>(s, g);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 // ---- rows ----------------------------------------------------------------

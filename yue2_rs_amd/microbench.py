@@ -213,8 +213,9 @@ def main(argv=None) -> int:
     if what in ("copy", "all"):
         print(json.dumps({"bench": "copy", **copy()}), flush=True)
     if what in ("gemm", "all"):
-        for name, n, k, pair in GEMM_SHAPES:
-            print(json.dumps({"bench": "gemm", "shape": name, **gemm(2048, n, k, pair)}), flush=True)
+        for m in (2048, 4096):  # the prefill's chunk rows
+            for name, n, k, pair in GEMM_SHAPES:
+                print(json.dumps({"bench": "gemm", "shape": name, **gemm(m, n, k, pair)}), flush=True)
     if what in ("nar", "all"):
         print(json.dumps({"bench": "nar_velocity", **nar()}), flush=True)
     if what in ("vae", "all"):

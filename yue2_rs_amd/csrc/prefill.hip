@@ -476,20 +476,22 @@ __global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const F
             }
             s[kt] = acc;
         }
-        // scale (in log2 units: exp2 is the hardware exponential), causal mask
-        // (tiles that reach past the wave's first query), online softmax
+        // causal mask (tiles that reach past the wave's first query), online
+        // softmax in log2 units (exp2 is the hardware exponential): the
+        // maximum of the raw scores times the positive scale is the scaled
+        // maximum, and each exponent is one fma, exp2(s scale2 - M)
         const bool masked = kb + KT - 1 > wave_first;
         float mx = -__builtin_huge_valf();
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float v = s[kt][r] * scale2;
+                float v = s[kt][r];
                 if (masked && kb + kt * 16 + 4 * j + r > qpos) v = -__builtin_huge_valf();
                 s[kt][r] = v;
                 mx = fmaxf(mx, v);
             }
-        mx = xor_max<32, 16>(mx);
+        mx = xor_max<32, 16>(mx) * scale2;
         const float mn = fmaxf(m, mx);
         const float alpha = mn == -__builtin_huge_valf() ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
         float sum = 0.0f;
@@ -497,7 +499,8 @@ __global__ __launch_bounds__(kFlashThreads, 2) void flash_prefill_kernel(const F
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(s[kt][r] - mn);
+                const float p =
+                    mn == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], scale2, -mn));
                 s[kt][r] = p;
                 sum += p;
             }

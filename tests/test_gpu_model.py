@@ -1,6 +1,7 @@
 """Full token step on the GPU against the oracle: logits bit-exact at every
 step, greedy ids equal, for the reduced config (256-token prompt, 64 greedy
-steps) and a short run of the 3B-class config."""
+steps), a short run of the 3B-class config, and 256 greedy tokens of the
+full 3B-class model through the device decode loop."""
 import numpy as np
 import pytest
 
@@ -51,4 +52,37 @@ def test_3b_short_run_bit_exact(gpu, oracle_threads, step_kernel):
         t = int(np.argmax(olog))
         glog, olog = gm.forward([t], gcache), om.forward([t], ocache)
         assert np.array_equal(_bits(glog), _bits(olog)), f"3B logits differ at step {step}"
+    gm.close()
+
+
+def test_3b_256_greedy_tokens_through_the_decode_loop(gpu, oracle_threads):
+    """The horizon the bit-exactness claim is made for: 256 greedy tokens of
+    the full 28-layer 3B-class model through the device decode loop (the
+    step kernel with its fused sampler, one launch per token; greedy choice
+    as sampling::generate makes it at temperature 0, src/sampling.rs:258-291)
+    against the oracle's loop: argmax of each step's logits, fed back.  The
+    ids must be equal at every step, and the prefill's logits bit for bit."""
+    ck = synthetic.checkpoint(synthetic.CLASS_3B, seed=0)
+    gm = y2.Model.open(ck)
+    assert gm.set_step_kernel(True)
+    om = O.Model(ck)
+    V, steps = ck.config.vocab_size, 256
+    ids = synthetic.prompt(16, V, seed=4)
+    gcache, glog = gm.prefill_phase(ids, 16 + steps)
+    dec = y2.Decoder(gm, gcache)
+    toks, _ = dec.run(steps, first_logits=glog)
+    dec.close()
+    ocache, olog = om.prefill(ids, 16 + steps)
+    assert np.array_equal(_bits(glog), _bits(olog))
+    want = []
+    for step in range(steps):
+        t = int(np.argmax(olog))
+        want.append(t)
+        if step < len(toks) and int(toks[step]) != t:
+            break
+        if step + 1 < steps:
+            olog = om.forward([t], ocache)
+    first_diff = next((i for i, (a, b) in enumerate(zip(toks, want)) if int(a) != b), None)
+    print(f"256 greedy 3B tokens: first difference at {first_diff}", flush=True)
+    assert list(toks) == want
     gm.close()

@@ -71,6 +71,42 @@ __device__ __forceinline__ void bitonic_sort(uint64_t* v, int n) {
     }
 }
 
+// Rank of `key` among v[0, n): the number of entries below it.  The threads
+// of a wave read the same entry at each step (LDS broadcasts), four at a time.
+__device__ __forceinline__ int rank_below(const uint64_t* v, int n, uint64_t key) {
+    int r = 0, j = 0;
+    for (; j + 4 <= n; j += 4) {
+        const uint64_t a0 = v[j], a1 = v[j + 1], a2 = v[j + 2], a3 = v[j + 3];
+        r += (a0 < key) + (a1 < key) + (a2 < key) + (a3 < key);
+    }
+    for (; j < n; ++j) r += v[j] < key;
+    return r;
+}
+
+// v[0, n) in ascending order, for n distinct keys (sort keys carry the token
+// id).  With at most one entry per thread, each thread moves its entry to its
+// rank in tmp (n entries apart from v) and the block copies tmp back: one
+// pass of n broadcast reads instead of the log2(n)^2 / 2 barrier-separated
+// stages of bitonic_sort, whose order it gives.  Otherwise bitonic_sort over
+// the next power of two (v must hold it; the padding is ~0).  Called by the
+// whole block.
+__device__ __forceinline__ void sort_distinct(uint64_t* v, int n, uint64_t* tmp) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if (n <= nt) {
+        const uint64_t mine = tid < n ? v[tid] : 0;
+        if (tid < n) tmp[rank_below(v, n, mine)] = mine;
+        __syncthreads();
+        if (tid < n) v[tid] = tmp[tid];
+        __syncthreads();
+        return;
+    }
+    int n2 = 2;
+    while (n2 < n) n2 <<= 1;
+    for (int i = n + tid; i < n2; i += nt) v[i] = ~0ull;
+    __syncthreads();
+    bitonic_sort(v, n2);
+}
+
 // CFG mix (src/sampling.rs:261-266) and phase mask (:116-129) of entry i.
 __device__ __forceinline__ float mixed_score(const SampleArgs& a, int i, int step) {
     const float c = a.logits[i];
@@ -159,11 +195,9 @@ __device__ __forceinline__ float seq_sum(const float* v, int n) {
 __device__ __forceinline__ int32_t race_tail(const SampleArgs& a, int step, uint64_t* surv, float* e_val, float* p_s, int n,
                                     int* s_kept, int* s_sel) {
     const int tid = threadIdx.x, nt = blockDim.x;
-    int n2 = 2;
-    while (n2 < n) n2 <<= 1;
-    for (int i = n + tid; i < n2; i += nt) surv[i] = ~0ull;
-    __syncthreads();
-    bitonic_sort(surv, n2);
+    // (e_val, not yet written, lends its room to the sort: n <= the block
+    // size there, at most 1024 keys in its kSurvivorMax floats)
+    sort_distinct(surv, n, reinterpret_cast<uint64_t*>(e_val));
     const float max = key_value(surv[0]);
     for (int i = tid; i < n; i += nt) e_val[i] = expf_cr(key_value(surv[i]) - max);
     __syncthreads();
@@ -222,11 +256,7 @@ __device__ __forceinline__ int32_t race_tail(const SampleArgs& a, int step, uint
         }
     }
     __syncthreads();
-    int k2 = 2;
-    while (k2 < kept) k2 <<= 1;
-    for (int i = kept + tid; i < k2; i += nt) surv[i] = ~0ull;
-    __syncthreads();
-    bitonic_sort(surv, k2);
+    sort_distinct(surv, kept, reinterpret_cast<uint64_t*>(e_val));  // e_val is rewritten below
     const uint32_t* stream = a.stream[step & 1];
     for (int i = tid; i < kept; i += nt) {
         const uint32_t id = (uint32_t)(surv[i] >> 32);

@@ -250,12 +250,16 @@ __device__ __forceinline__ void score_rows(const StepArgs* args, int r0, int r1,
         best = block_min_u64(best, reinterpret_cast<uint64_t*>(red));  // (red's ints are read: barrier inside)
         if (tid == 0) st_agent_u64(fs.cand + w, best);
     } else {
-        int n2 = 2;
-        while (n2 < span) n2 <<= 1;
-        __syncthreads();
-        bitonic_sort(keys, n2);
+        // the n smallest keys in order, each stored at its rank (the keys
+        // are distinct: they carry the id; the non-finite entries, ~0, rank
+        // above every finite one and are not listed)
         const int n = min(fs.list, fin);
-        for (int j = tid; j < n; j += kStepThreads) st_agent_u64(fs.cand + (size_t)w * fs.list + j, keys[j]);
+        for (int j = tid; j < span; j += kStepThreads) {
+            const uint64_t k = keys[j];
+            if (k == ~0ull) continue;
+            const int r = rank_below(keys, span, k);
+            if (r < n) st_agent_u64(fs.cand + (size_t)w * fs.list + r, k);
+        }
     }
     stores_done();  // every candidate and score is stored before the word that announces them
     __syncthreads();
@@ -320,10 +324,16 @@ __device__ __forceinline__ void sampler_wg(const StepArgs* args, const HeadRows 
         const uint64_t head_me = tid < nwork && fin_me > 0 ? ld_tag(mine) : ~0ull;
         const uint64_t last_me = tid < nwork && fin_me >= K ? ld_tag(mine + K - 1) : ~0ull;
         const uint64_t lb1 = block_min_u64(last_me, red);
+        // the K-th smallest head: the present heads are distinct, and the
+        // absent ones (~0) rank above them, so it is the head of rank K - 1,
+        // or absent when fewer than K are present
+        __shared__ uint64_t s_lb2;
+        if (tid == 0) s_lb2 = ~0ull;
         C[tid] = head_me;
         __syncthreads();
-        bitonic_sort(C, kStepThreads);  // the heads in order (absent ones last)
-        const uint64_t lb2 = C[K - 1];
+        if (head_me != ~0ull && rank_below(C, nwork, head_me) == K - 1) s_lb2 = head_me;
+        __syncthreads();
+        const uint64_t lb2 = s_lb2;
         const uint64_t lb_key = kmin(lb1, lb2);
         const bool lb_none = lb_key == ~0ull;
         const float LB = lb_none ? -__builtin_huge_valf() : key_value(lb_key);
@@ -359,11 +369,8 @@ __device__ __forceinline__ void sampler_wg(const StepArgs* args, const HeadRows 
             dst = a.big;
             cap = a.big_cap;
         }
-        int n2 = 2;
-        while (n2 < nc) n2 <<= 1;
-        for (int i = nc + tid; i < n2; i += kStepThreads) dst[i] = ~0ull;
         __syncthreads();
-        bitonic_sort(dst, n2);
+        sort_distinct(dst, nc, reinterpret_cast<uint64_t*>(e_val));  // e_val is free until race_tail
         // T, and the survivors among the listed entries: a prefix of dst
         float T;
         if (lb_none) {

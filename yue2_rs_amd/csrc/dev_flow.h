@@ -155,20 +155,37 @@ __device__ __forceinline__ bool gather(const uint64_t* src, int n, int cols, siz
         n, tag, dst, st);
 }
 
-// v[0] + v[1] + ... + v[n-1] (n >= 1) added left to right, the LDS reads
-// issued eight at a time ahead of their adds (a loop of read-then-add would
-// wait out the LDS latency at every element).
-__device__ __forceinline__ float sum_left_to_right(const float* v, int n) {
+// v[0] + v[1] + ... + v[n-1] (n >= 1) added left to right, v 16-byte
+// aligned: read four values at a time, the next 16 values requested while
+// the current 16 are added (at thousands of keys a workgroup adds hundreds
+// of block sums or partials in sequence, and a read-then-add loop waits out
+// the LDS latency every few adds).
+__device__ __forceinline__ float sum_left_to_right_a16(const float* v, int n) {
+    const float4* q = reinterpret_cast<const float4*>(v);
+    const int nq = n >> 2;
     float s = v[0];
-    int k = 1;
-    for (; k + 8 <= n; k += 8) {
-        float t[8];
+    if (nq > 0) {
+        float4 c[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = v[k + j];
+        for (int j = 0; j < 4; ++j) c[j] = q[min(j, nq - 1)];
+        for (int k = 0; k < nq; k += 4) {
+            float4 nx[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s = s + t[j];
+            for (int j = 0; j < 4; ++j) nx[j] = q[min(k + 4 + j, nq - 1)];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (k + j < nq) {
+                    if (k + j > 0) s = s + c[j].x;
+                    s = s + c[j].y;
+                    s = s + c[j].z;
+                    s = s + c[j].w;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) c[j] = nx[j];
+        }
     }
-    for (; k < n; ++k) s = s + v[k];
+    for (int k = max(nq * 4, 1); k < n; ++k) s = s + v[k];
     return s;
 }
 
@@ -225,11 +242,14 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     float(*q_s)[D] = reinterpret_cast<float(*)[D]>(qkv_s);
     __shared__ float hscale[G + 1];
     __shared__ float t_s[G];
-    __shared__ float red_s[G * MAXNB];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // The group size through an opaque copy outside the PV: with the count
-    // known, the compiler keeps more of the attention's per-head values live
-    // across the layer loop than the kernel has registers for (it spills).
+    __shared__ __align__(16) float red_s[G * MAXNB];
+    // The thread index and the group size through opaque copies: with them
+    // known, the compiler hoists the attention's per-lane offsets and keeps
+    // more of its per-head values live across the layer loop than the kernel
+    // has registers for (it spills).
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = tid >> 6;
     int Gq = G;
     asm volatile("" : "+s"(Gq));
     StepState* st = a.st;
@@ -267,10 +287,20 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                               : make_uint4(0, 0, 0, 0);
         }
     };
-    auto store_chunk = [&](uint4* dst, const uint4* r) {
+    // Unit u (16 bytes) of staged V row `key` holds unit u ^ vperm(key) of the
+    // cache row, so the S streams of a PV read fall in different LDS banks (a
+    // K row is read whole by 16 lanes and is staged as it is).
+    auto vperm = [](int key) { return D == 128 ? 2 * (key & 3) : (key >> 1) & 3; };
+    auto store_chunk = [&](uint4* dst, const uint4* r, bool isv) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (tid + i * NT < kAttnChunk * BLK_U4) dst[tid + i * NT] = r[i];
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT, key = u / (D / 8), part = u % (D / 8);
+            if (u < kAttnChunk * BLK_U4) dst[key * (D / 8) + (part ^ (isv ? vperm(key) : 0))] = r[i];
+        }
+    };
+    // element d of staged row `key` (permuted as above)
+    auto staged = [&](uint4* base, int key, int d, bool isv) {
+        return reinterpret_cast<uint16_t*>(base + key * (D / 8) + ((d >> 3) ^ (isv ? vperm(key) : 0))) + (d & 7);
     };
 
     // ---- phase 0: early requests, queries, new key/value --------------------
@@ -311,8 +341,8 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         const float s = norm_scale_wave(wave < Gq ? q_s[wave] : k_s, D, a.eps);
         if (lane == 0) hscale[wave] = s;
     }
-    store_chunk(Ks, kr);
-    store_chunk(Vs, vr);
+    store_chunk(Ks, kr, false);
+    store_chunk(Vs, vr, true);
     __syncthreads();
     // rotate-half RoPE (src/model.rs:151-168); the new key and value go to the
     // cache for later steps and straight into the staged chunk for this one
@@ -330,9 +360,8 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
             gblw(Kc)[(size_t)pos * D + d + HALF] = bf16_bits(y1);
             if (pos - j0 < kAttnChunk * kBlockKeys) {
-                uint16_t* kl = reinterpret_cast<uint16_t*>(Ks) + (size_t)(pos - j0) * D;
-                kl[d] = bf16_bits(y0);
-                kl[d + HALF] = bf16_bits(y1);
+                *staged(Ks, pos - j0, d, false) = bf16_bits(y0);
+                *staged(Ks, pos - j0, d + HALF, false) = bf16_bits(y1);
             }
         }
     }
@@ -340,66 +369,88 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         for (int d = tid; d < D; d += NT) {
             const uint16_t bits = bf16_bits(v_s[d]);
             gblw(Vc)[(size_t)pos * D + d] = bits;
-            if (pos - j0 < kAttnChunk * kBlockKeys) reinterpret_cast<uint16_t*>(Vs)[(size_t)(pos - j0) * D + d] = bits;
+            if (pos - j0 < kAttnChunk * kBlockKeys) *staged(Vs, pos - j0, d, true) = bits;
         }
     __syncthreads();
     mark();
 
     // ---- phase 1: scaled scores and block maxima ---------------------------
     // The DOT order of a score (one fma chain per 8-dim chunk, then the xor
-    // butterfly over the chunks, largest distance first): lane c of a
-    // SCPL-lane key group keeps the chains of chunks c, c + SCPL, ... and
-    // adds them in-lane in the butterfly's order (its distances of SCPL and
-    // more), then the group's lanes finish with the distances below SCPL.
+    // butterfly over the chunks, largest distance first), with lane c of a
+    // SCPL-lane group holding chunk c and its query chunks in registers.
+    // Each group takes four keys at a time; the butterfly's first two
+    // distances run as a reduce-scatter (a lane adds its partner's partials
+    // of the keys it keeps: the same two operands as the butterfly's add, a
+    // quarter of the exchanges), so lane c ends with key 2 b1 + b2 (b1, b2
+    // its bits of the two distances) and the rest of the butterfly runs on
+    // that key alone.
     const uint32_t t_bmax = flow_tag(a.epoch, a.layer, FK_BMAX);
     {
-        constexpr int SCPL = 4;              // lanes per key
-        constexpr int NCH = D / 8 / SCPL;    // chains per lane
-        constexpr int SKPW = 64 / SCPL;      // keys per wave pass
-        static_assert(NCH >= 1 && (NCH & (NCH - 1)) == 0, "chains per lane");
-        const int c = lane % SCPL, kk = lane / SCPL;
+        constexpr int SCPL = D / 8;          // lanes per key
+        constexpr int GPW = 64 / SCPL;       // lane groups per wave
+        constexpr int H1 = SCPL / 2, H2 = SCPL / 4;
+        static_assert(H2 >= 2, "a butterfly distance after the reduce-scatter");
+        const int c = lane % SCPL, grp = lane / SCPL;
+        const bool b1 = (c & H1) != 0, b2 = (c & H2) != 0;
+        float qr[G][8];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            if (h >= Gq) break;
+            const float4* qp = reinterpret_cast<const float4*>(q_s[h] + 8 * c);
+            const float4 q0 = qp[0], q1 = qp[1];
+            qr[h][0] = q0.x; qr[h][1] = q0.y; qr[h][2] = q0.z; qr[h][3] = q0.w;
+            qr[h][4] = q1.x; qr[h][5] = q1.y; qr[h][6] = q1.z; qr[h][7] = q1.w;
+        }
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
                 // a later chunk (long contexts), requested during the previous
                 // chunk's scores: stage it, then patch the new key
                 __syncthreads();
-                store_chunk(Ks, kr);
+                store_chunk(Ks, kr, false);
                 __syncthreads();
                 const int kp = pos - j0 - cb * kBlockKeys;
                 if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
                     for (int d = tid; d < D; d += NT)
-                        reinterpret_cast<uint16_t*>(Ks)[(size_t)kp * D + d] = bf16_bits(k_s[d]);
+                        *staged(Ks, kp, d, false) = bf16_bits(k_s[d]);
                 __syncthreads();
             }
             // the next chunk's loads stay in flight while this one is scored
             if (cb + kAttnChunk < nbl) load_chunk(Kc, cb + kAttnChunk, kr);
             const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
-            for (int kg = wave; kg * SKPW < keys; kg += NW) {
-                const int kl = kg * SKPW + kk;  // key within the chunk (rows past `keys` are never stored)
-                const int j = j0 + cb * kBlockKeys + kl;
-                float kf[NCH][8];
+            for (int qd0 = wave * GPW; qd0 * 4 < keys; qd0 += NW * GPW) {
+                const int kq = 4 * (qd0 + grp);  // the group's first key within the chunk
+                float v[4][G];
 #pragma unroll
-                for (int i = 0; i < NCH; ++i) unpack8a(Ks[(size_t)kl * (D / 8) + c + SCPL * i], kf[i]);
+                for (int r = 0; r < 4; ++r) {
+                    // (rows past the chunk's keys are read clamped and never stored)
+                    const int kl = min(kq + r, kAttnChunk * kBlockKeys - 1);
+                    float kf[8];
+                    unpack8a(Ks[(size_t)kl * (D / 8) + c], kf);
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    if (h >= Gq) break;
-                    float ch[NCH];
-#pragma unroll
-                    for (int i = 0; i < NCH; ++i) {
-                        const float4* qp = reinterpret_cast<const float4*>(q_s[h] + 8 * (c + SCPL * i));
-                        const float4 q0 = qp[0], q1 = qp[1];
-                        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                    for (int h = 0; h < G; ++h) {
                         float acc = 0.0f;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qv[e], kf[i][e], acc);
-                        ch[i] = acc;
+                        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qr[h][e], kf[e], acc);
+                        v[r][h] = acc;
                     }
+                }
+                // distance H1: keep keys 2 b1, 2 b1 + 1
+                float w[2][G];
 #pragma unroll
-                    for (int m = NCH / 2; m >= 1; m /= 2)
+                for (int i = 0; i < 2; ++i)
 #pragma unroll
-                        for (int i = 0; i < m; ++i) ch[i] = ch[i] + ch[i + m];
-                    const float acc = xor_sum<SCPL / 2>(ch[0]);
-                    if (c == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
+                    for (int h = 0; h < G; ++h) {
+                        const float keep = b1 ? v[2 + i][h] : v[i][h], send = b1 ? v[i][h] : v[2 + i][h];
+                        w[i][h] = keep + xor_lane<H1>(send);
+                    }
+                // distance H2: keep key b2 of the two
+                const int kl = kq + 2 * (b1 ? 1 : 0) + (b2 ? 1 : 0);
+                const int j = j0 + cb * kBlockKeys + kl;
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float keep = b2 ? w[1][h] : w[0][h], send = b2 ? w[0][h] : w[1][h];
+                    const float acc = xor_sum<H2 / 2>(keep + xor_lane<H2>(send));
+                    if (h < Gq && (c & (H2 - 1)) == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
                 }
             }
         }
@@ -445,10 +496,27 @@ m = xor_max<32>(m);
     // ---- phase 3: total, p = e / total, partial PV -------------------------
     const uint32_t t_part = flow_tag(a.epoch, a.layer, FK_PART);
     {
-        if (!gather<NT, (G * MAXNB + NT - 1) / NT>(a.bsum + hbase, Gq * nb, nb, a.blk_stride, t_bsum, red_s, st))
-            return false;
+        // head h's block sums at red_s[h * nbp + k] (rows 16-byte aligned)
+        const int nbp = (nb + 3) & ~3;
+        {
+            const FastDiv fnb(nb);
+            const uint64_t* src = a.bsum + hbase;
+            const size_t bstride = a.blk_stride;
+            if (!gather_put<NT, (G * MAXNB + NT - 1) / NT>(
+                    [=](int i) {
+                        const int h = fnb.div(i);
+                        return src + (size_t)h * bstride + (i - h * nb);
+                    },
+                    Gq * nb, t_bsum,
+                    [=](int i, uint32_t bits) {
+                        const int h = fnb.div(i);
+                        red_s[h * nbp + (i - h * nb)] = u2f(bits);
+                    },
+                    st))
+                return false;
+        }
         mark();
-        if (tid < Gq) t_s[tid] = sum_left_to_right(red_s + tid * nb, nb);  // block sums
+        if (tid < Gq) t_s[tid] = sum_left_to_right_a16(red_s + tid * nbp, nb);  // block sums
         __syncthreads();
         // p = e / total into the K region (the scores are done with it), in
         // stream order: p_s[h * estride + bl * 64 + t * KPS + i] is p of key
@@ -467,69 +535,64 @@ m = xor_max<32>(m);
             }
         }
         __syncthreads();
-        // PV: one (block, half of the dims) item per wave, all G heads at
-        // once (V read and unpacked once for them).  Lane (t, c): stream t,
-        // dims d0 .. d0 + 3.  The chains are branch-free: keys past the
-        // context have zero V rows (staged so) and p = 0, and fma(0, 0, acc)
-        // = acc (a chain from +0 is never -0).
+        // PV: one (block, eighth of the dims) item per wave, all G heads at
+        // once (V read and unpacked once for them), so a chunk's three blocks
+        // are three full passes of the eight waves.  Lane (t, c): stream t
+        // (keys t, t + S, ...), dimension d0 + c.  The chains are
+        // branch-free: keys past the context have zero V rows (staged so) and
+        // p = 0, and fma(0, 0, acc) = acc (a chain from +0 is never -0).
         constexpr int LPS = 64 / S;  // lanes per stream
-        static_assert(LPS * 4 * 2 == D, "two 4-dim parts per lane group");
+        static_assert(LPS * NW == D, "one dimension per lane, the eight waves over a block's dimensions");
         const int t = lane / LPS, c = lane % LPS;
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
                 // requested one chunk ahead, as the keys
                 __syncthreads();
-                store_chunk(Vs, vr);
+                store_chunk(Vs, vr, true);
                 __syncthreads();
                 const int kp = pos - j0 - cb * kBlockKeys;
                 if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
-                    for (int d = tid; d < D; d += NT)
-                        reinterpret_cast<uint16_t*>(Vs)[(size_t)kp * D + d] = bf16_bits(v_s[d]);
+                    for (int d = tid; d < D; d += NT) *staged(Vs, kp, d, true) = bf16_bits(v_s[d]);
                 __syncthreads();
                 if (cb + kAttnChunk < nbl) load_chunk(Vc, cb + kAttnChunk, vr);
             }
             const int cblocks = min(kAttnChunk, nbl - cb);
-            for (int it = wave; it < cblocks * 2; it += NW) {
-                const int bc = it >> 1, bl = cb + bc, d0 = (it & 1) * (D / 2) + 4 * c;
-                const uint16_t* vrow = reinterpret_cast<const uint16_t*>(Vs) + (size_t)(bc * kBlockKeys + t) * D + d0;
+            for (int it = wave; it < cblocks * NW; it += NW) {
+                const int bc = it / NW, bl = cb + bc, d = (it % NW) * LPS + c;
+                // (the keys t + S i of a stream share their unit permutation)
+                const uint16_t* vrow = staged(Vs, bc * kBlockKeys + t, d, true);
                 const float* pp = p_s + bl * kBlockKeys + t * KPS;
-                float acc[G][4];
+                float acc[G];
 #pragma unroll
-                for (int h = 0; h < G; ++h)
+                for (int h = 0; h < G; ++h) acc[h] = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[h][e] = 0.0f;
-#pragma unroll 1
                 for (int i0 = 0; i0 < KPS; i0 += 4) {
                     // four keys' V and the G heads' p requested together
-                    uint2 w[4];
+                    float vf[4];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const uint2*>(vrow + (size_t)S * (i0 + u) * D);
+                    for (int u = 0; u < 4; ++u) vf[u] = bf16(vrow[(size_t)S * (i0 + u) * D]);
                     float4 p4[G];
 #pragma unroll
                     for (int h = 0; h < G; ++h)
                         p4[h] = *reinterpret_cast<const float4*>(pp + h * estride + i0);
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
-                        const float vf[4] = {bf16_lo(w[u].x), bf16_hi(w[u].x), bf16_lo(w[u].y), bf16_hi(w[u].y)};
 #pragma unroll
                         for (int h = 0; h < G; ++h) {
                             const float pv = u == 0 ? p4[h].x : u == 1 ? p4[h].y : u == 2 ? p4[h].z : p4[h].w;
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) acc[h][e] = __builtin_fmaf(pv, vf[e], acc[h][e]);
+                            acc[h] = __builtin_fmaf(pv, vf[u], acc[h]);
                         }
                     }
                 }
                 // streams combined in the butterfly order (distances S/2 .. 1
-                // between streams = lane distances 32 .. LPS); the S stream
-                // lanes then hold the same sums and each stores its share
+                // between streams = lane distances 32 .. LPS); every stream
+                // lane then holds the same sums and lane t stores head h when
+                // h % S == t
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float v = xor_sum<32, LPS>(acc[h][e]);
-                        if ((h * 4 + e) % S == t)
-                            st_tag(a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + d0 + e, v, t_part);
-                    }
+                    const float v = xor_sum<32, LPS>(acc[h]);
+                    if (h % S == t)
+                        st_tag(a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + d, v, t_part);
                 }
             }
         }
@@ -541,25 +604,34 @@ m = xor_max<32>(m);
         const int outs = Gq * D, chunk = (outs + W - 1) / W;
         const int o0 = min(outs, wi * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
         __syncthreads();  // the K/V region is reused below
-        float* m_buf = lds;  // [no][nb]: partial of block k for output o0 + i
+        const int nbp = (nb + 3) & ~3;
+        float* m_buf = lds;  // [no][nbp]: partial of block k for output o0 + i (rows 16-byte aligned)
         const uint64_t* part = a.part + hbase * D;
         const size_t hstride = (size_t)a.blk_stride * D;
-        const FastDiv fnb(nb);
+        const FastDiv fno(max(no, 1));
         // in passes of at most kMergeBatch words per thread: one pass at
-        // short contexts, and the unrolled poll stays small
+        // short contexts, and the unrolled poll stays small; word i of the
+        // sequence is output o0 + i % no of block i / no, so neighbouring
+        // threads read neighbouring words of a block's partial
         for (int p0 = 0; p0 < no * nb; p0 += NT * kMergeBatch) {
-            if (!gather_at<NT, kMergeBatch>(
+            if (!gather_put<NT, kMergeBatch>(
                     [=](int i) {
                         i += p0;
-                        const int r = fnb.div(i), o = o0 + r, k = i - r * (int)fnb.d;
+                        const int k = fno.div(i), o = o0 + i - k * no;
                         return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
                     },
-                    min(no * nb - p0, NT * kMergeBatch), t_part, m_buf + p0, st))
+                    min(no * nb - p0, NT * kMergeBatch), t_part,
+                    [=](int i, uint32_t bits) {
+                        i += p0;
+                        const int k = fno.div(i);
+                        m_buf[(i - k * no) * nbp + k] = u2f(bits);
+                    },
+                    st))
                 return false;
         }
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
         for (int i = tid; i < no; i += NT) {
-            const float o = sum_left_to_right(m_buf + i * nb, nb);  // blocks left to right
+            const float o = sum_left_to_right_a16(m_buf + i * nbp, nb);  // blocks left to right
             st_tag(a.att + (size_t)b * a.att_stride + (size_t)g * Gq * D + o0 + i, rb(o), t_att);
         }
     }

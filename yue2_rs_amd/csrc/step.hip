@@ -699,8 +699,13 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const int max_blocks = (c.max_position_embeddings + kBlockKeys - 1) / kBlockKeys;
     const int bpw = (max_blocks + wpg - 1) / wpg;
     // the attention's p (G x bpw blocks of f32) is staged in its K region
+    // (the merge's partials, G x head_dim x bpw + blocks words at most, are
+    // gathered kMergePer per thread into the K/V region with rows padded to
+    // four floats)
+    const int merge_words = G * c.head_dim * bpw + max_blocks;
     return G <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows && max_blocks <= 24576 / kBlockKeys &&
-           G * c.head_dim * bpw + max_blocks <= kStepThreads * kMergePer &&
+           merge_words <= kStepThreads * kMergePer &&
+           (size_t)(merge_words + 3 * G * c.head_dim) * 4 <= (size_t)2 * kAttnChunk * kBlockKeys * c.head_dim * 2 &&
            G * bpw * kBlockKeys * 4 <= kAttnChunk * kBlockKeys * c.head_dim * 2;
 }
 

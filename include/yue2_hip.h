@@ -175,7 +175,9 @@ Yue2Model *yue2_hip_model_open_dir(const char *dir);
  * NULL) receives the configuration.  0 or a negative Yue2Error
  * (YUE2_ERR_CONFIG where the reference returns InvalidData). */
 int32_t yue2_hip_checkpoint_config(const char *dir, Yue2Config *out);
-/* Model's Drop (src/model.rs:411-416). */
+/* Model's Drop (src/model.rs:411-416).  Caches and decoders created on the
+ * model use its stream and workspace: free them first (freeing one after its
+ * model is a use after free). */
 void yue2_hip_model_free(Yue2Model *m);
 
 /* Cache::new (src/model.rs:292-305): a device BF16 KV cache of `capacity`

@@ -101,3 +101,53 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(api, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(FileNotFoundError):
         api.lib()
+
+
+def test_model_close_frees_its_caches_and_decoders_first():
+    """Model.close() closes the caches and decoders made on the model before
+    the model itself (their C objects use the model's stream and workspace),
+    so dropping one later -- as an interpreter does at exit with objects a
+    failed test left referenced -- calls nothing on a freed model.  Host
+    logic only: stand-in objects and library, no device calls."""
+    import weakref
+    from yue2_rs_amd import api
+
+    order = []
+
+    class Child:  # closes once, as Cache.close does
+        def __init__(self, name):
+            self.name, self.open = name, True
+
+        def close(self):
+            if self.open:
+                order.append(self.name)
+                self.open = False
+
+    class FakeDecoder(api.Decoder):
+        def __init__(self):  # no device call
+            self.open = True
+
+        def close(self):
+            if self.open:
+                order.append("decoder")
+                self.open = False
+
+    class FakeLib:
+        @staticmethod
+        def yue2_hip_model_free(h):
+            order.append("model")
+
+    m = api.Model.__new__(api.Model)
+    m._h, m._children = 1, weakref.WeakSet()
+    kids = [Child("cache1"), Child("cache2"), FakeDecoder()]
+    for ch in kids:
+        m._children.add(ch)
+    real_lib = api.lib
+    api.lib = lambda: FakeLib
+    try:
+        m.close()
+        m.close()  # a second close frees nothing
+    finally:
+        api.lib = real_lib
+    assert order[0] == "decoder" and order[-1] == "model" and len(order) == 4
+    assert sorted(order[1:3]) == ["cache1", "cache2"]

@@ -9,6 +9,7 @@ path, and loading fails loudly when the library is missing.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Optional, Sequence
@@ -279,6 +280,9 @@ class Model:
         self._h = handle
         self.config = config
         self._ckpt = checkpoint  # host arrays stay alive with the model
+        # caches and decoders on this model: freed before it (their C
+        # objects use the model's stream and workspace)
+        self._children = weakref.WeakSet()
 
     @classmethod
     def open(cls, checkpoint: Checkpoint) -> "Model":
@@ -308,6 +312,12 @@ class Model:
 
     def close(self) -> None:
         if self._h:
+            children = list(self._children)
+            for ch in children:  # decoders before the caches they run on
+                if isinstance(ch, Decoder):
+                    ch.close()
+            for ch in children:
+                ch.close()
             lib().yue2_hip_model_free(self._h)
             self._h = None
 
@@ -409,6 +419,7 @@ class Cache:
         if not self._h:
             raise Yue2Error(-10, lib().yue2_hip_last_error().decode())
         self.capacity = capacity
+        model._children.add(self)
 
     @property
     def length(self) -> int:
@@ -494,6 +505,7 @@ class Decoder:
         if not self._h:
             raise Yue2Error(-13, lib().yue2_hip_last_error().decode())
         self.rows = 2 if scale != 1.0 else 1
+        model._children.add(self)
 
     def run(self, steps: int, first_logits: Optional[np.ndarray] = None, timing: bool = False):
         """Run `steps` steps; returns (tokens, step_ms or None)."""

@@ -225,7 +225,8 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 //  - K and V go through LDS (kAttnChunk blocks at a time), and the owner of
 //    the newest key uses its freshly computed row from there, so the cache
 //    append needs no completion wait;
-//  - PV runs one (block, half of the dims) item per wave, for all heads.
+//  - the scores keep each lane's query chunk in registers; PV runs one
+//    (block, eighth of the dims) item per wave, for all heads.
 // G = heads / kv_heads, the query heads of a group (the host checks that the
 // launch's shape has this G).  lds: attn_flow_lds(G, D, bpw) bytes.  false:
 // timeout (error set).

@@ -131,12 +131,12 @@ def prefill_report(c, n, seconds, mode):
             "flops": fl}
 
 
-def measured_traffic(context):
+def measured_traffic(context, profile="step_kernel_3b_cfg_traffic.md"):
     """HBM bytes per launch of the CFG step kernel from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (calibrated against a plain copy)
     of the bench's own timing loop, when they were measured at this context;
     otherwise None."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "step_kernel_3b_cfg_traffic.md")
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
     try:
         text = open(path).read()
     except OSError:
@@ -489,8 +489,9 @@ def long_context(args, y2, synthetic, c, ckpt, model, step_kernel):
     assert c_pos.length == full and c_neg.length == full
     dec.close()
     achieved = dom_b / (dom_ms * 1e-3) / 1e9
+    traffic = measured_traffic(context, "step_kernel_3b_cfg_context24575_traffic.md") if step_kernel else None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(achieved / 8000.0, 4), "traffic": None, "kernel": dom_name,
+                "frac": round(achieved / 8000.0, 4), "traffic": traffic, "kernel": dom_name,
                 "launch_ms": round(dom_ms, 5), "bytes_per_launch": int(dom_b), "context": context}
     cpu = None
     if not args.no_cpu:

@@ -201,7 +201,7 @@ struct FlowAttn {
     float scale, eps;
     const float *q_norm, *k_norm, *cos_t, *sin_t;
     uint64_t *bmax, *bsum, *part;  // tagged [rows][heads][blk_stride] (part: x dim)
-    uint64_t* att;                 // tagged [rows][att_stride]
+    uint64_t* att;                 // tagged [rows][att_stride / 2]: outputs 2p, 2p + 1 packed
     uint32_t epoch;
     StepState* st;
 };
@@ -602,7 +602,9 @@ m = xor_max<32>(m);
 
     // ---- merge: workgroup wi adds the blocks of outputs [o0, o1) -----------
     {
-        const int outs = Gq * D, chunk = (outs + W - 1) / W;
+        // (an even count each: outputs 2p and 2p + 1, both BF16-exact, go out
+        // packed in one word, half the words the O projection gathers)
+        const int outs = Gq * D, chunk = ((outs + W - 1) / W + 1) & ~1;
         const int o0 = min(outs, wi * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
         __syncthreads();  // the K/V region is reused below
         const int nbp = (nb + 3) & ~3;
@@ -631,9 +633,13 @@ m = xor_max<32>(m);
                 return false;
         }
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
-        for (int i = tid; i < no; i += NT) {
-            const float o = sum_left_to_right_a16(m_buf + i * nbp, nb);  // blocks left to right
-            st_tag(a.att + (size_t)b * a.att_stride + (size_t)g * Gq * D + o0 + i, rb(o), t_att);
+        for (int i0 = 0; i0 < no; i0 += NT) {
+            const int i = i0 + tid;
+            const float o = i < no ? rb(sum_left_to_right_a16(m_buf + i * nbp, nb)) : 0.0f;  // blocks left to right
+            const float o_next = xor_lane<1>(o);  // output i + 1 (the odd neighbour lane's)
+            if (i < no && (tid & 1) == 0)
+                st_tag_bits(a.att + ((size_t)b * a.att_stride + (size_t)g * Gq * D + o0 + i) / 2, pack_rows(o, o_next),
+                            t_att);
         }
     }
     return true;

@@ -84,6 +84,21 @@ __device__ __forceinline__ bool stage_rows(float* xs, const uint64_t* tx, int k,
     }
 }
 
+// xs[b * k + i] = row b's attention output i, i < k: words tx[b * k / 2 + p]
+// each hold outputs 2p (low half) and 2p + 1 (high half) of a row.
+template <int B, int N>
+__device__ __forceinline__ bool stage_att(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
+    static_assert(B * N <= 32, "at most 16 words per thread in flight");
+    const int h = k / 2;
+    return gather_put<kStepThreads, (B * N + 1) / 2>([=](int i) { return tx + i; }, B * h, tag,
+                                                     [=](int i, uint32_t bits) {
+                                                         const int b = i >= h ? 1 : 0, p = i - b * h;
+                                                         xs[b * k + 2 * p] = bf16_lo(bits);
+                                                         xs[b * k + 2 * p + 1] = bf16_hi(bits);
+                                                     },
+                                                     st);
+}
+
 // stage_rows for x ahead of its RMSNorm, plus each thread's shares of the
 // norm's sums.  With packed words (two rows) the shares are added as the
 // words arrive (over the elements this thread stages, in arrival order), so
@@ -603,7 +618,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
             prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
             a = fresh(args);
-            if (!stage<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
+            if (!stage_att<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
             gemv_ring<B, EPI_RESID, ITQ, false, kPack<B>>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
@@ -702,7 +717,7 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     // (the merge's partials, G x head_dim x bpw + blocks words at most, are
     // gathered kMergePer per thread into the K/V region with rows padded to
     // four floats)
-    const int merge_words = G * c.head_dim * bpw + max_blocks;
+    const int merge_words = G * c.head_dim * bpw + 2 * max_blocks;
     return G <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows && max_blocks <= 24576 / kBlockKeys &&
            merge_words <= kStepThreads * kMergePer &&
            (size_t)(merge_words + 3 * G * c.head_dim) * 4 <= (size_t)2 * kAttnChunk * kBlockKeys * c.head_dim * 2 &&

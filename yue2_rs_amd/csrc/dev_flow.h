@@ -191,8 +191,9 @@ __device__ __forceinline__ float sum_left_to_right_a16(const float* v, int n) {
 
 // Arguments of one layer's attention in the step kernel.
 struct FlowAttn {
-    // tagged q heads, k heads, v heads: [rows][qkv_stride] words, or (packed)
-    // [qkv_stride] words holding both batch rows
+    // tagged q heads, k heads, v heads: (packed) [qkv_stride] words holding
+    // both batch rows, else [qkv_stride / 2] words of one row holding
+    // outputs 2p and 2p + 1
     const uint64_t* qkv;
     int qkv_stride;
     bool packed;
@@ -319,19 +320,33 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         c_cos = gbl(a.cos_t + (size_t)pos * HALF)[d];
         c_sin = gbl(a.sin_t + (size_t)pos * HALF)[d];
     }
-    {
-        // one gather for all three: a single wait
+    if (a.packed) {
+        // one gather for all three: a single wait; each word holds both
+        // batch rows, this row takes its half
         const int nq = Gq * D;
         const uint64_t* qsrc = row + (size_t)(g * Gq) * D;
         const uint64_t* ksrc = row + (size_t)(a.heads + g) * D;
         const uint64_t* vsrc = row + (size_t)(a.heads + a.kv_heads + g) * D;
-        // this batch row's half of a packed word
-        const int shift = a.packed ? (b ? 0 : 16) : 0;
-        const uint32_t keep = a.packed ? 0xffff0000u : 0xffffffffu;
+        const int shift = b ? 0 : 16;
         if (!gather_put<NT, ((G + 2) * D + NT - 1) / NT>(
                 [=](int i) { return i < nq ? qsrc + i : (i < nq + D ? ksrc + (i - nq) : vsrc + (i - nq - D)); },
                 nq + (owns_new ? 2 * D : 0), t_qkv,
-                [=](int i, uint32_t bits) { qkv_s[i] = u2f((bits << shift) & keep); }, st))
+                [=](int i, uint32_t bits) { qkv_s[i] = u2f((bits << shift) & 0xffff0000u); }, st))
+            return false;
+    } else {
+        // one batch row: word p holds outputs 2p and 2p + 1
+        const int nq = Gq * D / 2, hd = D / 2;
+        const uint64_t* qsrc = row + (size_t)(g * Gq) * hd;
+        const uint64_t* ksrc = row + (size_t)(a.heads + g) * hd;
+        const uint64_t* vsrc = row + (size_t)(a.heads + a.kv_heads + g) * hd;
+        if (!gather_put<NT, ((G + 2) * D / 2 + NT - 1) / NT>(
+                [=](int i) { return i < nq ? qsrc + i : (i < nq + hd ? ksrc + (i - nq) : vsrc + (i - nq - hd)); },
+                nq + (owns_new ? D : 0), t_qkv,
+                [=](int i, uint32_t bits) {
+                    qkv_s[2 * i] = bf16_lo(bits);
+                    qkv_s[2 * i + 1] = bf16_hi(bits);
+                },
+                st))
             return false;
     }
     mark();

@@ -160,13 +160,17 @@ __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t*
 // null); the ring holds the first R-1 items (prefetch_ring).  res: for
 // EPI_RESID, res[b * (r1 - r0) + (row - r0)] = the row's current value (LDS).
 // PACK (B == 2, the outputs BF16-exact): one packed word per row holds both
-// batch rows (ty[row]); y_stride then only applies to y.
+// batch rows (ty[row]); y_stride then only applies to y.  PAIRS (B == 1, the
+// outputs BF16-exact, r0 and r1 even): one word holds rows 2p and 2p + 1
+// (ty[p]); the rows are collected in pk (LDS, r1 - r0 floats) and stored
+// after a block barrier, so every thread of the block calls this.
 // (Writing the new value back to res here instead of re-reading it later
 // measured slower: the GEMVs of the whole kernel lost about half their rate.)
-template <int B, int EPI, int IT, bool MASK = false, bool PACK = false>
+template <int B, int EPI, int IT, bool MASK = false, bool PACK = false, bool PAIRS = false>
 __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2, const float* xs, int k,
                                           float* y, uint64_t* ty, uint32_t tag, int y_stride, int r0, int r1,
-                                          int n, uint4* ring, const float* res = nullptr) {
+                                          int n, uint4* ring, const float* res = nullptr, float* pk = nullptr) {
+    static_assert(!PAIRS || B == 1, "row pairs with one batch row");
     constexpr bool PAIR = EPI == EPI_SWIGLU;
     using C = Ring<IT, PAIR>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, span = r1 - r0;
@@ -197,7 +201,9 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
                     acc[b] = acc2[b] = 0.0f;
                 }
                 if (lane == 0) {
-                    if (PACK && ty) {
+                    if (PAIRS && ty) {
+                        pk[row - r0] = out_value<EPI>(v[0], v2[0], EPI == EPI_RESID ? res[row - r0] : 0.0f);
+                    } else if (PACK && ty) {
                         static_assert(!PACK || B == 2, "packed words hold two batch rows");
                         float o[B];
 #pragma unroll
@@ -217,6 +223,15 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
                     }
                 }
             }
+        }
+    }
+    if constexpr (PAIRS) {
+        if (ty) {
+            // every wave's rows are in pk (LDS only: the ring's last loads
+            // stay in flight)
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            for (int t = threadIdx.x; t < span / 2; t += blockDim.x)
+                st_tag_bits(ty + r0 / 2 + t, pack_rows(pk[2 * t], pk[2 * t + 1]), tag);
         }
     }
 }

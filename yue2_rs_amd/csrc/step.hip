@@ -63,24 +63,36 @@ struct Tracer {
 // two rows one packed word carries both (half the words to poll).
 template <int B>
 constexpr bool kPack = B == 2;
+// With one row, the GEMV outputs that other workgroups gather (x, q/k/v, the
+// SwiGLU activations; BF16-exact) go out two per word: rows 2p and 2p + 1.
+template <int B>
+constexpr bool kPair = B == 1;
+constexpr int kPairRowsMax = 64;  // rows of one such GEMV per workgroup
 
-// xs[b * k + i] = word tx[b * k + i] with the given tag, for b < B, i < k
-// (words of one f32 each).
-template <int B, int N>
-__device__ __forceinline__ bool stage(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
-    static_assert(B * N <= 16, "at most 16 words per thread in flight");
-    return gather_flat<kStepThreads, B * N>(tx, B * k, tag, xs, st);
+// First row of workgroup w's share of an exchanged GEMV output of n rows:
+// even for paired words (a pair never straddles two workgroups).
+template <int B>
+__device__ __forceinline__ int xlo(int n, int w, int parts) {
+    return kPair<B> ? 2 * part_lo(n / 2, w, parts) : part_lo(n, w, parts);
 }
 
+
 // xs[b * k + i] = row b's value of x-like words tx (packed for two rows,
-// else tx[b * k + i]), i < k.
+// for one row two values per word), i < k.
 template <int B, int N>
 __device__ __forceinline__ bool stage_rows(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
     if constexpr (kPack<B>) {
         static_assert(N <= 16, "at most 16 words per thread in flight");
         return gather_pair<kStepThreads, N>(tx, k, tag, xs, st);
     } else {
-        return stage<B, N>(xs, tx, k, tag, st);
+        // one row: word p holds rows 2p and 2p + 1
+        static_assert(kPair<B>, "one or two rows");
+        return gather_put<kStepThreads, (N + 1) / 2>([=](int i) { return tx + i; }, k / 2, tag,
+                                                     [=](int i, uint32_t bits) {
+                                                         xs[2 * i] = bf16_lo(bits);
+                                                         xs[2 * i + 1] = bf16_hi(bits);
+                                                     },
+                                                     st);
     }
 }
 
@@ -512,6 +524,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     // misaligned
     extern __shared__ __align__(16) float lds[];
     __shared__ float res_s[B * kResRows];  // this workgroup's rows of x (residual)
+    __shared__ float pk_s[kPairRowsMax];   // one row: a GEMV's outputs before they go out in pairs
     constexpr int RMAX = std::max(std::max(Ring<ITH, false>::SIZE, Ring<ITH, true>::SIZE),
                                   std::max(Ring<ITQ, false>::SIZE, Ring<ITI, false>::SIZE));
     const ArgsPtr args = (ArgsPtr)args_dev;
@@ -553,8 +566,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             }
         }
         load_gamma<ITH>(layer_at(a, 0)->in_norm, H, gam);
-        prefetch_ring<ITH, false>(layer_at(a, 0)->wqkv, nullptr, H, part_lo(qkvw, wg, nwg),
-                                  part_lo(qkvw, wg + 1, nwg), qkvw, ring);
+        prefetch_ring<ITH, false>(layer_at(a, 0)->wqkv, nullptr, H, xlo<B>(qkvw, wg, nwg),
+                                  xlo<B>(qkvw, wg + 1, nwg), qkvw, ring);
         for (int b = 0; b < B; ++b) {
             const auto* e = gbl(a->embed + (size_t)ids[b] * H);
             for (int i = tid; i < H; i += kStepThreads) lds[b * H + i] = bf16(e[i]);
@@ -575,7 +588,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int lc = min(l, layers_n - 1);  // layer pointers are never read past the table
             const int H = a->hidden, n = last ? hr.n : (a->heads + 2 * a->kv_heads) * D;
             const uint16_t* w = last ? a->lm_head + (size_t)hr.lo * H : layer_at(a, lc)->wqkv;
-            const int r0 = part_lo(n, wg, nwg), r1 = part_lo(n, wg + 1, nwg);
+            // (the LM head's rows are the fused sampler's HeadRows split)
+            const int r0 = last ? part_lo(n, wg, nwg) : xlo<B>(n, wg, nwg);
+            const int r1 = last ? part_lo(n, wg + 1, nwg) : xlo<B>(n, wg + 1, nwg);
             if (l > 0) {
                 // the gammas and first weights go out before the wait
                 load_gamma<ITH>(last ? a->final_norm : layer_at(a, lc)->in_norm, H, gam);
@@ -586,14 +601,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 norm_partials<kStepThreads, B>(lds, H, e_sum, w_sum);  // x from the embedding
             }
             // this workgroup's rows of x: the residual of the O projection
-            if (!last) copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
+            if (!last) copy_res<B>(res_s, lds, H, xlo<B>(H, wg, nwg), xlo<B>(H, wg + 1, nwg));
             a = fresh(args);
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(w, nullptr, lds, H, last ? a->logits + hr.lo : nullptr,
-                                                          last ? nullptr : a->tqkv, flow_tag(epoch, l, FK_QKV),
-                                                          last ? a->vocab : n, r0, r1, n, ring);
+            gemv_ring<B, EPI_STORE, ITH, false, kPack<B>, kPair<B>>(
+                w, nullptr, lds, H, last ? a->logits + hr.lo : nullptr, last ? nullptr : a->tqkv,
+                flow_tag(epoch, l, FK_QKV), last ? a->vocab : n, r0, r1, n, ring, nullptr, pk_s);
             tr.mark();
         }
         if (last) break;
@@ -615,14 +630,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qw = a->heads * D;
-            const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+            const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
             prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_att<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITQ, false, kPack<B>>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx, flow_tag(epoch, l, FK_XO),
-                                         H, h0, h1, H, ring, res_s);
+            gemv_ring<B, EPI_RESID, ITQ, false, kPack<B>, kPair<B>>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx,
+                                                                   flow_tag(epoch, l, FK_XO), H, h0, h1, H, ring, res_s, pk_s);
             tr.mark();
         }
         // ---- post-attention RMSNorm + gate/up + SwiGLU ----
@@ -630,32 +645,32 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
             load_gamma<ITH>(layer_at(a, l)->post_norm, H, gam);
-            prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg), I, ring);
+            prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, xlo<B>(I, wg, nwg), xlo<B>(I, wg + 1, nwg), I, ring);
             a = fresh(args);
             if (!stage_x<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st, e_sum, w_sum)) return;
             // this workgroup's rows of x: the residual of the down projection
-            copy_res<B>(res_s, lds, H, part_lo(H, wg, nwg), part_lo(H, wg + 1, nwg));
+            copy_res<B>(res_s, lds, H, xlo<B>(H, wg, nwg), xlo<B>(H, wg + 1, nwg));
             a = fresh(args);
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_SWIGLU, ITH, false, kPack<B>>(layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact,
-                                          flow_tag(epoch, l, FK_ACT), I, part_lo(I, wg, nwg), part_lo(I, wg + 1, nwg),
-                                          I, ring);
+            gemv_ring<B, EPI_SWIGLU, ITH, false, kPack<B>, kPair<B>>(
+                layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact, flow_tag(epoch, l, FK_ACT), I,
+                xlo<B>(I, wg, nwg), xlo<B>(I, wg + 1, nwg), I, ring, nullptr, pk_s);
             tr.mark();
         }
         // ---- down projection + residual ----
         {
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
-            const int h0 = part_lo(H, wg, nwg), h1 = part_lo(H, wg + 1, nwg);
+            const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
             prefetch_ring<ITI, false, MASKI>(layer_at(a, l)->wd, nullptr, I, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_rows<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITI, MASKI, kPack<B>>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx, flow_tag(epoch, l, FK_XD),
-                                         H, h0, h1, H, ring, res_s);
+            gemv_ring<B, EPI_RESID, ITI, MASKI, kPack<B>, kPair<B>>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx,
+                                                                   flow_tag(epoch, l, FK_XD), H, h0, h1, H, ring, res_s, pk_s);
             tr.mark();
         }
     }
@@ -718,7 +733,14 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     // gathered kMergePer per thread into the K/V region with rows padded to
     // four floats)
     const int merge_words = G * c.head_dim * bpw + 2 * max_blocks;
-    return G <= 4 && (c.hidden_size + nwg - 1) / nwg <= kResRows && max_blocks <= 24576 / kBlockKeys &&
+    // (with one row each workgroup's share of an exchanged output is even:
+    // at most 2 ceil(n / 2 / nwg) rows, paired in LDS)
+    auto share = [&](int n) { return std::max((n + nwg - 1) / nwg, 2 * ((n / 2 + nwg - 1) / nwg)); };
+    const int qkv_rows = (c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim;
+    const bool pairs_fit = share(c.hidden_size) <= kPairRowsMax && share(c.intermediate_size) <= kPairRowsMax &&
+                           share(qkv_rows) <= kPairRowsMax && c.hidden_size % 2 == 0 &&
+                           c.intermediate_size % 2 == 0 && qkv_rows % 2 == 0;
+    return pairs_fit && G <= 4 && share(c.hidden_size) <= kResRows && max_blocks <= 24576 / kBlockKeys &&
            merge_words <= kStepThreads * kMergePer &&
            (size_t)(merge_words + 3 * G * c.head_dim) * 4 <= (size_t)2 * kAttnChunk * kBlockKeys * c.head_dim * 2 &&
            G * bpw * kBlockKeys * 4 <= kAttnChunk * kBlockKeys * c.head_dim * 2;

@@ -175,14 +175,19 @@ Yue2Model *yue2_hip_model_open_dir(const char *dir);
  * NULL) receives the configuration.  0 or a negative Yue2Error
  * (YUE2_ERR_CONFIG where the reference returns InvalidData). */
 int32_t yue2_hip_checkpoint_config(const char *dir, Yue2Config *out);
-/* Model's Drop (src/model.rs:411-416).  Caches and decoders created on the
- * model use its stream and workspace: free them first (freeing one after its
- * model is a use after free). */
+/* Model's Drop (src/model.rs:411-416).  Models, caches and decoders may be
+ * freed in any order, as the reference lets a Cache outlive its Model
+ * (src/model.rs:286-290): the model's free detaches its live caches and
+ * decoders.  A detached decoder holds no device objects and its calls return
+ * YUE2_ERR_ARG; a detached cache keeps its KV memory, which
+ * yue2_hip_cache_export can still read, until yue2_hip_cache_free. */
 void yue2_hip_model_free(Yue2Model *m);
 
 /* Cache::new (src/model.rs:292-305): a device BF16 KV cache of `capacity`
  * positions, layout [layers][K,V][kv_heads][capacity][head_dim]. */
 Yue2Cache *yue2_hip_cache_new(Yue2Model *m, int32_t capacity);
+/* Cache's Drop (src/model.rs:286-290), before or after its model's free;
+ * decoders running on the cache are detached with it. */
 void yue2_hip_cache_free(Yue2Cache *c);
 int32_t yue2_hip_cache_length(const Yue2Cache *c);
 /* The device context of a cache from its host K/V mirror (Cache's key/value,
@@ -193,6 +198,17 @@ int32_t yue2_hip_cache_length(const Yue2Cache *c);
  * cache length becomes `length`.  Returns 0 or a negative Yue2Error. */
 int32_t yue2_hip_cache_load(Yue2Cache *c, const float *key, const float *value, int32_t length,
                             int32_t stride);
+/* The reverse of yue2_hip_cache_load: rows [start, start + n) of the device
+ * cache into the host K/V mirror layout (layer l, position p at row
+ * l * stride + p of kv_heads * head_dim f32, the stored BF16 values exactly).
+ * Replaces the `shadow` rows the reference's fast path returns per token for
+ * its host mirror, so that the CPU path can take over after a failed device
+ * step (src/metal.m:846-871, src/model.rs:556-566); start = length - 1,
+ * n = 1 gives the newest token's rows.  Needs start + n <= length and
+ * start + n <= stride; also valid after the model's free.  Returns 0 or a
+ * negative Yue2Error. */
+int32_t yue2_hip_cache_export(const Yue2Cache *c, float *key, float *value, int32_t start, int32_t n,
+                              int32_t stride);
 
 /* Model::forward_phase (src/model.rs:465-477): run n ids through the model,
  * appending to the cache; write the logits of the last row (vocab_size f32,
@@ -337,7 +353,11 @@ int32_t yue2_hip_choose_noalloc(const float *logits, int32_t vocab, const Yue2Sa
                                 const int32_t *history, int32_t history_len, int32_t step,
                                 int32_t phase, int32_t legacy, const uint32_t *draws, int32_t *id);
 
-/* sampling::generate (src/sampling.rs:222-294) on the device. */
+/* sampling::generate (src/sampling.rs:222-294) on the device.  Both rows are
+ * prefilled (src/sampling.rs:246, 252) in decode order, bit for bit the CPU
+ * path's caches and logits, unless yue2_hip_model_set_prefill chose the
+ * matrix cores; then the caches and first logits follow yue2_hip_prefill_mfma's
+ * tolerance contract and the loop after them is exact on those caches. */
 int32_t yue2_hip_generate(Yue2Model *m, const int32_t *prefix, int32_t prefix_len,
                           const Yue2Sampling *sampling, uint64_t seed, int32_t phase,
                           const int32_t *negative, int32_t negative_len, float scale,
@@ -389,6 +409,14 @@ int32_t yue2_hip_selftest_conv(int32_t transpose, int32_t cin, int32_t cout, int
  * step kernel is the default for shapes that have one.  Returns 1 when
  * enabled, 0 when off or when the model's shape has no step kernel. */
 int32_t yue2_hip_model_set_step_kernel(Yue2Model *m, int32_t on);
+/* Execution choice for yue2_hip_generate's prefill of the prompts (on = 1):
+ * yue2_hip_prefill_mfma (BF16 MFMA GEMMs and flash attention; a 2048-token
+ * 3B-class prompt in ~20 ms, agreeing with the decode-order prefill within
+ * its stated tolerance, not bit for bit -- as the reference's GPU prefill,
+ * MPS GEMMs, src/tensor.rs:991-993, differs from its CPU path) or, the
+ * default, the decode-order prefill (bit-exact, ~650 tokens/s).  Returns the
+ * setting now in force (1 or 0). */
+int32_t yue2_hip_model_set_prefill(Yue2Model *m, int32_t mfma);
 /* Diagnostics: advance the launch sequence of the model's own workspace (the
  * one yue2_hip_forward uses) by `add`, as if that many step-kernel launches
  * had run.  The step kernel's tagged words carry a 20-bit epoch of this

@@ -312,6 +312,17 @@ class Cache:
         return (np.ctypeslib.as_array(c.key, shape=(n,)).reshape(shape),
                 np.ctypeslib.as_array(c.value, shape=(n,)).reshape(shape))
 
+    def load(self, key: np.ndarray, value: np.ndarray, length: int) -> None:
+        """Take rows [0, length) of a host K/V mirror ([layers, stride,
+        width] each, e.g. a device cache's export) as this cache's
+        context."""
+        c = self.ptr.contents
+        assert length <= c.capacity and key.shape == value.shape and key.shape[1] >= length
+        k, v = self.arrays()
+        k[:, :length, :] = key[:, :length, :]
+        v[:, :length, :] = value[:, :length, :]
+        c.length = length
+
     def fill_random(self, length: int, seed: int) -> None:
         """Give the cache `length` positions of BF16-exact N(0, 1) keys and
         values (for timing a step at a given context without a prefill)."""

@@ -103,45 +103,22 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         api.lib()
 
 
-def test_model_close_frees_its_caches_and_decoders_first():
-    """Model.close() closes the caches and decoders made on the model before
-    the model itself (their C objects use the model's stream and workspace),
-    so dropping one later -- as an interpreter does at exit with objects a
-    failed test left referenced -- calls nothing on a freed model.  Host
-    logic only: stand-in objects and library, no device calls."""
-    import weakref
+def test_model_close_frees_only_the_model():
+    """Model.close() frees the model once and nothing else: the library
+    detaches the model's caches and decoders itself, so each may be closed
+    before or after it (the reference's Cache may outlive its Model,
+    src/model.rs:286-290).  Host logic only: a stand-in library."""
     from yue2_rs_amd import api
 
-    order = []
-
-    class Child:  # closes once, as Cache.close does
-        def __init__(self, name):
-            self.name, self.open = name, True
-
-        def close(self):
-            if self.open:
-                order.append(self.name)
-                self.open = False
-
-    class FakeDecoder(api.Decoder):
-        def __init__(self):  # no device call
-            self.open = True
-
-        def close(self):
-            if self.open:
-                order.append("decoder")
-                self.open = False
+    freed = []
 
     class FakeLib:
         @staticmethod
         def yue2_hip_model_free(h):
-            order.append("model")
+            freed.append(h)
 
     m = api.Model.__new__(api.Model)
-    m._h, m._children = 1, weakref.WeakSet()
-    kids = [Child("cache1"), Child("cache2"), FakeDecoder()]
-    for ch in kids:
-        m._children.add(ch)
+    m._h = 7
     real_lib = api.lib
     api.lib = lambda: FakeLib
     try:
@@ -149,5 +126,4 @@ def test_model_close_frees_its_caches_and_decoders_first():
         m.close()  # a second close frees nothing
     finally:
         api.lib = real_lib
-    assert order[0] == "decoder" and order[-1] == "model" and len(order) == 4
-    assert sorted(order[1:3]) == ["cache1", "cache2"]
+    assert freed == [7]

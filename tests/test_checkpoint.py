@@ -65,6 +65,32 @@ def test_rejections(tmp_path, ck):
     assert "Invalid transformer configuration" in _err(d)
 
 
+@pytest.mark.parametrize("field,value,message", [
+    ("latent_dim", 0, "Invalid transformer configuration"),
+    ("max_latent_frames", 0, "Invalid transformer configuration"),
+    ("timestep_shift", 0.0, "Invalid transformer configuration"),
+    ("timestep_shift", -1.5, "Invalid transformer configuration"),
+    ("model_type", 7, "Expected JSON string"),
+    ("latent_type", ["vae"], "Expected JSON string"),
+    ("hidden_size", "64", "Expected unsigned JSON integer"),
+    ("rope_theta", True, "Expected JSON number"),
+    ("tie_word_embeddings", 1, "Expected JSON boolean"),
+])
+def test_config_field_rejections(tmp_path, ck, field, value, message):
+    """Config::read's other checks (src/model.rs:44-71) and the JSON kind
+    errors of its accessors (src/json.rs:26-80): a present key of the wrong
+    kind is an error, never its default."""
+    d = write_checkpoint(tmp_path / "m", ck, config=config_json(SMALL, **{field: value}))
+    assert message in _err(d)
+
+
+def test_config_nonfinite_timestep_shift(tmp_path, ck):
+    d = write_checkpoint(tmp_path / "m", ck)
+    text = (d / "config.json").read_text()
+    (d / "config.json").write_text(text[:-1] + ', "timestep_shift": 1e999}')
+    assert "Invalid transformer configuration" in _err(d)
+
+
 def test_malformed_files(tmp_path, ck):
     ts = ar_tensors(ck)
     d = write_checkpoint(tmp_path / "a", ck)

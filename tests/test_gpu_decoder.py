@@ -75,6 +75,79 @@ def test_generate_sampling_matches_oracle(reduced, scale):
     assert got.truncated == trunc
 
 
+_LEGACY_WANT = {}
+
+
+@pytest.mark.parametrize("scale,temperature,top_k,seed,steps,sensitive", [
+    (1.0, 0.9, 50, 1234, 24, True), (1.0, 0.9, 65, 1234, 24, True),
+    (1.5, 1.5, 50, 1, 16, True), (1.5, 1.5, 65, 1, 16, False)])
+def test_generate_legacy_matches_oracle(reduced, scale, temperature, top_k, seed, steps, sensitive):
+    """Legacy rounding (cast, src/sampling.rs:100-102: the penalty factors,
+    the tempered scores, the nucleus probabilities and cumulative sums, the
+    race noise and scores rounded to BF16, three ids protected) on the
+    device loop: top-k 50 runs the step kernel's fused sampler, top-k 65 the
+    sampler kernels (after the step kernel or the per-phase kernels).  Where
+    `sensitive`, the oracle's legacy ids differ from its plain ids over the
+    horizon, so a device loop that ignored the flag would fail."""
+    ck, gm, om = reduced
+    V = ck.config.vocab_size
+    s = y2.Sampling(temperature=temperature, top_p=0.93, top_k=top_k, repetition_penalty=1.2, penalty_window=50,
+                    min_tokens=0, max_tokens=steps)
+    pos = synthetic.prompt(256, V, seed=0)
+    neg = synthetic.prompt(256, V, seed=1) if scale != 1.0 else None
+    key = (scale, temperature, top_k, seed, steps)
+    if key not in _LEGACY_WANT:
+        want, trunc = O.generate(om, pos, s, seed, negative=neg, scale=scale, legacy=True)
+        plain, _ = O.generate(om, pos, s, seed, negative=neg, scale=scale, legacy=False)
+        _LEGACY_WANT[key] = (want, trunc, plain)
+    want, trunc, plain = _LEGACY_WANT[key]
+    assert (want != plain) == sensitive
+    got = y2.generate(gm, pos, s, seed=seed, negative=neg, scale=scale, legacy=True)
+    assert got.tokens == want
+    assert got.truncated == trunc
+
+
+@pytest.mark.parametrize("scale", [1.0, 1.5])
+def test_generate_with_matrix_core_prefill(reduced, scale):
+    """generate() with the matrix-core prefill (yue2_hip_model_set_prefill):
+    the prompts' caches and first logits follow the MFMA tolerance contract,
+    and the loop after them is exact on those caches.  So the same prompts
+    prefilled through prefill_mfma (deterministic), exported into oracle
+    caches and replayed by the oracle from the MFMA first logits give the
+    generated ids."""
+    ck, gm, om = reduced
+    V = ck.config.vocab_size
+    s = y2.Sampling(temperature=0.9, top_p=0.93, top_k=50, repetition_penalty=1.2, penalty_window=50,
+                    min_tokens=0, max_tokens=24)
+    prompts = [synthetic.prompt(300, V, seed=0)] + ([synthetic.prompt(280, V, seed=1)] if scale != 1.0 else [])
+    assert gm.set_prefill_mfma(True)
+    try:
+        got = y2.generate(gm, prompts[0], s, seed=321, negative=prompts[1] if scale != 1.0 else None, scale=scale)
+    finally:
+        assert not gm.set_prefill_mfma(False)
+    ocs, logits = [], []
+    for ids in prompts:
+        gc, gl = gm.prefill_mfma(ids, len(ids) + 24)
+        k, v = gc.export()
+        oc = O.Cache(om, len(ids) + 24)
+        oc.load(k, v, len(ids))
+        gc.close()
+        _, ol = om.prefill(ids, len(ids) + 1)
+        d = np.abs(gl - ol).max()
+        assert d <= 0.08 * ol.std(), f"MFMA prefill logits {d} from the oracle's"
+        ocs.append(oc)
+        logits.append(gl)
+    gen = O.Generator(321)
+    want = []
+    for step in range(s.max_tokens):
+        mixed = O.cfg_mix(logits[0], logits[1], scale) if scale != 1.0 else logits[0]
+        t = O.choose(mixed, s, want, step, y2.PHASE_NONE, False, gen)
+        want.append(t)
+        if step + 1 < s.max_tokens:
+            logits = [om.forward([t], oc) for oc in ocs]
+    assert got.tokens == want and got.truncated
+
+
 def test_generate_greedy_with_penalty_matches_oracle(reduced):
     ck, gm, om = reduced
     s = y2.Sampling(temperature=0.0, top_p=1.0, top_k=1, repetition_penalty=1.2, penalty_window=50,

@@ -19,7 +19,8 @@ decode-order prefill on the same seeded checkpoint and prompt:
   * all 28 layers of the 3B config, 2048 tokens, against the bit-exact
     decode-order GPU prefill: <= 0.30 * std (measured about 0.16 * std, the
     difference growing as the square root of the depth);
-  * the argmax of every compared row is the same id;
+  * the argmax of every compared row is the same id (the 24000-token
+    full-depth case reports it only: see its test);
   * phase-restricted heads: the same -inf pattern.
 Prompts of 1 token (the attention over one key), 65 and 1100 tokens cross
 the 64-key and 128-query flash tiles; 4100 tokens (against the decode-order
@@ -87,14 +88,22 @@ def test_gemm_rejects_ragged_k(gpu):
     assert y2.lib().yue2_hip_selftest_gemm(x.ctypes.data, x.ctypes.data, out.ctypes.data, 4, 4, 96) < 0
 
 
-def _close(got, want, tol, what):
+def _close(got, want, tol, what, argmax=True):
+    """max |got - want| <= tol * std(want) over the finite entries, and
+    (argmax) the same argmax.  Without `argmax` the argmax is only reported:
+    where the oracle's two largest logits are closer than twice the measured
+    difference the bound allows either one, and where they are not the bound
+    implies the same argmax."""
     fin = np.isfinite(want)
     assert np.array_equal(fin, np.isfinite(got)), f"{what}: -inf pattern differs"
     d = np.abs(got[fin] - want[fin]).max()
     s = want[fin].std()
-    print(f"{what}: max |d| {d:.4g} = {d / s:.4f} std", flush=True)
+    top2 = np.sort(want[fin])[-2:]
+    print(f"{what}: max |d| {d:.4g} = {d / s:.4f} std; top-two margin {top2[1] - top2[0]:.4g}, "
+          f"argmax {int(np.argmax(got))} vs {int(np.argmax(want))}", flush=True)
     assert d <= tol * s, f"{what}: max |d| {d:.4g} > {tol} * std {s:.4g}"
-    assert int(np.argmax(got)) == int(np.argmax(want)), f"{what}: argmax differs"
+    if argmax:
+        assert int(np.argmax(got)) == int(np.argmax(want)), f"{what}: argmax differs"
 
 
 THREE_B_2L = dataclasses.replace(synthetic.CLASS_3B, num_hidden_layers=2, vocab_size=32768)
@@ -204,5 +213,32 @@ def test_full_depth_3b_against_decode_order_prefill(gpu):
         _close(gm.forward([t], c2), gm.forward([t], c1), FULL_DEPTH_TOL, "3B next-step logits")
         for c in (c1, c2, c3):
             c.close()
+    finally:
+        gm.close()
+
+
+@pytest.mark.timeout(900)
+def test_full_depth_3b_24000_tokens_against_decode_order_prefill(gpu):
+    """The long-context workload's prompt at full depth: 28 layers, 24000
+    tokens, the MFMA prefill against the bit-exact decode-order GPU prefill
+    (24000 token steps), within the same full-depth bound; then the decode
+    step after it through each cache.  At this depth and length the two
+    largest logits can sit closer than the bound (measured: a 0.17 std
+    difference flipped the next step's argmax), so the argmax is reported,
+    not required."""
+    ck = synthetic.checkpoint(synthetic.CLASS_3B, seed=0, threads=16)
+    gm = y2.Model.open(ck)
+    try:
+        n = 24000
+        ids = synthetic.prompt(n, synthetic.CLASS_3B.vocab_size, seed=0)
+        c2, l2 = gm.prefill_mfma(ids, n + 2)
+        print("matrix-core prefill done; decode-order prefill of 24000 tokens", flush=True)
+        c1, l1 = gm.prefill_phase(ids, n + 2)
+        _close(l2, l1, FULL_DEPTH_TOL, "3B 24000-token prefill logits", argmax=False)
+        t = int(np.argmax(l1))
+        _close(gm.forward([t], c2), gm.forward([t], c1), FULL_DEPTH_TOL, "3B next-step logits at 24001",
+               argmax=False)
+        c1.close()
+        c2.close()
     finally:
         gm.close()

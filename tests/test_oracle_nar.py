@@ -92,24 +92,23 @@ def timestep_sinus(raw_t, shift):
     return sinus
 
 
-@pytest.mark.parametrize("shift", [1.0, 3.0])
-def test_closed_form_without_layers(oracle_threads, shift):
-    c, H = TINY, TINY.hidden_size
-    ck = synthetic.checkpoint(c, seed=4)
-    nw = synthetic.nar_weights(c, seed=4, max_latent_frames=16, timestep_shift=shift)
+def one_hot_nar(c, nw):
+    """Zero NAR layers and one-hot vae2llm / time / llm2vae matrices: every
+    layer leaves x unchanged and every DOT picks one value exactly."""
+    H = c.hidden_size
     nw.layers = zero_layers(c)
     nw.vae2llm = one_hot(H, LATENT, lambda i: i % LATENT)
     nw.time_in = one_hot(H, 256, lambda i: i % 256)
     nw.time_out = one_hot(H, H, lambda i: i)
     nw.llm2vae = one_hot(LATENT, H, lambda j: (3 * j) % H)
-    om = O.Model(ck)
-    nar = O.Nar(om, nw)
-    oc, _ = om.prefill(synthetic.prompt(40, c.vocab_size, seed=2), 40)
-    frames, raw_t = 20, 0.7
-    rng = np.random.default_rng(1)
-    state = rb(rng.standard_normal((frames, LATENT)).astype(np.float32))
-    got = nar.velocity(state, oc, raw_t)
+    return nw
 
+
+def closed_velocity(c, nw, state, raw_t):
+    """The velocity of one_hot_nar's model stated directly from the
+    reference's lines (src/model.rs:611-698): x0 = rb(rb(rb(pad + rb(b)) +
+    time) + pe) per padded row, then llm2vae(final_norm(x0[1 .. n-1]))."""
+    H, frames = c.hidden_size, state.shape[0]
     n = frames + 2
     pad = np.zeros((n, LATENT), np.float32)
     pad[1:n - 1] = state
@@ -117,7 +116,7 @@ def test_closed_form_without_layers(oracle_threads, shift):
     x = np.empty((n, H), np.float32)
     for i in range(H):
         x[:, i] = rb(pad[:, i % LATENT] + b(nw.vae2llm_bias)[i])
-    sinus = timestep_sinus(raw_t, shift)
+    sinus = timestep_sinus(raw_t, nw.timestep_shift)
     t0 = rb(sinus[np.arange(H) % 256] + b(nw.time_in_bias))
     t0 = rb(t0 / (f32(1.0) + np.array([exp32(-v) for v in t0], np.float32)))
     time = rb(t0 + b(nw.time_out_bias))
@@ -128,6 +127,22 @@ def test_closed_form_without_layers(oracle_threads, shift):
     for f in range(frames):
         h = seq_norm(x[f + 1], np.ones(H, np.float32), c.rms_norm_eps)
         want[f] = rb(h[(3 * np.arange(LATENT)) % H] + b(nw.llm2vae_bias))
+    return want
+
+
+@pytest.mark.parametrize("shift", [1.0, 3.0])
+def test_closed_form_without_layers(oracle_threads, shift):
+    c = TINY
+    ck = synthetic.checkpoint(c, seed=4)
+    nw = one_hot_nar(c, synthetic.nar_weights(c, seed=4, max_latent_frames=16, timestep_shift=shift))
+    om = O.Model(ck)
+    nar = O.Nar(om, nw)
+    oc, _ = om.prefill(synthetic.prompt(40, c.vocab_size, seed=2), 40)
+    frames, raw_t = 20, 0.7
+    rng = np.random.default_rng(1)
+    state = rb(rng.standard_normal((frames, LATENT)).astype(np.float32))
+    got = nar.velocity(state, oc, raw_t)
+    want = closed_velocity(c, nw, state, raw_t)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
@@ -228,6 +243,28 @@ def test_condition_end_limits_the_keys(oracle_threads):
     assert not np.array_equal(nar.velocity(state, a, 0.1).view(np.uint32), nar.velocity(state, b, 0.1).view(np.uint32))
 
 
+def test_normal_tensor_box_muller_within_ulps():
+    """Every value of Generator::normal_tensor (src/sampling.rs:64-79) is the
+    Box-Muller transform of the same MT19937 uniform_f32 draws (u_i gives the
+    radius sqrt(-2 ln(1 - u_i)), u_(i+8) the angle 2 pi u, cos at i and sin at
+    i + 8 within each block of 16), evaluated here in float64 from the f32
+    angle: the oracle's f32 chain (logf, sqrtf, cosf / sinf and the product,
+    each within an ulp or a half) stays within 3 f32 ulps of it (measured
+    2.08).  A cos / sin swap, a wrong pairing or a wrong angle factor is off
+    by far more."""
+    n = 16 * 4000
+    got = O.normal(11, n).astype(np.float64)
+    g = synthetic.MT19937(11)
+    u = (np.array([g.next_u32() & 0xFFFFFF for _ in range(n)], np.float64) / 16777216.0).reshape(-1, 16)
+    r = np.sqrt(-2.0 * np.log(1.0 - u[:, :8]))
+    th = (2.0 * math.pi * u[:, 8:]).astype(np.float32).astype(np.float64)
+    want = np.concatenate([r * np.cos(th), r * np.sin(th)], axis=1).reshape(-1)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    worst = float(np.max(np.abs(got - want) / ulp))
+    print(f"normal_tensor: max {worst:.2f} ulp from float64 Box-Muller")
+    assert worst <= 3.0
+
+
 def test_normal_tensor_pairs():
     """Generator::normal_tensor (src/sampling.rs:64-79): in each block of 16
     the pair (i, i + 8) shares the radius, x^2 + y^2 = -2 ln(1 - u_i) for the
@@ -269,3 +306,42 @@ def test_synthesize_rejects(oracle_threads):
     for prefix, codec, steps in (([1] * 20, [], 2), ([1] * 20, [32768], 2), ([1] * 20, [5], 0), ([1] * 124, [5], 2)):
         with pytest.raises(RuntimeError):
             nar.synthesize(prefix, codec, 1, steps)
+
+
+def _logit(t):
+    """logit (src/model.rs:777-779) in float64, clamped to [-20, 20]."""
+    v = math.inf if t >= 1.0 else (-math.inf if t <= 0.0 else math.log(t / (1.0 - t)))
+    return min(20.0, max(-20.0, v))
+
+
+@pytest.mark.parametrize("steps", [1, 3])
+def test_synthesize_midpoint_schedule_closed_form(oracle_threads, steps):
+    """Model::synthesize's loop (src/model.rs:699-775) on a model whose
+    velocity is known in closed form and depends on both the state and the
+    time (one_hot_nar: the timestep embedding enters every row), restated
+    here: the song's noise sliced at the chunk cuts (size = (min(24576,
+    max positions) - prefix - 3) / 2), per step t = 1 - step / steps, the
+    first velocity at logit(t), the midpoint state rb(s - rb(v1 * (dt / 2))),
+    the second velocity at logit(t - 0.5 / steps), then rb(s - rb(v2 * dt)).
+    A wrong midpoint, dt, time schedule or chunk cut changes the bits."""
+    nw = one_hot_nar(MUSIC, synthetic.nar_weights(MUSIC, seed=5, max_latent_frames=64, timestep_shift=3.0))
+    nar = O.Nar(O.Model(synthetic.checkpoint(MUSIC, seed=5)), nw)
+    prefix = synthetic.prompt(20, 151643, seed=7)
+    codec = synthetic.prompt(90, 32768, seed=8)
+    got = nar.synthesize(prefix, codec, 42, steps)
+    size = (min(24576, MUSIC.max_position_embeddings) - len(prefix) - 3) // 2
+    assert 0 < size < len(codec), "the construction must cut the song into chunks"
+    noise = O.normal(42, len(codec) * LATENT).reshape(-1, LATENT)
+    dt = f32(1.0) / f32(steps)
+    want = []
+    for start in range(0, len(codec), size):
+        state = rb(noise[start:start + size])
+        for step in range(steps):
+            t = 1.0 - step / steps
+            v1 = closed_velocity(MUSIC, nw, state, _logit(t))
+            mid = rb(state - rb(v1 * f32(dt / f32(2.0))))
+            v2 = closed_velocity(MUSIC, nw, mid, _logit(t - 0.5 / steps))
+            state = rb(state - rb(v2 * dt))
+        want.append(state)
+    want = np.concatenate(want)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

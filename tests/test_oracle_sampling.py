@@ -152,3 +152,71 @@ def test_phase_masks():
         choose(np.zeros(CODEC_OFFSET + 5, np.float32), s, phase=O.PHASE_SEMANTIC)
     with pytest.raises(RuntimeError):
         choose(np.zeros(1000, np.float32), s, phase=O.PHASE_ABC)
+
+
+# ---------------------------------------------------------------------------
+# sampling::generate's loop (src/sampling.rs:222-294), restated in Python over
+# the oracle's separately pinned parts (prefill / forward_phase, the CFG mix,
+# choose, MT19937), against the oracle's own y2o_generate.
+
+def _generate_loop(om, prefix, s, seed, phase, negative, scale, legacy):
+    cache, cond = om.prefill(prefix, len(prefix) + s.max_tokens, phase)
+    ncache = unc = None
+    if scale != 1.0:
+        ncache, unc = om.prefill(negative, len(negative) + s.max_tokens, phase)
+    end = {O.PHASE_ABC: ABC_END, O.PHASE_SEMANTIC: MUSIC_END}.get(phase, -1)
+    gen = O.Generator(seed)
+    tokens, truncated = [], True
+    for step in range(s.max_tokens):
+        logits = O.cfg_mix(cond, unc, scale) if unc is not None else cond
+        t = O.choose(logits, s, tokens, step, phase, legacy, gen)
+        if t == end:
+            truncated = False
+            break
+        tokens.append(t)
+        if step + 1 < s.max_tokens:
+            cond = om.forward_phase([t], cache, phase)
+            if ncache is not None:
+                unc = om.forward_phase([t], ncache, phase)
+    return tokens, truncated
+
+
+LOOP = y2.Config(hidden_size=128, num_hidden_layers=2, num_attention_heads=2, num_key_value_heads=1, head_dim=64,
+                 intermediate_size=256, vocab_size=184704, max_position_embeddings=256, rms_norm_eps=1e-6,
+                 rope_theta=1e6)
+
+
+@pytest.fixture(scope="module")
+def loop_models():
+    """Two models with the protocol's vocabulary: `plain` (random), and
+    `ending` whose ABC_END / MUSIC_END rows win once min_tokens lets them
+    (every embedding carries 4.0 in dimension 0, which only those two LM-head
+    rows weigh)."""
+    plain = synthetic.checkpoint(LOOP, seed=21)
+    ending = synthetic.checkpoint(LOOP, seed=22)
+    ending.embed_tokens[:, 0] = 0x4080
+    ending.lm_head[:, 0] = 0
+    ending.lm_head[ABC_END, 0] = 0x3F80
+    ending.lm_head[MUSIC_END, 0] = 0x3F80
+    return {"plain": O.Model(plain), "ending": O.Model(ending)}
+
+
+@pytest.mark.parametrize("model,phase,temperature,scale,legacy,min_tokens", [
+    ("ending", O.PHASE_SEMANTIC, 0.9, 1.5, False, 4),   # end stop after min_tokens, CFG
+    ("ending", O.PHASE_ABC, 0.0, 1.0, True, 3),         # greedy, end stop, legacy
+    ("plain", O.PHASE_SEMANTIC, 0.9, 1.5, True, 0),     # truncated at max_tokens, CFG, legacy
+    ("plain", O.PHASE_ABC, 1.3, 1.0, False, 0),         # sampled batch 1
+])
+def test_generate_matches_its_loop(loop_models, model, phase, temperature, scale, legacy, min_tokens):
+    om = loop_models[model]
+    s = y2.Sampling(temperature=temperature, top_p=0.9, top_k=40, repetition_penalty=1.2, penalty_window=50,
+                    min_tokens=min_tokens, max_tokens=12)
+    prefix = synthetic.prompt(30, EOD, seed=1)
+    negative = synthetic.prompt(17, EOD, seed=2) if scale != 1.0 else None  # a different length
+    want = _generate_loop(om, prefix, s, 99, phase, negative, scale, legacy)
+    got = O.generate(om, prefix, s, 99, phase=phase, negative=negative, scale=scale, legacy=legacy)
+    assert got == want
+    if model == "ending":
+        assert want[1] is False and len(want[0]) == min_tokens, "the construction must stop at min_tokens"
+    else:
+        assert want[1] is True and len(want[0]) == s.max_tokens

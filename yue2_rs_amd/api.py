@@ -9,7 +9,6 @@ path, and loading fails loudly when the library is missing.
 from __future__ import annotations
 
 import ctypes as C
-import weakref
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Optional, Sequence
@@ -112,6 +111,8 @@ def lib() -> C.CDLL:
         "yue2_hip_cache_free": (None, [vp]),
         "yue2_hip_cache_length": (i32, [vp]),
         "yue2_hip_cache_load": (i32, [vp, vp, vp, i32, i32]),
+        "yue2_hip_cache_export": (i32, [vp, vp, vp, i32, i32, i32]),
+        "yue2_hip_model_set_prefill": (i32, [vp, i32]),
         "yue2_hip_forward": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_prefill": (i32, [vp, vp, vp, i32, i32, vp]),
         "yue2_hip_prefill_mfma": (i32, [vp, vp, vp, i32, i32, vp]),
@@ -280,9 +281,6 @@ class Model:
         self._h = handle
         self.config = config
         self._ckpt = checkpoint  # host arrays stay alive with the model
-        # caches and decoders on this model: freed before it (their C
-        # objects use the model's stream and workspace)
-        self._children = weakref.WeakSet()
 
     @classmethod
     def open(cls, checkpoint: Checkpoint) -> "Model":
@@ -311,13 +309,10 @@ class Model:
         return cls(h, config, None)
 
     def close(self) -> None:
+        """Model's Drop.  Its caches and decoders may be closed before or
+        after it (the library detaches them): a detached decoder's calls
+        raise, a detached cache can still be exported."""
         if self._h:
-            children = list(self._children)
-            for ch in children:  # decoders before the caches they run on
-                if isinstance(ch, Decoder):
-                    ch.close()
-            for ch in children:
-                ch.close()
             lib().yue2_hip_model_free(self._h)
             self._h = None
 
@@ -389,6 +384,11 @@ class Model:
         whether it is in use (False when the shape has none)."""
         return bool(_check(lib().yue2_hip_model_set_step_kernel(self._h, 1 if on else 0)))
 
+    def set_prefill_mfma(self, on: bool) -> bool:
+        """generate() prefills its prompts on the matrix cores (True) or in
+        decode order (False, the default, bit-exact); returns the setting."""
+        return bool(_check(lib().yue2_hip_model_set_prefill(self._h, 1 if on else 0)))
+
     def advance_sequence(self, add: int) -> None:
         """Diagnostics: advance the launch sequence of the model's forward
         workspace by `add` (the step kernel's tagged-word epoch)."""
@@ -419,7 +419,6 @@ class Cache:
         if not self._h:
             raise Yue2Error(-10, lib().yue2_hip_last_error().decode())
         self.capacity = capacity
-        model._children.add(self)
 
     @property
     def length(self) -> int:
@@ -434,6 +433,18 @@ class Cache:
         if k.shape != v.shape or k.ndim != 3:
             raise ValueError("key and value must both be [layers, stride, width]")
         _check(lib().yue2_hip_cache_load(self._h, _ptr(k), _ptr(v), int(length), k.shape[1]))
+
+    def export(self, start: int = 0, n: Optional[int] = None, stride: Optional[int] = None):
+        """The host K/V mirror of rows [start, start + n) (default: the whole
+        length): (key, value), each [layers, stride, kv_heads * head_dim] f32
+        with those rows filled (the rest zero)."""
+        cfg = self.model.config
+        n = self.length - start if n is None else n
+        stride = start + n if stride is None else stride
+        shape = (cfg.num_hidden_layers, stride, cfg.num_key_value_heads * cfg.head_dim)
+        k, v = np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+        _check(lib().yue2_hip_cache_export(self._h, _ptr(k), _ptr(v), int(start), int(n), int(stride)))
+        return k, v
 
     def close(self) -> None:
         if self._h:
@@ -505,7 +516,6 @@ class Decoder:
         if not self._h:
             raise Yue2Error(-13, lib().yue2_hip_last_error().decode())
         self.rows = 2 if scale != 1.0 else 1
-        model._children.add(self)
 
     def run(self, steps: int, first_logits: Optional[np.ndarray] = None, timing: bool = False):
         """Run `steps` steps; returns (tokens, step_ms or None)."""

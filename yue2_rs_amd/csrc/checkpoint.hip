@@ -340,30 +340,36 @@ int open_shard(const std::string& dir, const std::string& file, Checkpoint* ck) 
     return YUE2_OK;
 }
 
-// Config::read (src/model.rs:29-73): the fields of the decode path.
+// Config::read (src/model.rs:29-73): every field with the reference's
+// defaults and checks.  A present key of the wrong JSON kind is an error with
+// the reference's message (Value::string / usize / f64 / boolean,
+// src/json.rs:26-66), never a fallback to the default.
 int read_config(const std::string& dir, Checkpoint* ck) {
     std::string text, err;
     if (!read_file(dir + "/config.json", &text)) return fail(YUE2_ERR_ARG, "cannot read " + dir + "/config.json");
     Json v;
     if (!parse_json(text.data(), text.size(), &v, &err)) return invalid(err);
     if (v.kind != Json::OBJ) return invalid("Expected JSON object");
+    const char* bad = nullptr;  // the first wrong-kind message
     auto text_or = [&](const char* k, const char* d) {
         const Json* j = v.get(k);
+        if (j && j->kind != Json::STR && !bad) bad = "Expected JSON string";
         return j && j->kind == Json::STR ? j->str : std::string(d);
     };
-    if (text_or("model_type", "yue2") != "yue2" || text_or("latent_type", "vae") != "vae")
-        return invalid("Expected YuE2 VAE-latent model");
-    bool ok = true;
+    const std::string model_type = text_or("model_type", "yue2"), latent_type = text_or("latent_type", "vae");
+    if (bad) return invalid(bad);
+    if (model_type != "yue2" || latent_type != "vae") return invalid("Expected YuE2 VAE-latent model");
     auto size_or = [&](const char* k, size_t d) -> int32_t {
         const Json* j = v.get(k);
         size_t s = d;
-        if (j && !as_size(*j, &s)) ok = false;
-        if (s > 0x7fffffff) ok = false;
+        if (j && j->kind != Json::NUM && !bad) bad = "Expected unsigned JSON integer";
+        if (j && j->kind == Json::NUM && !as_size(*j, &s) && !bad) bad = "invalid digit found in string";
+        if (s > 0x7fffffff && !bad) bad = "Invalid transformer configuration";
         return (int32_t)s;
     };
     auto float_or = [&](const char* k, double d) {
         const Json* j = v.get(k);
-        if (j && j->kind != Json::NUM) ok = false;
+        if (j && j->kind != Json::NUM && !bad) bad = "Expected JSON number";
         return (float)(j && j->kind == Json::NUM ? j->num : d);
     };
     Yue2Config& c = ck->config;
@@ -377,11 +383,18 @@ int read_config(const std::string& dir, Checkpoint* ck) {
     c.rms_norm_eps = float_or("rms_norm_eps", 1e-6);
     c.rope_theta = float_or("rope_theta", 1e6);
     c.max_position_embeddings = size_or("max_position_embeddings", 24576);
+    // the NAR pathway's fields, read and checked here as the reference does
+    // although the decode path does not use them
+    const int32_t latent_dim = size_or("latent_dim", 64);
+    const int32_t max_latent_frames = size_or("max_latent_frames", 24576);
+    const float timestep_shift = float_or("timestep_shift", 1.0);
     const Json* tie = v.get("tie_word_embeddings");
-    if (tie && tie->kind != Json::BOOL) ok = false;
-    ck->tie = tie && tie->b;
-    if (!ok) return invalid("Invalid configuration value");
-    if (yue2_hip_config_validate(&c) != YUE2_OK) return invalid("Invalid transformer configuration");
+    if (tie && tie->kind != Json::BOOL && !bad) bad = "Expected JSON boolean";
+    ck->tie = tie && tie->kind == Json::BOOL && tie->b;
+    if (bad) return invalid(bad);
+    if (yue2_hip_config_validate(&c) != YUE2_OK || latent_dim == 0 || max_latent_frames == 0 ||
+        !(timestep_shift > 0.0f) || !std::isfinite(timestep_shift))
+        return invalid("Invalid transformer configuration");
     return YUE2_OK;
 }
 

@@ -200,6 +200,7 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     }
     // the graph's choose() picks the token after the one its launch forwards
     a.step_offset = 1;
+    m->decoders.push_back(d);  // detached by the free of the model or of a cache
     rc = YUE2_OK;
     if (d->fused) {
         FusedSampler fs{};
@@ -214,19 +215,42 @@ extern "C" Yue2Decoder* yue2_hip_decoder_new(Yue2Model* m, Yue2Cache* cond, Yue2
     }
     if (rc >= 0 && !d->fused && m->step_kernel) rc = prepare_step(m, d->w);
     if (rc < 0) {
-        decoder_release(d);
+        decoder_detach(d);
         delete d;
         return nullptr;
     }
     return d;
 }
 
+namespace y2 {
+void decoder_detach(Yue2Decoder* d) {
+    if (!d->m) return;
+    decoder_release(d);
+    auto& v = d->m->decoders;
+    v.erase(std::remove(v.begin(), v.end(), d), v.end());
+    d->m = nullptr;
+    d->caches[0] = d->caches[1] = nullptr;
+}
+
+bool decoder_uses(const Yue2Decoder* d, const Yue2Cache* c) {
+    return d->m && (d->caches[0] == c || (d->rows > 1 && d->caches[1] == c));
+}
+}  // namespace y2
+
+// Legal in any order with the free of its model and caches: a decoder they
+// detached holds no device objects any more.
 extern "C" void yue2_hip_decoder_free(Yue2Decoder* d) {
     if (!d) return;
     std::lock_guard<std::recursive_mutex> guard(library_lock());
-    (void)hipStreamSynchronize(d->m->stream);
-    decoder_release(d);
+    if (d->m) {
+        (void)hipStreamSynchronize(d->m->stream);
+        decoder_detach(d);
+    }
     delete d;
+}
+
+static int check_attached(const Yue2Decoder* d) {
+    return d->m ? YUE2_OK : fail(YUE2_ERR_ARG, "the decoder's model or cache was freed");
 }
 
 // Capture one loop iteration (forward -> choose -> advance) as a graph.
@@ -308,6 +332,7 @@ extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logit
                                         int32_t* tokens, float* step_ms) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!d || steps < 0) return fail(YUE2_ERR_ARG, "null decoder or negative steps");
+    if (int rc = check_attached(d)) return rc;
     if (d->ended || steps == 0) return 0;
     if (int rc = check_room(d, steps)) return rc;
     hipStream_t s = d->m->stream;
@@ -357,6 +382,7 @@ extern "C" int32_t yue2_hip_decoder_run(Yue2Decoder* d, const float* first_logit
 extern "C" int32_t yue2_hip_decoder_logits(Yue2Decoder* d, float* out) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!d || !out) return fail(YUE2_ERR_ARG, "null decoder or output");
+    if (int rc = check_attached(d)) return rc;
     if (!d->started) return fail(YUE2_ERR_ARG, "decoder has not run");
     hipStream_t s = d->m->stream;
     hipError_t e = hipMemcpyAsync(out, d->w.logits, sizeof(float) * (size_t)d->rows * d->m->c.vocab_size,
@@ -435,6 +461,7 @@ extern "C" int32_t yue2_hip_decoder_time_kernel(Yue2Decoder* d, int32_t kernel, 
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!d || !avg_ms || !bytes || iters <= 0 || kernel < 0 || kernel > 5)
         return fail(YUE2_ERR_ARG, "bad kernel timing request");
+    if (int rc = check_attached(d)) return rc;
     if (!d->started) return fail(YUE2_ERR_ARG, "decoder has not run");
     Yue2Model* m = d->m;
     const Yue2Config& c = m->c;
@@ -573,7 +600,12 @@ static int choose_run(char* p, const ChooseLayout& L, hipStream_t s, const float
     }
     if (e == hipSuccess) e = hipMemcpyAsync(&st, p + L.st, sizeof(st), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return hip_fail(e, "choose");
+    if (e != hipSuccess) {
+        // nothing enqueued may still run over p when the caller reuses it
+        // (the allocation-free entry's shared scratch)
+        (void)hipStreamSynchronize(s);
+        return hip_fail(e, "choose");
+    }
     if (int rc = step_error(st)) return rc;
     *id = st.ids[0];
     return YUE2_OK;
@@ -679,11 +711,15 @@ extern "C" int32_t yue2_hip_generate(Yue2Model* m, const int32_t* prefix, int32_
     Yue2Cache* neg = nullptr;
     Yue2Decoder* d = nullptr;
     int rc = cond ? YUE2_OK : YUE2_ERR_ALLOC;
-    if (rc == YUE2_OK) rc = yue2_hip_prefill(m, cond, prefix, prefix_len, phase, first.data());
+    // prefill_phase of both rows (src/sampling.rs:246, 252): decode order
+    // (bit-exact with the CPU path) or the matrix cores (the reference's own
+    // GPU prefill, src/tensor.rs:991-993), as yue2_hip_model_set_prefill chose
+    auto prefill = m->prefill_mfma ? yue2_hip_prefill_mfma : yue2_hip_prefill;
+    if (rc == YUE2_OK) rc = prefill(m, cond, prefix, prefix_len, phase, first.data());
     if (rc == YUE2_OK && scale != 1.0f) {
         neg = yue2_hip_cache_new(m, negative_len + sampling->max_tokens);
         rc = neg ? YUE2_OK : YUE2_ERR_ALLOC;
-        if (rc == YUE2_OK) rc = yue2_hip_prefill(m, neg, negative, negative_len, phase, first.data() + V);
+        if (rc == YUE2_OK) rc = prefill(m, neg, negative, negative_len, phase, first.data() + V);
     }
     if (rc == YUE2_OK) {
         d = yue2_hip_decoder_new(m, cond, neg, sampling, seed, phase, scale, legacy);

@@ -101,15 +101,25 @@ struct Yue2Model {
     y2::LayerDev* layers_dev = nullptr;  // the same table in device memory (step kernel)
     int cus = 0;                         // compute units: workgroups of the step kernel
     bool step_kernel = false;            // decode steps through the persistent kernel (default where supported)
+    bool prefill_mfma = false;           // yue2_hip_generate prefills on the matrix cores
     y2::Workspace ws;  // batch-1 workspace of the parity API
     int norm_fallbacks = 0;
     y2::NarDev nar;    // loaded by yue2_hip_nar_load
+    // The live caches and decoders made on this model.  yue2_hip_model_free
+    // detaches them: a decoder's device objects are released, a cache keeps
+    // its KV memory (and its shape, so it can still be exported) until its
+    // own free, and neither reaches the model again.  So the three may be
+    // freed in any order, as the reference lets a Cache outlive its Model
+    // (src/model.rs:286-290).
+    std::vector<Yue2Cache*> caches;
+    std::vector<Yue2Decoder*> decoders;
 };
 
 struct Yue2Cache {
-    Yue2Model* m = nullptr;
+    Yue2Model* m = nullptr;  // null once the model has been freed
     int capacity = 0;
     int length = 0;
+    int layers = 0, kv_heads = 0, head_dim = 0;  // the model's shape, kept past its free
     uint16_t* kv = nullptr;
 };
 
@@ -145,6 +155,13 @@ int check_phase_vocab(int phase, int vocab);
 int read_step_error(Workspace& w, hipStream_t s);
 // The error a step state carries (YUE2_OK when none), with its message set.
 int step_error(const StepState& st);
+
+// Release a decoder's device objects and detach it from its model and caches
+// (decoder.hip); later calls on it fail with YUE2_ERR_ARG.  The caller holds
+// the library lock and has synchronised the model's stream.
+void decoder_detach(Yue2Decoder* d);
+// Whether decoder d runs on cache c.
+bool decoder_uses(const Yue2Decoder* d, const Yue2Cache* c);
 
 // Small state kernels (kernels.hip).
 void launch_fill(hipStream_t s, float* p, size_t n, float v);

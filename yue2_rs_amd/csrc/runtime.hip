@@ -8,6 +8,7 @@
 // API) or captured once as a hipGraph and replayed (decoder).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -554,6 +555,11 @@ extern "C" void yue2_hip_model_free(Yue2Model* m) {
     if (!m) return;
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     (void)hipStreamSynchronize(m->stream);
+    // children outlive the model detached from it (see Yue2Model::caches)
+    for (Yue2Decoder* d : std::vector<Yue2Decoder*>(m->decoders)) decoder_detach(d);
+    for (Yue2Cache* c : m->caches) c->m = nullptr;
+    m->decoders.clear();
+    m->caches.clear();
     m->ws.release();
     if (m->layers_dev) (void)hipFree(m->layers_dev);
     if (m->block) (void)hipFree(m->block);
@@ -567,6 +573,13 @@ extern "C" int32_t yue2_hip_model_set_step_kernel(Yue2Model* m, int32_t on) {
     if (!m) return fail(YUE2_ERR_ARG, "null model");
     m->step_kernel = on != 0 && step_supported(m->c, 1, m->cus);
     return m->step_kernel ? 1 : 0;
+}
+
+extern "C" int32_t yue2_hip_model_set_prefill(Yue2Model* m, int32_t mfma) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!m) return fail(YUE2_ERR_ARG, "null model");
+    m->prefill_mfma = mfma != 0;
+    return m->prefill_mfma ? 1 : 0;
 }
 
 extern "C" int32_t yue2_hip_model_advance_sequence(Yue2Model* m, int32_t add) {
@@ -596,20 +609,32 @@ extern "C" Yue2Cache* yue2_hip_cache_new(Yue2Model* m, int32_t capacity) {
     auto* cache = new Yue2Cache();
     cache->m = m;
     cache->capacity = capacity;
+    cache->layers = c.num_hidden_layers;
+    cache->kv_heads = c.num_key_value_heads;
+    cache->head_dim = c.head_dim;
     hipError_t e = hipMalloc(&cache->kv, elems * sizeof(uint16_t));
     if (e != hipSuccess) {
         hip_fail(e, "hipMalloc(kv cache)");
         delete cache;
         return nullptr;
     }
+    m->caches.push_back(cache);
     return cache;
 }
 
+// Cache's Drop (src/model.rs:286-290, which releases the GPU context of the
+// cache id): legal before or after the model's free.  Decoders running on
+// the cache are detached with it.
 extern "C" void yue2_hip_cache_free(Yue2Cache* c) {
     if (!c) return;
     std::lock_guard<std::recursive_mutex> guard(library_lock());
-    (void)hipStreamSynchronize(c->m->stream);
-    (void)hipFree(c->kv);
+    if (Yue2Model* m = c->m) {
+        (void)hipStreamSynchronize(m->stream);
+        for (Yue2Decoder* d : std::vector<Yue2Decoder*>(m->decoders))
+            if (decoder_uses(d, c)) decoder_detach(d);
+        m->caches.erase(std::remove(m->caches.begin(), m->caches.end(), c), m->caches.end());
+    }
+    (void)hipFree(c->kv);  // hipFree waits for the device
     delete c;
 }
 
@@ -623,6 +648,7 @@ extern "C" int32_t yue2_hip_cache_load(Yue2Cache* c, const float* key, const flo
                                        int32_t stride) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!c || !key || !value) return fail(YUE2_ERR_ARG, "null cache or mirror");
+    if (!c->m) return fail(YUE2_ERR_ARG, "the cache's model was freed");
     const Yue2Config& cf = c->m->c;
     if (length < 0 || length > c->capacity || length > cf.max_position_embeddings || stride < length)
         return fail(YUE2_ERR_CONTEXT, "AR input exceeds cache/model context");
@@ -648,6 +674,42 @@ extern "C" int32_t yue2_hip_cache_load(Yue2Cache* c, const float* key, const flo
         }
     }
     c->length = length;
+    return YUE2_OK;
+}
+
+// The host K/V mirror rows of a device cache: the reverse of cache_load, and
+// what the reference's fast path hands back per token as `shadow` so that the
+// Rust side can append it to its mirror and the CPU path can take over after
+// a failed step (src/metal.m:846-871, src/model.rs:556-566).  Rows
+// [start, start + n) of every layer go to key/value at row l * stride + p, as
+// f32 holding the stored BF16 (exact).  Works after the model's free.
+extern "C" int32_t yue2_hip_cache_export(const Yue2Cache* c, float* key, float* value, int32_t start, int32_t n,
+                                         int32_t stride) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!c || !key || !value) return fail(YUE2_ERR_ARG, "null cache or mirror");
+    if (start < 0 || n < 0 || start + n > c->length || stride < start + n)
+        return fail(YUE2_ERR_CONTEXT, "export rows outside the cache length or the mirror stride");
+    if (n == 0) return YUE2_OK;
+    const int Hkv = c->kv_heads, D = c->head_dim, width = Hkv * D;
+    hipError_t e = c->m ? hipStreamSynchronize(c->m->stream) : hipSuccess;  // every step has landed
+    if (e != hipSuccess) return hip_fail(e, "cache export sync");
+    std::vector<uint16_t> slab((size_t)width * n);
+    for (int l = 0; l < c->layers; ++l) {
+        for (int which = 0; which < 2; ++which) {
+            const uint16_t* base = c->kv + ((size_t)l * 2 + which) * Hkv * (size_t)c->capacity * D + (size_t)start * D;
+            e = hipMemcpy2D(slab.data(), (size_t)n * D * sizeof(uint16_t), base,
+                            (size_t)c->capacity * D * sizeof(uint16_t), (size_t)n * D * sizeof(uint16_t), Hkv,
+                            hipMemcpyDeviceToHost);
+            if (e != hipSuccess) return hip_fail(e, "cache export");
+            float* dst = (which == 0 ? key : value) + ((size_t)l * stride + start) * width;
+            for (int p = 0; p < n; ++p)
+                for (int h = 0; h < Hkv; ++h) {
+                    const uint16_t* src = slab.data() + ((size_t)h * n + p) * D;
+                    uint32_t* row = reinterpret_cast<uint32_t*>(dst + (size_t)p * width + (size_t)h * D);
+                    for (int d = 0; d < D; ++d) row[d] = (uint32_t)src[d] << 16;
+                }
+        }
+    }
     return YUE2_OK;
 }
 

@@ -259,10 +259,13 @@ void y2o_rotary_apply(float *x, int rows, int cols, int half, const float *cos_t
 /* Attention (src/model.rs:313-397, softmax_row src/tensor.rs:706-724)      */
 /* ------------------------------------------------------------------------ */
 
+int y2o_superblock(int blocks) { return blocks < 128 ? 1 : blocks < 256 ? 2 : 4; }
+
 void y2o_attention_row(const float *q, const float *key, const float *value, int keys,
                        int heads, int kv, int dim, float *out) {
     int groups = heads / kv, width = kv * dim;
     int blocks = (keys + 63) / 64;
+    int sb = y2o_superblock(blocks);
     int streams = 512 / dim;
     float scale = 1.0f / sqrtf((float)dim);
 #pragma omp parallel for schedule(static) num_threads(g_threads)
@@ -280,8 +283,9 @@ void y2o_attention_row(const float *q, const float *key, const float *value, int
         }
         /* subtract (vDSP_vsadd of -max) and exp (vvexpf) */
         for (int j = 0; j < keys; ++j) e[j] = y2o_expf(e[j] - m);
-        /* vDSP_sve: 64-key blocks by butterfly, blocks left to right */
-        float total = 0.0f;
+        /* vDSP_sve: 64-key blocks by butterfly; the blocks of a super-block
+         * left to right, then the super-blocks left to right */
+        float total = 0.0f, part = 0.0f;
         for (int b = 0; b < blocks; ++b) {
             float acc[64];
             for (int l = 0; l < 64; ++l) {
@@ -289,13 +293,14 @@ void y2o_attention_row(const float *q, const float *key, const float *value, int
                 acc[l] = j < keys ? e[j] : 0.0f;
             }
             blk[b] = butterfly64(acc);
-            total = b == 0 ? blk[0] : total + blk[b];
+            part = b % sb == 0 ? blk[b] : part + blk[b];
+            if (b % sb == sb - 1 || b == blocks - 1) total = b < sb ? part : total + part;
         }
         /* vDSP_vsdiv */
         for (int j = 0; j < keys; ++j) e[j] = e[j] / total;
         /* PV: per block, `streams` key streams, butterfly over streams */
         for (int d = 0; d < dim; ++d) {
-            float o = 0.0f;
+            float o = 0.0f, po = 0.0f;
             for (int b = 0; b < blocks; ++b) {
                 float acc[64];
                 for (int t = 0; t < streams; ++t) {
@@ -306,7 +311,10 @@ void y2o_attention_row(const float *q, const float *key, const float *value, int
                 }
                 for (int s = streams / 2; s >= 1; s >>= 1)
                     for (int t = 0; t < s; ++t) acc[t] = acc[t] + acc[t + s];
-                o = b == 0 ? acc[0] : o + acc[0];
+                /* the blocks of a super-block left to right, then the
+                 * super-blocks left to right */
+                po = b % sb == 0 ? acc[0] : po + acc[0];
+                if (b % sb == sb - 1 || b == blocks - 1) o = b < sb ? po : o + po;
             }
             out[(size_t)h * dim + d] = rb(o);
         }

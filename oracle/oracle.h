@@ -24,15 +24,24 @@
  *                  Used for every Linear row (cblas_sgemv/sgemm substitute,
  *                  src/tensor.rs:847-883, 1026-1081) and for the attention
  *                  scores q.K_j (src/model.rs:362-374).
+ *   SUPER-BLOCK    nb = ceil(keys / 64) blocks of 64 keys are grouped in
+ *                  super-blocks of SB = y2o_superblock(nb) consecutive
+ *                  blocks (1 below 128 blocks, 2 below 256, else 4; the last
+ *                  super-block may be short).  SB depends on the key count
+ *                  alone, never on the hardware.
  *   SOFTMAX SUM    keys in blocks of 64 (block b = keys [64b, 64b+64));
  *                  block sum = xor butterfly (32..1) over lane = key - 64b,
- *                  missing keys = +0; total = ((blk0 + blk1) + blk2) + ...
- *                  (vDSP_sve substitute, src/tensor.rs:721).
+ *                  missing keys = +0; super-block sum = its block sums left
+ *                  to right; total = the super-block sums left to right
+ *                  ((u0 + u1) + u2) + ... (vDSP_sve substitute,
+ *                  src/tensor.rs:721).  With SB = 1 this is
+ *                  ((blk0 + blk1) + blk2) + ...
  *   PV             per output dim d, block of 64 keys, S = 512/head_dim
  *                  streams; key j of the block goes to stream (j-64b) mod S;
  *                  stream: acc = +0, acc = fma(p_j, V[j,d], acc) ascending;
  *                  streams combined by xor butterfly over the stream index
- *                  with offsets S/2, ..., 1; blocks summed left to right
+ *                  with offsets S/2, ..., 1; the blocks of a super-block
+ *                  summed left to right, then the super-blocks left to right
  *                  (cblas_sgemv transpose substitute, src/model.rs:380-392).
  *   RMSNorm sum    sequential f32 sum as the reference defines it
  *                  (src/tensor.rs:1144, 1160): no substitute needed.
@@ -184,6 +193,8 @@ void y2o_norm_heads(float *x, int heads, int dim, const float *gamma, float eps)
 void y2o_rotary_table(int start, int rows, int head_dim, float theta, float *cos, float *sin);
 void y2o_rotary_apply(float *x, int rows, int cols, int half, const float *cos, const float *sin);
 
+/* Blocks per super-block of the attention's sums for `blocks` 64-key blocks. */
+int y2o_superblock(int blocks);
 /* Single-query GQA attention over `keys` cached rows; K/V rows have stride
  * kv*dim (src/model.rs:313-397 with rows == 1). */
 void y2o_attention_row(const float *q, const float *key, const float *value, int keys,

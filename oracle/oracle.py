@@ -96,6 +96,7 @@ def lib() -> C.CDLL:
             "y2o_rotary_table": (None, [i32, i32, i32, f32, vp, vp]),
             "y2o_rotary_apply": (None, [vp, i32, i32, i32, vp, vp]),
             "y2o_attention_row": (None, [vp, vp, vp, i32, i32, i32, i32, vp]),
+            "y2o_superblock": (i32, [i32]),
             "y2o_cache_new": (C.POINTER(CacheS), [vp, i32]),
             "y2o_cache_free": (None, [C.POINTER(CacheS)]),
             "y2o_hidden": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),

@@ -190,7 +190,7 @@ def _f64_attention(q, K, V, heads, kv, dim):
 
 
 @pytest.mark.parametrize("dim", [64, 128, 256])
-@pytest.mark.parametrize("keys", [4096, 4097, 7169, 24576])
+@pytest.mark.parametrize("keys", [4096, 4097, 7169, 8192, 16385, 24576])
 def test_attention_reference_known_answer(dim, keys):
     heads, kv = 4, 2
     for append in ([0, 1] if keys < 24576 else [0]):
@@ -220,6 +220,32 @@ def test_attention_one_key_and_equal_keys():
     for h in range(heads):
         kh = h // (heads // kv)
         assert np.array_equal(out[h * dim:(h + 1) * dim], rb(mean[kh * dim:(kh + 1) * dim]))
+
+
+@pytest.mark.parametrize("L", [8192, 16384, 16448])
+def test_attention_equal_keys_over_super_blocks(L):
+    """Equal keys at 128 blocks (super-blocks of 2) and 256 / 257 blocks
+    (super-blocks of 4, the last one short at 16448 keys): p_j = 1/L, and
+    with V = small integers / 8 over a power-of-two L every product and
+    partial sum is exact, so any association gives rb(mean V); a
+    super-block dropped, counted twice or cut at the wrong block does not.
+    (16448 keys: p = 1/16448 rounds, so the check there is the f64 mean
+    within the known-answer tolerance.)"""
+    heads, kv, dim = 4, 2, 64
+    rng = np.random.default_rng(L)
+    q = rb(rng.standard_normal(heads * dim).astype(np.float32))
+    K = np.repeat(rb(rng.standard_normal((1, kv * dim)).astype(np.float32)), L, axis=0)
+    V = (rng.integers(-8, 9, size=(L, kv * dim)) / 8.0).astype(np.float32)
+    out = _attention(q, np.ascontiguousarray(K), V, heads, kv, dim)
+    mean = V.astype(np.float64).mean(axis=0)
+    for h in range(heads):
+        kh = h // (heads // kv)
+        want = mean[kh * dim:(kh + 1) * dim]
+        if L & (L - 1) == 0:
+            assert np.array_equal(out[h * dim:(h + 1) * dim], rb(want.astype(np.float32)))
+        else:
+            assert np.all(np.abs(out[h * dim:(h + 1) * dim] - want) <= 5e-5 + np.abs(want) * 0.008)
+    assert [O.lib().y2o_superblock(n) for n in (1, 127, 128, 255, 256, 384)] == [1, 1, 2, 2, 4, 4]
 
 
 def test_cfg_mix_closed_forms():

@@ -31,7 +31,7 @@ void attention_geometry(int kv_heads, int rows, int max_blocks, int* wgs, int* b
     int w = std::max(1, std::min(32, g_attn_cus / groups));
     w = std::min(w, std::max(1, max_blocks));
     *wgs = w;
-    *bpw = (max_blocks + w - 1) / w;
+    *bpw = attn_bpw_max(max_blocks, w);
 }
 
 hipError_t launch_attention(hipStream_t s, const AttnArgs& a) {
@@ -39,7 +39,8 @@ hipError_t launch_attention(hipStream_t s, const AttnArgs& a) {
     if (G < 1 || G > 8 || a.heads % a.kv_heads) return hipErrorInvalidValue;
     if (a.wgs * a.kv_heads * a.rows > 1024) return hipErrorInvalidValue;
     // the block statistics are gathered for at most 384 blocks (24576 keys)
-    if (a.wgs * a.bpw > 24576 / kBlockKeys && a.blk_stride > 24576 / kBlockKeys) return hipErrorInvalidValue;
+    // (wgs * bpw covers every block of the geometry's contexts, whole super-blocks)
+    if (std::min(a.wgs * a.bpw, a.blk_stride) > 24576 / kBlockKeys) return hipErrorInvalidValue;
     const dim3 grid(a.wgs, a.kv_heads, a.rows);
     const size_t lds = attn_group_lds(G, a.dim, a.wgs, a.bpw);
     if (lds > 96 * 1024) return hipErrorInvalidValue;

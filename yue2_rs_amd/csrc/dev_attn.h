@@ -15,9 +15,13 @@
 //      scaled scores of its blocks into LDS, block maxima to HBM.
 //   2. M = max of the group's block maxima; e_j = exp(s_j - M) in LDS; block
 //      sums (64-lane butterfly) to HBM.
-//   3. total = block sums left to right; p_j = e_j / total; partial PV per
-//      block (512/dim key streams, butterfly over streams) to HBM; the last
-//      workgroup to finish adds the blocks left to right and rounds to BF16.
+//   3. total = super-block sums left to right; p_j = e_j / total; partial PV
+//      per block (512/dim key streams, butterfly over streams), the blocks of
+//      each super-block added left to right, to HBM; the last workgroup to
+//      finish adds the super-blocks left to right and rounds to BF16.
+// Blocks are grouped in super-blocks (attn_superblock, kernels.h) and each
+// workgroup takes whole super-blocks, so it publishes one block sum and one
+// partial per super-block.
 // Each sync waits on a counter with a bounded spin: on timeout the device
 // error is set and the workgroup leaves, so every launch terminates.  All
 // workgroups of a group must be resident at once (callers launch at most one
@@ -117,7 +121,8 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
         return true;
     }
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const int bpw = (nb + a.wgs - 1) / a.wgs;  // <= a.bpw, which sizes e_s
+    const int sb = attn_superblock(nb), nsb = (nb + sb - 1) / sb;
+    const int bpw = attn_bpw(nb, a.wgs);  // <= a.bpw, which sizes e_s
     const int W = (nb + bpw - 1) / bpw;
     if (wg >= W) return true;
     const int G = a.heads / a.kv_heads;
@@ -247,12 +252,22 @@ m = xor_max<32>(m);
             e_s[h * estride + jl] = expf_cr(e_s[h * estride + jl] - m_s[h]);
         }
         __syncthreads();
+        float* bl_s = e_s + G * estride;  // [G][nbl] block sums (the gather region of phase 3)
         for (int i = wave; i < G * nbl; i += NW) {
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float v = jl < nk ? e_s[h * estride + jl] : 0.0f;
 v = xor_sum<32>(v);
-            if (lane == 0) st_dev(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v);
+            if (lane == 0) bl_s[h * nbl + bl] = v;
+        }
+        __syncthreads();
+        // each super-block's block sums left to right
+        const int nsbl = (nbl + sb - 1) / sb;
+        for (int i = tid; i < G * nsbl; i += NT) {
+            const int h = i / nsbl, k = i % nsbl, b0 = k * sb, b1 = min(nbl, b0 + sb);
+            float u = bl_s[h * nbl + b0];
+            for (int j = b0 + 1; j < b1; ++j) u = u + bl_s[h * nbl + j];
+            st_dev(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 / sb + k, u);
         }
         stores_done();
         __syncthreads();
@@ -262,25 +277,26 @@ v = xor_sum<32>(v);
 
     // ---- phase 3: p = e / total, partial PV, merge by the last workgroup ---
     {
-        // total = block sums added left to right; the sums are gathered into
-        // LDS by all threads first (a chain of dependent device loads would
-        // pay a memory round trip per block)
+        // total = super-block sums added left to right; the sums are
+        // gathered into LDS by all threads first (a chain of dependent device
+        // loads would pay a memory round trip per super-block)
         {
-            float* bs = e_s + G * estride;  // [G][nb] block sums, after the scores
-            const int total = G * nb;        // <= 8 * 384 = 6 * 512
+            float* bs = e_s + G * estride;  // [G][nsb] super-block sums, after the scores
+            const int total = G * nsb;       // <= 8 * 384 = 6 * 512
             float v[6];
 #pragma unroll
             for (int u = 0; u < 6; ++u) {
-                const int i = tid + u * NT, h = i / nb, j = i - h * nb;
+                const int i = tid + u * NT, h = i / nsb, j = i - h * nsb;
                 v[u] = i < total ? ld_dev(a.bsum + hbase + (size_t)h * a.blk_stride + j) : 0.0f;
             }
+            __syncthreads();  // every thread is done with the block sums in bs
 #pragma unroll
             for (int u = 0; u < 6; ++u)
                 if (tid + u * NT < total) bs[tid + u * NT] = v[u];
             __syncthreads();
             if (tid < G) {
-                float tot = bs[tid * nb];
-                for (int j = 1; j < nb; ++j) tot = tot + bs[tid * nb + j];
+                float tot = bs[tid * nsb];
+                for (int j = 1; j < nsb; ++j) tot = tot + bs[tid * nsb + j];
                 t_s[tid] = tot;
             }
         }
@@ -291,7 +307,9 @@ v = xor_sum<32>(v);
         }
         __syncthreads();
         const int t = lane / CPL, c = lane % CPL;
-        for (int bl = wave; bl < nbl; bl += NW) {
+        float sacc[MAXG][8];  // the super-block's blocks so far, left to right
+        for (int it = wave * sb; it < nbl; it += (it % sb == sb - 1 ? (NW - 1) * sb + 1 : 1)) {
+            const int bl = it;
             const int jb = (blk0 + bl) * kBlockKeys;
             uint4 vr[kBlockKeys / S];
 #pragma unroll
@@ -324,20 +342,23 @@ v = xor_sum<32>(v);
             for (int h = 0; h < MAXG; ++h)
                 if (h < G)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[h][e] = xor_sum<32, CPL>(acc[h][e]);
-            if (t == 0) {
+                    for (int e = 0; e < 8; ++e) {
+                        const float v = xor_sum<32, CPL>(acc[h][e]);
+                        sacc[h][e] = bl % sb == 0 ? v : sacc[h][e] + v;
+                    }
+            if (t == 0 && (bl % sb == sb - 1 || bl == nbl - 1)) {
 #pragma unroll
                 for (int h = 0; h < MAXG; ++h)
                     if (h < G) {
-                        float* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + 8 * c;
+                        float* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + (blk0 + bl) / sb) * D + 8 * c;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) st_dev(dst + e, acc[h][e]);
+                        for (int e = 0; e < 8; ++e) st_dev(dst + e, sacc[h][e]);
                     }
             }
         }
         stores_done();
         __syncthreads();
-        if (nb <= kMergeLastMax) {
+        if (nsb <= kMergeLastMax) {
             // short contexts: the last workgroup through merges every output
             __shared__ int s_last;
             if (tid == 0) s_last = signal(&cnt[2]) == W - 1;
@@ -348,11 +369,11 @@ v = xor_sum<32>(v);
                 const float* pp = a.part + (hbase + (size_t)h * a.blk_stride) * D + d;
                 float v[kMergeLastMax];
 #pragma unroll
-                for (int j = 0; j < kMergeLastMax; ++j) v[j] = j < nb ? ld_dev(pp + (size_t)j * D) : 0.0f;
+                for (int j = 0; j < kMergeLastMax; ++j) v[j] = j < nsb ? ld_dev(pp + (size_t)j * D) : 0.0f;
                 float o = v[0];
 #pragma unroll
                 for (int j = 1; j < kMergeLastMax; ++j)
-                    if (j < nb) o = o + v[j];  // blocks left to right
+                    if (j < nsb) o = o + v[j];  // super-blocks left to right
                 st_dev(a.out + (size_t)b * a.out_stride + (size_t)(g * G + h) * D + d, rb(o));
             }
             if (tid < 3) st_dev_i(&cnt[tid], 0);
@@ -366,9 +387,9 @@ v = xor_sum<32>(v);
         // device loads would pay a memory round trip per block.
         const int outs = G * D, chunk = (outs + W - 1) / W;
         const int o0 = min(outs, wg * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
-        float* mb = e_s;  // [no][nb]; the scores are no longer needed
+        float* mb = e_s;  // [no][nsb]; the scores are no longer needed
         const float* part = a.part + hbase * D;
-        const int total = no * nb;
+        const int total = no * nsb;
         for (int base = 0; base < total; base += 16 * NT) {
             float v[16];
 #pragma unroll
@@ -376,7 +397,7 @@ v = xor_sum<32>(v);
                 const int i = base + tid + u * NT;
                 float x = 0.0f;
                 if (i < total) {
-                    const int r = i / nb, k = i - r * nb, o = o0 + r;
+                    const int r = i / nsb, k = i - r * nsb, o = o0 + r;
                     x = ld_dev(part + ((size_t)(o / D) * a.blk_stride + k) * D + o % D);
                 }
                 v[u] = x;
@@ -387,9 +408,9 @@ v = xor_sum<32>(v);
         }
         __syncthreads();
         for (int i = tid; i < no; i += NT) {
-            const float* pp = mb + i * nb;
+            const float* pp = mb + i * nsb;
             float o = pp[0];
-            for (int k = 1; k < nb; ++k) o = o + pp[k];
+            for (int k = 1; k < nsb; ++k) o = o + pp[k];  // super-blocks left to right
             st_dev(a.out + (size_t)b * a.out_stride + (size_t)(g * G) * D + o0 + i, rb(o));
         }
         __syncthreads();

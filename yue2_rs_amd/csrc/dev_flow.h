@@ -257,7 +257,9 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     StepState* st = a.st;
     const int pos = a.pos, L = pos + 1, cap = a.cap;
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const int bpw = (nb + a.wpg - 1) / a.wpg;
+    // whole super-blocks per workgroup (the order spec's sums, kernels.h)
+    const int sb = attn_superblock(nb), nsb = (nb + sb - 1) / sb;
+    const int bpw = attn_bpw(nb, a.wpg);
     const int W = (nb + bpw - 1) / bpw;
     if (wi >= W) {
         for (int i = 0; i < 6; ++i) mark();  // keep the trace slots aligned
@@ -484,6 +486,10 @@ m = xor_max<32>(m);
     // ---- phase 2: M, exp(s - M) and block sums -----------------------------
     const uint32_t t_bsum = flow_tag(a.epoch, a.layer, FK_BSUM);
     {
+        // (super-blocks of more than one block) the block sums, in the K
+        // region: the scores are done with it and p is staged there only
+        // after the super-block sums are gathered
+        float* bl_s = reinterpret_cast<float*>(Ks);
         // (long contexts) the second V chunk is requested before the waits
         // for the group's block statistics
         if (kAttnChunk < nbl) load_chunk(Vc, kAttnChunk, vr);
@@ -505,34 +511,49 @@ m = xor_max<32>(m);
                 e_s[h * estride + jl] = v;
             }
             v = xor_sum<32>(v);
-            if (lane == 0) st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v, t_bsum);
+            if (sb == 1) {
+                if (lane == 0) st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 + bl, v, t_bsum);
+            } else if (lane == 0) {
+                bl_s[h * nbl + bl] = v;
+            }
+        }
+        if (sb > 1) {
+            // each super-block's block sums left to right
+            __syncthreads();
+            const int nsbl = (nbl + sb - 1) / sb;
+            for (int i = tid; i < Gq * nsbl; i += NT) {
+                const int h = i / nsbl, k = i - h * nsbl, b0 = k * sb, b1 = min(nbl, b0 + sb);
+                float u = bl_s[h * nbl + b0];
+                for (int j = b0 + 1; j < b1; ++j) u = u + bl_s[h * nbl + j];
+                st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 / sb + k, u, t_bsum);
+            }
         }
     }
 
     // ---- phase 3: total, p = e / total, partial PV -------------------------
     const uint32_t t_part = flow_tag(a.epoch, a.layer, FK_PART);
     {
-        // head h's block sums at red_s[h * nbp + k] (rows 16-byte aligned)
-        const int nbp = (nb + 3) & ~3;
+        // head h's super-block sums at red_s[h * nbp + k] (rows 16-byte aligned)
+        const int nbp = (nsb + 3) & ~3;
         {
-            const FastDiv fnb(nb);
+            const FastDiv fnb(nsb);
             const uint64_t* src = a.bsum + hbase;
             const size_t bstride = a.blk_stride;
             if (!gather_put<NT, (G * MAXNB + NT - 1) / NT>(
                     [=](int i) {
                         const int h = fnb.div(i);
-                        return src + (size_t)h * bstride + (i - h * nb);
+                        return src + (size_t)h * bstride + (i - h * nsb);
                     },
-                    Gq * nb, t_bsum,
+                    Gq * nsb, t_bsum,
                     [=](int i, uint32_t bits) {
                         const int h = fnb.div(i);
-                        red_s[h * nbp + (i - h * nb)] = u2f(bits);
+                        red_s[h * nbp + (i - h * nsb)] = u2f(bits);
                     },
                     st))
                 return false;
         }
         mark();
-        if (tid < Gq) t_s[tid] = sum_left_to_right_a16(red_s + tid * nbp, nb);  // block sums
+        if (tid < Gq) t_s[tid] = sum_left_to_right_a16(red_s + tid * nbp, nsb);  // super-block sums
         __syncthreads();
         // p = e / total into the K region (the scores are done with it), in
         // stream order: p_s[h * estride + bl * 64 + t * KPS + i] is p of key
@@ -560,6 +581,7 @@ m = xor_max<32>(m);
         constexpr int LPS = 64 / S;  // lanes per stream
         static_assert(LPS * NW == D, "one dimension per lane, the eight waves over a block's dimensions");
         const int t = lane / LPS, c = lane % LPS;
+        float sacc[G];  // this wave's super-block so far: its blocks left to right
         for (int cb = 0; cb < nbl; cb += kAttnChunk) {
             if (cb > 0) {
                 // requested one chunk ahead, as the keys
@@ -607,8 +629,10 @@ m = xor_max<32>(m);
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     const float v = xor_sum<32, LPS>(acc[h]);
-                    if (h % S == t)
-                        st_tag(a.part + ((hbase + (size_t)h * a.blk_stride) + blk0 + bl) * D + d, v, t_part);
+                    sacc[h] = bl % sb == 0 ? v : sacc[h] + v;
+                    if (h % S == t && (bl % sb == sb - 1 || bl == nbl - 1))
+                        st_tag(a.part + ((hbase + (size_t)h * a.blk_stride) + (blk0 + bl) / sb) * D + d, sacc[h],
+                               t_part);
                 }
             }
         }
@@ -622,23 +646,23 @@ m = xor_max<32>(m);
         const int outs = Gq * D, chunk = ((outs + W - 1) / W + 1) & ~1;
         const int o0 = min(outs, wi * chunk), o1 = min(outs, o0 + chunk), no = o1 - o0;
         __syncthreads();  // the K/V region is reused below
-        const int nbp = (nb + 3) & ~3;
-        float* m_buf = lds;  // [no][nbp]: partial of block k for output o0 + i (rows 16-byte aligned)
+        const int nbp = (nsb + 3) & ~3;
+        float* m_buf = lds;  // [no][nbp]: partial of super-block k for output o0 + i (rows 16-byte aligned)
         const uint64_t* part = a.part + hbase * D;
         const size_t hstride = (size_t)a.blk_stride * D;
         const FastDiv fno(max(no, 1));
         // in passes of at most kMergeBatch words per thread: one pass at
         // short contexts, and the unrolled poll stays small; word i of the
-        // sequence is output o0 + i % no of block i / no, so neighbouring
-        // threads read neighbouring words of a block's partial
-        for (int p0 = 0; p0 < no * nb; p0 += NT * kMergeBatch) {
+        // sequence is output o0 + i % no of super-block i / no, so
+        // neighbouring threads read neighbouring words of one partial
+        for (int p0 = 0; p0 < no * nsb; p0 += NT * kMergeBatch) {
             if (!gather_put<NT, kMergeBatch>(
                     [=](int i) {
                         i += p0;
                         const int k = fno.div(i), o = o0 + i - k * no;
                         return part + (size_t)(o / D) * hstride + (size_t)k * D + o % D;
                     },
-                    min(no * nb - p0, NT * kMergeBatch), t_part,
+                    min(no * nsb - p0, NT * kMergeBatch), t_part,
                     [=](int i, uint32_t bits) {
                         i += p0;
                         const int k = fno.div(i);
@@ -650,7 +674,7 @@ m = xor_max<32>(m);
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
         for (int i0 = 0; i0 < no; i0 += NT) {
             const int i = i0 + tid;
-            const float o = i < no ? rb(sum_left_to_right_a16(m_buf + i * nbp, nb)) : 0.0f;  // blocks left to right
+            const float o = i < no ? rb(sum_left_to_right_a16(m_buf + i * nbp, nsb)) : 0.0f;  // super-blocks left to right
             const float o_next = xor_lane<1>(o);  // output i + 1 (the odd neighbour lane's)
             if (i < no && (tid & 1) == 0)
                 st_tag_bits(a.att + ((size_t)b * a.att_stride + (size_t)g * Gq * D + o0 + i) / 2, pack_rows(o, o_next),

@@ -8,6 +8,25 @@ namespace y2 {
 constexpr int kMaxRows = 2;      // batch rows per step: 1, or 2 for CFG
 constexpr int kBlockKeys = 64;   // attention key block (order spec)
 
+// Attention super-blocks (order spec): the softmax sum and each output's PV
+// add the block results of a super-block of consecutive 64-key blocks left to
+// right, then the super-blocks left to right.  The size depends on the block
+// count alone (never on the hardware): 1 below 128 blocks, 2 below 256,
+// else 4.  A workgroup sums its own super-blocks, so a long context publishes
+// one partial per super-block instead of one per block.
+__host__ __device__ constexpr int attn_superblock(int nb) { return nb < 128 ? 1 : nb < 256 ? 2 : 4; }
+// Blocks per workgroup when nb blocks are split over wpg workgroups in whole
+// super-blocks (the last workgroup with work may hold fewer).
+__host__ __device__ constexpr int attn_bpw(int nb, int wpg) {
+    return ((nb + attn_superblock(nb) - 1) / attn_superblock(nb) + wpg - 1) / wpg * attn_superblock(nb);
+}
+// The largest attn_bpw over block counts 1 .. max_blocks.
+inline int attn_bpw_max(int max_blocks, int wpg) {
+    int m = 1;
+    for (int nb = 1; nb <= max_blocks; ++nb) m = attn_bpw(nb, wpg) > m ? attn_bpw(nb, wpg) : m;
+    return m;
+}
+
 // Per-row view of a KV cache: layout [layers][2][kv_heads][capacity][dim] BF16.
 struct KvView {
     uint16_t* base[kMaxRows];

@@ -727,7 +727,7 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     if (!shape || rows < 1 || rows > 2 || nwg < c.num_key_value_heads * rows) return false;
     const int wpg = nwg / (c.num_key_value_heads * rows);  // workgroups past the groups take no attention
     const int max_blocks = (c.max_position_embeddings + kBlockKeys - 1) / kBlockKeys;
-    const int bpw = (max_blocks + wpg - 1) / wpg;
+    const int bpw = attn_bpw_max(max_blocks, wpg);
     // the attention's p (G x bpw blocks of f32) is staged in its K region
     // (the merge's partials, G x head_dim x bpw + blocks words at most, are
     // gathered kMergePer per thread into the K/V region with rows padded to
@@ -749,7 +749,7 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
 size_t step_lds_bytes(const StepArgs& a, int nwg) {
     const int kmax = std::max(std::max(a.hidden, a.intermediate), a.heads * a.head_dim);
     const int G = a.heads / a.kv_heads, wpg = nwg / (a.kv_heads * a.rows);
-    const int bpw = (a.max_blocks + wpg - 1) / wpg;
+    const int bpw = attn_bpw_max(a.max_blocks, wpg);
     // staged GEMV inputs; the attention (staged K/V chunks + scores; its
     // merge reuses the K/V region)
     return std::max((size_t)a.rows * kmax * sizeof(float), attn_flow_lds(G, a.head_dim, bpw));

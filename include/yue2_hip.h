@@ -89,6 +89,34 @@ int32_t yue2_hip_cached_attention(const float *q, const float *k, const float *v
                                   size_t keys, size_t heads, size_t kv, size_t dim, size_t cache,
                                   size_t layer);
 
+/* The prefill / NAR bridge (src/tensor.rs:135-145, 194-219; src/metal.m:
+ * 164-237, 330-361): plain FP32 products on the platform BLAS and the
+ * multi-row attention on the matrix-core flash kernel.  Like the reference's
+ * MPS path they sum in another order than the CPU path, so they agree with
+ * it within FP32 rounding (gemm, linear) or the matrix-core prefill's
+ * tolerance (attention), and return 1 = done / 0 = fall back to the CPU.
+ * yue2_metal_gemm: c [m x n] = a [m x k] op(b) + beta c, row-major host
+ * matrices with row strides lda, ldb, ldc; op(b) = b [k x n], or with
+ * transpose_b b^T for b [n x k]. */
+int32_t yue2_hip_gemm(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                      int32_t transpose_b, size_t lda, size_t ldb, size_t ldc, float beta);
+/* yue2_metal_linear: c [m x n] = a [m x k] W^T for the host weight W [n x k]
+ * (dtype 0 BF16, 1 F32, 2 F16; rounded: F32/F16 values rounded to BF16, as
+ * convert_weight does, src/attention.metal:161-176), cached on the device
+ * under (mapping, raw, n, k, dtype, rounded); not rounded (the caller's
+ * Linear::finish rounds). */
+int32_t yue2_hip_linear(const float *a, const uint8_t *raw, size_t mapping, int32_t dtype, int32_t rounded,
+                        float *c, size_t m, size_t n, size_t k);
+/* yue2_metal_attention: `rows` query rows q [rows x heads*dim] over k, v
+ * [keys x kv*dim]; row r sees keys [0, min(keys, causal + r + 1)) (causal >=
+ * 0) or all (causal < 0); out [rows x heads*dim] rounded to BF16.  Falls back
+ * (0) for inputs that are not BF16-exact, head_dim other than 64 / 128, a
+ * scale other than 1/sqrt(dim) and causal windows past `keys`. */
+int32_t yue2_hip_attention(const float *q, const float *k, const float *v, float *out, size_t rows,
+                           size_t keys, size_t heads, size_t kv, size_t dim, int64_t causal, float scale);
+/* yue2_metal_stack (src/tensor.rs:164-180) is not twinned: the session API's
+ * yue2_hip_velocity runs the same NAR stack on the device. */
+
 /* Lifetime (src/tensor.rs:132-134; src/metal.m:73-103). */
 void yue2_hip_release_cache(size_t cache);
 void yue2_hip_clear_weights(void);

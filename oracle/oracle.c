@@ -259,7 +259,7 @@ void y2o_rotary_apply(float *x, int rows, int cols, int half, const float *cos_t
 /* Attention (src/model.rs:313-397, softmax_row src/tensor.rs:706-724)      */
 /* ------------------------------------------------------------------------ */
 
-int y2o_superblock(int blocks) { return blocks < 128 ? 1 : blocks < 256 ? 2 : 4; }
+int y2o_superblock(int blocks) { return blocks < 256 ? 1 : 2; }
 
 void y2o_attention_row(const float *q, const float *key, const float *value, int keys,
                        int heads, int kv, int dim, float *out) {

@@ -26,9 +26,9 @@
  *                  scores q.K_j (src/model.rs:362-374).
  *   SUPER-BLOCK    nb = ceil(keys / 64) blocks of 64 keys are grouped in
  *                  super-blocks of SB = y2o_superblock(nb) consecutive
- *                  blocks (1 below 128 blocks, 2 below 256, else 4; the last
- *                  super-block may be short).  SB depends on the key count
- *                  alone, never on the hardware.
+ *                  blocks (1 below 256 blocks, else 2; the last super-block
+ *                  may be short).  SB depends on the key count alone, never
+ *                  on the hardware.
  *   SOFTMAX SUM    keys in blocks of 64 (block b = keys [64b, 64b+64));
  *                  block sum = xor butterfly (32..1) over lane = key - 64b,
  *                  missing keys = +0; super-block sum = its block sums left

@@ -104,3 +104,118 @@ def test_lifetime_calls_and_names(gpu):
     L.yue2_hip_release_cache(123456)
     L.yue2_hip_clear_weights()
     L.yue2_hip_release_model()
+
+
+# ---- the prefill / NAR bridge: yue2_metal_gemm, linear, attention ----------
+
+def _p(a):
+    return a.ctypes.data
+
+
+def _gemm_bound(a, bt):
+    """|error| bound of an f32 dot product of length k: gamma_k sum |a||b|."""
+    k = a.shape[1]
+    g = k * 2.0 ** -24 / (1 - k * 2.0 ** -24)
+    return g * (np.abs(a).astype(np.float64) @ np.abs(bt).astype(np.float64).T) + 1e-30
+
+
+@pytest.mark.parametrize("transpose_b,beta", [(0, 0.0), (1, 0.0), (1, 0.5), (0, -1.25)])
+def test_gemm_twin(gpu, transpose_b, beta):
+    """src/tensor.rs:207-219 (MPS, src/metal.m:164-182): row-major operands
+    with padded row strides, C = A op(B) + beta C; within the f32 dot bound of
+    a float64 product, and exact on small integers (every partial sum exact,
+    so any order gives the same bits)."""
+    rng = np.random.default_rng(7 + transpose_b)
+    m, n, k = 70, 300, 513
+    lda, ldb, ldc = k + 3, (k if transpose_b else n) + 5, n + 2
+    for ints in (False, True):
+        draw = (lambda *s: rng.integers(-4, 5, size=s).astype(np.float32)) if ints else \
+            (lambda *s: rng.standard_normal(s).astype(np.float32))
+        A = np.zeros((m, lda), np.float32)
+        A[:, :k] = draw(m, k)
+        B = np.zeros(((n if transpose_b else k), ldb), np.float32)
+        B[:, :(k if transpose_b else n)] = draw(n, k) if transpose_b else draw(k, n)
+        Cin = np.zeros((m, ldc), np.float32)
+        Cin[:, :n] = draw(m, n)
+        c = Cin.copy()
+        ok = y2.lib().yue2_hip_gemm(_p(A), _p(B), _p(c), m, n, k, transpose_b, lda, ldb, ldc, beta)
+        assert ok == 1
+        Bt = B[:, :k] if transpose_b else B[:, :n].T  # [n, k]
+        want = A[:, :k].astype(np.float64) @ Bt.astype(np.float64).T + np.float64(beta) * Cin[:, :n]
+        if ints:
+            assert np.array_equal(c[:, :n], want.astype(np.float32))
+        else:
+            bound = _gemm_bound(A[:, :k], Bt) + abs(beta) * np.abs(Cin[:, :n]) * 2.0 ** -23
+            assert np.all(np.abs(c[:, :n] - want) <= 2 * bound)
+        assert np.array_equal(c[:, n:], Cin[:, n:]), "padding columns written"
+
+
+@pytest.mark.parametrize("dtype", [0, 1, 2])
+def test_linear_twin(gpu, dtype):
+    """src/tensor.rs:135-145 (src/metal.m:216-237): c = a W^T for BF16, F32
+    and F16 host weights; rounded F32/F16 weights are rounded to BF16 first
+    (convert_weight, src/attention.metal:161-176).  Checked against float64
+    on the converted weights within the f32 dot bound, the unrounded F32
+    weights against their own values, and the weight cache keyed by mapping."""
+    rng = np.random.default_rng(30 + dtype)
+    m, n, k = 48, 400, 768
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w32 = (0.05 * rng.standard_normal((n, k))).astype(np.float32)
+    if dtype == 0:
+        raw = (rb(w32).view(np.uint32) >> 16).astype(np.uint16)
+        conv = rb(w32)
+    elif dtype == 1:
+        raw = w32
+        conv = w32
+    else:
+        raw = w32.astype(np.float16)
+        conv = raw.astype(np.float32)
+    mapping = fresh_mapping()
+    for rounded in (1, 0):
+        want_w = rb(conv) if (rounded and dtype != 0) else conv
+        c = np.empty((m, n), np.float32)
+        assert y2.lib().yue2_hip_linear(_p(a), _p(raw), mapping, dtype, rounded, _p(c), m, n, k) == 1
+        want = a.astype(np.float64) @ want_w.astype(np.float64).T
+        assert np.all(np.abs(c - want) <= 2 * _gemm_bound(a, want_w))
+        if rounded and dtype != 0:
+            # the rounding is applied: the unrounded weights' product differs
+            assert not np.all(np.abs(c - a.astype(np.float64) @ conv.astype(np.float64).T) <= _gemm_bound(a, conv))
+
+
+def _attention_f64(q, k, v, rows, keys, heads, kv, dim, causal, scale):
+    out = np.empty((rows, heads * dim), np.float64)
+    G = heads // kv
+    for r in range(rows):
+        vis = keys if causal < 0 else min(keys, causal + r + 1)
+        for h in range(heads):
+            g = h // G
+            s = (k[:vis, g * dim:(g + 1) * dim].astype(np.float64) @ q[r, h * dim:(h + 1) * dim].astype(np.float64))
+            e = np.exp(s * scale - (s * scale).max())
+            out[r, h * dim:(h + 1) * dim] = (e @ v[:vis, g * dim:(g + 1) * dim].astype(np.float64)) / e.sum()
+    return out
+
+
+@pytest.mark.parametrize("dim,causal,rows,keys", [(128, 40, 90, 130), (64, 0, 200, 200), (128, -1, 33, 300),
+                                                   (64, -1, 128, 128)])
+def test_attention_twin(gpu, dim, causal, rows, keys):
+    """src/tensor.rs:194-206 (src/metal.m:330-361): multi-row attention, row r
+    over keys [0, causal + r] or all keys, BF16-rounded output; within the
+    reference's own tolerance for its GPU attention against float64
+    (5e-5 + 0.008 |x|, src/tensor.rs:73)."""
+    rng = np.random.default_rng(dim + rows)
+    heads, kv = 6, 2
+    q = rb(rng.standard_normal((rows, heads * dim)).astype(np.float32))
+    k = rb(rng.standard_normal((keys, kv * dim)).astype(np.float32))
+    v = rb(rng.standard_normal((keys, kv * dim)).astype(np.float32))
+    scale = np.float32(1.0) / np.sqrt(np.float32(dim))
+    out = np.empty((rows, heads * dim), np.float32)
+    assert y2.lib().yue2_hip_attention(_p(q), _p(k), _p(v), _p(out), rows, keys, heads, kv, dim, causal,
+                                       float(scale)) == 1
+    assert np.array_equal(out, rb(out)), "output not BF16-rounded"
+    want = _attention_f64(q, k, v, rows, keys, heads, kv, dim, causal, float(scale))
+    assert np.all(np.abs(out - want) <= 5e-5 + 0.008 * np.abs(want))
+    # inputs that are not BF16-exact fall back to the CPU
+    q2 = q.copy()
+    q2[0, 0] += np.float32(1e-3)
+    assert y2.lib().yue2_hip_attention(_p(q2), _p(k), _p(v), _p(out), rows, keys, heads, kv, dim, causal,
+                                       float(scale)) == 0

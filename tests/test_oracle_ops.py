@@ -222,10 +222,11 @@ def test_attention_one_key_and_equal_keys():
         assert np.array_equal(out[h * dim:(h + 1) * dim], rb(mean[kh * dim:(kh + 1) * dim]))
 
 
-@pytest.mark.parametrize("L", [8192, 16384, 16448])
+@pytest.mark.parametrize("L", [8192, 16384, 16448, 24576])
 def test_attention_equal_keys_over_super_blocks(L):
-    """Equal keys at 128 blocks (super-blocks of 2) and 256 / 257 blocks
-    (super-blocks of 4, the last one short at 16448 keys): p_j = 1/L, and
+    """Equal keys at 128 blocks (no super-blocks), 256 / 257 blocks
+    (super-blocks of 2, the last one short at 16448 keys) and 384 blocks:
+    p_j = 1/L, and
     with V = small integers / 8 over a power-of-two L every product and
     partial sum is exact, so any association gives rb(mean V); a
     super-block dropped, counted twice or cut at the wrong block does not.
@@ -245,7 +246,7 @@ def test_attention_equal_keys_over_super_blocks(L):
             assert np.array_equal(out[h * dim:(h + 1) * dim], rb(want.astype(np.float32)))
         else:
             assert np.all(np.abs(out[h * dim:(h + 1) * dim] - want) <= 5e-5 + np.abs(want) * 0.008)
-    assert [O.lib().y2o_superblock(n) for n in (1, 127, 128, 255, 256, 384)] == [1, 1, 2, 2, 4, 4]
+    assert [O.lib().y2o_superblock(n) for n in (1, 127, 128, 255, 256, 384)] == [1, 1, 1, 1, 2, 2]
 
 
 def test_cfg_mix_closed_forms():

@@ -98,6 +98,9 @@ def lib() -> C.CDLL:
         "yue2_hip_vector": (i32, [vp, vp, sz, i32, i32, i32, vp, sz, sz]),
         "yue2_hip_ar_stack": (i32, [vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, sz, sz, f32, vp, vp]),
         "yue2_hip_cached_attention": (i32, [vp, vp, vp, vp, sz, sz, sz, sz, sz, sz]),
+        "yue2_hip_gemm": (i32, [vp, vp, vp, sz, sz, sz, i32, sz, sz, sz, C.c_float]),
+        "yue2_hip_linear": (i32, [vp, vp, sz, i32, i32, vp, sz, sz, sz]),
+        "yue2_hip_attention": (i32, [vp, vp, vp, vp, sz, sz, sz, sz, sz, C.c_int64, C.c_float]),
         "yue2_hip_release_cache": (None, [sz]),
         "yue2_hip_clear_weights": (None, []),
         "yue2_hip_release_model": (None, []),

@@ -121,7 +121,7 @@ __device__ __forceinline__ bool attn_group(const AttnArgs& a, int wg, int g, int
         return true;
     }
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
-    const int sb = attn_superblock(nb), nsb = (nb + sb - 1) / sb;
+    const int sb = attn_superblock(nb), lsb = sb == 1 ? 0 : sb == 2 ? 1 : 2, nsb = (nb + sb - 1) >> lsb;
     const int bpw = attn_bpw(nb, a.wgs);  // <= a.bpw, which sizes e_s
     const int W = (nb + bpw - 1) / bpw;
     if (wg >= W) return true;
@@ -262,12 +262,12 @@ v = xor_sum<32>(v);
         }
         __syncthreads();
         // each super-block's block sums left to right
-        const int nsbl = (nbl + sb - 1) / sb;
+        const int nsbl = (nbl + sb - 1) >> lsb;
         for (int i = tid; i < G * nsbl; i += NT) {
             const int h = i / nsbl, k = i % nsbl, b0 = k * sb, b1 = min(nbl, b0 + sb);
             float u = bl_s[h * nbl + b0];
             for (int j = b0 + 1; j < b1; ++j) u = u + bl_s[h * nbl + j];
-            st_dev(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 / sb + k, u);
+            st_dev(a.bsum + hbase + (size_t)h * a.blk_stride + (blk0 >> lsb) + k, u);
         }
         stores_done();
         __syncthreads();
@@ -308,8 +308,9 @@ v = xor_sum<32>(v);
         __syncthreads();
         const int t = lane / CPL, c = lane % CPL;
         float sacc[MAXG][8];  // the super-block's blocks so far, left to right
-        for (int it = wave * sb; it < nbl; it += (it % sb == sb - 1 ? (NW - 1) * sb + 1 : 1)) {
+        for (int it = wave * sb; it < nbl; it += ((it & (sb - 1)) == sb - 1 ? (NW - 1) * sb + 1 : 1)) {
             const int bl = it;
+            const int bi = bl & (sb - 1);
             const int jb = (blk0 + bl) * kBlockKeys;
             uint4 vr[kBlockKeys / S];
 #pragma unroll
@@ -344,13 +345,13 @@ v = xor_sum<32>(v);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const float v = xor_sum<32, CPL>(acc[h][e]);
-                        sacc[h][e] = bl % sb == 0 ? v : sacc[h][e] + v;
+                        sacc[h][e] = bi == 0 ? v : sacc[h][e] + v;
                     }
-            if (t == 0 && (bl % sb == sb - 1 || bl == nbl - 1)) {
+            if (t == 0 && (bi == sb - 1 || bl == nbl - 1)) {
 #pragma unroll
                 for (int h = 0; h < MAXG; ++h)
                     if (h < G) {
-                        float* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + (blk0 + bl) / sb) * D + 8 * c;
+                        float* dst = a.part + ((hbase + (size_t)h * a.blk_stride) + ((blk0 + bl) >> lsb)) * D + 8 * c;
 #pragma unroll
                         for (int e = 0; e < 8; ++e) st_dev(dst + e, sacc[h][e]);
                     }

@@ -258,7 +258,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     const int pos = a.pos, L = pos + 1, cap = a.cap;
     const int nb = (L + kBlockKeys - 1) / kBlockKeys;
     // whole super-blocks per workgroup (the order spec's sums, kernels.h)
-    const int sb = attn_superblock(nb), nsb = (nb + sb - 1) / sb;
+    const int sb = attn_superblock(nb), lsb = sb == 1 ? 0 : sb == 2 ? 1 : 2, nsb = (nb + sb - 1) >> lsb;
     const int bpw = attn_bpw(nb, a.wpg);
     const int W = (nb + bpw - 1) / bpw;
     if (wi >= W) {
@@ -520,12 +520,12 @@ m = xor_max<32>(m);
         if (sb > 1) {
             // each super-block's block sums left to right
             __syncthreads();
-            const int nsbl = (nbl + sb - 1) / sb;
+            const int nsbl = (nbl + sb - 1) >> lsb;
             for (int i = tid; i < Gq * nsbl; i += NT) {
                 const int h = i / nsbl, k = i - h * nsbl, b0 = k * sb, b1 = min(nbl, b0 + sb);
                 float u = bl_s[h * nbl + b0];
                 for (int j = b0 + 1; j < b1; ++j) u = u + bl_s[h * nbl + j];
-                st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + blk0 / sb + k, u, t_bsum);
+                st_tag(a.bsum + hbase + (size_t)h * a.blk_stride + (blk0 >> lsb) + k, u, t_bsum);
             }
         }
     }
@@ -625,14 +625,15 @@ m = xor_max<32>(m);
                 // streams combined in the butterfly order (distances S/2 .. 1
                 // between streams = lane distances 32 .. LPS); every stream
                 // lane then holds the same sums and lane t stores head h when
-                // h % S == t
+                // h % S == t, once its super-block is complete
+                const int bi = bl & (sb - 1);
+                const bool first = bi == 0, full = bi == sb - 1 || bl == nbl - 1;
+                const size_t pidx = (size_t)((blk0 + bl) >> lsb) * D + d;
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     const float v = xor_sum<32, LPS>(acc[h]);
-                    sacc[h] = bl % sb == 0 ? v : sacc[h] + v;
-                    if (h % S == t && (bl % sb == sb - 1 || bl == nbl - 1))
-                        st_tag(a.part + ((hbase + (size_t)h * a.blk_stride) + (blk0 + bl) / sb) * D + d, sacc[h],
-                               t_part);
+                    sacc[h] = first ? v : sacc[h] + v;
+                    if (h % S == t && full) st_tag(a.part + (hbase + (size_t)h * a.blk_stride) * D + pidx, sacc[h], t_part);
                 }
             }
         }

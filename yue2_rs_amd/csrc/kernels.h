@@ -11,10 +11,12 @@ constexpr int kBlockKeys = 64;   // attention key block (order spec)
 // Attention super-blocks (order spec): the softmax sum and each output's PV
 // add the block results of a super-block of consecutive 64-key blocks left to
 // right, then the super-blocks left to right.  The size depends on the block
-// count alone (never on the hardware): 1 below 128 blocks, 2 below 256,
-// else 4.  A workgroup sums its own super-blocks, so a long context publishes
-// one partial per super-block instead of one per block.
-__host__ __device__ constexpr int attn_superblock(int nb) { return nb < 128 ? 1 : nb < 256 ? 2 : 4; }
+// count alone (never on the hardware): 1 below 256 blocks (16384 keys), else
+// 2.  A workgroup sums its own super-blocks, so a long context publishes one
+// partial per super-block instead of one per block.  (Super-blocks of 4 at
+// 256 blocks and more measured slower: whole super-blocks per workgroup then
+// give some workgroups more blocks.)
+__host__ __device__ constexpr int attn_superblock(int nb) { return nb < 256 ? 1 : 2; }
 // Blocks per workgroup when nb blocks are split over wpg workgroups in whole
 // super-blocks (the last workgroup with work may hold fewer).
 __host__ __device__ constexpr int attn_bpw(int nb, int wpg) {

@@ -9,6 +9,7 @@
 // token (src/metal.m:869-871).  The arithmetic is the same kernels and order
 // spec as the session API.
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 #include <unistd.h>
 
 #include <cmath>
@@ -19,6 +20,7 @@
 
 #include "../../include/yue2_hip.h"
 #include "kernels.h"
+#include "prefill.h"
 #include "runtime.h"
 #include "y2_math.h"
 
@@ -45,6 +47,10 @@ struct TwinState {
     hipStream_t stream = nullptr;
     std::map<WeightKey, uint16_t*> weights;
     size_t weight_bytes = 0;
+    // the prefill bridge's weights as f32 rows (src/metal.m:184-214), keyed
+    // as above with the rounding flag in the dtype's sign
+    std::map<WeightKey, float*> weights_f32;
+    rocblas_handle blas = nullptr;
     std::map<std::pair<size_t, size_t>, Context> contexts;
     // scratch
     void* scratch = nullptr;
@@ -91,6 +97,8 @@ void drop_weights() {
     TwinState& t = twin();
     for (auto& kv : t.weights) (void)hipFree(kv.second);
     t.weights.clear();
+    for (auto& kv : t.weights_f32) (void)hipFree(kv.second);
+    t.weights_f32.clear();
     t.weight_bytes = 0;
 }
 
@@ -453,4 +461,196 @@ extern "C" void yue2_hip_release_model(void) {
     if (t.scratch) (void)hipFree(t.scratch);
     t.scratch = nullptr;
     t.scratch_bytes = 0;
+}
+
+// ---- the prefill / NAR bridge: yue2_metal_gemm, linear, attention -----------
+//
+// The reference's GPU prefill hands plain FP32 matrix products (MPS,
+// src/metal.m:164-237) and the multi-row attention (src/metal.m:330-361) to
+// its bridge; the Rust caller rounds the results where its CPU path would
+// (Linear::finish).  Here the products go to the platform BLAS (a plain
+// library GEMM, column-major rocBLAS SGEMM on row-major operands by computing
+// C^T = op(B)^T A^T), the attention to the matrix-core flash kernel of the
+// matrix-core prefill.  As on the reference's GPU, the summation order is not
+// the CPU path's, so results agree with it within FP32 rounding (the GEMMs)
+// or the prefill's tolerance (the attention).  1 = done, 0 = fall back.
+
+namespace {
+
+rocblas_handle blas() {
+    TwinState& t = twin();
+    if (!t.blas) {
+        if (rocblas_create_handle(&t.blas) != rocblas_status_success) {
+            t.blas = nullptr;
+            return nullptr;
+        }
+        if (rocblas_set_stream(t.blas, t.stream) != rocblas_status_success) return nullptr;
+    }
+    return t.blas;
+}
+
+bool fits_int(size_t v) { return v <= 0x7fffffffu; }
+
+// C [m x n] (row stride ldc) = A [m x k] (lda) op(B) + beta C, row-major
+// device operands; op(B) = B [k x n] (ldb) or, tb, B^T with B [n x k] (ldb).
+bool sgemm_rows(const float* A, const float* B, float* C, size_t m, size_t n, size_t k, bool tb, size_t lda,
+                size_t ldb, size_t ldc, float beta) {
+    rocblas_handle h = blas();
+    if (!h) return false;
+    const float one = 1.0f;
+    return rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none, rocblas_operation_none,
+                         (rocblas_int)n, (rocblas_int)m, (rocblas_int)k, &one, B, (rocblas_int)ldb, A,
+                         (rocblas_int)lda, &beta, C, (rocblas_int)ldc) == rocblas_status_success;
+}
+
+// Device f32 rows of a host weight, as convert_weight reads it
+// (src/attention.metal:161-176): BF16 exactly, F32 and F16 as they are or
+// rounded to BF16 when the Linear rounds.
+float* device_weight_f32(const uint8_t* raw, size_t mapping, int dtype, int rounded, size_t n, size_t k) {
+    TwinState& t = twin();
+    const WeightKey key{mapping, raw, n, k, rounded ? -1 - dtype : dtype};
+    auto it = t.weights_f32.find(key);
+    if (it != t.weights_f32.end()) return it->second;
+    if (!raw || dtype < 0 || dtype > 2) return nullptr;
+    std::vector<float> host(n * k);
+    for (size_t i = 0; i < n * k; ++i) {
+        float v;
+        if (dtype == 0) {
+            uint16_t b;
+            std::memcpy(&b, raw + 2 * i, 2);
+            v = u2f((uint32_t)b << 16);
+        } else if (dtype == 1) {
+            std::memcpy(&v, raw + 4 * i, 4);
+        } else {
+            uint16_t b;
+            std::memcpy(&b, raw + 2 * i, 2);
+            v = (float)__builtin_bit_cast(_Float16, b);
+        }
+        host[i] = rounded && dtype != 0 ? rb(v) : v;
+    }
+    float* dev = nullptr;
+    if (hipMalloc(&dev, host.size() * sizeof(float)) != hipSuccess) return nullptr;
+    if (hipMemcpy(dev, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(dev);
+        return nullptr;
+    }
+    t.weights_f32[key] = dev;
+    t.weight_bytes += host.size() * sizeof(float);
+    return dev;
+}
+
+}  // namespace
+
+// yue2_metal_gemm (src/tensor.rs:207-219; src/metal.m:164-182): C = A op(B) +
+// beta C for row-major host matrices with row strides lda, ldb, ldc.
+extern "C" int32_t yue2_hip_gemm(const float* a, const float* b, float* c, size_t m, size_t n, size_t k,
+                                 int32_t transpose_b, size_t lda, size_t ldb, size_t ldc, float beta) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!a || !b || !c || m == 0 || n == 0 || k == 0 || lda < k || ldc < n || ldb < (transpose_b ? k : n) ||
+        !fits_int(m) || !fits_int(n) || !fits_int(k) || !twin_ready())
+        return 0;
+    const size_t brows = transpose_b ? n : k, bcols = transpose_b ? k : n;
+    float* d = static_cast<float*>(scratch(sizeof(float) * (m * k + brows * bcols + m * n)));
+    if (!d) return 0;
+    float *da = d, *db = da + m * k, *dc = db + brows * bcols;
+    TwinState& t = twin();
+    hipError_t e = hipMemcpy2DAsync(da, k * 4, a, lda * 4, k * 4, m, hipMemcpyHostToDevice, t.stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(db, bcols * 4, b, ldb * 4, bcols * 4, brows, hipMemcpyHostToDevice, t.stream);
+    if (e == hipSuccess && beta != 0.0f)
+        e = hipMemcpy2DAsync(dc, n * 4, c, ldc * 4, n * 4, m, hipMemcpyHostToDevice, t.stream);
+    bool ok = e == hipSuccess && sgemm_rows(da, db, dc, m, n, k, transpose_b != 0, k, bcols, n, beta);
+    if (ok) ok = hipMemcpy2DAsync(c, ldc * 4, dc, n * 4, n * 4, m, hipMemcpyDeviceToHost, t.stream) == hipSuccess;
+    return hipStreamSynchronize(t.stream) == hipSuccess && ok ? 1 : 0;
+}
+
+// yue2_metal_linear (src/tensor.rs:135-145; src/metal.m:216-237): c [m x n] =
+// a [m x k] W^T for the host weight W [n x k] (dtype 0 BF16, 1 F32, 2 F16;
+// rounded: F32/F16 rounded to BF16 first), the weight cached on the device
+// under (mapping, raw, n, k, dtype, rounded).  Not rounded: the caller's
+// Linear::finish rounds.
+extern "C" int32_t yue2_hip_linear(const float* a, const uint8_t* raw, size_t mapping, int32_t dtype,
+                                   int32_t rounded, float* c, size_t m, size_t n, size_t k) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!a || !raw || !c || m == 0 || n == 0 || k == 0 || !fits_int(m) || !fits_int(n) || !fits_int(k) ||
+        !twin_ready())
+        return 0;
+    const float* w = device_weight_f32(raw, mapping, dtype, rounded, n, k);
+    if (!w) return 0;
+    float* d = static_cast<float*>(scratch(sizeof(float) * (m * k + m * n)));
+    if (!d) return 0;
+    float *da = d, *dc = d + m * k;
+    TwinState& t = twin();
+    bool ok = hipMemcpyAsync(da, a, m * k * 4, hipMemcpyHostToDevice, t.stream) == hipSuccess &&
+              sgemm_rows(da, w, dc, m, n, k, true, k, k, n, 0.0f) &&
+              hipMemcpyAsync(c, dc, m * n * 4, hipMemcpyDeviceToHost, t.stream) == hipSuccess;
+    return hipStreamSynchronize(t.stream) == hipSuccess && ok ? 1 : 0;
+}
+
+// yue2_metal_attention (src/tensor.rs:194-206; src/metal.m:330-361): rows
+// query rows q [rows x heads*dim] over keys rows of k, v [keys x kv*dim];
+// row r sees keys [0, min(keys, causal + r + 1)) (causal >= 0) or all of them
+// (causal < 0); softmax with `scale`; out [rows x heads*dim], BF16-rounded
+// (unpack_attention, src/attention.metal:55-64).  Runs the matrix-core flash
+// kernel, whose operands are BF16: inputs that are not BF16-exact (the
+// model's always are), other head sizes than 64 and 128, a scale other than
+// 1/sqrt(dim) and causal windows that reach past `keys` fall back (0).
+extern "C" int32_t yue2_hip_attention(const float* q, const float* k, const float* v, float* out, size_t rows,
+                                      size_t keys, size_t heads, size_t kv, size_t dim, int64_t causal,
+                                      float scale) {
+    std::lock_guard<std::recursive_mutex> guard(library_lock());
+    if (!q || !k || !v || !out || rows == 0 || keys == 0 || kv == 0 || heads % kv || (dim != 64 && dim != 128) ||
+        scale != 1.0f / sqrtf((float)dim) || !fits_int(rows) || !fits_int(keys) || !twin_ready())
+        return 0;
+    const bool noncausal = causal < 0;
+    if (!noncausal && (size_t)causal + rows > keys) return 0;
+    if (noncausal && rows > keys) return 0;
+    const size_t qn = rows * heads * dim, kn = keys * kv * dim;
+    auto exact = [](const float* x, size_t n) {
+        for (size_t i = 0; i < n; ++i)
+            if (f2u(x[i]) & 0xffffu) return false;
+        return true;
+    };
+    if (!exact(q, qn) || !exact(k, kn) || !exact(v, kn)) return 0;
+    // q as [rows][heads][dim] BF16; K and V as one layer of the cache layout
+    // [K, V][kv][keys][dim]; the output [rows][heads * dim] BF16
+    std::vector<uint16_t> hq(qn), hkv(2 * kn);
+    for (size_t i = 0; i < qn; ++i) hq[i] = (uint16_t)(f2u(q[i]) >> 16);
+    for (size_t r = 0; r < keys; ++r)
+        for (size_t h = 0; h < kv; ++h)
+            for (size_t d = 0; d < dim; ++d) {
+                const size_t src = (r * kv + h) * dim + d;
+                hkv[(h * keys + r) * dim + d] = (uint16_t)(f2u(k[src]) >> 16);
+                hkv[((kv + h) * keys + r) * dim + d] = (uint16_t)(f2u(v[src]) >> 16);
+            }
+    uint16_t* d = static_cast<uint16_t*>(scratch(sizeof(uint16_t) * (2 * qn + 2 * kn)));
+    if (!d) return 0;
+    uint16_t *dq = d, *dkv = dq + qn, *dout = dkv + 2 * kn;
+    TwinState& t = twin();
+    bool ok = hipMemcpyAsync(dq, hq.data(), qn * 2, hipMemcpyHostToDevice, t.stream) == hipSuccess &&
+              hipMemcpyAsync(dkv, hkv.data(), 2 * kn * 2, hipMemcpyHostToDevice, t.stream) == hipSuccess;
+    FlashArgs f{};
+    f.q = dq;
+    f.kv_base = dkv;
+    f.cap = (int)keys;
+    f.layer = 0;
+    f.heads = (int)heads;
+    f.kv_heads = (int)kv;
+    f.rows = (int)rows;
+    f.scale = scale;
+    f.out = dout;
+    if (noncausal) {
+        // every row sees keys [0, split + rows), all from the one buffer
+        f.noncausal = 1;
+        f.split = (int)(keys - rows);
+        f.p0 = (int)(keys - rows);
+    } else {
+        f.p0 = (int)causal;
+    }
+    if (ok) ok = launch_flash(t.stream, f, (int)dim) == hipSuccess;
+    std::vector<uint16_t> ho(qn);
+    if (ok) ok = hipMemcpyAsync(ho.data(), dout, qn * 2, hipMemcpyDeviceToHost, t.stream) == hipSuccess;
+    if (hipStreamSynchronize(t.stream) != hipSuccess || !ok) return 0;
+    for (size_t i = 0; i < qn; ++i) out[i] = u2f((uint32_t)ho[i] << 16);
+    return 1;
 }

@@ -63,8 +63,11 @@
  *   y2o_rotary_*     position 0 is the identity; the table is rb(cos/sin) of
  *                    p * theta^(-2i/d) within one BF16 step of f64 libm.
  *   y2o_attention_row the reference's own known-answer generator and
- *                    tolerance (src/tensor.rs:9-83) against f64; one key gives
- *                    rb(V0); equal keys give rb(mean V) exactly.
+ *                    tolerance (src/tensor.rs:9-83) against f64, from 4096 to
+ *                    24576 keys (super-blocks of 1 and 2); one key gives
+ *                    rb(V0); equal keys give rb(mean V) exactly, also over
+ *                    16384 keys (a super-block dropped, doubled or cut at the
+ *                    wrong block changes it).
  *   y2o_cfg_mix      scale 1 / 0 give the conditional / unconditional row.
  *   y2o_mt_*         std::mt19937 known answer (10000th draw of seed 5489),
  *                    2000 draws equal numpy's RandomState for five seeds,
@@ -74,10 +77,17 @@
  *                    top-p keeps the crossing token and 1 (legacy 3) protected
  *                    ids; top-k keeps ties; penalty sign, powi and window;
  *                    NaN/+inf rejected; ABC/semantic masks and min_tokens.
- *   y2o_forward/generate  tests/golden/ fixtures (prefill logits digest, 64
- *                    greedy ids, 32 sampled CFG ids) written by
- *                    tests/golden/make_golden.py; chunked prefill equals the
- *                    token-by-token step (the GPU tests run both).
+ *   y2o_forward     an independent float64 numpy forward of the reference's
+ *                    formulas within 1e-3 of the largest logit (measured 0);
+ *                    each single-rounding mutant of that model (SiLU, g*u,
+ *                    attention output, O projection, inner RoPE products)
+ *                    exceeds the bound; W_o = W_down = 0 in closed form;
+ *                    chunked prefill equals the token-by-token step.
+ *   y2o_generate    equal to a Python restatement of the loop over the
+ *                    separately pinned prefill / forward_phase, cfg_mix,
+ *                    choose and MT19937 (end stop after min_tokens, unequal
+ *                    negative prefix, legacy, truncation); tests/golden/
+ *                    fixtures written by tests/golden/make_golden.py.
  *   y2o_velocity    linear biases, the timestep embedding and the position
  *                    rows from closed forms on a model whose NAR linears and
  *                    layers are zero (tests/test_oracle_nar.py); with
@@ -86,11 +96,15 @@
  *                    set -- permuting the frames permutes the outputs when
  *                    no position-dependent term enters (RoPE start, latent
  *                    position rows equal); parity unpinned beyond these.
- *   y2o_normal      pairs (i, i + 8) of a block share the radius: x^2 + y^2
- *                    = -2 ln(1 - u) of the MT19937 draw; moments of N(0, 1).
- *   y2o_synthesize  steps and chunking from the loop's invariants: with zero
- *                    velocity (zero llm2vae and bias) the output is the
- *                    rounded noise; chunks of (capacity - prefix - 3) / 2.
+ *   y2o_normal      every value within 3 ulps of a float64 Box-Muller of the
+ *                    same MT19937 uniform_f32 draws (measured 2.08); pairs
+ *                    share the radius; moments of N(0, 1).
+ *   y2o_synthesize  a model whose velocity has a closed form in the state
+ *                    and the time (zero NAR layers, one-hot linears): the
+ *                    chunk cuts, t schedule, midpoint state and both steps
+ *                    restated in the test give the same bits (a wrong dt,
+ *                    midpoint or second time fails); with zero velocity the
+ *                    output is the rounded noise.
  *   y2o_conv        the reference's own convolution known-answer cases and
  *                    scalar formula (src/vae.rs:812-892, tolerance 2e-6);
  *                    within 1e-5 of a float64 convolution on shapes with

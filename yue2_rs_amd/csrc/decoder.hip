@@ -89,6 +89,14 @@ static KvView kv_view(const Yue2Decoder* d) {
     return kv;
 }
 
+// The most keys a row attends in the decoder's next launch (its schedule,
+// not its arithmetic, depends on it).
+static int keys_now(const Yue2Decoder* d) {
+    int n = 0;
+    for (int b = 0; b < d->rows; ++b) n = std::max(n, d->caches[b]->length + 1);
+    return n;
+}
+
 static void decoder_release(Yue2Decoder* d) {
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
@@ -262,7 +270,7 @@ static int capture(Yue2Decoder* d) {
     if (e != hipSuccess) return hip_fail(e, "hipStreamBeginCapture");
     int rc = YUE2_OK;
     if (d->fused) {
-        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, 1);
+        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, 1, keys_now(d));
         if (rc == 1) rc = fail(YUE2_ERR_DEVICE, "fused step kernel unavailable");
     } else {
         if (d->need_rng) {
@@ -271,7 +279,7 @@ static int capture(Yue2Decoder* d) {
             launch_mt_generate(d->side, d->mt, d->streams, d->streams + draws, draws, d->w.st, 1);
             (void)hipEventRecord(d->join, d->side);
         }
-        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s);
+        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, 0, keys_now(d));
         if (rc == 1) rc = enqueue_step(m, d->w, kv_view(d), d->rows, true, d->phase, s);
         if (d->need_rng) (void)hipStreamWaitEvent(s, d->join, 0);
         launch_choose(s, d->sa);
@@ -435,10 +443,11 @@ static int time_step_kernel(Yue2Decoder* d, int32_t iters, float* avg_ms, double
         (void)hipEventDestroy(b0);
         return fail(YUE2_ERR_DEVICE, "hipEventCreate");
     }
-    int rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, sample);  // untimed
+    int rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, sample,
+                                keys_now(d));  // untimed
     if (rc == YUE2_OK) (void)hipEventRecord(b0, s);
     for (int i = 0; i < iters && rc == YUE2_OK; ++i)
-        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, sample);
+        rc = enqueue_step_fused(m, d->w, kv_view(d), d->rows, true, d->phase, s, nullptr, 0, sample, keys_now(d));
     if (rc == YUE2_OK) {
         (void)hipEventRecord(b1, s);
         hipError_t e = hipEventSynchronize(b1);

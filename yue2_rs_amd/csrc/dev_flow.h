@@ -231,8 +231,12 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 // G = heads / kv_heads, the query heads of a group (the host checks that the
 // launch's shape has this G).  lds: attn_flow_lds(G, D, bpw) bytes.  false:
 // timeout (error set).
-template <int NT, int D, int G, class Mark>
-__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark) {
+// pre(): called once the workgroup's q/k/v are gathered (or at once when it
+// has no keys): the caller's early requests for the phase after the
+// attention (the O projection's first weight items at long contexts).
+template <int NT, int D, int G, class Mark, class Pre>
+__device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark,
+                                          Pre&& pre) {
     constexpr int NW = NT / 64;
     constexpr int S = 512 / D;     // PV key streams per 64-key block
     constexpr int MAXNB = 24576 / kBlockKeys;
@@ -262,6 +266,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     const int bpw = attn_bpw(nb, a.wpg);
     const int W = (nb + bpw - 1) / bpw;
     if (wi >= W) {
+        pre();
         for (int i = 0; i < 6; ++i) mark();  // keep the trace slots aligned
         return true;
     }
@@ -352,6 +357,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             return false;
     }
     mark();
+    pre();
     // Norm::heads (src/tensor.rs:1160): the scale of the sequential sum of
     // squares per head, decided by a whole wave per head (wave Gq: the new key)
     static_assert(G + 1 <= NW, "one wave per head norm");

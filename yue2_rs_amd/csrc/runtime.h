@@ -140,7 +140,7 @@ int enqueue_head(Yue2Model* m, Workspace& w, const float* x, int phase, hipStrea
 // prepared with a sampler for a nonzero mode.
 int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
                        hipStream_t s, unsigned long long* trace = nullptr, int trace_slots = 0,
-                       int sample = 0);
+                       int sample = 0, int context = 0);
 // Upload the workspace's step kernel arguments (synchronous; call after
 // Workspace::ensure and before capturing a graph), with the fused sampler
 // when smp is set.  1 when the shape (or the launch with a sampler) has no

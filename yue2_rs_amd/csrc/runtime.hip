@@ -302,7 +302,7 @@ int prepare_step(Yue2Model* m, Workspace& w, const FusedSampler* smp) {
 }
 
 int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool head, int phase,
-                       hipStream_t s, unsigned long long* trace, int trace_slots, int sample) {
+                       hipStream_t s, unsigned long long* trace, int trace_slots, int sample, int context) {
     if (!trace && !m->step_kernel) return 1;
     if (!w.step_args_ready || (sample != 0) != (w.step_sample != 0)) return 1;  // not prepared for this call
     if (rows != w.rows || !step_supported(m->c, rows, m->cus - (sample ? 1 : 0))) return 1;
@@ -311,6 +311,7 @@ int enqueue_step_fused(Yue2Model* m, Workspace& w, const KvView& kv, int rows, b
     call.head = head ? 1 : 0;
     head_rows(phase, m->c.vocab_size, &call.head_lo, &call.head_n, &call.head_stop);
     call.sample = sample;
+    call.context = context;
     call.trace = trace;
     call.trace_slots = trace ? trace_slots : 0;
     hipError_t e = launch_step(s, static_cast<const StepArgs*>(w.step_args),
@@ -738,7 +739,7 @@ extern "C" int32_t yue2_hip_forward(Yue2Model* m, Yue2Cache* c, const int32_t* i
     for (int t = 0; t < n; ++t) {
         launch_set_state(s, m->ws.st, 1, c->length + t, 0, ids[t], 0);
         const bool head = logits && t == n - 1;
-        int rc = enqueue_step_fused(m, m->ws, kv, 1, head, phase, s);
+        int rc = enqueue_step_fused(m, m->ws, kv, 1, head, phase, s, nullptr, 0, 0, c->length + t + 1);
         if (rc == 1) rc = enqueue_step(m, m->ws, kv, 1, head, phase, s);
         if (rc) return rc;
     }

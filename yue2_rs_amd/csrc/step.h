@@ -52,6 +52,8 @@ struct StepArgs {
 };
 
 // Per-launch arguments.
+constexpr int kOEarlyKeys = 4096;
+
 struct StepCall {
     KvView kv;
     // 1: final norm + LM head into logits: rows [head_lo, head_lo + head_n)
@@ -65,6 +67,10 @@ struct StepCall {
     // without publishing anything (timing).  With a sampler the last
     // workgroup is the sampler and the others share the layers.
     int sample;
+    // the most keys a row of the launch attends (0: unknown); from
+    // kOEarlyKeys on, the kernel requests the O projection's first weights
+    // during the attention (same arithmetic, another schedule)
+    int context;
     int trace_slots;
     unsigned long long* trace;  // optional wall-clock stamps, kTraceSlotsPerLayer per layer + 1
 };

@@ -516,8 +516,11 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
 
 // G: query heads per KV head; MASKI: the intermediate size is short of
 // 512 * ITI (the down projection's rows are masked); TRACE: the traced
-// instantiation.
-template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE>
+// instantiation; OE: the O projection's first weight items are requested
+// during the attention, right after its q/k/v gather, instead of after it
+// (long contexts: the attention is long enough that they land before its
+// later gathers, which at short contexts they delay).
+template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE, bool OE>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
     // 16-byte aligned whatever the static LDS before it: staged inputs and K/V
     // chunks are read with 16-byte LDS reads, which are split and slow when
@@ -617,11 +620,18 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int groups = a->kv_heads * B, wpg = nwg / groups;
             const int group = wg / wpg, kvh = a->kv_heads;
+            const int H = a->hidden, qw = a->heads * D;
+            const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
+            auto pre_o = [&] {
+                if constexpr (OE) prefetch_ring<ITQ, false>(layer_at(fresh(args), l)->wo, nullptr, qw, h0, h1, H, ring);
+            };
             if (group < groups) {
                 const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
-                if (!attn_flow<kStepThreads, D, G>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); }))
+                if (!attn_flow<kStepThreads, D, G>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); },
+                                                   pre_o))
                     return;
             } else {
+                pre_o();
                 for (int i = 0; i < 6; ++i) tr.mark();  // a workgroup past the groups: no attention
             }
             tr.mark();
@@ -631,7 +641,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qw = a->heads * D;
             const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
-            prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
+            if constexpr (!OE) prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_att<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
@@ -702,9 +712,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
 template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
 static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCall& call, int nwg, size_t lds) {
     if (call.trace)
-        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, true, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
+    else if (call.context >= kOEarlyKeys)
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
     else
-        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
     return hipGetLastError();
 }
 
@@ -757,12 +769,16 @@ size_t step_lds_bytes(const StepArgs& a, int nwg) {
 
 template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
 static int resident_t(size_t lds) {
-    int n = 0;
+    // every instantiation a launch may pick must fit one workgroup per CU
+    int n = 0, n2 = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false>), kStepThreads,
-            lds) != hipSuccess)
+            &n, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, false>),
+            kStepThreads, lds) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n2, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, true>),
+            kStepThreads, lds) != hipSuccess)
         return 0;
-    return n;
+    return std::min(n, n2);
 }
 
 size_t step_launch_lds(const StepArgs& a, int nwg, int sample) {

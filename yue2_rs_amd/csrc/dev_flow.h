@@ -356,6 +356,12 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                 st))
             return false;
     }
+    // The RoPE / QK-norm constants, requested before the gather, are read
+    // here on every path (the RoPE below reads them on some), so their loads
+    // are known to be complete. Without this the compiler waits for every
+    // vector load in flight (the next K chunk's) wherever it reuses their
+    // registers, in the scores' inner loop among other places.
+    asm volatile("" ::"v"(c_cos), "v"(c_sin), "v"(c_g0), "v"(c_g1));
     mark();
     pre();
     // Norm::heads (src/tensor.rs:1160): the scale of the sequential sum of
@@ -444,12 +450,15 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             for (int qd0 = wave * GPW; qd0 * 4 < keys; qd0 += NW * GPW) {
                 const int kq = 4 * (qd0 + grp);  // the group's first key within the chunk
                 float v[4][G];
+                // the four keys' rows read together (rows past the chunk's
+                // keys are read clamped and never stored)
+                uint4 k4[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) k4[r] = Ks[(size_t)min(kq + r, kAttnChunk * kBlockKeys - 1) * (D / 8) + c];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    // (rows past the chunk's keys are read clamped and never stored)
-                    const int kl = min(kq + r, kAttnChunk * kBlockKeys - 1);
                     float kf[8];
-                    unpack8a(Ks[(size_t)kl * (D / 8) + c], kf);
+                    unpack8a(k4[r], kf);
 #pragma unroll
                     for (int h = 0; h < G; ++h) {
                         float acc = 0.0f;

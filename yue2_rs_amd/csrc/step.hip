@@ -165,15 +165,35 @@ __device__ __forceinline__ void load_gamma(const float* g, int k, float* gam) {
 template <int B, int N>
 __device__ __forceinline__ void norm_rows(float* xs, int k, const float* gam, float eps, int* fallbacks,
                                           double* e_sum, double* w_sum) {
+    // a thread's elements tid + 512 j, all read at once (past k: element
+    // k - 1, never written back), so their LDS reads are in flight together;
+    // read inside the stores' bounds test, each one was waited for before the
+    // next was issued
+    float v[B][N];
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[b][j] = xs[b * k + min((int)threadIdx.x + j * kStepThreads, k - 1)];
+    if constexpr (!kPack<B>) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) e_sum[b] = w_sum[b] = 0.0;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int i = threadIdx.x + j * kStepThreads;
+            if (i < k)
+#pragma unroll
+                for (int b = 0; b < B; ++b) norm_partial_add(e_sum[b], w_sum[b], v[b][j], i, k);
+        }
+    }
     float s[B];
-    if constexpr (!kPack<B>) norm_partials<kStepThreads, B>(xs, k, e_sum, w_sum);
     norm_scales_from<kStepThreads, B>(e_sum, w_sum, xs, k, eps, fallbacks, s);
 #pragma unroll
     for (int b = 0; b < B; ++b)
 #pragma unroll
         for (int j = 0; j < N; ++j) {
             const int i = threadIdx.x + j * kStepThreads;
-            if (i < k) xs[b * k + i] = rb(rb(xs[b * k + i] * s[b]) * gam[j]);
+            const float y = rb(rb(v[b][j] * s[b]) * gam[j]);
+            if (i < k) xs[b * k + i] = y;
         }
     __syncthreads();
 }

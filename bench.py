@@ -30,6 +30,11 @@ phase of Pipeline::generate_semantic: the LM head reads the 32768 codec rows
 and MUSIC_END (project_phase, src/model.rs:478-507); min_tokens keeps the
 end token out until the timed steps are done.
 
+--workload any: the same loop on a shape with no step kernel of its own, a
+1B-class one (hidden 2048, 16 layers, 32 q / 8 KV heads, head_dim 64, SwiGLU
+8192, vocab 128256): the generic head_dim-64 step kernel (--step-kernel 0:
+the per-phase kernels).
+
 Prints one JSON line.  Progress goes to stderr.
 """
 from __future__ import annotations
@@ -228,9 +233,10 @@ def main() -> int:
                     help="1 (default): one persistent kernel per token; 0: one kernel per phase")
     ap.add_argument("--prefill", default="mfma", choices=["mfma", "exact"],
                     help="mfma (default): matrix-core prefill; exact: decode-order (bit-exact) prefill")
-    ap.add_argument("--workload", default="decode", choices=["decode", "long", "yue2"],
+    ap.add_argument("--workload", default="decode", choices=["decode", "long", "yue2", "any"],
                     help="decode (default): 2048-token prompts; long: 24000-token prompts decoded to 24576; "
-                         "yue2: the YuE2 shape in the semantic phase")
+                         "yue2: the YuE2 shape in the semantic phase; any: a 1B-class shape on the generic "
+                         "step kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path (--gpus must be 1)",
@@ -245,7 +251,13 @@ def main() -> int:
         print("no gfx950 device available", file=sys.stderr)
         return 1
     if args.workload == "yue2":
-        return yue2_shape(args, y2, synthetic)
+        return shape_workload(args, y2, synthetic, synthetic.YUE2, y2.PHASE_SEMANTIC, 32768 + 1,
+                              "YuE2-shape AR decode loop, semantic phase",
+                              "YuE2 shape: 28 layers + semantic-phase LM head + sampler")
+    if args.workload == "any":
+        return shape_workload(args, y2, synthetic, synthetic.CLASS_1B_ANY, y2.PHASE_NONE, None,
+                              "1B-class AR decode loop (no shape-specific step kernel)",
+                              "1B-class shape: 16 layers + LM head + sampler, the generic head_dim-64 kernel")
     c = synthetic.CLASS_3B
     log("generating synthetic 3B-class weights")
     t = time.perf_counter()
@@ -352,18 +364,16 @@ def main() -> int:
     return 0
 
 
-def yue2_shape(args, y2, synthetic):
-    """The decode loop on the YuE2 shape in the semantic phase: CFG batch 2
-    and batch 1 after 2048-token prompts (matrix-core prefill), the step
-    kernel timed alone one position past the prompts."""
-    c = synthetic.YUE2
-    log("generating synthetic YuE2-shape weights")
+def shape_workload(args, y2, synthetic, c, phase, head_rows, name, kernel_desc):
+    """The decode loop on another shape (c) in a phase of the LM head
+    (head_rows: the rows that phase reads, None for all): CFG batch 2 and
+    batch 1 after 2048-token prompts (matrix-core prefill), the step kernel
+    timed alone one position past the prompts."""
+    log(f"generating synthetic weights: {name}")
     ckpt = synthetic.checkpoint(c, seed=0, threads=16)
     model = y2.Model.open(ckpt)
     step_kernel = model.set_step_kernel(bool(args.step_kernel))
     W, K, P = args.warmup, args.steps, args.prompt
-    phase = y2.PHASE_SEMANTIC
-    head_rows = 32768 + 1  # the codec rows and MUSIC_END
     cond_ids = synthetic.prompt(P, c.vocab_size, seed=0)
     neg_ids = synthetic.prompt(P, c.vocab_size, seed=1)
     cap = P + W + K + 1
@@ -386,10 +396,7 @@ def yue2_shape(args, y2, synthetic):
     d0 = y2.Decoder(model, c_pos, c_neg, sampling=sampling, seed=0, scale=args.scale, phase=phase)
     d0.run(1, first_logits=np.concatenate([l_pos, l_neg]))
     context = c_pos.length
-    if not step_kernel:
-        print("--workload yue2 times the step kernel: run it with --step-kernel 1", file=sys.stderr)
-        return 2
-    dom_ms, dom_b = d0.time_kernel("step", args.kernel_iters)
+    dom_ms, dom_b = d0.time_kernel("step", args.kernel_iters) if step_kernel else (None, None)
     l_pos, l_neg = [row.copy() for row in d0.logits()]
     d0.close()
     log(f"batch 1: {W} warmup + {K} timed steps")
@@ -400,12 +407,13 @@ def yue2_shape(args, y2, synthetic):
                       phase, head_rows)
     d2.close()
     log(f"CFG batch 2: {cfg['tokens_per_s']:.1f} steps/s, p50 {cfg['p50_ms']:.3f} ms")
-    achieved = dom_b / (dom_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(achieved / 8000.0, 4), "traffic": None,
-                "kernel": "step_kernel (whole CFG batch-2 token of the YuE2 shape: 28 layers + semantic-phase "
-                          "LM head + sampler)",
-                "launch_ms": round(dom_ms, 5), "bytes_per_launch": int(dom_b), "context": context}
+    roofline = None
+    if step_kernel:
+        achieved = dom_b / (dom_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+                    "frac": round(achieved / 8000.0, 4), "traffic": None,
+                    "kernel": f"step_kernel (whole CFG batch-2 token of the {kernel_desc})",
+                    "launch_ms": round(dom_ms, 5), "bytes_per_launch": int(dom_b), "context": context}
     out = {
         "metric": METRIC,
         "value": round(cfg["tokens_per_s"], 2),
@@ -419,13 +427,13 @@ def yue2_shape(args, y2, synthetic):
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "YuE2-shape AR decode loop, semantic phase, CFG batch 2 (guidance 1.5), T 0.9 / "
+        "config": {"workload": f"{name}, CFG batch 2 (guidance 1.5), T 0.9 / "
                                f"top-k 50 / top-p 0.93 / penalty 1.2, {P}-token prompts, {K} steps",
                    "layers": c.num_hidden_layers, "hidden": c.hidden_size, "heads": c.num_attention_heads,
                    "kv_heads": c.num_key_value_heads, "head_dim": c.head_dim,
                    "intermediate": c.intermediate_size, "vocab": c.vocab_size, "head_rows": head_rows,
                    "prompt": P, "global_batch": 2, "parallelism": "none (1 GPU)",
-                   "execution": "persistent step kernel"},
+                   "execution": "persistent step kernel" if step_kernel else "per-phase kernels"},
         "p50_ms": round(cfg["p50_ms"], 4),
         "p90_ms": round(cfg["p90_ms"], 4),
         "hbm_roofline_frac": round(cfg["hbm_roofline_frac"], 4),

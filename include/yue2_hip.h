@@ -434,8 +434,12 @@ int32_t yue2_hip_selftest_conv(int32_t transpose, int32_t cin, int32_t cout, int
  * afterwards) through the persistent token-step kernel -- one launch per
  * token, workgroups exchanging tagged words instead of meeting at barriers
  * -- or through one kernel per phase.  Both produce the same bits.  The
- * step kernel is the default for shapes that have one.  Returns 1 when
- * enabled, 0 when off or when the model's shape has no step kernel. */
+ * step kernel is the default for shapes that have one: head_dim 64 or 128,
+ * at most 4 query heads per KV head, hidden and heads * head_dim at most
+ * 3072 and intermediate at most 8192 (the 3B-class and YuE2 shapes on
+ * kernels of their own, the others on generic ones), contexts up to 24576.
+ * Returns 1 when enabled, 0 when off or when the model's shape has no step
+ * kernel. */
 int32_t yue2_hip_model_set_step_kernel(Yue2Model *m, int32_t on);
 /* Execution choice for yue2_hip_generate's prefill of the prompts (on = 1):
  * yue2_hip_prefill_mfma (BF16 MFMA GEMMs and flash attention; a 2048-token

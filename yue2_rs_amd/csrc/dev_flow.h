@@ -229,12 +229,13 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 //  - the scores keep each lane's query chunk in registers; PV runs one
 //    (block, eighth of the dims) item per wave, for all heads.
 // G = heads / kv_heads, the query heads of a group (the host checks that the
-// launch's shape has this G).  lds: attn_flow_lds(G, D, bpw) bytes.  false:
-// timeout (error set).
+// launch's shape has this G); GRT: G is only the most a group has, its
+// query heads are heads / kv_heads at run time.  lds: attn_flow_lds(G, D,
+// bpw) bytes.  false: timeout (error set).
 // pre(): called once the workgroup's q/k/v are gathered (or at once when it
 // has no keys): the caller's early requests for the phase after the
 // attention (the O projection's first weight items at long contexts).
-template <int NT, int D, int G, class Mark, class Pre>
+template <int NT, int D, int G, bool GRT, class Mark, class Pre>
 __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark,
                                           Pre&& pre) {
     constexpr int NW = NT / 64;
@@ -256,7 +257,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63, wave = tid >> 6;
-    int Gq = G;
+    int Gq = GRT ? a.heads / a.kv_heads : G;
     asm volatile("" : "+s"(Gq));
     StepState* st = a.st;
     const int pos = a.pos, L = pos + 1, cap = a.cap;
@@ -425,6 +426,11 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         float qr[G][8];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
+            if (GRT && h >= Gq) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qr[h][e] = 0.0f;  // (a head the group lacks: scores never stored)
+                continue;
+            }
             if (h >= Gq) break;
             const float4* qp = reinterpret_cast<const float4*>(q_s[h] + 8 * c);
             const float4 q0 = qp[0], q1 = qp[1];
@@ -627,7 +633,8 @@ m = xor_max<32>(m);
                     float4 p4[G];
 #pragma unroll
                     for (int h = 0; h < G; ++h)
-                        p4[h] = *reinterpret_cast<const float4*>(pp + h * estride + i0);
+                        p4[h] = !GRT || h < Gq ? *reinterpret_cast<const float4*>(pp + h * estride + i0)
+                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
 #pragma unroll
@@ -648,7 +655,8 @@ m = xor_max<32>(m);
                 for (int h = 0; h < G; ++h) {
                     const float v = xor_sum<32, LPS>(acc[h]);
                     sacc[h] = first ? v : sacc[h] + v;
-                    if (h % S == t && full) st_tag(a.part + (hbase + (size_t)h * a.blk_stride) * D + pidx, sacc[h], t_part);
+                    if ((!GRT || h < Gq) && h % S == t && full)
+                        st_tag(a.part + (hbase + (size_t)h * a.blk_stride) * D + pidx, sacc[h], t_part);
                 }
             }
         }

@@ -68,6 +68,10 @@ constexpr bool kPack = B == 2;
 template <int B>
 constexpr bool kPair = B == 1;
 constexpr int kPairRowsMax = 64;  // rows of one such GEMV per workgroup
+// The generic kernels' iterations (512 inputs each): hidden and heads *
+// head_dim up to 3072, intermediate up to 8192 (at 4096 the head_dim-128
+// kernels spill about 100 bytes per lane).
+constexpr int kStepAnyIth = 6, kStepAnyItq = 6, kStepAnyIti = 16;
 
 // First row of workgroup w's share of an exchanged GEMV output of n rows:
 // even for paired words (a pair never straddles two workgroups).
@@ -534,13 +538,16 @@ __device__ __forceinline__ FlowAttn layer_attn(ArgsPtr a, const KvView& kv, int 
     return f;
 }
 
-// G: query heads per KV head; MASKI: the intermediate size is short of
-// 512 * ITI (the down projection's rows are masked); TRACE: the traced
+// G: query heads per KV head; MASK 0: every GEMV input is exactly 512 IT
+// long, 1: the intermediate size is short of 512 * ITI (the down
+// projection's rows are masked), 2: any input may be short of its 512 IT
+// (every GEMV masked) and G is only the most query heads a KV head has (the
+// shape's own at run time); TRACE: the traced
 // instantiation; OE: the O projection's first weight items are requested
 // during the attention, right after its q/k/v gather, instead of after it
 // (long contexts: the attention is long enough that they land before its
 // later gathers, which at short contexts they delay).
-template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI, bool TRACE, bool OE>
+template <int B, int D, int G, int ITH, int ITQ, int ITI, int MASK, bool TRACE, bool OE>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args_dev, const StepCall call) {
     // 16-byte aligned whatever the static LDS before it: staged inputs and K/V
     // chunks are read with 16-byte LDS reads, which are split and slow when
@@ -550,6 +557,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     __shared__ float pk_s[kPairRowsMax];   // one row: a GEMV's outputs before they go out in pairs
     constexpr int RMAX = std::max(std::max(Ring<ITH, false>::SIZE, Ring<ITH, true>::SIZE),
                                   std::max(Ring<ITQ, false>::SIZE, Ring<ITI, false>::SIZE));
+    constexpr bool MH = MASK == 2, MQ = MASK == 2, MI = MASK >= 1;  // masked: hidden, heads * D, intermediate
     const ArgsPtr args = (ArgsPtr)args_dev;
     const int tid = threadIdx.x, wg = blockIdx.x;
     // with the fused sampler the last workgroup is the sampler and the
@@ -589,7 +597,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             }
         }
         load_gamma<ITH>(layer_at(a, 0)->in_norm, H, gam);
-        prefetch_ring<ITH, false>(layer_at(a, 0)->wqkv, nullptr, H, xlo<B>(qkvw, wg, nwg),
+        prefetch_ring<ITH, false, MH>(layer_at(a, 0)->wqkv, nullptr, H, xlo<B>(qkvw, wg, nwg),
                                   xlo<B>(qkvw, wg + 1, nwg), qkvw, ring);
         for (int b = 0; b < B; ++b) {
             const auto* e = gbl(a->embed + (size_t)ids[b] * H);
@@ -617,7 +625,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             if (l > 0) {
                 // the gammas and first weights go out before the wait
                 load_gamma<ITH>(last ? a->final_norm : layer_at(a, lc)->in_norm, H, gam);
-                prefetch_ring<ITH, false>(w, nullptr, H, r0, r1, n, ring);
+                prefetch_ring<ITH, false, MH>(w, nullptr, H, r0, r1, n, ring);
                 a = fresh(args);
                 if (!stage_x<B, ITH>(lds, a->tx, H, flow_tag(epoch, l - 1, FK_XD), st, e_sum, w_sum)) return;
             } else if constexpr (kPack<B>) {
@@ -629,7 +637,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 && !last ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_STORE, ITH, false, kPack<B>, kPair<B>>(
+            gemv_ring<B, EPI_STORE, ITH, MH, kPack<B>, kPair<B>>(
                 w, nullptr, lds, H, last ? a->logits + hr.lo : nullptr, last ? nullptr : a->tqkv,
                 flow_tag(epoch, l, FK_QKV), last ? a->vocab : n, r0, r1, n, ring, nullptr, pk_s);
             tr.mark();
@@ -643,11 +651,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             const int H = a->hidden, qw = a->heads * D;
             const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
             auto pre_o = [&] {
-                if constexpr (OE) prefetch_ring<ITQ, false>(layer_at(fresh(args), l)->wo, nullptr, qw, h0, h1, H, ring);
+                if constexpr (OE) prefetch_ring<ITQ, false, MQ>(layer_at(fresh(args), l)->wo, nullptr, qw, h0, h1, H, ring);
             };
             if (group < groups) {
                 const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
-                if (!attn_flow<kStepThreads, D, G>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); },
+                if (!attn_flow<kStepThreads, D, G, MASK == 2>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); },
                                                    pre_o))
                     return;
             } else {
@@ -661,12 +669,12 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, qw = a->heads * D;
             const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
-            if constexpr (!OE) prefetch_ring<ITQ, false>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
+            if constexpr (!OE) prefetch_ring<ITQ, false, MQ>(layer_at(a, l)->wo, nullptr, qw, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_att<B, ITQ>(lds, a->tatt, qw, flow_tag(epoch, l, FK_ATT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITQ, false, kPack<B>, kPair<B>>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx,
+            gemv_ring<B, EPI_RESID, ITQ, MQ, kPack<B>, kPair<B>>(layer_at(a, l)->wo, nullptr, lds, qw, nullptr, a->tx,
                                                                    flow_tag(epoch, l, FK_XO), H, h0, h1, H, ring, res_s, pk_s);
             tr.mark();
         }
@@ -675,7 +683,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
             load_gamma<ITH>(layer_at(a, l)->post_norm, H, gam);
-            prefetch_ring<ITH, true>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, xlo<B>(I, wg, nwg), xlo<B>(I, wg + 1, nwg), I, ring);
+            prefetch_ring<ITH, true, MH>(layer_at(a, l)->wg, layer_at(a, l)->wu, H, xlo<B>(I, wg, nwg), xlo<B>(I, wg + 1, nwg), I, ring);
             a = fresh(args);
             if (!stage_x<B, ITH>(lds, a->tx, H, flow_tag(epoch, l, FK_XO), st, e_sum, w_sum)) return;
             // this workgroup's rows of x: the residual of the down projection
@@ -684,7 +692,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             norm_rows<B, ITH>(lds, H, gam, a->eps, wg == 0 ? &st->norm_fallbacks : nullptr, e_sum, w_sum);
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_SWIGLU, ITH, false, kPack<B>, kPair<B>>(
+            gemv_ring<B, EPI_SWIGLU, ITH, MH, kPack<B>, kPair<B>>(
                 layer_at(a, l)->wg, layer_at(a, l)->wu, lds, H, nullptr, a->tact, flow_tag(epoch, l, FK_ACT), I,
                 xlo<B>(I, wg, nwg), xlo<B>(I, wg + 1, nwg), I, ring, nullptr, pk_s);
             tr.mark();
@@ -694,12 +702,12 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             ArgsPtr a = fresh(args);
             const int H = a->hidden, I = a->intermediate;
             const int h0 = xlo<B>(H, wg, nwg), h1 = xlo<B>(H, wg + 1, nwg);
-            prefetch_ring<ITI, false, MASKI>(layer_at(a, l)->wd, nullptr, I, h0, h1, H, ring);
+            prefetch_ring<ITI, false, MI>(layer_at(a, l)->wd, nullptr, I, h0, h1, H, ring);
             a = fresh(args);
             if (!stage_rows<B, ITI>(lds, a->tact, I, flow_tag(epoch, l, FK_ACT), st)) return;
             tr.mark();
             a = fresh(args);
-            gemv_ring<B, EPI_RESID, ITI, MASKI, kPack<B>, kPair<B>>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx,
+            gemv_ring<B, EPI_RESID, ITI, MI, kPack<B>, kPair<B>>(layer_at(a, l)->wd, nullptr, lds, I, nullptr, a->tx,
                                                                    flow_tag(epoch, l, FK_XD), H, h0, h1, H, ring, res_s, pk_s);
             tr.mark();
         }
@@ -712,8 +720,8 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
         const int H = a->hidden, V = a->vocab;
         const uint16_t* ws = a->lm_head + (size_t)hr.stop * H;
         const int rn = wg == 0 ? 1 : 0;
-        prefetch_ring<ITH, false>(ws, nullptr, H, 0, rn, 1, ring);
-        gemv_ring<B, EPI_STORE, ITH, false, kPack<B>>(ws, nullptr, lds, H, a->logits + hr.stop, nullptr, 0, V, 0, rn,
+        prefetch_ring<ITH, false, MH>(ws, nullptr, H, 0, rn, 1, ring);
+        gemv_ring<B, EPI_STORE, ITH, MH, kPack<B>>(ws, nullptr, lds, H, a->logits + hr.stop, nullptr, 0, V, 0, rn,
                                                       1, ring);
         const int f0 = part_lo(V, wg, nwg), f1 = part_lo(V, wg + 1, nwg);
         for (int b = 0; b < B; ++b)
@@ -729,34 +737,43 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
     if (!call.sample && wg == 0 && tid == 0) *gblw(&st->seq) = seq + 1;
 }
 
-template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
+template <int B, int D, int G, int ITH, int ITQ, int ITI, int MASK>
 static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCall& call, int nwg, size_t lds) {
     if (call.trace)
-        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, true, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASK, true, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
     else if (call.context >= kOEarlyKeys)
-        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASK, false, true><<<nwg, kStepThreads, lds, s>>>(dev, call);
     else
-        step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
+        step_kernel<B, D, G, ITH, ITQ, ITI, MASK, false, false><<<nwg, kStepThreads, lds, s>>>(dev, call);
     return hipGetLastError();
 }
 
-// Shapes with a compiled step kernel: {head_dim, query heads per KV head,
-// iterations for hidden, for heads*head_dim, for intermediate}.
+// The compiled step kernels.  Two shapes have their own, unmasked: the
+// 3B-class one (hidden 3072, 24 x 128 query heads, 3 per KV head,
+// intermediate 8192) and the YuE2 one (2048, 16 x 128, 2 per KV head, 6144).
+// Any other shape with head_dim 64 or 128, at most 4 query heads per KV
+// head, hidden and heads * head_dim at most 3072 and intermediate at most
+// 8192 (hidden and intermediate multiples of 8) runs on the generic kernel
+// of its head_dim, every GEMV input masked to its length.
+enum class StepShape { kNone, k3B, kYue2, kAny128, kAny64 };
+
+static StepShape step_shape(int hidden, int heads, int kv_heads, int dim, int inter) {
+    if (kv_heads < 1 || heads % kv_heads) return StepShape::kNone;
+    const int G = heads / kv_heads, qw = heads * dim;
+    if (dim == 128 && G == 3 && hidden == 3072 && qw == 3072 && inter == 8192) return StepShape::k3B;
+    if (dim == 128 && G == 2 && hidden == 2048 && qw == 2048 && inter == 6144) return StepShape::kYue2;
+    const bool fits = G <= 4 && hidden >= 8 && hidden <= 512 * kStepAnyIth && hidden % 8 == 0 && qw <= 512 * kStepAnyItq &&
+                      inter >= 8 && inter <= 512 * kStepAnyIti && inter % 8 == 0;
+    if (!fits) return StepShape::kNone;
+    return dim == 128 ? StepShape::kAny128 : dim == 64 ? StepShape::kAny64 : StepShape::kNone;
+}
+
 bool step_supported(const Yue2Config& c, int rows, int nwg) {
-    const int ith = (c.hidden_size / 8 + 63) / 64, itq = (c.num_attention_heads * c.head_dim / 8 + 63) / 64;
-    const int iti = (c.intermediate_size / 8 + 63) / 64;
-    // hidden and heads * head_dim exactly 512 * IT (their GEMVs are unmasked)
-    const bool exact = c.hidden_size == 512 * ith && c.num_attention_heads * c.head_dim == 512 * itq;
-    // (the head_dim-128 kernel also takes the intermediate size as exactly 512 * 16,
-    // and each kernel one group size)
-    const int G = c.num_key_value_heads > 0 ? c.num_attention_heads / c.num_key_value_heads : 0;
-    const bool grouped = G * c.num_key_value_heads == c.num_attention_heads;
-    const bool shape =
-        exact && grouped &&
-        ((c.head_dim == 128 && G == 3 && ith == 6 && itq == 6 && c.intermediate_size == 512 * 16) ||
-         (c.head_dim == 128 && G == 2 && ith == 4 && itq == 4 && c.intermediate_size == 512 * 12) ||
-         (c.head_dim == 64 && G == 4 && ith == 2 && itq == 2 && iti == 6));
-    if (!shape || rows < 1 || rows > 2 || nwg < c.num_key_value_heads * rows) return false;
+    if (step_shape(c.hidden_size, c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.intermediate_size) ==
+        StepShape::kNone)
+        return false;
+    const int G = c.num_attention_heads / c.num_key_value_heads;
+    if (rows < 1 || rows > 2 || nwg < c.num_key_value_heads * rows) return false;
     const int wpg = nwg / (c.num_key_value_heads * rows);  // workgroups past the groups take no attention
     const int max_blocks = (c.max_position_embeddings + kBlockKeys - 1) / kBlockKeys;
     const int bpw = attn_bpw_max(max_blocks, wpg);
@@ -787,15 +804,15 @@ size_t step_lds_bytes(const StepArgs& a, int nwg) {
     return std::max((size_t)a.rows * kmax * sizeof(float), attn_flow_lds(G, a.head_dim, bpw));
 }
 
-template <int B, int D, int G, int ITH, int ITQ, int ITI, bool MASKI>
+template <int B, int D, int G, int ITH, int ITQ, int ITI, int MASK>
 static int resident_t(size_t lds) {
     // every instantiation a launch may pick must fit one workgroup per CU
     int n = 0, n2 = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, false>),
+            &n, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASK, false, false>),
             kStepThreads, lds) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n2, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASKI, false, true>),
+            &n2, reinterpret_cast<const void*>(step_kernel<B, D, G, ITH, ITQ, ITI, MASK, false, true>),
             kStepThreads, lds) != hipSuccess)
         return 0;
     return std::min(n, n2);
@@ -809,14 +826,20 @@ size_t step_launch_lds(const StepArgs& a, int nwg, int sample) {
 int step_resident_per_cu(const StepArgs& a, int nwg, int sample) {
     const size_t lds = step_launch_lds(a, nwg, sample);
     if (lds > kStepLdsMax) return 0;
-    const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
-    if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16)
-        return a.rows == 1 ? resident_t<1, 128, 3, 6, 6, 16, false>(lds) : resident_t<2, 128, 3, 6, 6, 16, false>(lds);
-    if (a.head_dim == 128 && G == 2 && ith == 4 && a.intermediate == 512 * 12)
-        return a.rows == 1 ? resident_t<1, 128, 2, 4, 4, 12, false>(lds) : resident_t<2, 128, 2, 4, 4, 12, false>(lds);
-    if (a.head_dim == 64 && G == 4 && ith == 2)
-        return a.rows == 1 ? resident_t<1, 64, 4, 2, 2, 6, true>(lds) : resident_t<2, 64, 4, 2, 2, 6, true>(lds);
-    return 0;
+    switch (step_shape(a.hidden, a.heads, a.kv_heads, a.head_dim, a.intermediate)) {
+        case StepShape::k3B:
+            return a.rows == 1 ? resident_t<1, 128, 3, 6, 6, 16, 0>(lds) : resident_t<2, 128, 3, 6, 6, 16, 0>(lds);
+        case StepShape::kYue2:
+            return a.rows == 1 ? resident_t<1, 128, 2, 4, 4, 12, 0>(lds) : resident_t<2, 128, 2, 4, 4, 12, 0>(lds);
+        case StepShape::kAny128:
+            return a.rows == 1 ? resident_t<1, 128, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds)
+                               : resident_t<2, 128, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds);
+        case StepShape::kAny64:
+            return a.rows == 1 ? resident_t<1, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds)
+                               : resident_t<2, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds);
+        default:
+            return 0;
+    }
 }
 
 bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, float temperature, int top_k,
@@ -831,20 +854,22 @@ bool fused_sampler_supported(const Yue2Config& c, int rows, int nwg, int mode, f
 hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, const StepCall& call, int nwg) {
     const size_t lds = step_launch_lds(a, nwg, call.sample);
     if (lds > kStepLdsMax) return hipErrorInvalidValue;
-    const int ith = (a.hidden / 8 + 63) / 64, G = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
-    if (a.head_dim == 128 && G == 3 && ith == 6 && a.intermediate == 512 * 16) {
-        if (a.rows == 1) return launch_step_t<1, 128, 3, 6, 6, 16, false>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 128, 3, 6, 6, 16, false>(s, dev, call, nwg, lds);
+    switch (step_shape(a.hidden, a.heads, a.kv_heads, a.head_dim, a.intermediate)) {
+        case StepShape::k3B:
+            return a.rows == 1 ? launch_step_t<1, 128, 3, 6, 6, 16, 0>(s, dev, call, nwg, lds)
+                               : launch_step_t<2, 128, 3, 6, 6, 16, 0>(s, dev, call, nwg, lds);
+        case StepShape::kYue2:
+            return a.rows == 1 ? launch_step_t<1, 128, 2, 4, 4, 12, 0>(s, dev, call, nwg, lds)
+                               : launch_step_t<2, 128, 2, 4, 4, 12, 0>(s, dev, call, nwg, lds);
+        case StepShape::kAny128:
+            return a.rows == 1 ? launch_step_t<1, 128, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds)
+                               : launch_step_t<2, 128, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds);
+        case StepShape::kAny64:
+            return a.rows == 1 ? launch_step_t<1, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds)
+                               : launch_step_t<2, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds);
+        default:
+            return hipErrorInvalidValue;
     }
-    if (a.head_dim == 128 && G == 2 && ith == 4 && a.intermediate == 512 * 12) {
-        if (a.rows == 1) return launch_step_t<1, 128, 2, 4, 4, 12, false>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 128, 2, 4, 4, 12, false>(s, dev, call, nwg, lds);
-    }
-    if (a.head_dim == 64 && G == 4 && ith == 2) {
-        if (a.rows == 1) return launch_step_t<1, 64, 4, 2, 2, 6, true>(s, dev, call, nwg, lds);
-        return launch_step_t<2, 64, 4, 2, 2, 6, true>(s, dev, call, nwg, lds);
-    }
-    return hipErrorInvalidValue;
 }
 
 }  // namespace y2

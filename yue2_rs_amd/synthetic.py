@@ -33,6 +33,11 @@ YUE2 = Config(hidden_size=2048, num_hidden_layers=28, num_attention_heads=16, nu
 CLASS_3B = Config(hidden_size=3072, num_hidden_layers=28, num_attention_heads=24, num_key_value_heads=8,
                   head_dim=128, intermediate_size=8192, vocab_size=84000, max_position_embeddings=24576,
                   rms_norm_eps=1e-6, rope_theta=10000.0)
+# A 1B-class shape with no step kernel of its own (the generic head_dim-64
+# kernel runs it): 4 query heads per KV head, contexts up to 16384.
+CLASS_1B_ANY = Config(hidden_size=2048, num_hidden_layers=16, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=64, intermediate_size=8192, vocab_size=128256, max_position_embeddings=16384,
+                      rms_norm_eps=1e-6, rope_theta=500000.0)
 
 
 def bf16_normal(shape, seed: int, tensor: int, std: float = 0.02, threads: int = 0) -> np.ndarray:

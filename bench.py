@@ -30,10 +30,11 @@ phase of Pipeline::generate_semantic: the LM head reads the 32768 codec rows
 and MUSIC_END (project_phase, src/model.rs:478-507); min_tokens keeps the
 end token out until the timed steps are done.
 
---workload any: the same loop on a shape with no step kernel of its own, a
-1B-class one (hidden 2048, 16 layers, 32 q / 8 KV heads, head_dim 64, SwiGLU
-8192, vocab 128256): the generic head_dim-64 step kernel (--step-kernel 0:
-the per-phase kernels).
+--workload any: the same loop on a shape with no step kernel of its own
+(--shape 1b: hidden 2048, 16 layers, 32 q / 8 KV heads, head_dim 64, SwiGLU
+8192; --shape 8b: hidden 4096, 32 layers, 32 q / 8 KV heads, head_dim 128,
+SwiGLU 14336; vocab 128256): the generic step kernel of its head_dim
+(--step-kernel 0: the per-phase kernels).
 
 Prints one JSON line.  Progress goes to stderr.
 """
@@ -237,6 +238,7 @@ def main() -> int:
                     help="decode (default): 2048-token prompts; long: 24000-token prompts decoded to 24576; "
                          "yue2: the YuE2 shape in the semantic phase; any: a 1B-class shape on the generic "
                          "step kernel")
+    ap.add_argument("--shape", default="1b", choices=["1b", "8b"], help="--workload any: the shape")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path (--gpus must be 1)",
@@ -254,10 +256,14 @@ def main() -> int:
         return shape_workload(args, y2, synthetic, synthetic.YUE2, y2.PHASE_SEMANTIC, 32768 + 1,
                               "YuE2-shape AR decode loop, semantic phase",
                               "YuE2 shape: 28 layers + semantic-phase LM head + sampler")
-    if args.workload == "any":
+    if args.workload == "any" and args.shape == "1b":
         return shape_workload(args, y2, synthetic, synthetic.CLASS_1B_ANY, y2.PHASE_NONE, None,
                               "1B-class AR decode loop (no shape-specific step kernel)",
                               "1B-class shape: 16 layers + LM head + sampler, the generic head_dim-64 kernel")
+    if args.workload == "any":
+        return shape_workload(args, y2, synthetic, synthetic.CLASS_8B_ANY, y2.PHASE_NONE, None,
+                              "8B-class AR decode loop (no shape-specific step kernel)",
+                              "8B-class shape: 32 layers + LM head + sampler, the generic head_dim-128 kernel")
     c = synthetic.CLASS_3B
     log("generating synthetic 3B-class weights")
     t = time.perf_counter()

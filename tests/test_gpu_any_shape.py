@@ -2,8 +2,8 @@
 
 The reference's Metal fast path runs any Config (yue2_metal_ar_stack,
 src/metal.m:718-874).  Here a shape with head_dim 64 or 128, at most four
-query heads per KV head, hidden and heads * head_dim up to 3072 and
-intermediate up to 8192 runs on the generic step kernel of its head_dim:
+query heads per KV head, hidden and heads * head_dim up to 4608 and
+intermediate up to 14336 runs on the generic step kernel of its head_dim:
 every GEMV input masked to its length, the group size taken at run time.
 (The reduced config of the other tests, hidden 1024 / intermediate 2816 /
 4 query heads per KV head at head_dim 64, runs on it as well.)  Each shape
@@ -38,6 +38,12 @@ SHAPES = {
     "d64-g1": _config(768, 12, 12, 64, 2048),
     # 3 per KV head at head_dim 64
     "d64-g3": _config(1152, 18, 6, 64, 3072),
+    # 8B-class layers (two of them): hidden 4096, 32 x 128 query heads, 4 per
+    # KV head, intermediate 14336 (the down projection's input in two
+    # gather passes)
+    "d128-g4-h4096": _config(4096, 32, 8, 128, 14336),
+    # 7B-class layers without grouping, intermediate 11008
+    "d128-g1-h4096": _config(4096, 32, 32, 128, 11008),
 }
 
 
@@ -111,9 +117,36 @@ def test_sampled_cfg_generate(shape):
 
 
 def test_shapes_past_the_limits_use_the_phase_kernels(gpu):
-    """Six query heads per KV head, or hidden 4096, have no step kernel: the
+    """Six query heads per KV head, or hidden 5120, have no step kernel: the
     model decodes on the per-phase kernels."""
-    for c in (_config(1536, 12, 2, 128, 4096), _config(4096, 32, 8, 128, 4096)):
+    for c in (_config(1536, 12, 2, 128, 4096), _config(5120, 40, 8, 128, 4096)):
         gm = y2.Model.open(synthetic.checkpoint(c, seed=0))
         assert not gm.set_step_kernel(True)
         gm.close()
+
+
+def test_8b_class_layers_on_the_phase_kernels(gpu, oracle_threads):
+    """The per-phase kernels take the same 8B-class layers (intermediate
+    14336: the down projection's two staged input rows, 115 KB, in one
+    workgroup's LDS): CFG batch-2 logits of both rows bit for bit."""
+    ck = synthetic.checkpoint(SHAPES["d128-g4-h4096"], seed=3)
+    gm, om = y2.Model.open(ck), O.Model(ck)
+    assert not gm.set_step_kernel(False)
+    V, steps, scale = ck.config.vocab_size, 2, 1.5
+    (g0, o0), (g1, o1) = (_caches(gm, om, n, n + steps, 21 + i) for i, n in enumerate((2048, 2011)))
+    dec = y2.Decoder(gm, g0, g1, scale=scale)
+    t = 55
+    first = np.zeros(2 * V, np.float32)
+    first[t] = first[V + t] = 1.0
+    for s in range(steps):
+        toks, _ = dec.run(1, first_logits=first if s == 0 else None)
+        assert list(toks) == [t]
+        got = dec.logits()
+        w0, w1 = om.forward([t], o0), om.forward([t], o1)
+        assert np.array_equal(bits(got[0]), bits(w0)), f"conditional row differs at step {s}"
+        assert np.array_equal(bits(got[1]), bits(w1)), f"unconditional row differs at step {s}"
+        t = int(np.argmax(O.cfg_mix(w0, w1, scale)))
+    dec.close()
+    for c in (g0, g1):
+        c.close()
+    gm.close()

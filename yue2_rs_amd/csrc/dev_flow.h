@@ -41,10 +41,6 @@ namespace y2 {
 enum FlowKind { FK_QKV = 1, FK_ATT = 2, FK_XO = 3, FK_ACT = 4, FK_XD = 5, FK_BMAX = 6, FK_BSUM = 7,
                 FK_PART = 8, FK_SMP = 9 };
 constexpr int kDevErrFlow = 8;
-// Words a thread gathers in the attention merge (512 threads): a workgroup
-// merges ceil(G*D/W) outputs over nb <= W * bpw blocks, at most
-// G*D*bpw + nb <= 512 * 24 + 384 words for G*D <= 512 and bpw <= 24.
-constexpr int kMergePer = 26;
 // Words per thread in one gather pass of the merge.
 constexpr int kMergeBatch = 8;
 

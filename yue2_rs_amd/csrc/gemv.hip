@@ -58,6 +58,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs a) {
 
 static int g_cus = 0;
 
+constexpr size_t kGemvLdsMax = 128 * 1024;
+
 static int cu_count() {
     if (g_cus <= 0) {
         int v = 0;
@@ -75,10 +77,14 @@ static hipError_t gemv_dispatch(hipStream_t s, const GemvArgs& a) {
     // a residual epilogue stages the workgroup's output rows (at most kResRows)
     if (EPI == EPI_RESID && (a.n + blocks - 1) / blocks > kResRows) return hipErrorInvalidValue;
     const size_t lds = (size_t)B * (a.k + kResRows) * sizeof(float);
-#define Y2_GEMV_CASE(N)                                                       \
-    if (iters <= N) {                                                         \
-        gemv_kernel<B, EPI, N, NORM><<<blocks, kGemvThreads, lds, s>>>(a);    \
-        return hipGetLastError();                                             \
+#define Y2_GEMV_CASE(N)                                                                               \
+    if (iters <= N) {                                                                                 \
+        static const hipError_t attr = hipFuncSetAttribute(                                           \
+            reinterpret_cast<const void*>(&gemv_kernel<B, EPI, N, NORM>),                             \
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsMax);                            \
+        if (attr != hipSuccess) return attr;                                                          \
+        gemv_kernel<B, EPI, N, NORM><<<blocks, kGemvThreads, lds, s>>>(a);                            \
+        return hipGetLastError();                                                                     \
     }
     Y2_GEMV_CASE(1)
     Y2_GEMV_CASE(2)
@@ -106,8 +112,8 @@ static hipError_t gemv_epi(hipStream_t s, int epi, const GemvArgs& a) {
 hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a) {
     if (a.k % 8 != 0 || a.k <= 0 || a.k > 32 * 512 || a.n <= 0 || a.rows < 1 || a.rows > kMaxRows)
         return hipErrorInvalidValue;
-    // LDS holds rows * k f32 inputs (64 KiB per workgroup).
-    if ((size_t)a.rows * a.k * sizeof(float) > 64 * 1024) return hipErrorInvalidValue;
+    // LDS holds rows * k f32 inputs and the residual rows (one workgroup per CU)
+    if ((size_t)a.rows * (a.k + kResRows) * sizeof(float) > kGemvLdsMax) return hipErrorInvalidValue;
     const bool norm = a.gamma != nullptr;
     if (a.rows == 1) return norm ? gemv_epi<1, true>(s, epi, a) : gemv_epi<1, false>(s, epi, a);
     return norm ? gemv_epi<2, true>(s, epi, a) : gemv_epi<2, false>(s, epi, a);

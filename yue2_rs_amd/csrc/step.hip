@@ -69,9 +69,10 @@ template <int B>
 constexpr bool kPair = B == 1;
 constexpr int kPairRowsMax = 64;  // rows of one such GEMV per workgroup
 // The generic kernels' iterations (512 inputs each): hidden and heads *
-// head_dim up to 3072, intermediate up to 8192 (at 4096 the head_dim-128
-// kernels spill about 100 bytes per lane).
-constexpr int kStepAnyIth = 6, kStepAnyItq = 6, kStepAnyIti = 16;
+// head_dim up to 4608, intermediate up to 14336.  (Nine, not eight: a row's
+// items are then three chunks per lane, as the 3B-class kernel's; with four
+// the head_dim-128 kernels spilled ~35 registers, with three 8.)
+constexpr int kStepAnyIth = 9, kStepAnyItq = 9, kStepAnyIti = 28;
 
 // First row of workgroup w's share of an exchanged GEMV output of n rows:
 // even for paired words (a pair never straddles two workgroups).
@@ -83,20 +84,45 @@ __device__ __forceinline__ int xlo(int n, int w, int parts) {
 
 // xs[b * k + i] = row b's value of x-like words tx (packed for two rows,
 // for one row two values per word), i < k.
+// (Past 16 words per thread, in passes of 16: the first pass's words are
+// all in before the second's are polled.)
 template <int B, int N>
 __device__ __forceinline__ bool stage_rows(float* xs, const uint64_t* tx, int k, uint32_t tag, StepState* st) {
     if constexpr (kPack<B>) {
-        static_assert(N <= 16, "at most 16 words per thread in flight");
-        return gather_pair<kStepThreads, N>(tx, k, tag, xs, st);
+        if constexpr (N <= 16) {
+            return gather_pair<kStepThreads, N>(tx, k, tag, xs, st);
+        } else {
+            static_assert(N <= 32, "two passes");
+            constexpr int F = 16 * kStepThreads;
+            const auto put = [=](int base) {
+                return [=](int i, uint32_t bits) {
+                    xs[base + i] = bf16_lo(bits);
+                    xs[k + base + i] = bf16_hi(bits);
+                };
+            };
+            return gather_put<kStepThreads, 16>([=](int i) { return tx + i; }, min(k, F), tag, put(0), st) &&
+                   (k <= F || gather_put<kStepThreads, N - 16>([=](int i) { return tx + F + i; }, k - F, tag,
+                                                               put(F), st));
+        }
     } else {
-        // one row: word p holds rows 2p and 2p + 1
+        // one row: word p holds rows 2p and 2p + 1 (past 8 words per
+        // thread, in passes of 8)
         static_assert(kPair<B>, "one or two rows");
-        return gather_put<kStepThreads, (N + 1) / 2>([=](int i) { return tx + i; }, k / 2, tag,
-                                                     [=](int i, uint32_t bits) {
-                                                         xs[2 * i] = bf16_lo(bits);
-                                                         xs[2 * i + 1] = bf16_hi(bits);
-                                                     },
-                                                     st);
+        constexpr int M = (N + 1) / 2, F = 8 * kStepThreads;
+        static_assert(M <= 16, "two passes");
+        const auto put = [=](int base) {
+            return [=](int i, uint32_t bits) {
+                xs[2 * (base + i)] = bf16_lo(bits);
+                xs[2 * (base + i) + 1] = bf16_hi(bits);
+            };
+        };
+        if constexpr (M <= 8) {
+            return gather_put<kStepThreads, M>([=](int i) { return tx + i; }, k / 2, tag, put(0), st);
+        } else {
+            return gather_put<kStepThreads, 8>([=](int i) { return tx + i; }, min(k / 2, F), tag, put(0), st) &&
+                   (k / 2 <= F ||
+                    gather_put<kStepThreads, M - 8>([=](int i) { return tx + F + i; }, k / 2 - F, tag, put(F), st));
+        }
     }
 }
 
@@ -752,8 +778,8 @@ static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCa
 // 3B-class one (hidden 3072, 24 x 128 query heads, 3 per KV head,
 // intermediate 8192) and the YuE2 one (2048, 16 x 128, 2 per KV head, 6144).
 // Any other shape with head_dim 64 or 128, at most 4 query heads per KV
-// head, hidden and heads * head_dim at most 3072 and intermediate at most
-// 8192 (hidden and intermediate multiples of 8) runs on the generic kernel
+// head, hidden and heads * head_dim at most 4608 and intermediate at most
+// 14336 (hidden and intermediate multiples of 8) runs on the generic kernel
 // of its head_dim, every GEMV input masked to its length.
 enum class StepShape { kNone, k3B, kYue2, kAny128, kAny64 };
 
@@ -779,8 +805,7 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const int bpw = attn_bpw_max(max_blocks, wpg);
     // the attention's p (G x bpw blocks of f32) is staged in its K region
     // (the merge's partials, G x head_dim x bpw + blocks words at most, are
-    // gathered kMergePer per thread into the K/V region with rows padded to
-    // four floats)
+    // gathered into the K/V region with rows padded to four floats)
     const int merge_words = G * c.head_dim * bpw + 2 * max_blocks;
     // (with one row each workgroup's share of an exchanged output is even:
     // at most 2 ceil(n / 2 / nwg) rows, paired in LDS)
@@ -790,7 +815,6 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
                            share(qkv_rows) <= kPairRowsMax && c.hidden_size % 2 == 0 &&
                            c.intermediate_size % 2 == 0 && qkv_rows % 2 == 0;
     return pairs_fit && G <= 4 && share(c.hidden_size) <= kResRows && max_blocks <= 24576 / kBlockKeys &&
-           merge_words <= kStepThreads * kMergePer &&
            (size_t)(merge_words + 3 * G * c.head_dim) * 4 <= (size_t)2 * kAttnChunk * kBlockKeys * c.head_dim * 2 &&
            G * bpw * kBlockKeys * 4 <= kAttnChunk * kBlockKeys * c.head_dim * 2;
 }

@@ -38,6 +38,11 @@ CLASS_3B = Config(hidden_size=3072, num_hidden_layers=28, num_attention_heads=24
 CLASS_1B_ANY = Config(hidden_size=2048, num_hidden_layers=16, num_attention_heads=32, num_key_value_heads=8,
                       head_dim=64, intermediate_size=8192, vocab_size=128256, max_position_embeddings=16384,
                       rms_norm_eps=1e-6, rope_theta=500000.0)
+# An 8B-class shape (the generic head_dim-128 kernel): hidden 4096, 32 x 128
+# query heads, 4 per KV head, SwiGLU 14336.
+CLASS_8B_ANY = Config(hidden_size=4096, num_hidden_layers=32, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, intermediate_size=14336, vocab_size=128256, max_position_embeddings=16384,
+                      rms_norm_eps=1e-6, rope_theta=500000.0)
 
 
 def bf16_normal(shape, seed: int, tensor: int, std: float = 0.02, threads: int = 0) -> np.ndarray:

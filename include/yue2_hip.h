@@ -435,7 +435,7 @@ int32_t yue2_hip_selftest_conv(int32_t transpose, int32_t cin, int32_t cout, int
  * token, workgroups exchanging tagged words instead of meeting at barriers
  * -- or through one kernel per phase.  Both produce the same bits.  The
  * step kernel is the default for shapes that have one: head_dim 64 or 128,
- * at most 4 query heads per KV head, hidden and heads * head_dim at most
+ * at most 8 query heads per KV head, hidden and heads * head_dim at most
  * 4608 and intermediate at most 14336 (the 3B-class and YuE2 shapes on
  * kernels of their own, the others on generic ones), contexts up to 24576.
  * Returns 1 when enabled, 0 when off or when the model's shape has no step

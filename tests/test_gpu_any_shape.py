@@ -1,10 +1,12 @@
 """The generic step kernels: shapes that have no kernel of their own.
 
 The reference's Metal fast path runs any Config (yue2_metal_ar_stack,
-src/metal.m:718-874).  Here a shape with head_dim 64 or 128, at most four
+src/metal.m:718-874).  Here a shape with head_dim 64 or 128, at most eight
 query heads per KV head, hidden and heads * head_dim up to 4608 and
-intermediate up to 14336 runs on the generic step kernel of its head_dim:
-every GEMV input masked to its length, the group size taken at run time.
+intermediate up to 14336 runs on a generic step kernel of its head_dim:
+every GEMV input masked to its length, the group size taken at run time
+(past four query heads per KV head, the scores and PV take them four at a
+time).
 (The reduced config of the other tests, hidden 1024 / intermediate 2816 /
 4 query heads per KV head at head_dim 64, runs on it as well.)  Each shape
 below is checked against the oracle bit for bit: a decode-order prefill and
@@ -44,6 +46,10 @@ SHAPES = {
     "d128-g4-h4096": _config(4096, 32, 8, 128, 14336),
     # 7B-class layers without grouping, intermediate 11008
     "d128-g1-h4096": _config(4096, 32, 32, 128, 11008),
+    # 6, 7 and 8 query heads per KV head (two head passes)
+    "d128-g6": _config(1536, 12, 2, 128, 8960),
+    "d64-g7": _config(896, 14, 2, 64, 4864),
+    "d128-g8": _config(2048, 16, 2, 128, 11008),
 }
 
 
@@ -117,9 +123,9 @@ def test_sampled_cfg_generate(shape):
 
 
 def test_shapes_past_the_limits_use_the_phase_kernels(gpu):
-    """Six query heads per KV head, or hidden 5120, have no step kernel: the
-    model decodes on the per-phase kernels."""
-    for c in (_config(1536, 12, 2, 128, 4096), _config(5120, 40, 8, 128, 4096)):
+    """Hidden 5120, or intermediate 16384, have no step kernel: the model
+    decodes on the per-phase kernels."""
+    for c in (_config(5120, 40, 8, 128, 4096), _config(2048, 16, 8, 128, 16384)):
         gm = y2.Model.open(synthetic.checkpoint(c, seed=0))
         assert not gm.set_step_kernel(True)
         gm.close()

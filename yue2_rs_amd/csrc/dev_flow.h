@@ -226,7 +226,7 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 //    (block, eighth of the dims) item per wave, for all heads.
 // G = heads / kv_heads, the query heads of a group (the host checks that the
 // launch's shape has this G); GRT: G is only the most a group has, its
-// query heads are heads / kv_heads at run time.  lds: attn_flow_lds(G, D,
+// query heads are heads / kv_heads at run time (up to 8).  lds: attn_flow_lds(G, D,
 // bpw) bytes.  false: timeout (error set).
 // pre(): called once the workgroup's q/k/v are gathered (or at once when it
 // has no keys): the caller's early requests for the phase after the
@@ -240,6 +240,9 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     constexpr int BLK_U4 = kBlockKeys * D / 8;           // uint4 per staged block
     constexpr int PER = (kAttnChunk * BLK_U4 + NT - 1) / NT;  // uint4 per thread per chunk
     constexpr int HALF = D / 2;
+    // the scores and PV take the group's query heads HP at a time (more
+    // per-head values would not fit the registers), in NP passes
+    constexpr int HP = G < 4 ? G : 4, NP = (G + HP - 1) / HP;
     // the group's queries, then (owner of the new key) its key and value rows
     __shared__ __align__(16) float qkv_s[(G + 2) * D];  // read as float4 in the scores
     float(*q_s)[D] = reinterpret_cast<float(*)[D]>(qkv_s);
@@ -313,9 +316,13 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     uint4 kr[PER], vr[PER];
     load_chunk(Kc, 0, kr);
     load_chunk(Vc, 0, vr);
-    // RoPE / QK-norm constants of the (head, d) pair this thread rotates
+    // RoPE / QK-norm constants of the (head, d) pair this thread rotates.
+    // XP: more pairs than threads (eight query heads at head_dim 128): thread
+    // t also rotates pair t + NT, a pair of the new key with the same d.
+    constexpr bool XP = (G + 1) * HALF > NT;
+    static_assert(NT % HALF == 0 && (G + 1) * HALF <= 2 * NT, "at most two pairs per thread");
     const int pairs = (Gq + (owns_new ? 1 : 0)) * HALF;
-    float c_cos = 0.0f, c_sin = 0.0f, c_g0 = 0.0f, c_g1 = 0.0f;
+    float c_cos = 0.0f, c_sin = 0.0f, c_g0 = 0.0f, c_g1 = 0.0f, c_g0k = 0.0f, c_g1k = 0.0f;
     if (tid < pairs) {
         const int h = tid / HALF, d = tid % HALF;
         const float* gam = h < Gq ? a.q_norm : a.k_norm;
@@ -323,6 +330,12 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         c_g1 = gbl(gam)[d + HALF];
         c_cos = gbl(a.cos_t + (size_t)pos * HALF)[d];
         c_sin = gbl(a.sin_t + (size_t)pos * HALF)[d];
+    }
+    if constexpr (XP) {
+        if (tid + NT < pairs) {
+            c_g0k = gbl(a.k_norm)[tid % HALF];
+            c_g1k = gbl(a.k_norm)[tid % HALF + HALF];
+        }
     }
     if (a.packed) {
         // one gather for all three: a single wait; each word holds both
@@ -359,36 +372,68 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     // vector load in flight (the next K chunk's) wherever it reuses their
     // registers, in the scores' inner loop among other places.
     asm volatile("" ::"v"(c_cos), "v"(c_sin), "v"(c_g0), "v"(c_g1));
+    if constexpr (XP) asm volatile("" ::"v"(c_g0k), "v"(c_g1k));
     mark();
     pre();
     // Norm::heads (src/tensor.rs:1160): the scale of the sequential sum of
     // squares per head, decided by a whole wave per head (wave Gq: the new key)
-    static_assert(G + 1 <= NW, "one wave per head norm");
-    if (wave < Gq + (owns_new ? 1 : 0)) {
-        const float s = norm_scale_wave(wave < Gq ? q_s[wave] : k_s, D, a.eps);
-        if (lane == 0) hscale[wave] = s;
+    if constexpr (G + 1 <= NW) {
+        if (wave < Gq + (owns_new ? 1 : 0)) {
+            const float s = norm_scale_wave(wave < Gq ? q_s[wave] : k_s, D, a.eps);
+            if (lane == 0) hscale[wave] = s;
+        }
+    } else {
+        for (int h = wave; h < Gq + (owns_new ? 1 : 0); h += NW) {
+            const float s = norm_scale_wave(h < Gq ? q_s[h] : k_s, D, a.eps);
+            if (lane == 0) hscale[h] = s;
+        }
     }
     store_chunk(Ks, kr, false);
     store_chunk(Vs, vr, true);
     __syncthreads();
     // rotate-half RoPE (src/model.rs:151-168); the new key and value go to the
     // cache for later steps and straight into the staged chunk for this one
-    if (tid < pairs) {
-        const int h = tid / HALF, d = tid % HALF;
-        float* v = h < Gq ? q_s[h] : k_s;
-        const float s = hscale[h];
-        const float x0 = rb(rb(v[d] * s) * c_g0);
-        const float x1 = rb(rb(v[d + HALF] * s) * c_g1);
-        const float y0 = rb(rb(x0 * c_cos) - rb(x1 * c_sin));
-        const float y1 = rb(rb(x1 * c_cos) + rb(x0 * c_sin));
-        v[d] = y0;
-        v[d + HALF] = y1;
-        if (h == Gq) {
-            gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
-            gblw(Kc)[(size_t)pos * D + d + HALF] = bf16_bits(y1);
-            if (pos - j0 < kAttnChunk * kBlockKeys) {
-                *staged(Ks, pos - j0, d, false) = bf16_bits(y0);
-                *staged(Ks, pos - j0, d + HALF, false) = bf16_bits(y1);
+    if constexpr (!XP) {
+        if (tid < pairs) {
+            const int h = tid / HALF, d = tid % HALF;
+            float* v = h < Gq ? q_s[h] : k_s;
+            const float s = hscale[h];
+            const float x0 = rb(rb(v[d] * s) * c_g0);
+            const float x1 = rb(rb(v[d + HALF] * s) * c_g1);
+            const float y0 = rb(rb(x0 * c_cos) - rb(x1 * c_sin));
+            const float y1 = rb(rb(x1 * c_cos) + rb(x0 * c_sin));
+            v[d] = y0;
+            v[d + HALF] = y1;
+            if (h == Gq) {
+                gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
+                gblw(Kc)[(size_t)pos * D + d + HALF] = bf16_bits(y1);
+                if (pos - j0 < kAttnChunk * kBlockKeys) {
+                    *staged(Ks, pos - j0, d, false) = bf16_bits(y0);
+                    *staged(Ks, pos - j0, d + HALF, false) = bf16_bits(y1);
+                }
+            }
+        }
+    } else {
+        // the same over two pairs per thread (the second one the new key's,
+        // with the key's gammas); the one-pair form above is kept apart
+        // because folding both into one loop changed the other kernels' code
+        for (int pr = tid; pr < pairs; pr += NT) {
+            const int h = pr / HALF, d = pr % HALF;
+            float* v = h < Gq ? q_s[h] : k_s;
+            const float s = hscale[h];
+            const float x0 = rb(rb(v[d] * s) * (pr < NT ? c_g0 : c_g0k));
+            const float x1 = rb(rb(v[d + HALF] * s) * (pr < NT ? c_g1 : c_g1k));
+            const float y0 = rb(rb(x0 * c_cos) - rb(x1 * c_sin));
+            const float y1 = rb(rb(x1 * c_cos) + rb(x0 * c_sin));
+            v[d] = y0;
+            v[d + HALF] = y1;
+            if (h == Gq) {
+                gblw(Kc)[(size_t)pos * D + d] = bf16_bits(y0);
+                gblw(Kc)[(size_t)pos * D + d + HALF] = bf16_bits(y1);
+                if (pos - j0 < kAttnChunk * kBlockKeys) {
+                    *staged(Ks, pos - j0, d, false) = bf16_bits(y0);
+                    *staged(Ks, pos - j0, d + HALF, false) = bf16_bits(y1);
+                }
             }
         }
     }
@@ -419,73 +464,158 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         static_assert(H2 >= 2, "a butterfly distance after the reduce-scatter");
         const int c = lane % SCPL, grp = lane / SCPL;
         const bool b1 = (c & H1) != 0, b2 = (c & H2) != 0;
-        float qr[G][8];
+        // (one pass: all heads at once; kept apart from the pass form below,
+        // whose code for a single pass measured slower at long contexts)
+        if constexpr (NP == 1) {
+            float qr[G][8];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            if (GRT && h >= Gq) {
+            for (int h = 0; h < G; ++h) {
+                if (GRT && h >= Gq) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) qr[h][e] = 0.0f;  // (a head the group lacks: scores never stored)
-                continue;
+                    for (int e = 0; e < 8; ++e) qr[h][e] = 0.0f;  // (a head the group lacks: scores never stored)
+                    continue;
+                }
+                if (h >= Gq) break;
+                const float4* qp = reinterpret_cast<const float4*>(q_s[h] + 8 * c);
+                const float4 q0 = qp[0], q1 = qp[1];
+                qr[h][0] = q0.x; qr[h][1] = q0.y; qr[h][2] = q0.z; qr[h][3] = q0.w;
+                qr[h][4] = q1.x; qr[h][5] = q1.y; qr[h][6] = q1.z; qr[h][7] = q1.w;
             }
-            if (h >= Gq) break;
-            const float4* qp = reinterpret_cast<const float4*>(q_s[h] + 8 * c);
-            const float4 q0 = qp[0], q1 = qp[1];
-            qr[h][0] = q0.x; qr[h][1] = q0.y; qr[h][2] = q0.z; qr[h][3] = q0.w;
-            qr[h][4] = q1.x; qr[h][5] = q1.y; qr[h][6] = q1.z; qr[h][7] = q1.w;
-        }
-        for (int cb = 0; cb < nbl; cb += kAttnChunk) {
-            if (cb > 0) {
-                // a later chunk (long contexts), requested during the previous
-                // chunk's scores: stage it, then patch the new key
-                __syncthreads();
-                store_chunk(Ks, kr, false);
-                __syncthreads();
-                const int kp = pos - j0 - cb * kBlockKeys;
-                if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
-                    for (int d = tid; d < D; d += NT)
-                        *staged(Ks, kp, d, false) = bf16_bits(k_s[d]);
-                __syncthreads();
-            }
-            // the next chunk's loads stay in flight while this one is scored
-            if (cb + kAttnChunk < nbl) load_chunk(Kc, cb + kAttnChunk, kr);
-            const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
-            for (int qd0 = wave * GPW; qd0 * 4 < keys; qd0 += NW * GPW) {
-                const int kq = 4 * (qd0 + grp);  // the group's first key within the chunk
-                float v[4][G];
-                // the four keys' rows read together (rows past the chunk's
-                // keys are read clamped and never stored)
-                uint4 k4[4];
+            for (int cb = 0; cb < nbl; cb += kAttnChunk) {
+                if (cb > 0) {
+                    // a later chunk (long contexts), requested during the previous
+                    // chunk's scores: stage it, then patch the new key
+                    __syncthreads();
+                    store_chunk(Ks, kr, false);
+                    __syncthreads();
+                    const int kp = pos - j0 - cb * kBlockKeys;
+                    if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
+                        for (int d = tid; d < D; d += NT)
+                            *staged(Ks, kp, d, false) = bf16_bits(k_s[d]);
+                    __syncthreads();
+                }
+                // the next chunk's loads stay in flight while this one is scored
+                if (cb + kAttnChunk < nbl) load_chunk(Kc, cb + kAttnChunk, kr);
+                const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
+                for (int qd0 = wave * GPW; qd0 * 4 < keys; qd0 += NW * GPW) {
+                    const int kq = 4 * (qd0 + grp);  // the group's first key within the chunk
+                    float v[4][G];
+                    // the four keys' rows read together (rows past the chunk's
+                    // keys are read clamped and never stored)
+                    uint4 k4[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) k4[r] = Ks[(size_t)min(kq + r, kAttnChunk * kBlockKeys - 1) * (D / 8) + c];
+                    for (int r = 0; r < 4; ++r) k4[r] = Ks[(size_t)min(kq + r, kAttnChunk * kBlockKeys - 1) * (D / 8) + c];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float kf[8];
-                    unpack8a(k4[r], kf);
+                    for (int r = 0; r < 4; ++r) {
+                        float kf[8];
+                        unpack8a(k4[r], kf);
+#pragma unroll
+                        for (int h = 0; h < G; ++h) {
+                            float acc = 0.0f;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qr[h][e], kf[e], acc);
+                            v[r][h] = acc;
+                        }
+                    }
+                    // distance H1: keep keys 2 b1, 2 b1 + 1
+                    float w[2][G];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int h = 0; h < G; ++h) {
+                            const float keep = b1 ? v[2 + i][h] : v[i][h], send = b1 ? v[i][h] : v[2 + i][h];
+                            w[i][h] = keep + xor_lane<H1>(send);
+                        }
+                    // distance H2: keep key b2 of the two
+                    const int kl = kq + 2 * (b1 ? 1 : 0) + (b2 ? 1 : 0);
+                    const int j = j0 + cb * kBlockKeys + kl;
 #pragma unroll
                     for (int h = 0; h < G; ++h) {
-                        float acc = 0.0f;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qr[h][e], kf[e], acc);
-                        v[r][h] = acc;
+                        const float keep = b2 ? w[1][h] : w[0][h], send = b2 ? w[0][h] : w[1][h];
+                        const float acc = xor_sum<H2 / 2>(keep + xor_lane<H2>(send));
+                        if (h < Gq && (c & (H2 - 1)) == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
                     }
                 }
-                // distance H1: keep keys 2 b1, 2 b1 + 1
-                float w[2][G];
+            }
+        } else {
+            // the query chunks of heads h0 .. h0 + HP - 1
+            float qr[HP][8];
+            auto load_q = [&](int h0) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int h = 0; h < HP; ++h) {
+                    if (GRT && h0 + h >= Gq) {
 #pragma unroll
-                    for (int h = 0; h < G; ++h) {
-                        const float keep = b1 ? v[2 + i][h] : v[i][h], send = b1 ? v[i][h] : v[2 + i][h];
-                        w[i][h] = keep + xor_lane<H1>(send);
+                        for (int e = 0; e < 8; ++e) qr[h][e] = 0.0f;  // (a head the group lacks: scores never stored)
+                        continue;
                     }
-                // distance H2: keep key b2 of the two
-                const int kl = kq + 2 * (b1 ? 1 : 0) + (b2 ? 1 : 0);
-                const int j = j0 + cb * kBlockKeys + kl;
+                    if (h0 + h >= Gq) break;
+                    const float4* qp = reinterpret_cast<const float4*>(q_s[h0 + h] + 8 * c);
+                    const float4 q0 = qp[0], q1 = qp[1];
+                    qr[h][0] = q0.x; qr[h][1] = q0.y; qr[h][2] = q0.z; qr[h][3] = q0.w;
+                    qr[h][4] = q1.x; qr[h][5] = q1.y; qr[h][6] = q1.z; qr[h][7] = q1.w;
+                }
+            };
+            for (int cb = 0; cb < nbl; cb += kAttnChunk) {
+                if (cb > 0) {
+                    // a later chunk (long contexts), requested during the previous
+                    // chunk's scores: stage it, then patch the new key
+                    __syncthreads();
+                    store_chunk(Ks, kr, false);
+                    __syncthreads();
+                    const int kp = pos - j0 - cb * kBlockKeys;
+                    if (kp >= 0 && kp < kAttnChunk * kBlockKeys)
+                        for (int d = tid; d < D; d += NT)
+                            *staged(Ks, kp, d, false) = bf16_bits(k_s[d]);
+                    __syncthreads();
+                }
+                // the next chunk's loads stay in flight while this one is scored
+                if (cb + kAttnChunk < nbl) load_chunk(Kc, cb + kAttnChunk, kr);
+                const int keys = min(kAttnChunk * kBlockKeys, nk - cb * kBlockKeys);
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float keep = b2 ? w[1][h] : w[0][h], send = b2 ? w[0][h] : w[1][h];
-                    const float acc = xor_sum<H2 / 2>(keep + xor_lane<H2>(send));
-                    if (h < Gq && (c & (H2 - 1)) == 0 && j < j1) e_s[h * estride + (j - j0)] = acc * a.scale;
+                for (int pass = 0; pass < NP; ++pass) {
+                    const int h0 = pass * HP;
+                    if (h0 >= Gq) break;
+                    load_q(h0);
+                    for (int qd0 = wave * GPW; qd0 * 4 < keys; qd0 += NW * GPW) {
+                        const int kq = 4 * (qd0 + grp);  // the group's first key within the chunk
+                        float v[4][HP];
+                        // the four keys' rows read together (rows past the chunk's
+                        // keys are read clamped and never stored)
+                        uint4 k4[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) k4[r] = Ks[(size_t)min(kq + r, kAttnChunk * kBlockKeys - 1) * (D / 8) + c];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            float kf[8];
+                            unpack8a(k4[r], kf);
+#pragma unroll
+                            for (int h = 0; h < HP; ++h) {
+                                float acc = 0.0f;
+#pragma unroll
+                                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(qr[h][e], kf[e], acc);
+                                v[r][h] = acc;
+                            }
+                        }
+                        // distance H1: keep keys 2 b1, 2 b1 + 1
+                        float w[2][HP];
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+#pragma unroll
+                            for (int h = 0; h < HP; ++h) {
+                                const float keep = b1 ? v[2 + i][h] : v[i][h], send = b1 ? v[i][h] : v[2 + i][h];
+                                w[i][h] = keep + xor_lane<H1>(send);
+                            }
+                        // distance H2: keep key b2 of the two
+                        const int kl = kq + 2 * (b1 ? 1 : 0) + (b2 ? 1 : 0);
+                        const int j = j0 + cb * kBlockKeys + kl;
+#pragma unroll
+                        for (int h = 0; h < HP; ++h) {
+                            const float keep = b2 ? w[1][h] : w[0][h], send = b2 ? w[0][h] : w[1][h];
+                            const float acc = xor_sum<H2 / 2>(keep + xor_lane<H2>(send));
+                            if (h0 + h < Gq && (c & (H2 - 1)) == 0 && j < j1)
+                                e_s[(h0 + h) * estride + (j - j0)] = acc * a.scale;
+                        }
+                    }
                 }
             }
         }
@@ -494,7 +624,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             const int h = i / nbl, bl = i % nbl;
             const int jl = bl * kBlockKeys + lane;
             float m = jl < nk ? e_s[h * estride + jl] : -__builtin_huge_valf();
-m = xor_max<32>(m);
+            m = xor_max<32>(m);
             if (lane == 0) st_tag(a.bmax + hbase + (size_t)h * a.blk_stride + blk0 + bl, m, t_bmax);
         }
     }
@@ -617,42 +747,92 @@ m = xor_max<32>(m);
                 // (the keys t + S i of a stream share their unit permutation)
                 const uint16_t* vrow = staged(Vs, bc * kBlockKeys + t, d, true);
                 const float* pp = p_s + bl * kBlockKeys + t * KPS;
-                float acc[G];
+                // (one pass: all heads at once; this form is kept apart from
+                // the pass loop below, whose code for a single pass measured
+                // 0.2-0.5 % slower)
+                if constexpr (NP == 1) {
+                    float acc[G];
 #pragma unroll
-                for (int h = 0; h < G; ++h) acc[h] = 0.0f;
+                    for (int h = 0; h < G; ++h) acc[h] = 0.0f;
 #pragma unroll
-                for (int i0 = 0; i0 < KPS; i0 += 4) {
-                    // four keys' V and the G heads' p requested together
-                    float vf[4];
+                    for (int i0 = 0; i0 < KPS; i0 += 4) {
+                        // four keys' V and the G heads' p requested together
+                        float vf[4];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) vf[u] = bf16(vrow[(size_t)S * (i0 + u) * D]);
-                    float4 p4[G];
+                        for (int u = 0; u < 4; ++u) vf[u] = bf16(vrow[(size_t)S * (i0 + u) * D]);
+                        float4 p4[G];
 #pragma unroll
-                    for (int h = 0; h < G; ++h)
-                        p4[h] = !GRT || h < Gq ? *reinterpret_cast<const float4*>(pp + h * estride + i0)
-                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                        for (int h = 0; h < G; ++h)
+                            p4[h] = !GRT || h < Gq ? *reinterpret_cast<const float4*>(pp + h * estride + i0)
+                                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
+                        for (int u = 0; u < 4; ++u) {
 #pragma unroll
-                        for (int h = 0; h < G; ++h) {
-                            const float pv = u == 0 ? p4[h].x : u == 1 ? p4[h].y : u == 2 ? p4[h].z : p4[h].w;
-                            acc[h] = __builtin_fmaf(pv, vf[u], acc[h]);
+                            for (int h = 0; h < G; ++h) {
+                                const float pv = u == 0 ? p4[h].x : u == 1 ? p4[h].y : u == 2 ? p4[h].z : p4[h].w;
+                                acc[h] = __builtin_fmaf(pv, vf[u], acc[h]);
+                            }
                         }
                     }
-                }
-                // streams combined in the butterfly order (distances S/2 .. 1
-                // between streams = lane distances 32 .. LPS); every stream
-                // lane then holds the same sums and lane t stores head h when
-                // h % S == t, once its super-block is complete
-                const int bi = bl & (sb - 1);
-                const bool first = bi == 0, full = bi == sb - 1 || bl == nbl - 1;
-                const size_t pidx = (size_t)((blk0 + bl) >> lsb) * D + d;
+                    // streams combined in the butterfly order (distances S/2 .. 1
+                    // between streams = lane distances 32 .. LPS); every stream
+                    // lane then holds the same sums and lane t stores head h when
+                    // h % S == t, once its super-block is complete
+                    const int bi = bl & (sb - 1);
+                    const bool first = bi == 0, full = bi == sb - 1 || bl == nbl - 1;
+                    const size_t pidx = (size_t)((blk0 + bl) >> lsb) * D + d;
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float v = xor_sum<32, LPS>(acc[h]);
-                    sacc[h] = first ? v : sacc[h] + v;
-                    if ((!GRT || h < Gq) && h % S == t && full)
-                        st_tag(a.part + (hbase + (size_t)h * a.blk_stride) * D + pidx, sacc[h], t_part);
+                    for (int h = 0; h < G; ++h) {
+                        const float v = xor_sum<32, LPS>(acc[h]);
+                        sacc[h] = first ? v : sacc[h] + v;
+                        if ((!GRT || h < Gq) && h % S == t && full)
+                            st_tag(a.part + (hbase + (size_t)h * a.blk_stride) * D + pidx, sacc[h], t_part);
+                    }
+                } else {
+#pragma unroll
+                    for (int pass = 0; pass < NP; ++pass) {
+                        const int h0 = pass * HP;
+                        if (h0 >= Gq) break;
+                        float acc[HP];
+#pragma unroll
+                        for (int h = 0; h < HP; ++h) acc[h] = 0.0f;
+#pragma unroll
+                        for (int i0 = 0; i0 < KPS; i0 += 4) {
+                            // four keys' V and the heads' p requested together
+                            float vf[4];
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) vf[u] = bf16(vrow[(size_t)S * (i0 + u) * D]);
+                            float4 p4[HP];
+#pragma unroll
+                            for (int h = 0; h < HP; ++h)
+                                p4[h] = !GRT || h0 + h < Gq
+                                            ? *reinterpret_cast<const float4*>(pp + (h0 + h) * estride + i0)
+                                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                                for (int h = 0; h < HP; ++h) {
+                                    const float pv = u == 0 ? p4[h].x : u == 1 ? p4[h].y : u == 2 ? p4[h].z : p4[h].w;
+                                    acc[h] = __builtin_fmaf(pv, vf[u], acc[h]);
+                                }
+                            }
+                        }
+                        // streams combined in the butterfly order (distances S/2
+                        // .. 1 between streams = lane distances 32 .. LPS); every
+                        // stream lane then holds the same sums and lane t stores
+                        // head h when h % S == t, once its super-block is complete
+                        const int bi = bl & (sb - 1);
+                        const bool first = bi == 0, full = bi == sb - 1 || bl == nbl - 1;
+                        const size_t pidx = (size_t)((blk0 + bl) >> lsb) * D + d;
+#pragma unroll
+                        for (int h = 0; h < HP; ++h) {
+                            const int hh = h0 + h;
+                            const float v = xor_sum<32, LPS>(acc[h]);
+                            sacc[hh] = first ? v : sacc[hh] + v;
+                            if ((!GRT || hh < Gq) && hh % S == t && full)
+                                st_tag(a.part + (hbase + (size_t)hh * a.blk_stride) * D + pidx, sacc[hh], t_part);
+                        }
+                    }
                 }
             }
         }

@@ -777,21 +777,23 @@ static hipError_t launch_step_t(hipStream_t s, const StepArgs* dev, const StepCa
 // The compiled step kernels.  Two shapes have their own, unmasked: the
 // 3B-class one (hidden 3072, 24 x 128 query heads, 3 per KV head,
 // intermediate 8192) and the YuE2 one (2048, 16 x 128, 2 per KV head, 6144).
-// Any other shape with head_dim 64 or 128, at most 4 query heads per KV
+// Any other shape with head_dim 64 or 128, at most 8 query heads per KV
 // head, hidden and heads * head_dim at most 4608 and intermediate at most
-// 14336 (hidden and intermediate multiples of 8) runs on the generic kernel
-// of its head_dim, every GEMV input masked to its length.
-enum class StepShape { kNone, k3B, kYue2, kAny128, kAny64 };
+// 14336 (hidden and intermediate multiples of 8) runs on a generic kernel
+// of its head_dim (one for up to 4 query heads per KV head, one for up to
+// 8), every GEMV input masked to its length.
+enum class StepShape { kNone, k3B, kYue2, kAny128, kAny64, kAny128G8, kAny64G8 };
 
 static StepShape step_shape(int hidden, int heads, int kv_heads, int dim, int inter) {
     if (kv_heads < 1 || heads % kv_heads) return StepShape::kNone;
     const int G = heads / kv_heads, qw = heads * dim;
     if (dim == 128 && G == 3 && hidden == 3072 && qw == 3072 && inter == 8192) return StepShape::k3B;
     if (dim == 128 && G == 2 && hidden == 2048 && qw == 2048 && inter == 6144) return StepShape::kYue2;
-    const bool fits = G <= 4 && hidden >= 8 && hidden <= 512 * kStepAnyIth && hidden % 8 == 0 && qw <= 512 * kStepAnyItq &&
+    const bool fits = G <= 8 && hidden >= 8 && hidden <= 512 * kStepAnyIth && hidden % 8 == 0 && qw <= 512 * kStepAnyItq &&
                       inter >= 8 && inter <= 512 * kStepAnyIti && inter % 8 == 0;
-    if (!fits) return StepShape::kNone;
-    return dim == 128 ? StepShape::kAny128 : dim == 64 ? StepShape::kAny64 : StepShape::kNone;
+    if (!fits || (dim != 128 && dim != 64)) return StepShape::kNone;
+    if (G <= 4) return dim == 128 ? StepShape::kAny128 : StepShape::kAny64;
+    return dim == 128 ? StepShape::kAny128G8 : StepShape::kAny64G8;
 }
 
 bool step_supported(const Yue2Config& c, int rows, int nwg) {
@@ -814,7 +816,7 @@ bool step_supported(const Yue2Config& c, int rows, int nwg) {
     const bool pairs_fit = share(c.hidden_size) <= kPairRowsMax && share(c.intermediate_size) <= kPairRowsMax &&
                            share(qkv_rows) <= kPairRowsMax && c.hidden_size % 2 == 0 &&
                            c.intermediate_size % 2 == 0 && qkv_rows % 2 == 0;
-    return pairs_fit && G <= 4 && share(c.hidden_size) <= kResRows && max_blocks <= 24576 / kBlockKeys &&
+    return pairs_fit && G <= 8 && share(c.hidden_size) <= kResRows && max_blocks <= 24576 / kBlockKeys &&
            (size_t)(merge_words + 3 * G * c.head_dim) * 4 <= (size_t)2 * kAttnChunk * kBlockKeys * c.head_dim * 2 &&
            G * bpw * kBlockKeys * 4 <= kAttnChunk * kBlockKeys * c.head_dim * 2;
 }
@@ -861,6 +863,12 @@ int step_resident_per_cu(const StepArgs& a, int nwg, int sample) {
         case StepShape::kAny64:
             return a.rows == 1 ? resident_t<1, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds)
                                : resident_t<2, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds);
+        case StepShape::kAny128G8:
+            return a.rows == 1 ? resident_t<1, 128, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds)
+                               : resident_t<2, 128, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds);
+        case StepShape::kAny64G8:
+            return a.rows == 1 ? resident_t<1, 64, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds)
+                               : resident_t<2, 64, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(lds);
         default:
             return 0;
     }
@@ -891,6 +899,12 @@ hipError_t launch_step(hipStream_t s, const StepArgs* dev, const StepArgs& a, co
         case StepShape::kAny64:
             return a.rows == 1 ? launch_step_t<1, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds)
                                : launch_step_t<2, 64, 4, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds);
+        case StepShape::kAny128G8:
+            return a.rows == 1 ? launch_step_t<1, 128, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds)
+                               : launch_step_t<2, 128, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds);
+        case StepShape::kAny64G8:
+            return a.rows == 1 ? launch_step_t<1, 64, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds)
+                               : launch_step_t<2, 64, 8, kStepAnyIth, kStepAnyItq, kStepAnyIti, 2>(s, dev, call, nwg, lds);
         default:
             return hipErrorInvalidValue;
     }

@@ -39,13 +39,21 @@ struct Ring {
     static constexpr int SIZE = R * W;                    // uint4 of the ring
 };
 
-// The rows of this wave in [r0, r1) as items; item q of a wave is segment
-// q % NSEG of row r0 + wave + 8 * (q / NSEG).  Items past the last one (the
-// ring's look-ahead at the end of a GEMV) re-read the last item, and a wave
-// without rows reads row min(r0, n - 1): loads stay unconditional and in
-// bounds, and the re-reads hit in L2.
-template <int NSEG>
-__device__ __forceinline__ void item_at(int q, int Q, int r0, int n, int* row, int* seg) {
+// Items of a row: NSEG, or with MASK (k may be short of 512 IT) only those
+// that hold some of the row's chunks -- the chunks of the others would all be
+// masked, so skipping them changes no chain (a masked chunk adds +0).
+template <int SEG, int NSEG, bool MASK>
+__device__ __forceinline__ int row_items(int k) {
+    if constexpr (MASK) return min(NSEG, ((k >> 3) + 64 * SEG - 1) / (64 * SEG));
+    else return NSEG;
+}
+
+// The rows of this wave in [r0, r1) as items, ns per row; item q of a wave
+// is segment q % ns of row r0 + wave + 8 * (q / ns).  Items past the last
+// one (the ring's look-ahead at the end of a GEMV) re-read the last item,
+// and a wave without rows reads row min(r0, n - 1): loads stay unconditional
+// and in bounds, and the re-reads hit in L2.
+__device__ __forceinline__ void item_at(int q, int Q, int r0, int n, int ns, int* row, int* seg) {
     const int wave = threadIdx.x >> 6;
     if (Q == 0) {
         *row = min(r0, n - 1);
@@ -53,8 +61,8 @@ __device__ __forceinline__ void item_at(int q, int Q, int r0, int n, int* row, i
         return;
     }
     const int qq = min(q, Q - 1);
-    *row = r0 + wave + kRingWaves * (qq / NSEG);
-    *seg = qq % NSEG;
+    *row = r0 + wave + kRingWaves * (qq / ns);
+    *seg = qq % ns;
 }
 
 // MASK: k may be short of 64 * 8 * IT (the lane's chunks past the row end
@@ -145,12 +153,12 @@ template <int IT, bool PAIR, bool MASK = false>
 __device__ __forceinline__ void prefetch_ring(const uint16_t* w, const uint16_t* w2, int k, int r0, int r1,
                                               int n, uint4* ring) {
     using C = Ring<IT, PAIR>;
-    const int wave = threadIdx.x >> 6, span = r1 - r0;
-    const int Q = (span > wave ? (span - wave + kRingWaves - 1) / kRingWaves : 0) * C::NSEG;
+    const int wave = threadIdx.x >> 6, span = r1 - r0, ns = row_items<C::SEG, C::NSEG, MASK>(k);
+    const int Q = (span > wave ? (span - wave + kRingWaves - 1) / kRingWaves : 0) * ns;
 #pragma unroll
     for (int s = 0; s < C::R - 1; ++s) {
         int row, seg;
-        item_at<C::NSEG>(s, Q, r0, n, &row, &seg);
+        item_at(s, Q, r0, n, ns, &row, &seg);
         load_item<C::SEG, PAIR, MASK>(w, w2, k, row, seg, ring + s * C::W);
     }
 }
@@ -174,7 +182,8 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
     constexpr bool PAIR = EPI == EPI_SWIGLU;
     using C = Ring<IT, PAIR>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, span = r1 - r0;
-    const int Q = (span > wave ? (span - wave + kRingWaves - 1) / kRingWaves : 0) * C::NSEG;
+    const int ns = row_items<C::SEG, C::NSEG, MASK>(k);
+    const int Q = (span > wave ? (span - wave + kRingWaves - 1) / kRingWaves : 0) * ns;
     float acc[B], acc2[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) acc[b] = acc2[b] = 0.0f;
@@ -186,13 +195,13 @@ __device__ __forceinline__ void gemv_ring(const uint16_t* w, const uint16_t* w2,
             {
                 // refill the slot of item q - 1 with item q + R - 1
                 int row, seg;
-                item_at<C::NSEG>(q + C::R - 1, Q, r0, n, &row, &seg);
+                item_at(q + C::R - 1, Q, r0, n, ns, &row, &seg);
                 load_item<C::SEG, PAIR, MASK>(w, w2, k, row, seg, ring + ((s + C::R - 1) % C::R) * C::W);
             }
-            const int seg = q % C::NSEG;
+            const int seg = q % ns;
             dot_item<B, C::SEG, PAIR, MASK>(xs, k, seg, ring + s * C::W, acc, acc2);
-            if (seg == C::NSEG - 1) {
-                const int row = r0 + wave + kRingWaves * (q / C::NSEG);
+            if (seg == ns - 1) {
+                const int row = r0 + wave + kRingWaves * (q / ns);
                 float v[B], v2[B];
 #pragma unroll
                 for (int b = 0; b < B; ++b) {

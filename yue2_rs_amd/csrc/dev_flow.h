@@ -201,6 +201,11 @@ struct FlowAttn {
     uint64_t* att;                 // tagged [rows][att_stride / 2]: outputs 2p, 2p + 1 packed
     uint32_t epoch;
     StepState* st;
+    // a launch of its own (PLAIN): q/k/v read from the f32 rows an earlier
+    // launch wrote, [rows][qkv_stride], and the output stored as f32 rows
+    // [rows][att_stride] (both BF16-exact), in place of qkv and att
+    const float* qkv_f;
+    float* out_f;
 };
 
 // K/V blocks staged in LDS at a time by the attention (64 keys each).
@@ -231,7 +236,10 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 // pre(): called once the workgroup's q/k/v are gathered (or at once when it
 // has no keys): the caller's early requests for the phase after the
 // attention (the O projection's first weight items at long contexts).
-template <int NT, int D, int G, bool GRT, class Mark, class Pre>
+// PLAIN: the standalone decode attention (q/k/v and the output as plain f32
+// rows, qkv_f and out_f); the block statistics and partials are exchanged
+// as tagged words all the same.
+template <int NT, int D, int G, bool GRT, bool PLAIN = false, class Mark, class Pre>
 __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark,
                                           Pre&& pre) {
     constexpr int NW = NT / 64;
@@ -337,7 +345,18 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
             c_g1k = gbl(a.k_norm)[tid % HALF + HALF];
         }
     }
-    if (a.packed) {
+    if constexpr (PLAIN) {
+        // written by an earlier launch: plain loads, no tags
+        const int nq = Gq * D;
+        const float* rowf = a.qkv_f + (size_t)b * a.qkv_stride;
+        const float* qsrc = rowf + (size_t)(g * Gq) * D;
+        const float* ksrc = rowf + (size_t)(a.heads + g) * D;
+        const float* vsrc = rowf + (size_t)(a.heads + a.kv_heads + g) * D;
+        const int n = nq + (owns_new ? 2 * D : 0);
+        for (int i = tid; i < n; i += NT)
+            qkv_s[i] = *gbl(i < nq ? qsrc + i : (i < nq + D ? ksrc + (i - nq) : vsrc + (i - nq - D)));
+        __syncthreads();
+    } else if (a.packed) {
         // one gather for all three: a single wait; each word holds both
         // batch rows, this row takes its half
         const int nq = Gq * D;
@@ -870,6 +889,11 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                     },
                     st))
                 return false;
+        }
+        if constexpr (PLAIN) {
+            float* out = a.out_f + (size_t)b * a.att_stride + (size_t)g * Gq * D + o0;
+            for (int i = tid; i < no; i += NT) out[i] = rb(sum_left_to_right_a16(m_buf + i * nbp, nsb));
+            return true;
         }
         const uint32_t t_att = flow_tag(a.epoch, a.layer, FK_ATT);
         for (int i0 = 0; i0 < no; i0 += NT) {

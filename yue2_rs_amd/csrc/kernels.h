@@ -77,6 +77,12 @@ struct AttnArgs {
     int wgs, bpw;        // workgroups per (kv head, row); 64-key blocks per workgroup
     int* counters;       // [rows][kv_heads][4], zero between launches
     StepState* st;
+    // Tagged-word block maxima, sums and partials (same shapes, zero or
+    // written by earlier launches); non-null: launch_attention runs the
+    // tagged-word kernel where the shape allows (q_norm non-null, head_dim
+    // 64 or 128), its tags from st->seq and the layer, so st->seq must
+    // change between two launches of one layer.
+    uint64_t *tbmax, *tbsum, *tpart;
 };
 
 // Workgroups per (kv head, row) and 64-key blocks per workgroup for caches

@@ -163,12 +163,14 @@ extern "C" int32_t yue2_hip_bench_attention(int32_t context, int32_t rows, int32
     float* bsum = static_cast<float*>(m.alloc(blk * sizeof(float)));
     float* part = static_cast<float*>(m.alloc(blk * D * sizeof(float)));
     int32_t* counters = static_cast<int32_t*>(m.alloc((size_t)rows * Hkv * 4 * sizeof(int32_t)));
+    // the tagged-word attention's block maxima, sums and partials
+    uint64_t* tags = static_cast<uint64_t*>(m.alloc((2 + D) * blk * sizeof(uint64_t)));
     StepState* st = static_cast<StepState*>(m.alloc(sizeof(StepState)));
     float* cos_t = static_cast<float*>(m.alloc((size_t)cap * (D / 2) * sizeof(float)));
     float* sin_t = static_cast<float*>(m.alloc((size_t)cap * (D / 2) * sizeof(float)));
     float* gam = static_cast<float*>(m.alloc(D * sizeof(float)));
     uint16_t* qb = static_cast<uint16_t*>(m.alloc((size_t)rows * qkvw * 2));
-    if (!qkv || !out || !bmax || !bsum || !part || !counters || !st || !cos_t || !sin_t || !gam || !qb)
+    if (!qkv || !out || !bmax || !bsum || !part || !counters || !tags || !st || !cos_t || !sin_t || !gam || !qb)
         return fail(YUE2_ERR_ALLOC, "attention benchmark buffers");
     hipStream_t s = nullptr;
     // K, V and q ~ N(0, 1)-sized BF16 values; RoPE at the positions
@@ -195,7 +197,8 @@ extern "C" int32_t yue2_hip_bench_attention(int32_t context, int32_t rows, int32
             hipMemcpy(sin_t, hs.data(), hs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(gam, hg.data(), D * 4, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(st, &hst, sizeof(hst), hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemset(counters, 0, (size_t)rows * Hkv * 4 * sizeof(int32_t)) != hipSuccess)
+            hipMemset(counters, 0, (size_t)rows * Hkv * 4 * sizeof(int32_t)) != hipSuccess ||
+            hipMemset(tags, 0, (2 + D) * blk * sizeof(uint64_t)) != hipSuccess)
             return fail(YUE2_ERR_DEVICE, "attention benchmark input");
     }
     AttnArgs aa{};
@@ -221,17 +224,25 @@ extern "C" int32_t yue2_hip_bench_attention(int32_t context, int32_t rows, int32
     attention_geometry(Hkv, rows, max_blocks, &aa.wgs, &aa.bpw);
     aa.counters = counters;
     aa.st = st;
+    aa.tbmax = tags;
+    aa.tbsum = tags + blk;
+    aa.tpart = tags + 2 * blk;
     Events ev;
     if (!ev.ok()) return fail(YUE2_ERR_DEVICE, "hipEventCreate");
     hipError_t e = hipSuccess;
+    // the tagged-word attention's tags take the sequence and the layer: the
+    // sequence advances after each pass over the layers (as after a decode
+    // step), so no launch can pass a poll on an earlier launch's word
     for (int l = 0; l < layers && e == hipSuccess; ++l) {
         aa.layer = l;
         e = launch_attention(s, aa);
     }
+    launch_sequence(s, st, 0, 1);
     if (e == hipSuccess) e = hipEventRecord(ev.a, s);
     for (int i = 0; i < iters && e == hipSuccess; ++i) {
         aa.layer = i % layers;
         e = launch_attention(s, aa);
+        if (aa.layer == layers - 1) launch_sequence(s, st, 0, 1);
     }
     if (e == hipSuccess) e = hipEventRecord(ev.b, s);
     if (e == hipSuccess) e = hipEventSynchronize(ev.b);

@@ -48,13 +48,15 @@ struct Workspace {
     StepState* st = nullptr;
     int32_t* token_log = nullptr;
     void* step_args = nullptr;  // device copy of the step kernel's arguments
-    void* flow_block = nullptr; // the step kernel's tagged-word buffers
+    void* flow_block = nullptr; // tagged-word buffers: the step kernel's, the per-phase attention's
     size_t flow_words = 0;      // 64-bit words in flow_block
+    uint64_t *tbmax = nullptr, *tbsum = nullptr, *tpart = nullptr;  // in flow_block
     void* step_host = nullptr;  // host copy of the same (StepArgs)
     bool step_args_ready = false;
     int step_sample = 0;        // the step arguments carry a fused sampler
     // Upper bound of the launch-sequence increments since the tagged words
-    // were last cleared (each reset adds 2, each step-kernel launch 1).
+    // were last cleared (each reset adds 2, each step-kernel launch or
+    // per-phase step 1).
     int64_t seq_bound = 0;
     int ensure(int rows, int max_blocks, const Yue2Config& c);
     // Clear the step state and every sync counter (stream-ordered).

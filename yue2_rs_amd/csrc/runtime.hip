@@ -69,6 +69,28 @@ struct Carve {
     }
 };
 
+// Word counts of the tagged-word buffers (flow_block, in this order): the
+// step kernel's exchanges, and the block maxima, sums and partials that the
+// step kernel and the per-phase attention both use.
+struct FlowLayout {
+    size_t x, qkv, att, act, blk, part, smp;
+    FlowLayout(const Yue2Config& c, int rows, int blk_stride) {
+        const size_t D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
+        x = rows * (size_t)c.hidden_size;
+        qkv = rows * (Hq + 2 * Hkv) * D;
+        att = rows * Hq * D;
+        act = rows * (size_t)c.intermediate_size;
+        blk = rows * Hq * (size_t)blk_stride;
+        part = blk * D;
+        smp = kStepThreadsMax;  // one sampler word per worker
+    }
+    size_t total() const { return x + qkv + att + act + 2 * blk + part + smp; }
+    size_t bmax() const { return x + qkv + att + act; }
+    size_t bsum() const { return bmax() + blk; }
+    size_t part_at() const { return bsum() + blk; }
+    size_t smp_at() const { return part_at() + part; }
+};
+
 int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     if (block && rows == want_rows && max_blocks >= want_blocks) return YUE2_OK;
     release();
@@ -123,11 +145,28 @@ int Workspace::ensure(int want_rows, int want_blocks, const Yue2Config& c) {
     if (e == hipSuccess) e = hipMemset(counters, 0, sizeof(int32_t) * rows * Hkv * 4);
     if (e == hipSuccess) e = hipMemset(bars, 0, sizeof(int32_t) * 2);
     if (e != hipSuccess) return hip_fail(e, "hipMemset(step state)");
+    // tagged words, zero (= no tag) until first written; the sequence (in
+    // the cleared state) starts at 0 with them
+    const FlowLayout fl(c, rows, blk_stride);
+    const size_t words = fl.total();
+    e = hipMalloc(&flow_block, words * sizeof(uint64_t));
+    if (e != hipSuccess) {
+        flow_block = nullptr;
+        return hip_fail(e, "hipMalloc(dataflow words)");
+    }
+    e = hipMemset(flow_block, 0, words * sizeof(uint64_t));
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(dataflow words)");
+    flow_words = words;
+    seq_bound = 0;
+    uint64_t* fw = static_cast<uint64_t*>(flow_block);
+    tbmax = fw + fl.bmax();
+    tbsum = fw + fl.bsum();
+    tpart = fw + fl.part_at();
     return YUE2_OK;
 }
 
 void Workspace::reserve_launches(hipStream_t s, int64_t n) {
-    if (!flow_block) return;  // no step kernel on this workspace: no tagged words
+    if (!flow_block) return;  // not allocated yet: no tagged words
     if (seq_bound + n + 2 + 8 < kEpochLaunches) {
         seq_bound += n;
         return;
@@ -144,6 +183,7 @@ void Workspace::release() {
     flow_block = nullptr;
     flow_words = 0;
     seq_bound = 0;
+    tbmax = tbsum = tpart = nullptr;
     step_args = nullptr;
     step_args_ready = false;
     rows = max_blocks = 0;
@@ -195,6 +235,11 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
         attention_geometry(Hkv, rows, w.max_blocks, &aa.wgs, &aa.bpw);
         aa.counters = w.counters;
         aa.st = w.st;
+        // the tagged-word attention where the shape allows; its tags take the
+        // sequence, which advances after the step
+        aa.tbmax = w.tbmax;
+        aa.tbsum = w.tbsum;
+        aa.tpart = w.tpart;
         if ((e = launch_attention(s, aa)) != hipSuccess) return hip_fail(e, "attention");
         GemvArgs oa{L.wo, nullptr, w.att, w.x, qw, H, H, qw, rows};
         if ((e = launch_gemv(s, EPI_RESID, oa)) != hipSuccess) return hip_fail(e, "gemv(o)");
@@ -203,6 +248,9 @@ int enqueue_step(Yue2Model* m, Workspace& w, const KvView& kv, int rows, bool he
         GemvArgs da{L.wd, nullptr, w.act, w.x, I, H, H, I, rows};
         if ((e = launch_gemv(s, EPI_RESID, da)) != hipSuccess) return hip_fail(e, "gemv(down)");
     }
+    // the next step's tags (one sequence value per step, as a step-kernel
+    // launch takes; the callers reserve one per step)
+    launch_sequence(s, w.st, 0, 1);
     if (!head) return YUE2_OK;
     return enqueue_head(m, w, w.x, phase, s, rows);
 }
@@ -239,7 +287,6 @@ int prepare_step(Yue2Model* m, Workspace& w, const FusedSampler* smp) {
     if (w.step_args_ready && w.step_sample == sample) return YUE2_OK;
     const int D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
     const int H = c.hidden_size, I = c.intermediate_size;
-    const size_t qw = (size_t)Hq * D, qkvw = (size_t)(Hq + 2 * Hkv) * D;
     StepArgs a{};
     a.layers = m->layers_dev;
     a.embed = m->embed;
@@ -266,33 +313,18 @@ int prepare_step(Yue2Model* m, Workspace& w, const FusedSampler* smp) {
     // one workgroup per CU, all resident together: the polls between them
     // would otherwise wait for a workgroup that cannot start
     if (step_resident_per_cu(a, m->cus, sample) < 1) return 1;
-    // tagged-word buffers, zero (= no tag) until first written
-    const size_t n_x = rows * (size_t)H, n_qkv = rows * qkvw, n_att = rows * qw, n_act = rows * (size_t)I;
-    const size_t n_blk = rows * (size_t)Hq * w.blk_stride, n_part = n_blk * D;
-    const size_t n_smp = kStepThreadsMax;  // one sampler word per worker
-    const size_t words = n_x + n_qkv + n_att + n_act + 2 * n_blk + n_part + n_smp;
-    if (!w.flow_block) {
-        hipError_t e = hipMalloc(&w.flow_block, words * sizeof(uint64_t));
-        if (e != hipSuccess) {
-            w.flow_block = nullptr;
-            return hip_fail(e, "hipMalloc(step dataflow words)");
-        }
-        e = hipMemset(w.flow_block, 0, words * sizeof(uint64_t));
-        // the sequence restarts with the cleared words
-        if (e == hipSuccess) e = hipMemset(&w.st->seq, 0, sizeof(int32_t));
-        if (e != hipSuccess) return hip_fail(e, "hipMemset(step dataflow words)");
-        w.flow_words = words;
-        w.seq_bound = 0;
-    }
+    // the tagged-word buffers (allocated and cleared with the workspace)
+    if (!w.flow_block) return fail(YUE2_ERR_DEVICE, "no dataflow words");
+    const FlowLayout fl(c, rows, w.blk_stride);
     uint64_t* p = static_cast<uint64_t*>(w.flow_block);
     a.tx = p;
-    a.tqkv = a.tx + n_x;
-    a.tatt = a.tqkv + n_qkv;
-    a.tact = a.tatt + n_att;
-    a.tbmax = a.tact + n_act;
-    a.tbsum = a.tbmax + n_blk;
-    a.tpart = a.tbsum + n_blk;
-    a.tsmp = a.tpart + n_part;
+    a.tqkv = a.tx + fl.x;
+    a.tatt = a.tqkv + fl.qkv;
+    a.tact = a.tatt + fl.att;
+    a.tbmax = p + fl.bmax();
+    a.tbsum = p + fl.bsum();
+    a.tpart = p + fl.part_at();
+    a.tsmp = p + fl.smp_at();
     hipError_t e = hipMemcpy(w.step_args, &a, sizeof(StepArgs), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(e, "step arguments upload");
     *reinterpret_cast<StepArgs*>(w.step_host) = a;
@@ -587,7 +619,7 @@ extern "C" int32_t yue2_hip_model_advance_sequence(Yue2Model* m, int32_t add) {
     std::lock_guard<std::recursive_mutex> guard(library_lock());
     if (!m || add < 0) return fail(YUE2_ERR_ARG, "null model or negative advance");
     Workspace& w = m->ws;
-    if (!w.flow_block) return fail(YUE2_ERR_ARG, "the model has run no step-kernel forward");
+    if (!w.flow_block) return fail(YUE2_ERR_ARG, "the model has run no forward");
     launch_sequence(m->stream, w.st, 0, add);
     w.seq_bound += add;
     hipError_t e = hipStreamSynchronize(m->stream);

@@ -490,11 +490,12 @@ int32_t yue2_hip_trace_step(Yue2Model *m, Yue2Cache *c, Yue2Cache *c2, int32_t i
  * FP32 accumulation, rounded output) over `copies` weight copies; *avg_ms =
  * mean launch time over `iters` launches, *bytes = n k 2 + rows k 2 +
  * rows n 4 (the weights, BF16 inputs and f32 outputs).
- * yue2_hip_bench_attention: the split-KV decode attention of one layer (24
- * query heads, 8 KV heads, head_dim 128, QK-norm + RoPE + KV append
- * included) for `rows` rows whose new token attends `context` positions,
- * cycling over `layers` distinct layer caches; *bytes = rows 4096 context
- * (the K and V rows read).
+ * yue2_hip_bench_attention: the per-phase split-KV decode attention of one
+ * layer (24 query heads, 8 KV heads, head_dim 128, QK-norm + RoPE + KV
+ * append included) for `rows` rows whose new token attends `context`
+ * positions, cycling over `layers` distinct layer caches (the step sequence
+ * advanced after each pass over them, as after a decode step); *bytes =
+ * rows 4096 context (the K and V rows read).
  * yue2_hip_bench_copy: hipMemcpyAsync of `bytes` (a multiple of 256) from
  * one device buffer to another, once untimed and then `iters` times;
  * *avg_ms = mean time per copy (each reads and writes `bytes`).

@@ -427,6 +427,80 @@ int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, 
     return hidden_impl(m, cache, ids, n, x_out, 1);
 }
 
+/* hidden_impl for one new token in each of R caches (CFG's two rows) in one
+ * pass over the weights: every row's arithmetic is the single-cache
+ * forward's (y2o_linear computes each row's DOTs on their own; norms,
+ * rotary at each row's own position, attention over each row's own cache).
+ * A test-speed device for the replays of batch-2 decode loops. */
+static int hidden_rows(const y2o_model *m, y2o_cache *const *caches, const int32_t *ids, int R, float *x_out) {
+    const y2o_config *c = &m->c;
+    if (R <= 0 || R > 8) return Y2O_ERR_CONTEXT;
+    for (int r = 0; r < R; ++r) {
+        const y2o_cache *ca = caches[r];
+        if (ca->length + 1 > ca->capacity || ca->length + 1 > c->max_pos || ca->layers != c->layers)
+            return Y2O_ERR_CONTEXT;
+        if (ids[r] < 0 || ids[r] >= c->vocab) return Y2O_ERR_TOKEN;
+    }
+    int H = c->hidden, d = c->head_dim, qw = c->heads * d, kw = c->kv_heads * d;
+    int I = c->intermediate;
+    float *x = (float *)malloc(sizeof(float) * (size_t)R * H);
+    float *h = (float *)malloc(sizeof(float) * (size_t)R * H);
+    float *q = (float *)malloc(sizeof(float) * (size_t)R * qw);
+    float *k = (float *)malloc(sizeof(float) * (size_t)R * kw);
+    float *v = (float *)malloc(sizeof(float) * (size_t)R * kw);
+    float *att = (float *)malloc(sizeof(float) * (size_t)R * qw);
+    float *g = (float *)malloc(sizeof(float) * (size_t)R * I);
+    float *u = (float *)malloc(sizeof(float) * (size_t)R * I);
+    float *cs = (float *)malloc(sizeof(float) * (size_t)R * (d / 2));
+    float *sn = (float *)malloc(sizeof(float) * (size_t)R * (d / 2));
+    int rc = Y2O_OK;
+    if (!x || !h || !q || !k || !v || !att || !g || !u || !cs || !sn) {
+        rc = Y2O_ERR_ALLOC;
+        goto done;
+    }
+    for (int r = 0; r < R; ++r) {
+        for (int i = 0; i < H; ++i) x[(size_t)r * H + i] = rb(y2o_bf16_to_f32(m->embed[(size_t)ids[r] * H + i]));
+        y2o_rotary_table(caches[r]->length, 1, d, c->theta, cs + (size_t)r * (d / 2), sn + (size_t)r * (d / 2));
+    }
+    for (int l = 0; l < c->layers; ++l) {
+        const y2o_layer *L = &m->layers[l];
+        y2o_norm_apply(x, R, H, L->input_norm, c->eps, h);
+        y2o_linear(L->q, qw, H, h, R, q);
+        y2o_linear(L->k, kw, H, h, R, k);
+        y2o_linear(L->v, kw, H, h, R, v);
+        y2o_norm_heads(q, R * c->heads, d, L->q_norm, c->eps);
+        y2o_norm_heads(k, R * c->kv_heads, d, L->k_norm, c->eps);
+        for (int r = 0; r < R; ++r) {
+            y2o_cache *ca = caches[r];
+            float *qr = q + (size_t)r * qw, *kr = k + (size_t)r * kw;
+            y2o_rotary_apply(qr, 1, qw, d / 2, cs + (size_t)r * (d / 2), sn + (size_t)r * (d / 2));
+            y2o_rotary_apply(kr, 1, kw, d / 2, cs + (size_t)r * (d / 2), sn + (size_t)r * (d / 2));
+            float *kc = ca->key + (size_t)l * ca->capacity * kw;
+            float *vc = ca->value + (size_t)l * ca->capacity * kw;
+            memcpy(kc + (size_t)ca->length * kw, kr, sizeof(float) * (size_t)kw);
+            memcpy(vc + (size_t)ca->length * kw, v + (size_t)r * kw, sizeof(float) * (size_t)kw);
+            y2o_attention_row(qr, kc, vc, ca->length + 1, c->heads, c->kv_heads, d, att + (size_t)r * qw);
+        }
+        y2o_linear(L->o, H, qw, att, R, h);
+        for (size_t i = 0; i < (size_t)R * H; ++i) x[i] = rb(x[i] + h[i]);
+        y2o_norm_apply(x, R, H, L->post_norm, c->eps, h);
+        y2o_linear(L->gate, I, H, h, R, g);
+        y2o_linear(L->up, I, H, h, R, u);
+        for (size_t i = 0; i < (size_t)R * I; ++i) {
+            float gv = g[i];
+            gv = rb(gv / (1.0f + y2o_expf(-gv)));
+            g[i] = rb(gv * u[i]);
+        }
+        y2o_linear(L->down, H, I, g, R, h);
+        for (size_t i = 0; i < (size_t)R * H; ++i) x[i] = rb(x[i] + h[i]);
+    }
+    for (int r = 0; r < R; ++r) caches[r]->length += 1;
+    y2o_norm_apply(x, R, H, m->final_norm, c->eps, x_out);
+done:
+    free(x); free(h); free(q); free(k); free(v); free(att); free(g); free(u); free(cs); free(sn);
+    return rc;
+}
+
 /* The hidden state before final_norm: what yue2_metal_ar_stack returns
  * (src/metal.m:836-846; Rust applies the final norm, src/model.rs:567). */
 int y2o_hidden_prenorm(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out) {
@@ -457,6 +531,20 @@ int y2o_project_phase(const y2o_model *m, const float *x, int phase, float *logi
     y2o_linear(m->lm_head + (size_t)start * H, end - start, H, x, 1, logits + start);
     y2o_linear(m->lm_head + (size_t)stop * H, 1, H, x, 1, logits + stop);
     return Y2O_OK;
+}
+
+/* y2o_forward_phase of one token in each of R caches (ids[r] into
+ * caches[r]), logits[r * vocab ...]; the same results as R calls. */
+int y2o_forward_rows(const y2o_model *m, y2o_cache *const *caches, const int32_t *ids, int R, int phase,
+                     float *logits) {
+    int H = m->c.hidden, V = m->c.vocab;
+    if (R <= 0 || R > 8) return Y2O_ERR_CONTEXT;
+    float *x = (float *)malloc(sizeof(float) * (size_t)R * H);
+    if (!x) return Y2O_ERR_ALLOC;
+    int rc = hidden_rows(m, caches, ids, R, x);
+    for (int r = 0; r < R && rc == Y2O_OK; ++r) rc = y2o_project_phase(m, x + (size_t)r * H, phase, logits + (size_t)r * V);
+    free(x);
+    return rc;
 }
 
 int y2o_forward_phase(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,

@@ -224,6 +224,11 @@ int y2o_hidden(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, 
 int y2o_hidden_prenorm(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *x_out);
 /* Model::forward (src/model.rs:465-468): logits of the last row. */
 int y2o_forward(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n, float *logits);
+/* y2o_forward_phase of one token in each of R <= 8 caches in one pass over
+ * the weights (the replay of a batch-2 decode step); the same results as R
+ * calls. */
+int y2o_forward_rows(const y2o_model *m, y2o_cache *const *caches, const int32_t *ids, int R, int phase,
+                     float *logits);
 /* Model::forward_phase / project_phase (src/model.rs:469-507). */
 int y2o_forward_phase(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,
                       int phase, float *logits);

@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
             "y2o_hidden_prenorm": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_forward": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_forward_phase": (i32, [vp, C.POINTER(CacheS), vp, i32, i32, vp]),
+            "y2o_forward_rows": (i32, [vp, vp, vp, i32, i32, vp]),
             "y2o_prefill": (i32, [vp, C.POINTER(CacheS), vp, i32, vp]),
             "y2o_velocity": (i32, [vp, vp, C.POINTER(CacheS), vp, i32, f64, i32, vp]),
             "y2o_normal": (None, [C.c_uint64, i32, vp]),
@@ -171,6 +172,19 @@ class Model:
 
     def forward(self, ids, cache):
         return self.forward_phase(ids, cache, PHASE_NONE)
+
+    def forward_rows(self, ids: Sequence[int], caches: Sequence["Cache"], phase: int = PHASE_NONE) -> np.ndarray:
+        """forward_phase([ids[r]], caches[r]) for every r in one pass over the
+        weights: [len(ids), vocab] logits, the same as separate calls."""
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        if len(arr) != len(caches) or not 1 <= len(arr) <= 8:
+            raise ValueError("one id per cache, 1 to 8 rows")
+        ptrs = (C.POINTER(CacheS) * len(caches))(*[c.ptr for c in caches])
+        out = np.empty((len(arr), self.config.vocab_size), dtype=np.float32)
+        rc = lib().y2o_forward_rows(self.ref, ptrs, _p(arr), len(arr), phase, _p(out))
+        if rc:
+            raise RuntimeError(f"oracle error {rc}")
+        return out
 
     def prefill(self, ids, capacity: int, phase: int = PHASE_NONE):
         cache = Cache(self, capacity)

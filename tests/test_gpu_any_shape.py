@@ -99,7 +99,7 @@ def test_cfg_batch2_both_rows(shape, length):
         toks, _ = dec.run(1, first_logits=first if s == 0 else None)
         assert list(toks) == [t]
         got = dec.logits()
-        w0, w1 = om.forward([t], o0), om.forward([t], o1)
+        w0, w1 = om.forward_rows([t, t], [o0, o1])
         assert np.array_equal(bits(got[0]), bits(w0)), f"conditional row differs at step {s}"
         assert np.array_equal(bits(got[1]), bits(w1)), f"unconditional row differs at step {s}"
         t = int(np.argmax(O.cfg_mix(w0, w1, scale)))
@@ -148,7 +148,7 @@ def test_8b_class_layers_on_the_phase_kernels(gpu, oracle_threads):
         toks, _ = dec.run(1, first_logits=first if s == 0 else None)
         assert list(toks) == [t]
         got = dec.logits()
-        w0, w1 = om.forward([t], o0), om.forward([t], o1)
+        w0, w1 = om.forward_rows([t, t], [o0, o1])
         assert np.array_equal(bits(got[0]), bits(w0)), f"conditional row differs at step {s}"
         assert np.array_equal(bits(got[1]), bits(w1)), f"unconditional row differs at step {s}"
         t = int(np.argmax(O.cfg_mix(w0, w1, scale)))

@@ -56,7 +56,7 @@ def test_cfg_greedy_decoder_matches_oracle(reduced):
     for _ in range(steps):
         t = int(np.argmax(O.cfg_mix(ol1, ol2, scale)))
         want.append(t)
-        ol1, ol2 = om.forward([t], o1), om.forward([t], o2)
+        ol1, ol2 = om.forward_rows([t, t], [o1, o2])
     assert list(toks) == want
 
 
@@ -144,7 +144,7 @@ def test_generate_with_matrix_core_prefill(reduced, scale):
         t = O.choose(mixed, s, want, step, y2.PHASE_NONE, False, gen)
         want.append(t)
         if step + 1 < s.max_tokens:
-            logits = [om.forward([t], oc) for oc in ocs]
+            logits = list(om.forward_rows([t] * len(ocs), ocs))
     assert got.tokens == want and got.truncated
 
 
@@ -197,7 +197,7 @@ def test_3b_cfg_greedy_step_kernel_matches_oracle(gpu, oracle_threads):
     for _ in range(steps):
         t = int(np.argmax(O.cfg_mix(ol1, ol2, scale)))
         want.append(t)
-        ol1, ol2 = om.forward([t], o1), om.forward([t], o2)
+        ol1, ol2 = om.forward_rows([t, t], [o1, o2])
     assert list(toks) == want
     gm.close()
 

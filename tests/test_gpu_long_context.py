@@ -75,7 +75,7 @@ def _check_batch2(gm, om, lengths, steps, seed, scale=1.5):
         assert list(toks) == [t]
         ids.append(t)
         got = dec.logits()
-        w0, w1 = om.forward([t], o0), om.forward([t], o1)
+        w0, w1 = om.forward_rows([t, t], [o0, o1])
         assert np.array_equal(bits(got[0]), bits(w0)), f"conditional row differs at step {s}"
         assert np.array_equal(bits(got[1]), bits(w1)), f"unconditional row differs at step {s}"
         t = int(np.argmax(O.cfg_mix(w0, w1, scale)))
@@ -141,7 +141,7 @@ def test_3b_cfg_sampled_context_2048(model_3b):
         want.append(t)
         print(f"sampled CFG step {step}: oracle {t}, device {int(got[step]) if step < len(got) else None}", flush=True)
         if step + 1 < steps:
-            cond, uncond = om.forward([t], o0), om.forward([t], o1)
+            cond, uncond = om.forward_rows([t, t], [o0, o1])
     assert list(got) == want
 
 

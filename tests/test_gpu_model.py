@@ -118,6 +118,6 @@ def test_3b_256_cfg_greedy_tokens_through_the_decode_loop(full_3b):
         if step < len(toks) and int(toks[step]) != t:
             break
         if step + 1 < steps:
-            ol1, ol2 = om.forward([t], o1), om.forward([t], o2)
+            ol1, ol2 = om.forward_rows([t, t], [o1, o2])
     print(f"256 CFG greedy 3B tokens: first difference at {_first_difference(toks, want)}", flush=True)
     assert list(toks) == want

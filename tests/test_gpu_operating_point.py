@@ -71,7 +71,7 @@ def _run(model_3b, rows, steps, sampling, seed=2024, scale=1.5):
         print(f"rows {rows} step {step}: device {list(got)} oracle {want}", flush=True)
         assert list(got) == [want], f"id differs at step {step}"
         history.append(want)
-        logits = [om.forward([want], oc) for oc in ocs]
+        logits = list(om.forward_rows([want] * len(ocs), ocs))
         dev = dec.logits()
         for r in range(rows):
             assert np.array_equal(bits(dev[r]), bits(logits[r])), f"row {r} logits differ at step {step}"

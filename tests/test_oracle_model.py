@@ -300,3 +300,28 @@ def test_project_phase_ranges(phase, lo, hi, stop):
     keep[stop] = True
     assert np.array_equal(ph[keep].view(np.uint32), full[keep].view(np.uint32))
     assert np.all(ph[~keep] == -np.inf)
+
+
+def test_forward_rows_equals_separate_forwards(small):
+    """forward_rows (one new token in each of several caches, one pass over
+    the weights) gives each row what its own forward gives: caches of
+    different lengths (so different RoPE angles and attention spans), the
+    rows' caches then hold the same K/V, for several steps."""
+    om = O.Model(small)
+    V = SMALL.vocab_size
+    pa, pb = synthetic.prompt(11, V, seed=21), synthetic.prompt(4, V, seed=22)
+    sep = [om.prefill(pa, 32)[0], om.prefill(pb, 32)[0]]
+    row = [om.prefill(pa, 32)[0], om.prefill(pb, 32)[0]]
+    ta, tb = 7, 300
+    for step in range(6):
+        want = np.stack([om.forward([ta], sep[0]), om.forward([tb], sep[1])])
+        got = om.forward_rows([ta, tb], row)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"step {step}"
+        ta, tb = int(np.argmax(want[0])), int(np.argmax(want[1]))
+    for s, r in zip(sep, row):
+        assert s.length == r.length
+        (ks, vs), (kr, vr) = s.arrays(), r.arrays()
+        assert np.array_equal(ks.view(np.uint32), kr.view(np.uint32))
+        assert np.array_equal(vs.view(np.uint32), vr.view(np.uint32))
+    with pytest.raises(ValueError):
+        om.forward_rows([1, 2], row[:1])

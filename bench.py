@@ -328,7 +328,7 @@ def main() -> int:
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
         threads = min(16, os.cpu_count() or 1)  # one GPU's share of the host's CPUs
-        cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 64)
+        cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 512)
         log(f"CPU baseline: {cpu['value']:.3f} steps/s with {threads} threads")
 
     out = {
@@ -511,7 +511,7 @@ def long_context(args, y2, synthetic, c, ckpt, model, step_kernel):
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
         threads = min(16, os.cpu_count() or 1)
-        cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 16)
+        cpu = cpu_baseline(ckpt, c, P, args.scale, sampling, threads, args.cpu_budget, 64)
         log(f"CPU baseline: {cpu['value']:.3f} steps/s with {threads} threads")
     timed = steps - 1
     out = {

@@ -14,6 +14,10 @@
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+#if defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+#define Y2O_SIMD 1
+#endif
 
 /* Protocol constants (src/protocol.rs:6-16). */
 #define EOD 151643
@@ -175,22 +179,127 @@ float y2o_dot_f32(const float *a, const float *b, int k) {
     return butterfly64(acc);
 }
 
-/* Linear::apply_range + finish without bias (src/tensor.rs:946-1118): every
- * output is DOT(W[i], x[r]) rounded to BF16. */
-void y2o_linear(const uint16_t *w, int out, int in, const float *x, int rows, float *y) {
+#ifdef Y2O_SIMD
+/* The same DOT eight lanes at a time (speed only: every lane's chain is the
+ * same fmaf sequence, so the result is y2o_dot_bf16's bit for bit).  xt is
+ * x in lane-major order, xt[blk * 512 + e * 64 + l] = x[blk * 512 + 8 l + e]
+ * (lane_major).  Lanes of a partial group of eight (k not a multiple of 64
+ * in the last 512-block) run the scalar chain. */
+static float dot_bf16_lanes(const uint16_t *a, const float *x, const float *xt, int k) {
+    __m256 va[8];
+    for (int v = 0; v < 8; ++v) va[v] = _mm256_setzero_ps();
+    for (int base = 0; base < k; base += 512) {
+        int lanes = (k - base) / 8;
+        if (lanes > 64) lanes = 64;
+        const int groups = lanes / 8;
+        const float *xb = xt + base;
+        for (int v = 0; v < groups; ++v) {
+            /* lanes 8v .. 8v + 7: 64 consecutive weights, transposed so that
+             * c[e] holds element e of each of the eight lanes */
+            const __m128i *ap = (const __m128i *)(a + base + 64 * v);
+            const __m128i r0 = _mm_loadu_si128(ap + 0), r1 = _mm_loadu_si128(ap + 1);
+            const __m128i r2 = _mm_loadu_si128(ap + 2), r3 = _mm_loadu_si128(ap + 3);
+            const __m128i r4 = _mm_loadu_si128(ap + 4), r5 = _mm_loadu_si128(ap + 5);
+            const __m128i r6 = _mm_loadu_si128(ap + 6), r7 = _mm_loadu_si128(ap + 7);
+            const __m128i t0 = _mm_unpacklo_epi16(r0, r1), t1 = _mm_unpackhi_epi16(r0, r1);
+            const __m128i t2 = _mm_unpacklo_epi16(r2, r3), t3 = _mm_unpackhi_epi16(r2, r3);
+            const __m128i t4 = _mm_unpacklo_epi16(r4, r5), t5 = _mm_unpackhi_epi16(r4, r5);
+            const __m128i t6 = _mm_unpacklo_epi16(r6, r7), t7 = _mm_unpackhi_epi16(r6, r7);
+            const __m128i u0 = _mm_unpacklo_epi32(t0, t2), u1 = _mm_unpackhi_epi32(t0, t2);
+            const __m128i u2 = _mm_unpacklo_epi32(t1, t3), u3 = _mm_unpackhi_epi32(t1, t3);
+            const __m128i u4 = _mm_unpacklo_epi32(t4, t6), u5 = _mm_unpackhi_epi32(t4, t6);
+            const __m128i u6 = _mm_unpacklo_epi32(t5, t7), u7 = _mm_unpackhi_epi32(t5, t7);
+            __m128i c[8];
+            c[0] = _mm_unpacklo_epi64(u0, u4); c[1] = _mm_unpackhi_epi64(u0, u4);
+            c[2] = _mm_unpacklo_epi64(u1, u5); c[3] = _mm_unpackhi_epi64(u1, u5);
+            c[4] = _mm_unpacklo_epi64(u2, u6); c[5] = _mm_unpackhi_epi64(u2, u6);
+            c[6] = _mm_unpacklo_epi64(u3, u7); c[7] = _mm_unpackhi_epi64(u3, u7);
+            __m256 acc = va[v];
+            for (int e = 0; e < 8; ++e) {
+                const __m256 av = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(c[e]), 16));
+                acc = _mm256_fmadd_ps(av, _mm256_loadu_ps(xb + e * 64 + 8 * v), acc);
+            }
+            va[v] = acc;
+        }
+        if (lanes % 8) {
+            float part[8];
+            _mm256_storeu_ps(part, va[groups]);
+            for (int j = 0; j < lanes % 8; ++j) {
+                const int l = 8 * groups + j;
+                const uint16_t *ap = a + base + 8 * l;
+                const float *bp = x + base + 8 * l;
+                float sacc = part[j];
+                for (int e = 0; e < 8; ++e) sacc = fmaf(y2o_bf16_to_f32(ap[e]), bp[e], sacc);
+                part[j] = sacc;
+            }
+            va[groups] = _mm256_loadu_ps(part);
+        }
+    }
+    float acc[64];
+    for (int v = 0; v < 8; ++v) _mm256_storeu_ps(acc + 8 * v, va[v]);
+    return butterfly64(acc);
+}
+
+/* rows x vectors of length k in lane-major order (dot_bf16_lanes), each
+ * padded to whole 512-blocks; NULL when out of memory. */
+static float *lane_major(const float *x, int rows, int k) {
+    const size_t xs = (size_t)((k + 511) / 512) * 512;
+    float *xt = (float *)calloc(xs * (size_t)(rows > 0 ? rows : 1), sizeof(float));
+    if (!xt) return NULL;
+    for (int r = 0; r < rows; ++r)
+        for (int base = 0; base < k; base += 512) {
+            int lanes = (k - base) / 8;
+            if (lanes > 64) lanes = 64;
+            for (int l = 0; l < lanes; ++l)
+                for (int e = 0; e < 8; ++e)
+                    xt[(size_t)r * xs + base + e * 64 + l] = x[(size_t)r * k + base + 8 * l + e];
+        }
+    return xt;
+}
+#endif
+
+/* DOT(W[i], x[r]) for i < out, r < rows into y[r * out + i] (rb: rounded to
+ * BF16), optionally plus rb(bias[i]) before the rounding. */
+static void dot_rows(const uint16_t *w, int out, int in, const float *x, int rows, const float *bias, int round,
+                     float *y) {
+#ifdef Y2O_SIMD
+    float *xt = lane_major(x, rows, in);
+    if (xt) {
+        const size_t xs = (size_t)((in + 511) / 512) * 512;
+#pragma omp parallel for schedule(static) num_threads(g_threads)
+        for (int i = 0; i < out; ++i) {
+            const uint16_t *wi = w + (size_t)i * in;
+            const float bi = bias ? rb(bias[i]) : 0.0f;
+            for (int r = 0; r < rows; ++r) {
+                const float d = dot_bf16_lanes(wi, x + (size_t)r * in, xt + (size_t)r * xs, in);
+                y[(size_t)r * out + i] = bias ? rb(d + bi) : round ? rb(d) : d;
+            }
+        }
+        free(xt);
+        return;
+    }
+#endif
 #pragma omp parallel for schedule(static) num_threads(g_threads)
     for (int i = 0; i < out; ++i) {
         const uint16_t *wi = w + (size_t)i * in;
-        for (int r = 0; r < rows; ++r)
-            y[(size_t)r * out + i] = rb(y2o_dot_bf16(wi, x + (size_t)r * in, in));
+        const float bi = bias ? rb(bias[i]) : 0.0f;
+        for (int r = 0; r < rows; ++r) {
+            const float d = y2o_dot_bf16(wi, x + (size_t)r * in, in);
+            y[(size_t)r * out + i] = bias ? rb(d + bi) : round ? rb(d) : d;
+        }
     }
+}
+
+/* Linear::apply_range + finish without bias (src/tensor.rs:946-1118): every
+ * output is DOT(W[i], x[r]) rounded to BF16. */
+void y2o_linear(const uint16_t *w, int out, int in, const float *x, int rows, float *y) {
+    dot_rows(w, out, in, x, rows, NULL, 1, y);
 }
 
 /* Unrounded DOT of every row: the yue2_metal_vector contract (the caller's
  * Linear::finish rounds), src/metal.m:545-603. */
 void y2o_gemv_raw(const uint16_t *w, int rows, int cols, const float *x, float *out) {
-#pragma omp parallel for schedule(static) num_threads(g_threads)
-    for (int i = 0; i < rows; ++i) out[i] = y2o_dot_bf16(w + (size_t)i * cols, x, cols);
+    dot_rows(w, rows, cols, x, 1, NULL, 0, out);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -591,12 +700,7 @@ int y2o_prefill(const y2o_model *m, y2o_cache *cache, const int32_t *ids, int n,
  * y = rb(DOT(W[i], x[r]) + rb(b[i])). */
 static void linear_bias(const uint16_t *w, const float *b, int out, int in, const float *x, int rows,
                         float *y) {
-#pragma omp parallel for schedule(static) num_threads(g_threads)
-    for (int i = 0; i < out; ++i) {
-        const uint16_t *wi = w + (size_t)i * in;
-        float bi = rb(b[i]);
-        for (int r = 0; r < rows; ++r) y[(size_t)r * out + i] = rb(y2o_dot_bf16(wi, x + (size_t)r * in, in) + bi);
-    }
+    dot_rows(w, out, in, x, rows, b, 1, y);
 }
 
 int y2o_velocity(const y2o_model *m, const y2o_nar *nar, const y2o_cache *cache, const float *state,

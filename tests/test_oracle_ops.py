@@ -17,6 +17,8 @@ transposed operand, a wrong index, a sum in the wrong order) fails it:
 - CFG mix (src/sampling.rs:261-266): scale 1 gives the conditional row and
   scale 0 the unconditional one when the difference is exact.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -76,6 +78,36 @@ def test_linear_small_integers_is_exact(k, oracle_threads):
     y = linear(_bf16(wi.astype(np.float32)), xi.astype(np.float32))
     exact = (xi @ wi.T).astype(np.float64)  # |sum| < 2^24: every partial sum is exact in f32
     assert np.array_equal(y, rb(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("k", [8, 24, 64, 72, 504, 512, 520, 1000, 3072, 4104])
+def test_linear_lanes_equal_the_scalar_dot(k, oracle_threads):
+    """The linears run the DOT eight lanes at a time (vector fmas, the same
+    chain per lane); every output equals the scalar y2o_dot_bf16 bit for bit,
+    signed zeros included, for row lengths with partial 64- and 8-lane
+    groups."""
+    rng = np.random.default_rng(100 + k)
+    n = 40
+    w = rng.standard_normal((n, k)).astype(np.float32) * 0.05
+    w[rng.random((n, k)) < 0.2] = 0.0
+    w[3, :] = -0.0  # a row of negative zeros: -0 products
+    w[5, :] = 0.0
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    x[0, rng.random(k) < 0.3] = -0.0
+    x[1, ::7] = 1e-30  # tiny products (flushed or subnormal: as the scalar chain)
+    w16 = _bf16(w)
+    got = linear(w16, x)
+    dot = O.lib().y2o_dot_bf16
+    dot.restype = C.c_float
+    raw_want = np.empty_like(got)
+    for r in range(2):
+        xr = np.ascontiguousarray(x[r])
+        for i in range(n):
+            raw_want[r, i] = dot(C.c_void_p(_p(w16[i])), C.c_void_p(_p(xr)), k)
+    want = rb(raw_want)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    raw = gemv_raw(w16, x[0])
+    assert np.array_equal(rb(raw).view(np.uint32), want[0].view(np.uint32))
 
 
 def test_gemv_within_dot_product_bound(oracle_threads):

@@ -238,8 +238,11 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 // attention (the O projection's first weight items at long contexts).
 // PLAIN: the standalone decode attention (q/k/v and the output as plain f32
 // rows, qkv_f and out_f); the block statistics and partials are exchanged
-// as tagged words all the same.
-template <int NT, int D, int G, bool GRT, bool PLAIN = false, class Mark, class Pre>
+// as tagged words all the same.  HOIST: a wave takes a head's softmax
+// maximum from the gathered block maxima once for its consecutive items of
+// that head (long contexts, where a workgroup has many blocks per head),
+// not once per item.
+template <int NT, int D, int G, bool GRT, bool PLAIN = false, bool HOIST = PLAIN, class Mark, class Pre>
 __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark,
                                           Pre&& pre) {
     constexpr int NW = NT / 64;
@@ -665,11 +668,22 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         // exp(s - M) and the block sums in one pass, one (head, block) item
         // per wave; each wave takes its head's M from the gathered block
         // maxima itself, so no barrier separates the steps
+        float m_head = 0.0f;  // HOIST: the maximum of head h_last
+        int h_last = -1;
         for (int i = wave; i < Gq * nbl; i += NW) {
             const int h = i / nbl, bl = i % nbl;
-            float m = -__builtin_huge_valf();
-            for (int k = lane; k < nb; k += 64) m = fmaxf(m, red_s[h * nb + k]);
-            m = xor_max<32>(m);
+            float m;
+            if (!HOIST || h != h_last) {  // (uniform over the wave)
+                m = -__builtin_huge_valf();
+                for (int k = lane; k < nb; k += 64) m = fmaxf(m, red_s[h * nb + k]);
+                m = xor_max<32>(m);
+                if constexpr (HOIST) {
+                    m_head = m;
+                    h_last = h;
+                }
+            } else {
+                m = m_head;
+            }
             const int jl = bl * kBlockKeys + lane;
             float v = 0.0f;  // keys past the context add +0
             if (jl < nk) {

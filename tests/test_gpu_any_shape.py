@@ -156,3 +156,52 @@ def test_8b_class_layers_on_the_phase_kernels(gpu, oracle_threads):
     for c in (g0, g1):
         c.close()
     gm.close()
+
+
+# Shapes the per-phase attention hands to its counter-sync body (dev_attn.h)
+# instead of the tagged-word one: head_dim 256, and 40 KV heads of 64 at CFG
+# batch 2 over caches of 24576 positions (80 (KV head, row) groups leave the
+# tagged-word body three workgroups each, and their staged p of 128 blocks
+# would outgrow its K region).
+PHASE_ONLY = {
+    "d256-g2": _config(1024, 4, 2, 256, 2048),
+    "d64-kv40": _config(2560, 40, 40, 64, 4096),
+}
+
+
+@pytest.mark.parametrize("name", list(PHASE_ONLY))
+def test_counter_sync_attention_shapes(name, gpu, oracle_threads):
+    """Batch-1 greedy steps after a decode-order prefill, then CFG batch-2
+    steps from 2048-position caches of capacity 24576 through the captured
+    decoder: every logit bit for bit against the oracle."""
+    ck = synthetic.checkpoint(PHASE_ONLY[name], seed=4)
+    gm, om = y2.Model.open(ck), O.Model(ck)
+    gm.set_step_kernel(False)
+    ids = synthetic.prompt(40, ck.config.vocab_size, seed=5)
+    gcache, glog = gm.prefill_phase(ids, 40 + 6)
+    ocache, olog = om.prefill(ids, 40 + 6)
+    assert np.array_equal(bits(glog), bits(olog)), "prefill logits differ"
+    for step in range(6):
+        t = int(np.argmax(olog))
+        glog, olog = gm.forward([t], gcache), om.forward([t], ocache)
+        assert np.array_equal(bits(glog), bits(olog)), f"logits differ at step {step}"
+    gcache.close()
+    V, steps, scale = ck.config.vocab_size, 2, 1.5
+    (g0, o0), (g1, o1) = (_caches(gm, om, n, 24576, 31 + i) for i, n in enumerate((2048, 2011)))
+    dec = y2.Decoder(gm, g0, g1, scale=scale)
+    t = 77
+    first = np.zeros(2 * V, np.float32)
+    first[t] = first[V + t] = 1.0
+    for s in range(steps):
+        print(f"{name}: CFG step {s}, token {t}", flush=True)
+        toks, _ = dec.run(1, first_logits=first if s == 0 else None)
+        assert list(toks) == [t]
+        got = dec.logits()
+        w0, w1 = om.forward_rows([t, t], [o0, o1])
+        assert np.array_equal(bits(got[0]), bits(w0)), f"conditional row differs at step {s}"
+        assert np.array_equal(bits(got[1]), bits(w1)), f"unconditional row differs at step {s}"
+        t = int(np.argmax(O.cfg_mix(w0, w1, scale)))
+    dec.close()
+    for c in (g0, g1):
+        c.close()
+    gm.close()

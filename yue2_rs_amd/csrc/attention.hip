@@ -116,10 +116,14 @@ template <int D, int G, bool GRT>
 static bool launch_flow_t(hipStream_t s, const AttnArgs& a, int wpg, size_t lds, hipError_t* e) {
     const void* fn = reinterpret_cast<const void*>(&attention_flow_kernel<D, G, GRT>);
     static const hipError_t attr = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFlowLdsMax);
-    int per_cu = 0;
-    if (attr != hipSuccess || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kAttnThreads, lds) != hipSuccess ||
-        per_cu < 1)
-        return false;
+    static size_t fits = 0;  // the largest lds found to fit (fewer bytes fit as well)
+    if (attr != hipSuccess) return false;
+    if (lds > fits) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kAttnThreads, lds) != hipSuccess || per_cu < 1)
+            return false;
+        fits = lds;
+    }
     attention_flow_kernel<D, G, GRT><<<dim3(wpg, a.kv_heads, a.rows), kAttnThreads, lds, s>>>(a);
     *e = hipGetLastError();
     return true;

@@ -108,6 +108,35 @@ def test_cfg_batch2_both_rows(shape, length):
         c.close()
 
 
+def test_phase_kernels_cfg_batch2(shape):
+    """The same shape on the per-phase kernels (their attention: the step
+    kernel's attention body in a launch of its own, the group size at run
+    time past two and three query heads per KV head): CFG batch-2 steps
+    from 4096-position caches, both rows' logits bit for bit."""
+    ck, gm, om = shape
+    assert not gm.set_step_kernel(False)
+    try:
+        V, steps, scale = ck.config.vocab_size, 2, 1.5
+        (g0, o0), (g1, o1) = (_caches(gm, om, n, n + steps, 41 + i) for i, n in enumerate((4096, 4059)))
+        dec = y2.Decoder(gm, g0, g1, scale=scale)
+        t = 123
+        first = np.zeros(2 * V, np.float32)
+        first[t] = first[V + t] = 1.0
+        for s in range(steps):
+            toks, _ = dec.run(1, first_logits=first if s == 0 else None)
+            assert list(toks) == [t]
+            got = dec.logits()
+            w0, w1 = om.forward_rows([t, t], [o0, o1])
+            assert np.array_equal(bits(got[0]), bits(w0)), f"conditional row differs at step {s}"
+            assert np.array_equal(bits(got[1]), bits(w1)), f"unconditional row differs at step {s}"
+            t = int(np.argmax(O.cfg_mix(w0, w1, scale)))
+        dec.close()
+        for c in (g0, g1):
+            c.close()
+    finally:
+        assert gm.set_step_kernel(True)
+
+
 def test_sampled_cfg_generate(shape):
     """sampling::generate with T 0.9, top-k 50, top-p 0.93, penalty 1.2/50, CFG 1.5."""
     ck, gm, om = shape

@@ -35,22 +35,48 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(const GemvArgs a) {
     constexpr bool PAIR = EPI == EPI_SWIGLU;
     const int tid = threadIdx.x, k = a.k, n = a.n;
     const int r0 = part_lo(n, blockIdx.x, gridDim.x), r1 = part_lo(n, blockIdx.x + 1, gridDim.x);
+    // The inputs, the residual rows and the gammas (all written before this
+    // launch) are requested before the ring's first items: loads complete in
+    // order, so staging them then waits for them alone, and the norm runs
+    // while the ring's loads are in flight.  Element tid + 512 j of each row
+    // (k <= 512 IT); the loads are unconditional (past the end they re-read
+    // the last element, never staged), so that no branch join makes the
+    // compiler wait for everything issued before them.
+    float xv[B][IT], gv[NORM ? IT : 1], rv = 0.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int j = 0; j < IT; ++j) xv[b][j] = a.x[(size_t)b * a.x_stride + min(tid + j * kGemvThreads, k - 1)];
+    if constexpr (NORM)
+#pragma unroll
+        for (int j = 0; j < IT; ++j) gv[j] = a.gamma[min(tid + j * kGemvThreads, k - 1)];
+    const int span = r1 - r0;
+    if constexpr (EPI == EPI_RESID) {
+        const int t = min(tid, max(B * span - 1, 0));
+        rv = a.y[(size_t)(t / max(span, 1)) * a.y_stride + r0 + t % max(span, 1)];
+    }
     uint4 ring[Ring<IT, PAIR>::SIZE];
     prefetch_ring<IT, PAIR, true>(a.w, a.w2, k, r0, r1, n, ring);
+#pragma unroll
     for (int b = 0; b < B; ++b)
-        for (int i = tid; i < k; i += kGemvThreads) xs[b * k + i] = a.x[(size_t)b * a.x_stride + i];
+#pragma unroll
+        for (int j = 0; j < IT; ++j)
+            if (tid + j * kGemvThreads < k) xs[b * k + tid + j * kGemvThreads] = xv[b][j];
     float* res = xs + B * k;
-    if constexpr (EPI == EPI_RESID) {
-        const int span = r1 - r0;
-        if (tid < B * span) res[tid] = a.y[(size_t)(tid / span) * a.y_stride + r0 + tid % span];
-    }
+    if constexpr (EPI == EPI_RESID)
+        if (tid < B * span) res[tid] = rv;
     __syncthreads();
     if constexpr (NORM) {
         float s[B];
         norm_scales_block<kGemvThreads, B>(xs, k, a.eps, (blockIdx.x == 0 && a.st) ? &a.st->norm_fallbacks : nullptr,
                                            s);
+#pragma unroll
         for (int b = 0; b < B; ++b)
-            for (int i = tid; i < k; i += kGemvThreads) xs[b * k + i] = rb(rb(xs[b * k + i] * s[b]) * a.gamma[i]);
+#pragma unroll
+            for (int j = 0; j < IT; ++j) {
+                const int i = tid + j * kGemvThreads;
+                if (i < k) xs[b * k + i] = rb(rb(xs[b * k + i] * s[b]) * gv[j]);
+            }
         __syncthreads();
     }
     gemv_ring<B, EPI, IT, true>(a.w, a.w2, xs, k, a.y, nullptr, 0, a.y_stride, r0, r1, n, ring, res);

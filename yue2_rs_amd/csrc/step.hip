@@ -622,13 +622,25 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
                 return;
             }
         }
+        // the rows' embeddings are requested before the ring's first items
+        // (loads complete in order: staging them then waits for them alone);
+        // element tid + 512 j (H <= 512 ITH), unconditional loads (past the
+        // end they re-read element H - 1, never staged)
+        float ev[B][ITH];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const auto* e = gbl(a->embed + (size_t)ids[b] * H);
+#pragma unroll
+            for (int j = 0; j < ITH; ++j) ev[b][j] = bf16(e[min(tid + j * kStepThreads, H - 1)]);
+        }
         load_gamma<ITH>(layer_at(a, 0)->in_norm, H, gam);
         prefetch_ring<ITH, false, MH>(layer_at(a, 0)->wqkv, nullptr, H, xlo<B>(qkvw, wg, nwg),
                                   xlo<B>(qkvw, wg + 1, nwg), qkvw, ring);
-        for (int b = 0; b < B; ++b) {
-            const auto* e = gbl(a->embed + (size_t)ids[b] * H);
-            for (int i = tid; i < H; i += kStepThreads) lds[b * H + i] = bf16(e[i]);
-        }
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int j = 0; j < ITH; ++j)
+                if (tid + j * kStepThreads < H) lds[b * H + tid + j * kStepThreads] = ev[b][j];
         __syncthreads();
     }
 

@@ -241,8 +241,12 @@ __host__ __device__ constexpr size_t attn_flow_lds(int G, int D, int bpw) {
 // as tagged words all the same.  HOIST: a wave takes a head's softmax
 // maximum from the gathered block maxima once for its consecutive items of
 // that head (long contexts, where a workgroup has many blocks per head),
-// not once per item.
-template <int NT, int D, int G, bool GRT, bool PLAIN = false, bool HOIST = PLAIN, class Mark, class Pre>
+// not once per item.  LATEV: the first V chunk is requested after the
+// q/k/v gather instead of before it (the gather's polls retire behind every
+// load issued before them, and V is not needed before the block
+// statistics) and staged before the block-maximum gather.
+template <int NT, int D, int G, bool GRT, bool PLAIN = false, bool HOIST = PLAIN, bool LATEV = PLAIN, class Mark,
+          class Pre>
 __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int b, float* lds, Mark&& mark,
                                           Pre&& pre) {
     constexpr int NW = NT / 64;
@@ -326,7 +330,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     // ---- phase 0: early requests, queries, new key/value --------------------
     uint4 kr[PER], vr[PER];
     load_chunk(Kc, 0, kr);
-    load_chunk(Vc, 0, vr);
+    if constexpr (!LATEV) load_chunk(Vc, 0, vr);
     // RoPE / QK-norm constants of the (head, d) pair this thread rotates.
     // XP: more pairs than threads (eight query heads at head_dim 128): thread
     // t also rotates pair t + NT, a pair of the new key with the same d.
@@ -396,6 +400,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
     asm volatile("" ::"v"(c_cos), "v"(c_sin), "v"(c_g0), "v"(c_g1));
     if constexpr (XP) asm volatile("" ::"v"(c_g0k), "v"(c_g1k));
     mark();
+    if constexpr (LATEV) load_chunk(Vc, 0, vr);
     pre();
     // Norm::heads (src/tensor.rs:1160): the scale of the sequential sum of
     // squares per head, decided by a whole wave per head (wave Gq: the new key)
@@ -411,7 +416,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         }
     }
     store_chunk(Ks, kr, false);
-    store_chunk(Vs, vr, true);
+    if constexpr (!LATEV) store_chunk(Vs, vr, true);
     __syncthreads();
     // rotate-half RoPE (src/model.rs:151-168); the new key and value go to the
     // cache for later steps and straight into the staged chunk for this one
@@ -463,7 +468,7 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         for (int d = tid; d < D; d += NT) {
             const uint16_t bits = bf16_bits(v_s[d]);
             gblw(Vc)[(size_t)pos * D + d] = bits;
-            if (pos - j0 < kAttnChunk * kBlockKeys) *staged(Vs, pos - j0, d, true) = bits;
+            if (!LATEV && pos - j0 < kAttnChunk * kBlockKeys) *staged(Vs, pos - j0, d, true) = bits;
         }
     __syncthreads();
     mark();
@@ -659,6 +664,15 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
         // region: the scores are done with it and p is staged there only
         // after the super-block sums are gathered
         float* bl_s = reinterpret_cast<float*>(Ks);
+        if constexpr (LATEV) {
+            // the first V chunk staged, and the owner's new value row patched
+            // in after a barrier (other threads stage that row)
+            store_chunk(Vs, vr, true);
+            if (owns_new && pos - j0 < kAttnChunk * kBlockKeys) {
+                __syncthreads();
+                for (int d = tid; d < D; d += NT) *staged(Vs, pos - j0, d, true) = bf16_bits(v_s[d]);
+            }
+        }
         // (long contexts) the second V chunk is requested before the waits
         // for the group's block statistics
         if (kAttnChunk < nbl) load_chunk(Vc, kAttnChunk, vr);

@@ -693,7 +693,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(const StepArgs* args
             };
             if (group < groups) {
                 const FlowAttn fa = layer_attn(a, call.kv, group / kvh, l, epoch, wpg, D, kPack<B>);
-                if (!attn_flow<kStepThreads, D, G, MASK == 2, false, OE>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); },
+                if (!attn_flow<kStepThreads, D, G, MASK == 2, false, OE, !OE && MASK == 0>(fa, wg % wpg, group % kvh, group / kvh, lds, [&] { tr.mark(); },
                                                    pre_o))
                     return;
             } else {

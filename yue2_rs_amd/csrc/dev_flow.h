@@ -673,9 +673,6 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                 for (int d = tid; d < D; d += NT) *staged(Vs, pos - j0, d, true) = bf16_bits(v_s[d]);
             }
         }
-        // (long contexts) the second V chunk is requested before the waits
-        // for the group's block statistics
-        if (kAttnChunk < nbl) load_chunk(Vc, kAttnChunk, vr);
         if (!gather<NT, (G * MAXNB + NT - 1) / NT>(a.bmax + hbase, Gq * nb, nb, a.blk_stride, t_bmax, red_s, st))
             return false;
         mark();
@@ -747,6 +744,11 @@ __device__ __forceinline__ bool attn_flow(const FlowAttn& a, int wi, int g, int 
                 return false;
         }
         mark();
+        // (long contexts) the second V chunk, requested only now: the two
+        // statistic gathers above would have waited behind it (their polls
+        // retire after every load issued before them); it lands during the
+        // total, p and the first chunk's PV
+        if (kAttnChunk < nbl) load_chunk(Vc, kAttnChunk, vr);
         if (tid < Gq) t_s[tid] = sum_left_to_right_a16(red_s + tid * nbp, nsb);  // super-block sums
         __syncthreads();
         // p = e / total into the K region (the scores are done with it), in
